@@ -1,0 +1,366 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X fused layer kernels (one JSON line on stdout).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workloads c1,c2,...]
+
+A step is one call of a fused kernel on one batch of synthetic input already
+resident in HBM. The headline workload (`value`) is configs[1], the partial
+rotary f32 q,k [1,8,1024,64]; every config (c0..c4b) is measured and
+reported under `per_config`.
+
+Timing: W untimed warm-up calls, then the stream is held by a short spin
+kernel while the K timed calls are enqueued with a HIP event pair around each,
+so the GPU runs them back to back and the events time the kernels, not the
+Python launch path. Input/output buffer sets rotate so the footprint is
+>= 512 MB (twice the 256 MB Infinity Cache): the timed calls read HBM, not
+MALL. `warm_*` figures repeat one buffer set and are labelled as such.
+
+The CPU baseline is the oracle's C restatement of the reference CPU path
+(oracle/nsr_oracle.c) timed on this host on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+MALL_DEFEAT_BYTES = 512 << 20
+METRIC = "achieved HBM GB/s (% of MI355X peak) and µs/call per fused kernel"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workloads", default="c0,c1,c1t,c2,c3,c4a,c4b")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline (0 = skip)")
+    ap.add_argument("--no-rotate", action="store_true", help="one buffer set (warm MALL) for all timings")
+    return ap.parse_args()
+
+
+# ----------------------------------------------------------- workloads ---
+
+class Workload:
+    """Buffer sets and a launch(i) closure for one config."""
+
+    def __init__(self, name, desc, alg_bytes, set_bytes, make_set, launch, kernel, dtype):
+        self.name, self.desc, self.alg_bytes = name, desc, alg_bytes
+        self.set_bytes, self.make_set, self.launch = set_bytes, make_set, launch
+        self.kernel, self.dtype = kernel, dtype
+
+
+def build_workload(name):
+    import numpy as np
+    import torch
+
+    from nspeech_amd import abi, configs
+
+    L = abi.lib()
+    dev = "cuda:0"
+    stream = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+
+    def T(a):
+        a = np.ascontiguousarray(a)
+        if a.dtype == np.uint16:
+            return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).to(dev)
+        if a.dtype == np.uint32:
+            return torch.from_numpy(a.view(np.int32)).to(dev)
+        return torch.from_numpy(a).to(dev)
+
+    if name == "c0":
+        c = configs.c0()
+        x0, g, b = T(c["x"]), T(c["gamma"]), T(c["beta"])
+
+        def make_set(_):
+            return {"x": x0.clone(), "y": torch.empty_like(x0)}
+
+        def launch(s):
+            abi.check(L.nsr_layernorm(s["x"].data_ptr(), 0, g.data_ptr(), b.data_ptr(), 0, s["y"].data_ptr(), 0,
+                                      125, 1024, 1024, 1024, 1e-5, 0, 0, stream()))
+
+        return Workload(name, "LayerNorm f32 x[1,125,1024] affine eps 1e-5", configs.algorithmic_bytes("c0"),
+                        2 * 125 * 1024 * 4, make_set, launch, "nsrk_ln_f32_f32_nc4", "f32")
+
+    if name in ("c1", "c1t"):
+        c = configs.c1()
+        q0, k0 = T(c["q"]), T(c["k"])
+        table = abi.rope_table(1024, 32, 10000.0).to(dev) if name == "c1t" else None
+        tp = table.data_ptr() if table is not None else None
+
+        def make_set(_):
+            return {"q": q0.clone(), "k": k0.clone(), "qo": torch.empty_like(q0), "ko": torch.empty_like(k0)}
+
+        def launch(s):
+            abi.check(L.nsr_rotary_partial_interleaved_f32(s["q"].data_ptr(), s["k"].data_ptr(), s["qo"].data_ptr(),
+                                                           s["ko"].data_ptr(), 1, 8, 8, 1024, 64, 32, 10000.0, 0, tp,
+                                                           1024 if tp else 0, stream()))
+
+        extra = 1024 * 32 * 4 if name == "c1t" else 0
+        return Workload(name, "partial interleaved rotary f32 q,k [1,8,1024,64] rot 32 theta 1e4"
+                        + (" (host RoPE table)" if name == "c1t" else " (in-kernel sincos)"),
+                        configs.algorithmic_bytes("c1") + extra, 4 * 8 * 1024 * 64 * 4, make_set, launch,
+                        "nsrk_rope_table_f32" if name == "c1t" else "nsrk_rope_compute_f32", "f32")
+
+    if name in ("c2", "c4b"):
+        c = configs.c2() if name == "c2" else configs.c4b()
+        x0 = T(c["x"])
+        g, b, a = T(c["gamma"]), T(c["beta"]), T(c["alpha"])
+        B, C, TT = c["x"].shape
+        gs = C if c["gamma"].ndim == 2 else 0
+
+        def make_set(_):
+            return {"x": x0.clone() if name == "c2" else x0, "o": torch.empty_like(x0)}
+
+        def launch(s):
+            abi.check(L.nsr_adain_snake_f32(s["x"].data_ptr(), g.data_ptr(), b.data_ptr(), a.data_ptr(), 0, gs, gs,
+                                            s["o"].data_ptr(), B, C, TT, 1e-5, stream()))
+
+        kern = "nsrk_adain_res_b256_nv5_a" if name == "c2" else "nsrk_adain_res_b1024_nv20_a"
+        return Workload(name, f"AdaIN1d+Snake f32 x[{B},{C},{TT}]", configs.algorithmic_bytes(name),
+                        2 * x0.numel() * 4, make_set, launch, kern, "f32")
+
+    if name == "c3":
+        c = configs.c3()
+        blocks0, ids = T(c["blocks"]), T(c["ids"])
+
+        def make_set(_):
+            return {"b": blocks0.clone(), "o": torch.empty((4096, 416), dtype=torch.float32, device=dev)}
+
+        def launch(s):
+            abi.check(L.nsr_q8_0_embed_gather(s["b"].data_ptr(), 32768, 416, ids.data_ptr(), 0, 4096,
+                                              s["o"].data_ptr(), 1, None, stream()))
+
+        return Workload(name, "GGUF Q8_0 gather-dequant + SiLU, table 32768x416, 4096 ids -> f32 [4096,416]",
+                        configs.algorithmic_bytes("c3"), blocks0.numel() + 4096 * 416 * 4, make_set, launch,
+                        "nsrk_q8_0_gather_silu_u32", "i8xf16->f32")
+
+    if name == "c4a":
+        c = configs.c4a()
+        x0, r0 = T(c["x"]), T(c["res"])
+        g, b = T(c["gamma"]), T(c["beta"])
+
+        def make_set(_):
+            return {"x": x0.clone(), "r": r0.clone(), "h": torch.empty_like(x0), "y": torch.empty_like(x0)}
+
+        def launch(s):
+            abi.check(L.nsr_residual_add_layernorm(s["x"].data_ptr(), 2, s["r"].data_ptr(), 2, s["h"].data_ptr(), 2,
+                                                   g.data_ptr(), b.data_ptr(), 0, s["y"].data_ptr(), 2, 24000, 1024,
+                                                   1e-5, 0, 2, stream()))
+
+        return Workload(name, "residual add + LayerNorm + GELU(erf) bf16 x,res[32,750,1024] (writes h and y)",
+                        configs.algorithmic_bytes("c4a"), 4 * x0.numel() * 2, make_set, launch,
+                        "nsrk_resln_bf16_nc2", "bf16")
+    raise KeyError(name)
+
+
+def spin_rate_cycles_per_ms():
+    import torch
+
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(1000)
+    s.record()
+    torch.cuda._sleep(2_000_000)
+    e.record()
+    torch.cuda.synchronize()
+    return 2_000_000 / max(s.elapsed_time(e), 1e-3)
+
+
+def time_workload(w, steps, warmup, rotate, cyc_per_ms):
+    import torch
+
+    nsets = max(1, math.ceil(MALL_DEFEAT_BYTES / w.set_bytes)) if rotate else 1
+    sets = [w.make_set(i) for i in range(nsets)]
+    torch.cuda.synchronize()
+    for i in range(warmup):
+        w.launch(sets[i % nsets])
+    torch.cuda.synchronize()
+
+    def run(order):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in order]
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        # hold the stream while the calls are enqueued (~40 us of host work each)
+        torch.cuda._sleep(int(cyc_per_ms * (5.0 + 0.06 * len(order))))
+        t0.record()
+        for (a, b), i in zip(ev, order):
+            a.record()
+            w.launch(sets[i])
+            b.record()
+        t1.record()
+        torch.cuda.synchronize()
+        per = [a.elapsed_time(b) * 1e3 for a, b in ev]  # us
+        return per, t0.elapsed_time(t1) * 1e3 / len(order)
+
+    cold_per, cold_total = run([i % nsets for i in range(steps)])
+    warm_per, warm_total = run([0] * steps)
+    del sets
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    gbs = lambda us: w.alg_bytes / (us * 1e-6) / 1e9  # noqa: E731
+    mean_us = statistics.fmean(cold_per)
+    return {
+        "workload": w.desc,
+        "kernel": w.kernel,
+        "dtype": w.dtype,
+        "algorithmic_bytes": w.alg_bytes,
+        "buffer_sets": nsets,
+        "footprint_MB": round(nsets * w.set_bytes / 2**20, 1),
+        "us_per_call": round(mean_us, 3),
+        "us_per_call_median": round(statistics.median(cold_per), 3),
+        "us_per_call_min": round(min(cold_per), 3),
+        "us_per_call_back_to_back": round(cold_total, 3),
+        "GBs": round(gbs(mean_us), 1),
+        "frac_of_peak": round(gbs(mean_us) / HBM_PEAK_GBS, 4),
+        "GBs_back_to_back": round(gbs(cold_total), 1),
+        "warm_us_per_call": round(statistics.fmean(warm_per), 3),
+        "warm_GBs": round(gbs(statistics.fmean(warm_per)), 1),
+    }
+
+
+# -------------------------------------------------------- CPU baseline ---
+
+def cpu_baseline(budget_s, names):
+    """Oracle restatement of the reference CPU path on a bounded sample."""
+    import numpy as np
+
+    from nspeech_amd import configs
+    from oracle import restated as R
+
+    ncores = len(os.sched_getaffinity(0))
+    out = {}
+
+    def timed(fn, alg_bytes, seconds):
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            dt = time.perf_counter() - t0
+            if dt >= seconds:
+                break
+        us = dt / n * 1e6
+        return {"us_per_call": round(us, 1), "GBs": round(alg_bytes / (us * 1e-6) / 1e9, 3), "calls": n}
+
+    per = budget_s / max(1, 2 * len(names))
+    for nm in names:
+        if nm == "c1" or nm == "c1t":
+            c = configs.c1()
+            f1 = lambda: (R.rotary(c["q"], 32, 1e4, 0), R.rotary(c["k"], 32, 1e4, 0))  # noqa: E731
+            fn = lambda: (R.rotary(c["q"], 32, 1e4, 0, nthreads=ncores), R.rotary(c["k"], 32, 1e4, 0,  # noqa: E731
+                                                                                   nthreads=ncores))
+            sample = "full config (q and k)"
+        elif nm == "c0":
+            c = configs.c0()
+            f1 = lambda: R.layernorm_candle(c["x"], c["gamma"], c["beta"])  # noqa: E731
+            fn = lambda: R.layernorm_candle(c["x"], c["gamma"], c["beta"], nthreads=ncores)  # noqa: E731
+            sample = "full config"
+        elif nm in ("c2", "c4b"):
+            c = configs.c2() if nm == "c2" else configs.c4b(B=1, C=8)
+            f1 = lambda: R.adain_snake(c["x"], c["gamma"], c["beta"], c["alpha"])  # noqa: E731
+            fn = lambda: R.adain_snake(c["x"], c["gamma"], c["beta"], c["alpha"], nthreads=ncores)  # noqa: E731
+            sample = "full config" if nm == "c2" else "8 of the 1024 rows (x[1,8,115200]), scaled"
+        elif nm == "c3":
+            c = configs.c3()
+            ids = c["ids"].astype(np.int64)
+            f1 = lambda: R.q8_0_embedding(c["blocks"], 32768, 416, ids, act=1)  # noqa: E731
+            fn = None
+            sample = "full config (whole-table dequantize, index_select, silu)"
+        elif nm == "c4a":
+            c = configs.c4a(rows=750)
+            wb, bb = configs.f32_to_bf16_bits(c["gamma"]), configs.f32_to_bf16_bits(c["beta"])
+            f1 = lambda: R.resadd_ln_gelu_bf16(c["x"], c["res"], wb, bb)  # noqa: E731
+            fn = lambda: R.resadd_ln_gelu_bf16(c["x"], c["res"], wb, bb, nthreads=ncores)  # noqa: E731
+            sample = "750 of the 24000 rows, scaled"
+        else:
+            continue
+        alg = configs.algorithmic_bytes("c1" if nm == "c1t" else nm)
+        scale = {"c4b": 1024 // 8, "c4a": 24000 // 750}.get(nm, 1)
+        r1 = timed(f1, alg / scale, per)
+        entry = {"sample": sample, "threads_1": {"us_per_call": round(r1["us_per_call"] * scale, 1),
+                                                 "GBs": r1["GBs"]}}
+        if fn is not None:
+            rn = timed(fn, alg / scale, per)
+            entry[f"threads_{ncores}"] = {"us_per_call": round(rn["us_per_call"] * scale, 1), "GBs": rn["GBs"]}
+        out[nm] = entry
+    return out, ncores
+
+
+# ----------------------------------------------------------------- main ---
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs on a single MI355X (got --gpus {args.gpus}). "
+              "The kernels shard with no exchange along rows/positions; see DESIGN.md.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from nspeech_amd import abi
+
+    abi.init()
+    names = [n for n in args.workloads.split(",") if n]
+    cyc = spin_rate_cycles_per_ms()
+    results = {}
+    for nm in names:
+        w = build_workload(nm)
+        results[nm] = time_workload(w, args.steps, args.warmup, not args.no_rotate, cyc)
+        del w
+        torch.cuda.empty_cache()
+        print(f"[bench] {nm}: {results[nm]['us_per_call']} us/call, {results[nm]['GBs']} GB/s "
+              f"({100 * results[nm]['frac_of_peak']:.1f}% of peak)", file=sys.stderr, flush=True)
+
+    head = results.get("c1") or next(iter(results.values()))
+    cpu = None
+    if args.cpu_seconds > 0:
+        per_cfg, ncores = cpu_baseline(args.cpu_seconds, [n for n in names if n != "c1t"])
+        h = per_cfg.get("c1") or next(iter(per_cfg.values()))
+        cpu = {"value": h["threads_1"]["GBs"], "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": "oracle C restatement of the reference CPU path (apply_rotary_pos_emb, "
+                         "src/moonshine/decoder.rs:85-183) on the full configs[1] input, 1 thread; "
+                         f"{ncores}-thread and per-config figures under per_config",
+               "per_config": per_cfg, "host_cores": ncores}
+
+    traffic = None
+    tf = ROOT / "profiles" / "pmc_traffic.txt"
+    if tf.exists():
+        for line in tf.read_text().splitlines():
+            parts = line.split()
+            if len(parts) >= 2 and parts[0] == head["kernel"]:
+                traffic = int(parts[1])
+
+    line = {
+        "metric": METRIC,
+        "value": round(head["algorithmic_bytes"] / (head["us_per_call_back_to_back"] * 1e-6) / 1e9, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us_per_call_back_to_back"] / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": head["dtype"],
+        "data": "synthetic (seeded numpy inputs of the benchmark configs; no model weights needed)",
+        "config": {"workload": "configs[1]: " + head["workload"], "buffer_sets": head["buffer_sets"],
+                   "footprint_MB": head["footprint_MB"], "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": head["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": head["frac_of_peak"], "traffic": traffic, "kernel": head["kernel"],
+                     "us_per_call": head["us_per_call"]},
+        "cpu_baseline": cpu,
+        "per_config": results,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

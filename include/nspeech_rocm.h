@@ -1,0 +1,226 @@
+/*
+ * nspeech_rocm.h — C ABI of the MI355X (gfx950) fused layer kernels.
+ *
+ * Drop-in boundary for nspeech's GPU kernel dispatch layer. Every entry point
+ * below names the reference interface it replaces (paths relative to the
+ * dropbox/nspeech source tree). The reference binds its kernels from Rust
+ * (src/triton_kernels.rs, src/kokoro/gpu_backend.rs); a Rust `rocm` feature
+ * binds these symbols with plain `extern "C"` declarations.
+ *
+ * Conventions (mirroring src/triton_kernels.rs):
+ *   - All tensor arguments are DEVICE pointers, caller-owned, contiguous,
+ *     row-major. Outputs are written, never allocated (the reference's
+ *     `out: &Tensor` / `enc_*` style, triton_kernels.rs:598,713,742,862-1423).
+ *   - Launches are asynchronous on `stream` (a hipStream_t; NULL = the null
+ *     stream). Nothing here synchronises, except where noted.
+ *   - Every function returns nsr_status. On failure nothing is launched and
+ *     nsr_last_error() returns a message (thread-local), the equivalent of the
+ *     reference's anyhow::bail! (triton_kernels.rs:138).
+ *   - Kernels come from precompiled gfx950 code objects (one per kernel
+ *     unit), embedded in the library and loaded with hipModuleLoadData on
+ *     first use per device (or from files named by nsr_init). Module handles
+ *     are immutable after load; the launch functions are thread-safe.
+ */
+#ifndef NSPEECH_ROCM_H
+#define NSPEECH_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum nsr_status {
+  NSR_OK = 0,
+  NSR_ERR_BAD_ARG = 1,     /* null pointer, bad shape, misaligned, ... */
+  NSR_ERR_NOT_INIT = 2,    /* code object could not be loaded */
+  NSR_ERR_HIP = 3,         /* a HIP runtime call failed (message has hipGetErrorString) */
+  NSR_ERR_UNSUPPORTED = 4  /* valid request this build does not implement */
+} nsr_status;
+
+typedef enum nsr_dtype {
+  NSR_F32 = 0,
+  NSR_F16 = 1,
+  NSR_BF16 = 2
+} nsr_dtype;
+
+typedef enum nsr_index_dtype {
+  NSR_IDX_U32 = 0,
+  NSR_IDX_I64 = 1
+} nsr_index_dtype;
+
+/* Epilogue activation applied to a kernel's main output. */
+typedef enum nsr_act {
+  NSR_ACT_NONE = 0,
+  NSR_ACT_SILU = 1,      /* x / (1 + exp(-x))          candle silu */
+  NSR_ACT_GELU_ERF = 2   /* x * 0.5 * (1 + erf(x/√2))  candle gelu_erf */
+} nsr_act;
+
+/* LayerNorm flags. */
+#define NSR_LN_UNIT_OFFSET 1u /* scale = gamma + 1 (moonshine/encoder.rs:68-76) */
+
+typedef void* nsr_stream_t; /* hipStream_t */
+
+/* ---- library ------------------------------------------------------------ */
+
+/* Version string of this library. */
+const char* nsr_version(void);
+
+/* Load the gfx950 code objects on the current device. code_object_dir ==
+ * NULL uses the code objects embedded in the library; otherwise the directory
+ * holding nsr_<unit>_gfx950.hsaco files. Calling it is optional: every launch
+ * loads the embedded objects on first use on a device. The first call on a
+ * device decides; later calls only report its status.
+ * Replaces TritonKernels::load / DecoderKernels::load / KokoroKernels::load
+ * (kernels/out/generated/triton_metal_gen.rs:39-106) and load_kernel_pipeline
+ * (src/triton_kernels.rs:1401). */
+nsr_status nsr_init(const char* code_object_dir);
+
+/* Message describing the last failure on this thread ("" if none). */
+const char* nsr_last_error(void);
+
+/* Number of kernels in the loaded code object for the current device (0 if
+ * not loaded). Used by tests to check the module is complete. */
+int nsr_kernel_count(void);
+
+/* ---- LayerNorm family ---------------------------------------------------- */
+
+/* y[r, :] = act( (x[r,:] - mean) / sqrt(var + eps) * scale + beta )
+ *   scale = gamma (or gamma + 1 with NSR_LN_UNIT_OFFSET, or 1 if gamma NULL),
+ *   beta NULL = 0. Mean and biased variance over the row, two-pass, fp32.
+ * x_dtype/y_dtype: F32, F16 or BF16; gamma/beta: F32 or F16 (param_dtype).
+ * ld_x / ld_y: row strides in elements (>= n_cols).
+ * Replaces: candle_nn::LayerNorm::forward as configured at
+ *   src/parakeet/fast_conformer.rs:721-725,778-782 (f32, affine);
+ *   UnitOffsetLayerNorm::forward src/moonshine/encoder.rs:68-76;
+ *   LayerNorm::forward (weight only) src/moonshine/decoder.rs:67-74;
+ *   triton_layernorm_unit_offset src/triton_kernels.rs:312,
+ *   triton_layernorm_bare :345, triton_layernorm_std_f32in :598,
+ *   enc_layernorm_std_f32in :880, enc_layernorm_bare :1291,
+ *   enc_layernorm_unit_offset :1309. */
+nsr_status nsr_layernorm(const void* x, nsr_dtype x_dtype,
+                         const void* gamma, const void* beta, nsr_dtype param_dtype,
+                         void* y, nsr_dtype y_dtype,
+                         int64_t n_rows, int64_t n_cols, int64_t ld_x, int64_t ld_y,
+                         float eps, unsigned flags, nsr_act act,
+                         nsr_stream_t stream);
+
+/* Fused residual add + LayerNorm (+ activation):
+ *   h = x + res            (rounded to h_dtype; written to h_out unless NULL)
+ *   y = act(LN(h) * scale + beta)
+ * LN statistics are taken over the ROUNDED h, exactly as an unfused
+ * add -> store -> LayerNorm chain would see it. Row stride = n_cols.
+ * Replaces residual_add_layernorm_fused (kernels/moonshine_kernels.py:955-991)
+ * dispatched by triton_residual_add_layernorm src/triton_kernels.rs:742 and
+ * enc_residual_add_layernorm :1012; and the CPU chain fast_add
+ * (src/fast_ops.rs:41-47) followed by LayerNorm and gelu_erf
+ * (src/moonshine/encoder.rs:106). */
+nsr_status nsr_residual_add_layernorm(const void* x, nsr_dtype x_dtype,
+                                      const void* res, nsr_dtype res_dtype,
+                                      void* h_out, nsr_dtype h_dtype,
+                                      const void* gamma, const void* beta,
+                                      nsr_dtype param_dtype,
+                                      void* y, nsr_dtype y_dtype,
+                                      int64_t n_rows, int64_t n_cols, float eps,
+                                      unsigned flags, nsr_act act,
+                                      nsr_stream_t stream);
+
+/* ---- Partial interleaved rotary ----------------------------------------- */
+
+/* Host-side (no GPU work): fill table[max_pos][2*half] (half = rotary_dim/2)
+ * with cos (first half) then sin (second half) of pos * inv_freq[i],
+ * inv_freq[i] = 1 / theta^(2i/rotary_dim), all in f32 exactly as
+ * src/moonshine/gpu_decoder.rs:326-340 builds its RoPE table. */
+nsr_status nsr_rope_table_f32(float* host_table, int64_t max_pos, int rotary_dim,
+                              float theta);
+
+/* Out-of-place (or in-place when q_out == q) partial interleaved rotary over
+ * q [B, Hq, T, Dh] and k [B, Hk, T, Dh] (k may be NULL):
+ *   for pair i < rotary_dim/2 at position p = pos0 + t:
+ *     o[2i]   = x[2i]*cos(p*f_i) - x[2i+1]*sin(p*f_i)
+ *     o[2i+1] = x[2i+1]*cos(p*f_i) + x[2i]*sin(p*f_i)
+ *   dims >= rotary_dim are copied unchanged.
+ * rope_table: NULL = cos/sin computed in-kernel from theta (f32 angle, as the
+ * reference); otherwise a DEVICE table laid out as nsr_rope_table_f32 writes,
+ * with at least pos0 + T rows (table_rows).
+ * Replaces apply_rotary_pos_emb + RotaryEmbedding::forward
+ * (src/moonshine/decoder.rs:85-183) and the rope part of
+ * enc_rope_qk_cache_fused (src/triton_kernels.rs:975). */
+nsr_status nsr_rotary_partial_interleaved_f32(const float* q, const float* k,
+                                              float* q_out, float* k_out,
+                                              int64_t B, int64_t Hq, int64_t Hk,
+                                              int64_t T, int64_t Dh, int rotary_dim,
+                                              float theta, int64_t pos0,
+                                              const float* rope_table,
+                                              int64_t table_rows,
+                                              nsr_stream_t stream);
+
+/* ---- AdaIN1d + Snake ------------------------------------------------------ */
+
+/* For x [B, C, T] f32, per (b, c) row:
+ *   mean, var = biased statistics over T (two-pass accuracy, f32)
+ *   y   = (1 + gamma[b,c]) * (x - mean) / sqrt(var + eps) + beta[b,c]
+ *   out = y + sin(alpha[c]*y)^2 * (1 / (alpha[c] + 1e-9))
+ * gamma/beta/alpha have param_dtype F32 or F16. gamma_bstride/beta_bstride:
+ * elements between batches of gamma/beta (0 = shared over the batch, C =
+ * per batch). alpha is per channel [C].
+ * x is read from HBM once while a row fits on chip (T up to about 150k
+ * elements); longer rows use a two-kernel stats + apply path.
+ * Replaces adain (src/kokoro/decoder.rs:1416-1428) followed by
+ * snake_activation_tensor (:1471-1476), and
+ * KokoroGpuBackend::adain_snake_f32 (src/kokoro/gpu_backend.rs:181-185,
+ * Metal impl src/kokoro/gpu_decoder.rs:886-950). */
+nsr_status nsr_adain_snake_f32(const float* x, const void* gamma, const void* beta,
+                               const void* alpha, nsr_dtype param_dtype,
+                               int64_t gamma_bstride, int64_t beta_bstride,
+                               float* out, int64_t B, int64_t C, int64_t T,
+                               float eps, nsr_stream_t stream);
+
+/* ---- GGUF Q8_0 embedding gather-dequant ----------------------------------- */
+
+/* blocks: the GGUF Q8_0 table, vocab rows of d/32 blocks of 34 bytes
+ * ({f16 d; int8 qs[32]}), row stride 34*d/32 bytes (2-byte aligned rows are
+ * fine). ids: n_ids token ids (U32 or I64). out[n, j] = act(qs * d) as f32.
+ * An id >= vocab (or < 0) writes a zero row and, when err_flag is not NULL,
+ * stores 1 to *err_flag (device int32); the reference's index_select fails
+ * on such ids instead.
+ * Replaces QEmbedding::forward (src/parakeet/quantized_layers.rs:65-71:
+ * QTensor::dequantize of the whole table, then index_select) and the
+ * dequantized-table lookups of src/moonshine/decoder.rs:508-515,569 and
+ * src/moonshine/gpu_decoder.rs:244-248,474-477; act = NSR_ACT_SILU fuses the
+ * following silu (src/parakeet/fast_conformer.rs:207). */
+nsr_status nsr_q8_0_embed_gather(const void* blocks, int64_t vocab, int64_t d,
+                                 const void* ids, nsr_index_dtype id_dtype,
+                                 int64_t n_ids, float* out, nsr_act act,
+                                 int32_t* err_flag, nsr_stream_t stream);
+
+/* ---- Elementwise ----------------------------------------------------------- */
+
+/* y = act(x) elementwise (act SILU or GELU_ERF); dtype F32, F16 or BF16
+ * (computed in f32). Replaces triton_gelu src/triton_kernels.rs:412 /
+ * enc_gelu :1328 (kernels/moonshine_kernels.py:388-400), Tensor::gelu_erf
+ * (src/moonshine/encoder.rs:106), candle_nn::ops::silu
+ * (src/moonshine/decoder.rs:409, src/parakeet/fast_conformer.rs:207,574) and
+ * silu_forward (kernels/moonshine_kernels.py:473-485). */
+nsr_status nsr_activation(const void* x, void* y, nsr_dtype dtype, int64_t n,
+                          nsr_act act, nsr_stream_t stream);
+
+/* out[i] = silu(fc1[n + i]) * fc1[i] for i < n (fc1 holds 2n elements:
+ * x part first, gate second). Replaces triton_glu_silu
+ * src/triton_kernels.rs:713 (glu_silu_fused, kernels/moonshine_kernels.py:846-862)
+ * and the GLU of DecoderMLP::forward src/moonshine/decoder.rs:403-411. */
+nsr_status nsr_glu_silu(const void* fc1, void* out, nsr_dtype dtype, int64_t n,
+                        nsr_stream_t stream);
+
+/* out = x + res elementwise (same dtype). Replaces fast_add
+ * (src/fast_ops.rs:16-47), triton_residual_add src/triton_kernels.rs:383 and
+ * enc_residual_add :1340. */
+nsr_status nsr_residual_add(const void* x, const void* res, void* out,
+                            nsr_dtype dtype, int64_t n, nsr_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NSPEECH_ROCM_H */

@@ -1,0 +1,215 @@
+"""ctypes binding of libnspeech_rocm.so (include/nspeech_rocm.h) for torch tensors.
+
+PyTorch supplies device memory and streams; every computation happens in the
+library's gfx950 kernels. Importing this module imports torch first so the
+library binds to the HIP runtime torch already loaded (same SONAME).
+There is no fallback: if the library is missing or a call fails, NsrError
+is raised.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import torch  # noqa: F401  (load torch's HIP runtime before the library)
+
+LIB_DIR = Path(__file__).resolve().parent / "lib"
+LIB_PATH = LIB_DIR / "libnspeech_rocm.so"
+HEADER = Path(__file__).resolve().parent.parent / "include" / "nspeech_rocm.h"
+
+NSR_OK, NSR_ERR_BAD_ARG, NSR_ERR_NOT_INIT, NSR_ERR_HIP, NSR_ERR_UNSUPPORTED = range(5)
+NSR_F32, NSR_F16, NSR_BF16 = 0, 1, 2
+NSR_IDX_U32, NSR_IDX_I64 = 0, 1
+ACT = {"none": 0, "silu": 1, "gelu": 2, "gelu_erf": 2}
+NSR_LN_UNIT_OFFSET = 1
+
+_DT = {torch.float32: NSR_F32, torch.float16: NSR_F16, torch.bfloat16: NSR_BF16}
+
+
+class NsrError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"nspeech_rocm error {status}: {msg}")
+        self.status = status
+
+
+_lib = None
+_P = C.c_void_p
+_I64 = C.c_int64
+
+
+def lib() -> C.CDLL:
+    """Load the library (once). Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise ImportError(f"{LIB_PATH} is not built: run `python -m nspeech_amd.build`")
+        L = C.CDLL(str(LIB_PATH))
+        L.nsr_version.restype = C.c_char_p
+        L.nsr_last_error.restype = C.c_char_p
+        L.nsr_init.argtypes = [C.c_char_p]
+        L.nsr_kernel_count.restype = C.c_int
+        L.nsr_layernorm.argtypes = [_P, C.c_int, _P, _P, C.c_int, _P, C.c_int, _I64, _I64, _I64, _I64,
+                                    C.c_float, C.c_uint, C.c_int, _P]
+        L.nsr_residual_add_layernorm.argtypes = [_P, C.c_int, _P, C.c_int, _P, C.c_int, _P, _P, C.c_int, _P,
+                                                 C.c_int, _I64, _I64, C.c_float, C.c_uint, C.c_int, _P]
+        L.nsr_rope_table_f32.argtypes = [_P, _I64, C.c_int, C.c_float]
+        L.nsr_rotary_partial_interleaved_f32.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, C.c_int,
+                                                         C.c_float, _I64, _P, _I64, _P]
+        L.nsr_adain_snake_f32.argtypes = [_P, _P, _P, _P, C.c_int, _I64, _I64, _P, _I64, _I64, _I64, C.c_float,
+                                          _P]
+        L.nsr_q8_0_embed_gather.argtypes = [_P, _I64, _I64, _P, C.c_int, _I64, _P, C.c_int, _P, _P]
+        L.nsr_activation.argtypes = [_P, _P, C.c_int, _I64, C.c_int, _P]
+        L.nsr_glu_silu.argtypes = [_P, _P, C.c_int, _I64, _P]
+        L.nsr_residual_add.argtypes = [_P, _P, _P, C.c_int, _I64, _P]
+        for name in ("nsr_init", "nsr_layernorm", "nsr_residual_add_layernorm", "nsr_rope_table_f32",
+                     "nsr_rotary_partial_interleaved_f32", "nsr_adain_snake_f32", "nsr_q8_0_embed_gather",
+                     "nsr_activation", "nsr_glu_silu", "nsr_residual_add"):
+            getattr(L, name).restype = C.c_int
+        _lib = L
+    return _lib
+
+
+def header_functions() -> list[str]:
+    """Names of the functions include/nspeech_rocm.h declares."""
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nsr_[a-z0-9_]+)\s*\(", text)))
+
+
+def check(status: int) -> None:
+    if status != NSR_OK:
+        raise NsrError(status, lib().nsr_last_error().decode())
+
+
+def version() -> str:
+    return lib().nsr_version().decode()
+
+
+def init(code_object_dir: str | None = None) -> None:
+    check(lib().nsr_init(code_object_dir.encode() if code_object_dir else None))
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
+
+
+def _ptr(t: torch.Tensor | None):
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("nspeech_rocm kernels take device tensors")
+    if not t.is_contiguous():
+        raise ValueError("nspeech_rocm kernels take contiguous tensors")
+    return t.data_ptr()
+
+
+def _dt(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {t.dtype}") from None
+
+
+# ------------------------------------------------------------------ ops ---
+
+def layernorm(x, gamma=None, beta=None, *, eps=1e-5, unit_offset=False, act="none", out=None,
+              out_dtype=None, stream=None):
+    """LN over the last dim of a contiguous tensor."""
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    if out is None:
+        out = torch.empty(x.shape, dtype=out_dtype or x.dtype, device=x.device)
+    pdt = NSR_F32
+    if gamma is not None:
+        pdt = _dt(gamma)
+    elif beta is not None:
+        pdt = _dt(beta)
+    check(lib().nsr_layernorm(_ptr(x), _dt(x), _ptr(gamma), _ptr(beta), pdt, _ptr(out), _dt(out), rows, cols,
+                              cols, cols, eps, NSR_LN_UNIT_OFFSET if unit_offset else 0, ACT[act], _stream(stream)))
+    return out
+
+
+def residual_add_layernorm(x, res, gamma=None, beta=None, *, eps=1e-5, act="none", h_out=None, write_h=True,
+                           out=None, h_dtype=None, out_dtype=None, unit_offset=False, stream=None):
+    """Returns (h, y); h is None when write_h is False."""
+    cols = x.shape[-1]
+    rows = x.numel() // cols
+    if write_h and h_out is None:
+        h_out = torch.empty(x.shape, dtype=h_dtype or x.dtype, device=x.device)
+    if out is None:
+        out = torch.empty(x.shape, dtype=out_dtype or x.dtype, device=x.device)
+    hd = _dt(h_out) if h_out is not None else (_DT[h_dtype] if h_dtype is not None else _dt(x))
+    pdt = _dt(gamma) if gamma is not None else (_dt(beta) if beta is not None else NSR_F32)
+    check(lib().nsr_residual_add_layernorm(_ptr(x), _dt(x), _ptr(res), _dt(res), _ptr(h_out), hd, _ptr(gamma),
+                                           _ptr(beta), pdt, _ptr(out), _dt(out), rows, cols, eps,
+                                           NSR_LN_UNIT_OFFSET if unit_offset else 0, ACT[act], _stream(stream)))
+    return h_out, out
+
+
+def rope_table(max_pos: int, rotary_dim: int, theta: float) -> torch.Tensor:
+    """Host-built f32 RoPE table [max_pos, rotary_dim] (CPU tensor)."""
+    t = torch.empty((max_pos, rotary_dim), dtype=torch.float32)
+    check(lib().nsr_rope_table_f32(t.data_ptr(), max_pos, rotary_dim, theta))
+    return t
+
+
+def rotary(q, k, rotary_dim, theta=10000.0, pos0=0, *, table=None, q_out=None, k_out=None, stream=None):
+    """q [B,Hq,T,Dh], k [B,Hk,T,Dh] or None. Returns (q_out, k_out)."""
+    B, Hq, T, Dh = q.shape
+    Hk = k.shape[1] if k is not None else 0
+    if q_out is None:
+        q_out = torch.empty_like(q)
+    if k is not None and k_out is None:
+        k_out = torch.empty_like(k)
+    rows = table.shape[0] if table is not None else 0
+    check(lib().nsr_rotary_partial_interleaved_f32(_ptr(q), _ptr(k), _ptr(q_out), _ptr(k_out), B, Hq, Hk, T, Dh,
+                                                   rotary_dim, theta, pos0, _ptr(table), rows, _stream(stream)))
+    return q_out, k_out
+
+
+def adain_snake(x, gamma, beta, alpha, *, eps=1e-5, out=None, stream=None):
+    """x [B,C,T] f32; gamma/beta [C] or [B,C]; alpha [C]; params f32 or f16."""
+    B, Cc, T = x.shape
+    if out is None:
+        out = torch.empty_like(x)
+    gs = Cc if gamma.dim() == 2 else 0
+    bs = Cc if beta.dim() == 2 else 0
+    check(lib().nsr_adain_snake_f32(_ptr(x), _ptr(gamma), _ptr(beta), _ptr(alpha), _dt(gamma), gs, bs, _ptr(out),
+                                    B, Cc, T, eps, _stream(stream)))
+    return out
+
+
+def q8_0_embed_gather(blocks, vocab, d, ids, *, act="none", out=None, err_flag=None, stream=None):
+    """blocks: uint8 device tensor of the GGUF Q8_0 table; ids int32/uint32 or int64."""
+    n = ids.numel()
+    if out is None:
+        out = torch.empty((n, d), dtype=torch.float32, device=ids.device)
+    idt = NSR_IDX_I64 if ids.dtype == torch.int64 else NSR_IDX_U32
+    check(lib().nsr_q8_0_embed_gather(_ptr(blocks), vocab, d, _ptr(ids), idt, n, _ptr(out), ACT[act],
+                                      _ptr(err_flag), _stream(stream)))
+    return out
+
+
+def activation(x, act, *, out=None, stream=None):
+    if out is None:
+        out = torch.empty_like(x)
+    check(lib().nsr_activation(_ptr(x), _ptr(out), _dt(x), x.numel(), ACT[act], _stream(stream)))
+    return out
+
+
+def glu_silu(fc1, *, out=None, stream=None):
+    n = fc1.numel() // 2
+    if out is None:
+        out = torch.empty(n, dtype=fc1.dtype, device=fc1.device)
+    check(lib().nsr_glu_silu(_ptr(fc1), _ptr(out), _dt(fc1), n, _stream(stream)))
+    return out
+
+
+def residual_add(x, res, *, out=None, stream=None):
+    if out is None:
+        out = torch.empty_like(x)
+    check(lib().nsr_residual_add(_ptr(x), _ptr(res), _ptr(out), _dt(x), x.numel(), _stream(stream)))
+    return out

@@ -1,0 +1,104 @@
+"""Build the gfx950 code objects, libnspeech_rocm.so and the CPU oracle.
+
+Run as ``python -m nspeech_amd.build`` (or through ``__graft_entry__.build``).
+Every call recompiles. Outputs (git-ignored, shipped to the GPU box with the
+tree):
+
+  nspeech_amd/lib/nsr_<unit>_gfx950.hsaco   one code object per kernel unit
+  nspeech_amd/lib/libnspeech_rocm.so        C ABI (include/nspeech_rocm.h),
+                                            code objects embedded
+  oracle/_build/libnsr_oracle.so            CPU oracle (test infrastructure)
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+LIB = PKG / "lib"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+HIPCC = ROCM / "bin" / "hipcc"
+ARCH = "gfx950"
+
+# Kernel units: kernels/<unit>.hip -> lib/nsr_<unit>_gfx950.hsaco. The same
+# list is embedded by runtime/nsr_embed.S and searched by nsr_runtime.cpp.
+UNITS = ["q8_0_gather", "layernorm", "rotary", "adain_snake", "elementwise"]
+
+HIP_FLAGS = [
+    "--genco",
+    f"--offload-arch={ARCH}",
+    "--no-gpu-bundle-output",
+    "-O3",
+    "-std=c++17",
+    "-mcode-object-version=5",
+    # keep the compiler from forming packed-FP32 instructions
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _run(cmd: list[str], cwd: Path = ROOT) -> None:
+    proc = subprocess.run(cmd, cwd=cwd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout + proc.stderr)
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}")
+
+
+def code_object_path(unit: str) -> Path:
+    return LIB / f"nsr_{unit}_{ARCH}.hsaco"
+
+
+def build_code_objects() -> list[Path]:
+    LIB.mkdir(parents=True, exist_ok=True)
+
+    def one(unit: str) -> Path:
+        out = code_object_path(unit)
+        tmp = out.with_suffix(".hsaco.tmp")
+        _run([str(HIPCC), *HIP_FLAGS, "-o", str(tmp), str(CSRC / "kernels" / f"{unit}.hip")])
+        os.replace(tmp, out)
+        return out
+
+    with ThreadPoolExecutor(max_workers=len(UNITS)) as ex:
+        return list(ex.map(one, UNITS))
+
+
+def build_library() -> Path:
+    out = LIB / "libnspeech_rocm.so"
+    tmp = LIB / "libnspeech_rocm.so.tmp"
+    cmd = [
+        "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math",
+        "-Wall", "-Wextra", "-Wno-unused-parameter",
+        "-D__HIP_PLATFORM_AMD__",
+        f"-I{ROOT / 'include'}", f"-I{ROCM / 'include'}",
+        f"-DNSR_CO_DIR={LIB}",
+        str(CSRC / "runtime" / "nsr_runtime.cpp"),
+        str(CSRC / "runtime" / "nsr_embed.S"),
+        f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}",
+        "-Wl,--no-undefined",
+        "-o", str(tmp),
+    ]
+    _run(cmd)
+    os.replace(tmp, out)
+    return out
+
+
+def build_oracle() -> Path:
+    sys.path.insert(0, str(ROOT))
+    from oracle import build as oracle_build  # noqa: E402
+
+    return oracle_build.build()
+
+
+def build_all() -> None:
+    build_code_objects()
+    build_library()
+    build_oracle()
+
+
+if __name__ == "__main__":
+    build_all()
+    print("built:", *(str(p.relative_to(ROOT)) for p in sorted(LIB.glob("*"))), sep="\n  ")

@@ -1,0 +1,114 @@
+/*
+ * Elementwise kernels: SiLU / GELU(erf) activation, GLU-SiLU, residual add.
+ *
+ * Reference semantics:
+ *   gelu_erf: x * 0.5 * (1 + erf(x / sqrt(2)))  (Tensor::gelu_erf,
+ *     src/moonshine/encoder.rs:106; gelu_forward kernels/moonshine_kernels.py:388-400)
+ *   silu: x / (1 + exp(-x))  (candle_nn::ops::silu, src/moonshine/decoder.rs:409;
+ *     silu kernels/moonshine_kernels.py:96-98)
+ *   glu_silu: out[i] = silu(fc1[n + i]) * fc1[i]  (glu_silu_fused,
+ *     kernels/moonshine_kernels.py:846-862; DecoderMLP::forward decoder.rs:403-411)
+ *   residual add: out = x + res  (FastAddOp, src/fast_ops.rs:16-36)
+ *
+ * One lane per 16-byte chunk (4 f32 or 8 f16/bf16 elements), flat grid,
+ * arithmetic in f32 and one rounding to the storage dtype. The _s variants
+ * take one element per lane for unaligned pointers and ragged tails.
+ */
+#include "device_common.h"
+
+template <int DT, int ACT>
+NSR_DEV void act_vec(const nsr_ew_args& a) {
+  constexpr int VEC = 16 / dt_size<DT>::value;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.n / VEC) return;
+  float v[VEC];
+  unpack16<DT>(ld16((const char*)a.a + i * 16), v);
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) v[e] = apply_act<ACT>(v[e]);
+  st16((char*)a.out + i * 16, pack16<DT>(v));
+}
+
+template <int DT, int ACT>
+NSR_DEV void act_scalar(const nsr_ew_args& a, int64_t first) {
+  const int64_t i = first + (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.n) return;
+  store_scalar<DT>(a.out, i, apply_act<ACT>(load_scalar<DT>(a.a, i)));
+}
+
+template <int DT>
+NSR_DEV void glu_vec(const nsr_ew_args& a) {
+  constexpr int VEC = 16 / dt_size<DT>::value;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.n / VEC) return;
+  float x[VEC], g[VEC];
+  unpack16<DT>(ld16((const char*)a.a + i * 16), x);
+  unpack16<DT>(ld16((const char*)a.a + (a.n * dt_size<DT>::value) + i * 16), g);
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) x[e] = act_silu(g[e]) * x[e];
+  st16((char*)a.out + i * 16, pack16<DT>(x));
+}
+
+template <int DT>
+NSR_DEV void glu_scalar(const nsr_ew_args& a, int64_t first) {
+  const int64_t i = first + (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.n) return;
+  const float x = load_scalar<DT>(a.a, i);
+  const float g = load_scalar<DT>(a.a, a.n + i);
+  store_scalar<DT>(a.out, i, act_silu(g) * x);
+}
+
+template <int DT>
+NSR_DEV void add_vec(const nsr_ew_args& a) {
+  constexpr int VEC = 16 / dt_size<DT>::value;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.n / VEC) return;
+  float x[VEC], r[VEC];
+  unpack16<DT>(ld16((const char*)a.a + i * 16), x);
+  unpack16<DT>(ld16((const char*)a.b + i * 16), r);
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) x[e] = x[e] + r[e];
+  st16((char*)a.out + i * 16, pack16<DT>(x));
+}
+
+template <int DT>
+NSR_DEV void add_scalar(const nsr_ew_args& a, int64_t first) {
+  const int64_t i = first + (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.n) return;
+  store_scalar<DT>(a.out, i, load_scalar<DT>(a.a, i) + load_scalar<DT>(a.b, i));
+}
+
+/* Vector kernels cover n - n % VEC elements; the scalar kernels take `first`
+ * (the first element they handle) so the host can launch them for the tail. */
+#define NSR_EW_SET(DN, DT)                                                                  \
+  extern "C" __global__ void __launch_bounds__(256) nsrk_silu_##DN##_v(const nsr_ew_args a) { \
+    act_vec<DT, ACT_SILU>(a);                                                               \
+  }                                                                                         \
+  extern "C" __global__ void __launch_bounds__(256) nsrk_gelu_##DN##_v(const nsr_ew_args a) { \
+    act_vec<DT, ACT_GELU>(a);                                                               \
+  }                                                                                         \
+  extern "C" __global__ void __launch_bounds__(256)                                         \
+      nsrk_silu_##DN##_s(const nsr_ew_args a, const int64_t first) {                        \
+    act_scalar<DT, ACT_SILU>(a, first);                                                     \
+  }                                                                                         \
+  extern "C" __global__ void __launch_bounds__(256)                                         \
+      nsrk_gelu_##DN##_s(const nsr_ew_args a, const int64_t first) {                        \
+    act_scalar<DT, ACT_GELU>(a, first);                                                     \
+  }                                                                                         \
+  extern "C" __global__ void __launch_bounds__(256) nsrk_glu_##DN##_v(const nsr_ew_args a) {  \
+    glu_vec<DT>(a);                                                                         \
+  }                                                                                         \
+  extern "C" __global__ void __launch_bounds__(256)                                         \
+      nsrk_glu_##DN##_s(const nsr_ew_args a, const int64_t first) {                         \
+    glu_scalar<DT>(a, first);                                                               \
+  }                                                                                         \
+  extern "C" __global__ void __launch_bounds__(256) nsrk_add_##DN##_v(const nsr_ew_args a) {  \
+    add_vec<DT>(a);                                                                         \
+  }                                                                                         \
+  extern "C" __global__ void __launch_bounds__(256)                                         \
+      nsrk_add_##DN##_s(const nsr_ew_args a, const int64_t first) {                         \
+    add_scalar<DT>(a, first);                                                               \
+  }
+
+NSR_EW_SET(f32, DT_F32)
+NSR_EW_SET(f16, DT_F16)
+NSR_EW_SET(bf16, DT_BF16)

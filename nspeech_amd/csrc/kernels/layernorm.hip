@@ -1,0 +1,268 @@
+/*
+ * LayerNorm family and fused residual-add + LayerNorm (+ activation).
+ *
+ * Reference semantics:
+ *   candle_nn::LayerNorm (eps 1e-5, affine) as used by the Parakeet conformer
+ *     (src/parakeet/fast_conformer.rs:721-725,778-782,793-811);
+ *   UnitOffsetLayerNorm::forward src/moonshine/encoder.rs:68-76 (scale gamma+1);
+ *   LayerNorm::forward src/moonshine/decoder.rs:67-74 (weight only);
+ *   residual_add_layernorm_fused kernels/moonshine_kernels.py:955-991
+ *     (h = proj + residual written out, LN(h) * w written out);
+ *   the CPU chain fast_add (src/fast_ops.rs:16-36) -> LayerNorm -> gelu_erf.
+ *
+ * Design (gfx950): one wave64 per row, the row held in VGPRs as NC chunks of
+ * 16 bytes per lane (128-bit coalesced loads), statistics in two passes over
+ * the registers (mean, then centred sum of squares) with DPP wave reductions,
+ * so x (and res) are read from HBM exactly once and y (and h) written once.
+ * Four rows per 256-thread workgroup; no LDS and no block barriers.
+ * Rows that are not 16-byte aligned or longer than 4096 columns take the
+ * generic kernel at the bottom (one workgroup per row, scalar access).
+ */
+#include "device_common.h"
+
+/* Chunk = VEC elements; 16 bytes of the narrowest tensor involved. */
+template <int X, int R, int H, int Y>
+struct ln_vec {
+  static constexpr bool all32 = (X == DT_F32) && (R == DT_F32) && (H == DT_F32) && (Y == DT_F32);
+  static constexpr int value = all32 ? 4 : 8;
+};
+
+template <int DT, int VEC>
+NSR_DEV void load_vec(const void* base, int64_t elem, float* v) {
+  constexpr int BYTES = VEC * dt_size<DT>::value;
+  const char* p = (const char*)base + elem * dt_size<DT>::value;
+  if constexpr (BYTES == 16) {
+    unpack16<DT>(ld16(p), v);
+  } else if constexpr (BYTES == 32) {
+    unpack16<DT>(ld16(p), v);
+    unpack16<DT>(ld16(p + 16), v + 16 / dt_size<DT>::value);
+  } else { /* 8 bytes: 4 x 16-bit */
+    const nsr_uint2 r = *(const nsr_uint2*)p;
+    nsr_uint4 r4 = {r[0], r[1], 0u, 0u};
+    float t[8];
+    unpack16<DT>(r4, t);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = t[i];
+  }
+}
+
+template <int DT, int VEC>
+NSR_DEV void store_vec(void* base, int64_t elem, const float* v) {
+  constexpr int BYTES = VEC * dt_size<DT>::value;
+  char* p = (char*)base + elem * dt_size<DT>::value;
+  if constexpr (BYTES == 16) {
+    st16(p, pack16<DT>(v));
+  } else if constexpr (BYTES == 32) {
+    st16(p, pack16<DT>(v));
+    st16(p + 16, pack16<DT>(v + 16 / dt_size<DT>::value));
+  } else {
+    float t[8] = {v[0], v[1], v[2], v[3], 0.f, 0.f, 0.f, 0.f};
+    const nsr_uint4 r4 = pack16<DT>(t);
+    *(nsr_uint2*)p = nsr_uint2{r4[0], r4[1]};
+  }
+}
+
+NSR_DEV float load_param(const void* p, int pdt, int64_t i) {
+  return pdt == DT_F32 ? ((const float*)p)[i] : f16_bits_to_f32(((const uint16_t*)p)[i]);
+}
+
+/* VEC gamma/beta values (f32 or f16, uniform branch); `fill` when p is NULL. */
+template <int VEC>
+NSR_DEV void load_param_vec(const void* p, int pdt, int col0, float* v, float fill) {
+  if (!p) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) v[e] = fill;
+  } else if (pdt == DT_F32) {
+    load_vec<DT_F32, VEC>(p, col0, v);
+  } else {
+    load_vec<DT_F16, VEC>(p, col0, v);
+  }
+}
+
+/*
+ * FUSED = false: h = x.  FUSED = true: h = round_H(x + res), stored if a.h.
+ * PDT runtime (gamma/beta are read once per chunk), ACT compile time.
+ */
+template <int X, int R, int H, int Y, int NC, bool FUSED, int ACT>
+NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
+  constexpr int VEC = ln_vec<X, R, H, Y>::value;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.n_rows) return; /* whole wave leaves; no barriers below */
+  const int nchunk = a.n_cols / VEC;
+  const int64_t xrow = row * a.ld_x;
+  const int64_t yrow = row * a.ld_y;
+
+  float v[NC][VEC];
+  float sum = 0.f;
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const int j = lane + 64 * k;
+    if (j < nchunk) {
+      load_vec<X, VEC>(a.x, xrow + (int64_t)j * VEC, v[k]);
+      if constexpr (FUSED) {
+        float r[VEC];
+        load_vec<R, VEC>(a.res, xrow + (int64_t)j * VEC, r);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[k][e] = round_to<H>(v[k][e] + r[e]);
+        if (a.h) store_vec<H, VEC>(a.h, xrow + (int64_t)j * VEC, v[k]);
+      }
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) sum += v[k][e];
+    }
+  }
+  const float mean = wave_sum(sum) * a.inv_n;
+
+  /* centred pass; sum(d) corrects the f32 mean (corrected two-pass), which
+   * keeps rows with |mean| >> std accurate */
+  float sq = 0.f, sd = 0.f;
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const int j = lane + 64 * k;
+    if (j < nchunk) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        v[k][e] -= mean;
+        sq = __builtin_fmaf(v[k][e], v[k][e], sq);
+        sd += v[k][e];
+      }
+    }
+  }
+  sq = wave_sum(sq);
+  sd = wave_sum(sd);
+  const float c = sd * a.inv_n;
+  const float var = fmaxf(__builtin_fmaf(-c, sd, sq) * a.inv_n, 0.0f);
+  const float rstd = 1.0f / sqrtf(var + a.eps);
+  const float crs = -c * rstd; /* (d - c) * rstd = d * rstd + crs */
+
+#pragma unroll
+  for (int k = 0; k < NC; ++k) {
+    const int j = lane + 64 * k;
+    if (j < nchunk) {
+      const int col0 = j * VEC;
+      float g[VEC], b[VEC], o[VEC];
+      load_param_vec<VEC>(a.gamma, pdt, col0, g, 1.0f);
+      load_param_vec<VEC>(a.beta, pdt, col0, b, 0.0f);
+      const float goff = a.unit_offset ? 1.0f : 0.0f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        o[e] = apply_act<ACT>(__builtin_fmaf(__builtin_fmaf(v[k][e], rstd, crs), g[e] + goff, b[e]));
+      }
+      store_vec<Y, VEC>(a.y, yrow + col0, o);
+    }
+  }
+}
+
+/* Kernel: PDT and ACT switch uniformly outside the row body. */
+template <int X, int R, int H, int Y, int NC, bool FUSED>
+NSR_DEV void ln_wave_entry(const nsr_ln_args& a, int pdt, int act) {
+  if (act == ACT_GELU) {
+    ln_row_wave<X, R, H, Y, NC, FUSED, ACT_GELU>(a, pdt);
+  } else if (act == ACT_SILU) {
+    ln_row_wave<X, R, H, Y, NC, FUSED, ACT_SILU>(a, pdt);
+  } else {
+    ln_row_wave<X, R, H, Y, NC, FUSED, ACT_NONE>(a, pdt);
+  }
+}
+
+/* ---------------------------------------------------------------- generic -- */
+
+/* One 256-thread workgroup per row, scalar loads, three passes over the row
+ * (global memory): any n_cols, any alignment. The fused variant writes h in
+ * the first pass and the later passes read h back from memory (or recompute
+ * it when h is not stored). */
+template <int X, int R, int H, int Y, bool FUSED>
+NSR_DEV void ln_row_generic(const nsr_ln_args& a, int pdt, int act) {
+  __shared__ float red[8];
+  const int64_t row = blockIdx.x;
+  if (row >= a.n_rows) return;
+  const int n = a.n_cols;
+  const int64_t xrow = row * a.ld_x;
+  const int64_t yrow = row * a.ld_y;
+
+  auto hval = [&](int c) -> float {
+    float v = load_scalar<X>(a.x, xrow + c);
+    if constexpr (FUSED) v = round_to<H>(v + load_scalar<R>(a.res, xrow + c));
+    return v;
+  };
+
+  float s = 0.f;
+  for (int c = threadIdx.x; c < n; c += 256) {
+    const float v = hval(c);
+    if constexpr (FUSED) {
+      if (a.h) store_scalar<H>(a.h, xrow + c, v);
+    }
+    s += v;
+  }
+  const float mean = block_sum<4>(s, red) * a.inv_n;
+  float q = 0.f, sd = 0.f;
+  for (int c = threadIdx.x; c < n; c += 256) {
+    const float d = hval(c) - mean;
+    q = __builtin_fmaf(d, d, q);
+    sd += d;
+  }
+  block_sum2<4>(q, sd, red);
+  const float corr = sd * a.inv_n;
+  const float var = fmaxf(__builtin_fmaf(-corr, sd, q) * a.inv_n, 0.0f);
+  const float rstd = 1.0f / sqrtf(var + a.eps);
+  for (int c = threadIdx.x; c < n; c += 256) {
+    const float d = hval(c) - mean - corr;
+    float g = a.gamma ? load_param(a.gamma, pdt, c) : 1.0f;
+    if (a.unit_offset) g += 1.0f;
+    const float b = a.beta ? load_param(a.beta, pdt, c) : 0.0f;
+    float o = __builtin_fmaf(d * rstd, g, b);
+    if (act == ACT_GELU) o = act_gelu_erf(o);
+    else if (act == ACT_SILU) o = act_silu(o);
+    store_scalar<Y>(a.y, yrow + c, o);
+  }
+}
+
+/* ------------------------------------------------------------ instances -- */
+/* Kernel argument tail: pdt and act are packed into one int (pdt | act<<8). */
+
+#define NSR_LN_WAVE(NAME, X, R, H, Y, NC, FUSED)                                \
+  extern "C" __global__ void __launch_bounds__(256)                            \
+      NAME(const nsr_ln_args a, const int mode) {                              \
+    ln_wave_entry<X, R, H, Y, NC, FUSED>(a, mode & 0xff, mode >> 8);            \
+  }
+
+#define NSR_LN_GENERIC(NAME, X, R, H, Y, FUSED)                                 \
+  extern "C" __global__ void __launch_bounds__(256)                            \
+      NAME(const nsr_ln_args a, const int mode) {                              \
+    ln_row_generic<X, R, H, Y, FUSED>(a, mode & 0xff, mode >> 8);               \
+  }
+
+/* Plain LayerNorm: x dtype -> y dtype, NC chunks per lane. */
+#define NSR_LN_PLAIN_SET(XN, X, YN, Y)                                          \
+  NSR_LN_WAVE(nsrk_ln_##XN##_##YN##_nc1, X, X, X, Y, 1, false)                   \
+  NSR_LN_WAVE(nsrk_ln_##XN##_##YN##_nc2, X, X, X, Y, 2, false)                   \
+  NSR_LN_WAVE(nsrk_ln_##XN##_##YN##_nc4, X, X, X, Y, 4, false)                   \
+  NSR_LN_WAVE(nsrk_ln_##XN##_##YN##_nc8, X, X, X, Y, 8, false)                   \
+  NSR_LN_GENERIC(nsrk_ln_##XN##_##YN##_generic, X, X, X, Y, false)
+
+NSR_LN_PLAIN_SET(f32, DT_F32, f32, DT_F32)
+NSR_LN_PLAIN_SET(f32, DT_F32, f16, DT_F16)
+NSR_LN_PLAIN_SET(f32, DT_F32, bf16, DT_BF16)
+NSR_LN_PLAIN_SET(f16, DT_F16, f32, DT_F32)
+NSR_LN_PLAIN_SET(f16, DT_F16, f16, DT_F16)
+NSR_LN_PLAIN_SET(f16, DT_F16, bf16, DT_BF16)
+NSR_LN_PLAIN_SET(bf16, DT_BF16, f32, DT_F32)
+NSR_LN_PLAIN_SET(bf16, DT_BF16, f16, DT_F16)
+NSR_LN_PLAIN_SET(bf16, DT_BF16, bf16, DT_BF16)
+/* f32 rows up to 4096 columns need 16 chunks of 4 per lane */
+NSR_LN_WAVE(nsrk_ln_f32_f32_nc16, DT_F32, DT_F32, DT_F32, DT_F32, 16, false)
+
+/* Fused residual add + LN profiles: x, res, h, y dtypes. */
+#define NSR_RESLN_SET(PN, X, R, H, Y)                                           \
+  NSR_LN_WAVE(nsrk_resln_##PN##_nc1, X, R, H, Y, 1, true)                        \
+  NSR_LN_WAVE(nsrk_resln_##PN##_nc2, X, R, H, Y, 2, true)                        \
+  NSR_LN_WAVE(nsrk_resln_##PN##_nc4, X, R, H, Y, 4, true)                        \
+  NSR_LN_WAVE(nsrk_resln_##PN##_nc8, X, R, H, Y, 8, true)                        \
+  NSR_LN_GENERIC(nsrk_resln_##PN##_generic, X, R, H, Y, true)
+
+NSR_RESLN_SET(f32, DT_F32, DT_F32, DT_F32, DT_F32)
+NSR_RESLN_SET(f16, DT_F16, DT_F16, DT_F16, DT_F16)
+NSR_RESLN_SET(bf16, DT_BF16, DT_BF16, DT_BF16, DT_BF16)
+/* moonshine decoder: f16 projection + f32 residual -> f32 residual, f16 norm */
+NSR_RESLN_SET(f16f32, DT_F16, DT_F32, DT_F32, DT_F16)
+NSR_LN_WAVE(nsrk_resln_f32_nc16, DT_F32, DT_F32, DT_F32, DT_F32, 16, true)

@@ -1,0 +1,66 @@
+/*
+ * GGUF Q8_0 embedding gather with the dequantisation fused into the gather.
+ *
+ * Reference semantics: QEmbedding::forward (src/parakeet/quantized_layers.rs:65-71)
+ * dequantises the WHOLE table (QTensor::dequantize) and then index_selects
+ * rows; a GGUF Q8_0 block is {f16 d; int8 qs[32]} and element j of block b is
+ * qs[j] * d. Here only the gathered rows are read: per output float4 one lane
+ * reads the block scale and 4 quant bytes, so HBM traffic is n_ids * row_bytes
+ * in and n_ids * d * 4 out. int8 * f16 has at most 8 + 11 significant bits,
+ * so every product is exact in f32 and the result is bit-identical to the
+ * reference's dequantize-then-select, in any evaluation order.
+ *
+ * Rows are 34*d/32 bytes, so a row start is only 2-byte aligned: quant bytes
+ * are fetched as two aligned 16-bit loads.
+ */
+#include "device_common.h"
+
+template <int ACT, bool IDS_I64>
+NSR_DEV void q8_0_gather_body(const nsr_q8_args& a) {
+  const uint32_t f = blockIdx.x * 256u + threadIdx.x; /* float4 index */
+  if (f >= (uint32_t)a.total4) return;
+  const uint32_t d4 = (uint32_t)a.d4;
+  const uint32_t row = f / d4;
+  const uint32_t c4 = f - row * d4;
+
+  int64_t id;
+  if constexpr (IDS_I64) {
+    id = ((const int64_t*)a.ids)[row];
+  } else {
+    id = (int64_t)((const uint32_t*)a.ids)[row];
+  }
+
+  nsr_float4 o;
+  if (id < 0 || id >= a.vocab) {
+    o = nsr_float4{0.f, 0.f, 0.f, 0.f};
+    if (a.err_flag) *a.err_flag = 1;
+  } else {
+    const uint8_t* bp = a.blocks + id * (int64_t)a.row_bytes + (c4 >> 3) * 34u;
+    const float d = f16_bits_to_f32(*(const uint16_t*)bp);
+    const uint16_t* qp = (const uint16_t*)(bp + 2 + (c4 & 7u) * 4u);
+    const uint32_t q = (uint32_t)qp[0] | ((uint32_t)qp[1] << 16);
+    o.x = (float)(int32_t)(int8_t)(q & 0xffu) * d;
+    o.y = (float)(int32_t)(int8_t)((q >> 8) & 0xffu) * d;
+    o.z = (float)(int32_t)(int8_t)((q >> 16) & 0xffu) * d;
+    o.w = (float)(int32_t)(int8_t)(q >> 24) * d;
+    if constexpr (ACT != ACT_NONE) {
+      o.x = apply_act<ACT>(o.x);
+      o.y = apply_act<ACT>(o.y);
+      o.z = apply_act<ACT>(o.z);
+      o.w = apply_act<ACT>(o.w);
+    }
+  }
+  __builtin_nontemporal_store(o, (nsr_float4*)(a.out) + f);
+}
+
+#define NSR_Q8_KERNEL(NAME, ACT, I64)                                          \
+  extern "C" __global__ void __launch_bounds__(256) NAME(const nsr_q8_args a) { \
+    q8_0_gather_body<ACT, I64>(a);                                             \
+  }
+
+NSR_Q8_KERNEL(nsrk_q8_0_gather_none_u32, ACT_NONE, false)
+NSR_Q8_KERNEL(nsrk_q8_0_gather_silu_u32, ACT_SILU, false)
+NSR_Q8_KERNEL(nsrk_q8_0_gather_gelu_u32, ACT_GELU, false)
+NSR_Q8_KERNEL(nsrk_q8_0_gather_none_i64, ACT_NONE, true)
+NSR_Q8_KERNEL(nsrk_q8_0_gather_silu_i64, ACT_SILU, true)
+NSR_Q8_KERNEL(nsrk_q8_0_gather_gelu_i64, ACT_GELU, true)

@@ -1,0 +1,72 @@
+/*
+ * Partial interleaved rotary embedding over q [B,Hq,T,Dh] and k [B,Hk,T,Dh].
+ *
+ * Reference semantics: RotaryEmbedding::{new,forward} and
+ * apply_rotary_pos_emb (src/moonshine/decoder.rs:85-183):
+ *   inv_freq[i] = 1 / theta^(2i/rot)              (f32, glibc powf)
+ *   angle       = f32(pos) * inv_freq[i]          (one f32 multiply)
+ *   out         = x*cos + rotate_half_interleaved(x)*sin  on dims < rot,
+ *                 rotate_half maps the pair (x0, x1) to (-x1, x0);
+ *   dims >= rot pass through (Tensor::cat of q_pass).
+ * The GPU RoPE table of src/moonshine/gpu_decoder.rs:326-340 holds, per
+ * position, cos[0..half) then sin[0..half) of the same f32 angles.
+ *
+ * One lane per float4 (two rotation pairs or four pass-through values), a
+ * flat grid over q then k: fully coalesced 128-bit loads and stores, 8 B of
+ * HBM traffic per element. With a table the cos/sin values are the
+ * reference's own f32 values and the products are kept unfused
+ * (fp contract off), giving the reference's rounding sequence exactly.
+ * Without a table cos/sin are evaluated in-kernel (accurate sincosf) from
+ * the same f32 angle.
+ */
+#include "device_common.h"
+
+template <bool TABLE>
+NSR_DEV void rope_body(const nsr_rope_args& a) {
+#pragma clang fp contract(off)
+  const uint32_t f = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t nq = (uint32_t)a.n4[0];
+  const int which = f >= nq ? 1 : 0;
+  const uint32_t g = which ? f - nq : f;
+  if (g >= (uint32_t)a.n4[which]) return;
+  const float* src = which ? a.src[1] : a.src[0];
+  float* dst = which ? a.dst[1] : a.dst[0];
+
+  const uint32_t dh4 = (uint32_t)a.dh4;
+  const uint32_t row = g / dh4;
+  const uint32_t c4 = g - row * dh4;
+  const nsr_float4 x = ldf4(src + (size_t)g * 4);
+  nsr_float4 o = x;
+  if (c4 < (uint32_t)a.rot4) {
+    const uint32_t t = row % (uint32_t)a.T;
+    const int64_t pos = a.pos0 + (int64_t)t;
+    const int i0 = 2 * (int)c4; /* pair index of (x.x, x.y); i0+1 for (x.z, x.w) */
+    float c0, s0, c1, s1;
+    if constexpr (TABLE) {
+      const float* tb = a.table + pos * (int64_t)(2 * a.half);
+      const float2 cc = *(const float2*)(tb + i0);
+      const float2 ss = *(const float2*)(tb + a.half + i0);
+      c0 = cc.x; c1 = cc.y; s0 = ss.x; s1 = ss.y;
+    } else {
+      const float p = (float)pos;
+      const float ang0 = p * a.inv_freq[i0];
+      const float ang1 = p * a.inv_freq[i0 + 1];
+      sincosf(ang0, &s0, &c0);
+      sincosf(ang1, &s1, &c1);
+    }
+    /* x*cos + rotate_half(x)*sin with the products rounded separately */
+    o.x = x.x * c0 + (-x.y) * s0;
+    o.y = x.y * c0 + x.x * s0;
+    o.z = x.z * c1 + (-x.w) * s1;
+    o.w = x.w * c1 + x.z * s1;
+  }
+  stf4(dst + (size_t)g * 4, o);
+}
+
+extern "C" __global__ void __launch_bounds__(256) nsrk_rope_table_f32(const nsr_rope_args a) {
+  rope_body<true>(a);
+}
+
+extern "C" __global__ void __launch_bounds__(256) nsrk_rope_compute_f32(const nsr_rope_args a) {
+  rope_body<false>(a);
+}

@@ -1,0 +1,85 @@
+/*
+ * Kernel argument blocks, shared by the host launcher (nsr_runtime.cpp) and
+ * the gfx950 kernels (the .hip files under kernels/). Each kernel takes exactly one of these
+ * structs by value, so hipModuleLaunchKernel gets a single kernelParams entry
+ * and host and device agree on the layout by construction.
+ * Plain C: no HIP or C++ types, fixed-width integers only.
+ */
+#ifndef NSR_KARGS_H
+#define NSR_KARGS_H
+
+#include <stdint.h>
+
+#define NSR_MAX_HALF_ROT 128 /* rotary_dim <= 256 */
+
+typedef struct nsr_q8_args {
+  const uint8_t* blocks;   /* Q8_0 table, vocab rows of row_bytes */
+  const void* ids;         /* n_ids ids, u32 or i64 */
+  float* out;              /* [n_ids, d] */
+  int32_t* err_flag;       /* may be NULL */
+  int64_t vocab;
+  int64_t n_ids;
+  int64_t total4;          /* n_ids * d / 4 float4 outputs */
+  int32_t d4;              /* d / 4 */
+  int32_t row_bytes;       /* 34 * d / 32 */
+  int32_t act;             /* nsr_act */
+  int32_t ids_i64;         /* 1: ids are int64 */
+} nsr_q8_args;
+
+typedef struct nsr_ln_args {
+  const void* x;
+  const void* res;         /* residual (fused variant) */
+  void* h;                 /* x + res output, may be NULL */
+  const void* gamma;       /* may be NULL */
+  const void* beta;        /* may be NULL */
+  void* y;
+  int64_t n_rows;
+  int64_t ld_x;            /* elements */
+  int64_t ld_y;            /* elements */
+  int32_t n_cols;
+  int32_t unit_offset;     /* scale = gamma + 1 */
+  float eps;
+  float inv_n;             /* 1 / n_cols */
+} nsr_ln_args;
+
+typedef struct nsr_rope_args {
+  const float* src[2];     /* q, k */
+  float* dst[2];           /* q_out, k_out */
+  const float* table;      /* [table_rows][2*half] cos..., sin... or NULL */
+  int64_t rows[2];         /* B*Hq*T, B*Hk*T  (k rows 0 when k is NULL) */
+  int64_t n4[2];           /* float4 count of q and k */
+  int64_t pos0;
+  int32_t T;
+  int32_t dh4;             /* Dh / 4 */
+  int32_t rot4;            /* rotary_dim / 4 */
+  int32_t half;            /* rotary_dim / 2 */
+  float inv_freq[NSR_MAX_HALF_ROT];
+} nsr_rope_args;
+
+typedef struct nsr_adain_args {
+  const float* x;          /* [B, C, T] */
+  const void* gamma;       /* [B?, C] */
+  const void* beta;        /* [B?, C] */
+  const void* alpha;       /* [C] */
+  float* out;              /* [B, C, T] */
+  float* stats;            /* [B*C][2] mean, rstd (split path only) */
+  int64_t n_rows;          /* B * C */
+  int64_t T;
+  int64_t gamma_bstride;
+  int64_t beta_bstride;
+  int32_t C;
+  int32_t lds_chunks;      /* float4 chunks per thread kept in LDS */
+  float eps;
+  float inv_t;             /* 1 / T */
+} nsr_adain_args;
+
+typedef struct nsr_ew_args {
+  const void* a;
+  const void* b;
+  void* out;
+  int64_t n;               /* elements (GLU: output elements) */
+  int32_t act;
+  int32_t pad_;
+} nsr_ew_args;
+
+#endif /* NSR_KARGS_H */

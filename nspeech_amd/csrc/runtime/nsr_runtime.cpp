@@ -1,0 +1,598 @@
+// C-ABI runtime of libnspeech_rocm.so: code-object loading, argument
+// validation, kernel selection and launch for every entry point declared in
+// include/nspeech_rocm.h.
+//
+// The kernels live in one gfx950 code object (nsr_kernels.hip) embedded in
+// this library (nsr_embed.S) and loaded per device with hipModuleLoadData on
+// first use; launches go through hipModuleLaunchKernel on the caller's
+// stream. This replaces the reference's Metal pipeline loading and dispatch
+// (src/triton_kernels.rs:1401, kernels/out/generated/triton_metal_gen.rs:39-106)
+// and its per-call encoder setup (src/triton_kernels.rs:312-1423).
+#include "nspeech_rocm.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "../nsr_kargs.h"
+
+// Embedded code objects, one per kernel unit (nsr_embed.S).
+extern "C" const unsigned char nsr_co_q8_0_gather[];
+extern "C" const unsigned char nsr_co_layernorm[];
+extern "C" const unsigned char nsr_co_rotary[];
+extern "C" const unsigned char nsr_co_adain_snake[];
+extern "C" const unsigned char nsr_co_elementwise[];
+
+namespace {
+
+struct Unit {
+  const char* name;
+  const unsigned char* image;
+};
+const Unit kUnits[] = {{"q8_0_gather", nsr_co_q8_0_gather},
+                       {"layernorm", nsr_co_layernorm},
+                       {"rotary", nsr_co_rotary},
+                       {"adain_snake", nsr_co_adain_snake},
+                       {"elementwise", nsr_co_elementwise}};
+constexpr int kNumUnits = sizeof(kUnits) / sizeof(kUnits[0]);
+
+constexpr int kMaxDevices = 64;
+thread_local std::string g_last_error;
+
+nsr_status fail(nsr_status st, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return st;
+}
+
+struct DeviceModule {
+  std::once_flag once;
+  nsr_status status = NSR_ERR_NOT_INIT;
+  std::string error;
+  hipModule_t modules[kNumUnits] = {};
+  std::unordered_map<std::string, hipFunction_t> fns;
+  int max_lds = 0;
+};
+
+DeviceModule g_dev[kMaxDevices];
+std::mutex g_path_mu;
+std::string g_code_object_path;  // empty: embedded image
+
+void load_module(DeviceModule& dm, int dev) {
+  hipDeviceProp_t prop;
+  hipError_t e = hipGetDeviceProperties(&prop, dev);
+  if (e != hipSuccess) {
+    dm.error = std::string("hipGetDeviceProperties: ") + hipGetErrorString(e);
+    dm.status = NSR_ERR_HIP;
+    return;
+  }
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    dm.error = std::string("device ") + std::to_string(dev) + " is " + prop.gcnArchName +
+               "; this library carries gfx950 code only";
+    dm.status = NSR_ERR_NOT_INIT;
+    return;
+  }
+  std::string path;
+  {
+    std::lock_guard<std::mutex> lk(g_path_mu);
+    path = g_code_object_path;
+  }
+  for (int u = 0; u < kNumUnits; ++u) {
+    const std::string file = path + "/nsr_" + kUnits[u].name + "_gfx950.hsaco";
+    if (path.empty()) {
+      e = hipModuleLoadData(&dm.modules[u], kUnits[u].image);
+    } else {
+      e = hipModuleLoad(&dm.modules[u], file.c_str());
+    }
+    if (e != hipSuccess) {
+      dm.error = std::string("loading gfx950 code object ") + (path.empty() ? kUnits[u].name : file) +
+                 ": " + hipGetErrorString(e);
+      dm.status = NSR_ERR_NOT_INIT;
+      return;
+    }
+  }
+  int lds = 0;
+  hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+  dm.max_lds = lds;
+  dm.status = NSR_OK;
+}
+
+// Module of the current device, loaded on first use.
+nsr_status current_module(DeviceModule** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(NSR_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(NSR_ERR_HIP, "device index %d out of range", dev);
+  DeviceModule& dm = g_dev[dev];
+  std::call_once(dm.once, [&] { load_module(dm, dev); });
+  if (dm.status != NSR_OK) return fail(dm.status, "%s", dm.error.c_str());
+  *out = &dm;
+  return NSR_OK;
+}
+
+std::mutex g_fn_mu;
+
+// Code-object unit of a kernel, from its name prefix.
+int unit_of(const std::string& name) {
+  struct P {
+    const char* prefix;
+    int unit;
+  };
+  static const P map[] = {{"nsrk_q8_0_", 0}, {"nsrk_ln_", 1},    {"nsrk_resln_", 1}, {"nsrk_rope_", 2},
+                          {"nsrk_adain_", 3}, {"nsrk_silu_", 4}, {"nsrk_gelu_", 4},  {"nsrk_glu_", 4},
+                          {"nsrk_add_", 4}};
+  for (const P& p : map)
+    if (name.compare(0, std::strlen(p.prefix), p.prefix) == 0) return p.unit;
+  return -1;
+}
+
+nsr_status get_function(DeviceModule* dm, const std::string& name, hipFunction_t* f) {
+  std::lock_guard<std::mutex> lk(g_fn_mu);
+  auto it = dm->fns.find(name);
+  if (it != dm->fns.end()) {
+    *f = it->second;
+    return NSR_OK;
+  }
+  // Each kernel lives in the unit its name prefix names, so the lookup never
+  // misses (a failed hipModuleGetFunction would leave a sticky runtime error
+  // that the caller's next HIP call reports).
+  const int u = unit_of(name);
+  if (u < 0) return fail(NSR_ERR_NOT_INIT, "kernel %s belongs to no code-object unit", name.c_str());
+  hipError_t e = hipModuleGetFunction(f, dm->modules[u], name.c_str());
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(NSR_ERR_NOT_INIT, "kernel %s not in code object %s: %s", name.c_str(), kUnits[u].name,
+                hipGetErrorString(e));
+  }
+  dm->fns.emplace(name, *f);
+  return NSR_OK;
+}
+
+nsr_status launch(const std::string& name, unsigned gx, unsigned gy, unsigned block,
+                  unsigned shmem, nsr_stream_t stream, void** params) {
+  DeviceModule* dm = nullptr;
+  nsr_status st = current_module(&dm);
+  if (st != NSR_OK) return st;
+  hipFunction_t f;
+  st = get_function(dm, name, &f);
+  if (st != NSR_OK) return st;
+  if (shmem > (unsigned)dm->max_lds)
+    return fail(NSR_ERR_UNSUPPORTED, "%s needs %u bytes of LDS, device allows %d", name.c_str(), shmem,
+                dm->max_lds);
+  hipError_t e = hipModuleLaunchKernel(f, gx, gy, 1, block, 1, 1, shmem, (hipStream_t)stream, params, nullptr);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();  // reported through nsr_status, not left sticky
+    return fail(NSR_ERR_HIP, "launch %s: %s", name.c_str(), hipGetErrorString(e));
+  }
+  return NSR_OK;
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+int dt_size(nsr_dtype d) { return d == NSR_F32 ? 4 : 2; }
+bool dt_valid(nsr_dtype d) { return d == NSR_F32 || d == NSR_F16 || d == NSR_BF16; }
+const char* dt_name(nsr_dtype d) { return d == NSR_F32 ? "f32" : d == NSR_F16 ? "f16" : "bf16"; }
+bool act_valid(nsr_act a) { return a == NSR_ACT_NONE || a == NSR_ACT_SILU || a == NSR_ACT_GELU_ERF; }
+
+unsigned cdiv_u(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
+
+}  // namespace
+
+extern "C" {
+
+const char* nsr_version(void) { return "nspeech-rocm 0.1.0 (gfx950)"; }
+
+const char* nsr_last_error(void) { return g_last_error.c_str(); }
+
+nsr_status nsr_init(const char* code_object_dir) {
+  {
+    std::lock_guard<std::mutex> lk(g_path_mu);
+    g_code_object_path = code_object_dir ? code_object_dir : "";
+  }
+  DeviceModule* dm = nullptr;
+  return current_module(&dm);
+}
+
+int nsr_kernel_count(void) {
+  DeviceModule* dm = nullptr;
+  if (current_module(&dm) != NSR_OK) return 0;
+  // Count kernels by probing the names this runtime launches.
+  static const char* probe[] = {"nsrk_q8_0_gather_none_u32", "nsrk_ln_f32_f32_nc4",
+                                "nsrk_resln_bf16_nc2",       "nsrk_rope_table_f32",
+                                "nsrk_rope_compute_f32",     "nsrk_adain_res_b256_nv5_a",
+                                "nsrk_adain_res_b1024_nv20_a", "nsrk_adain_stats",
+                                "nsrk_adain_apply",          "nsrk_gelu_f32_v"};
+  int n = 0;
+  for (const char* p : probe) {
+    hipFunction_t f;
+    if (get_function(dm, p, &f) == NSR_OK) ++n;
+  }
+  return n;
+}
+
+// ------------------------------------------------------------ LayerNorm --
+
+static nsr_status ln_common(const void* x, nsr_dtype xd, const void* res, nsr_dtype rd, void* h,
+                            nsr_dtype hd, const void* gamma, const void* beta, nsr_dtype pd, void* y,
+                            nsr_dtype yd, int64_t n_rows, int64_t n_cols, int64_t ld_x, int64_t ld_y,
+                            float eps, unsigned flags, nsr_act act, bool fused, nsr_stream_t stream) {
+  if (!x || !y || (fused && !res)) return fail(NSR_ERR_BAD_ARG, "layernorm: null tensor pointer");
+  if (!dt_valid(xd) || !dt_valid(yd) || (fused && (!dt_valid(rd) || !dt_valid(hd))))
+    return fail(NSR_ERR_BAD_ARG, "layernorm: invalid dtype");
+  if (pd != NSR_F32 && pd != NSR_F16) return fail(NSR_ERR_BAD_ARG, "layernorm: params must be F32 or F16");
+  if (!act_valid(act)) return fail(NSR_ERR_BAD_ARG, "layernorm: invalid activation %d", (int)act);
+  if (flags & ~NSR_LN_UNIT_OFFSET) return fail(NSR_ERR_BAD_ARG, "layernorm: unknown flags 0x%x", flags);
+  if (n_rows < 0 || n_cols <= 0 || n_cols > (1 << 30))
+    return fail(NSR_ERR_BAD_ARG, "layernorm: bad shape rows=%lld cols=%lld", (long long)n_rows,
+                (long long)n_cols);
+  if (ld_x < n_cols || ld_y < n_cols) return fail(NSR_ERR_BAD_ARG, "layernorm: row stride < n_cols");
+  if (!(eps >= 0.0f)) return fail(NSR_ERR_BAD_ARG, "layernorm: eps must be >= 0");
+  if (n_rows == 0) return NSR_OK;
+
+  std::string prefix;
+  if (fused) {
+    if (xd == rd && rd == hd && hd == yd) {
+      prefix = std::string("nsrk_resln_") + dt_name(xd);
+    } else if (xd == NSR_F16 && rd == NSR_F32 && hd == NSR_F32 && yd == NSR_F16) {
+      prefix = "nsrk_resln_f16f32";
+    } else {
+      return fail(NSR_ERR_UNSUPPORTED,
+                  "residual_add_layernorm: dtype profile x=%s res=%s h=%s y=%s not built "
+                  "(supported: all equal, or f16/f32/f32/f16)",
+                  dt_name(xd), dt_name(rd), dt_name(hd), dt_name(yd));
+    }
+  } else {
+    prefix = std::string("nsrk_ln_") + dt_name(xd) + "_" + dt_name(yd);
+  }
+
+  const bool all32 = xd == NSR_F32 && yd == NSR_F32 && (!fused || (rd == NSR_F32 && hd == NSR_F32));
+  const int vec = all32 ? 4 : 8;
+  bool vector_ok = (n_cols % vec == 0) && (ld_x % vec == 0) && (ld_y % vec == 0) && aligned(x, 16) &&
+                   aligned(y, 16) && (!fused || aligned(res, 16)) && (!h || aligned(h, 16)) &&
+                   aligned(gamma, 16) && aligned(beta, 16);
+  int nc = 0;
+  if (vector_ok) {
+    const int64_t nchunk = n_cols / vec;
+    const int opts[] = {1, 2, 4, 8, 16};
+    for (int o : opts) {
+      if (o == 16 && !all32) break;
+      if (64 * (int64_t)o >= nchunk) {
+        nc = o;
+        break;
+      }
+    }
+  }
+  nsr_ln_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.x = x;
+  a.res = res;
+  a.h = h;
+  a.gamma = gamma;
+  a.beta = beta;
+  a.y = y;
+  a.n_rows = n_rows;
+  a.ld_x = ld_x;
+  a.ld_y = ld_y;
+  a.n_cols = (int32_t)n_cols;
+  a.unit_offset = (flags & NSR_LN_UNIT_OFFSET) ? 1 : 0;
+  a.eps = eps;
+  a.inv_n = 1.0f / (float)n_cols;
+  int mode = (pd == NSR_F32 ? 0 : 1) | ((int)act << 8);
+  void* params[] = {&a, &mode};
+  if (nc > 0) {
+    if (cdiv_u(n_rows, 4) == 0 || (n_rows + 3) / 4 > 0x7fffffffLL)
+      return fail(NSR_ERR_UNSUPPORTED, "layernorm: too many rows");
+    return launch(prefix + "_nc" + std::to_string(nc), cdiv_u(n_rows, 4), 1, 256, 0, stream, params);
+  }
+  if (n_rows > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "layernorm: too many rows");
+  return launch(prefix + "_generic", (unsigned)n_rows, 1, 256, 0, stream, params);
+}
+
+nsr_status nsr_layernorm(const void* x, nsr_dtype x_dtype, const void* gamma, const void* beta,
+                         nsr_dtype param_dtype, void* y, nsr_dtype y_dtype, int64_t n_rows,
+                         int64_t n_cols, int64_t ld_x, int64_t ld_y, float eps, unsigned flags,
+                         nsr_act act, nsr_stream_t stream) {
+  return ln_common(x, x_dtype, nullptr, x_dtype, nullptr, x_dtype, gamma, beta, param_dtype, y, y_dtype,
+                   n_rows, n_cols, ld_x, ld_y, eps, flags, act, false, stream);
+}
+
+nsr_status nsr_residual_add_layernorm(const void* x, nsr_dtype x_dtype, const void* res,
+                                      nsr_dtype res_dtype, void* h_out, nsr_dtype h_dtype,
+                                      const void* gamma, const void* beta, nsr_dtype param_dtype,
+                                      void* y, nsr_dtype y_dtype, int64_t n_rows, int64_t n_cols,
+                                      float eps, unsigned flags, nsr_act act, nsr_stream_t stream) {
+  return ln_common(x, x_dtype, res, res_dtype, h_out, h_dtype, gamma, beta, param_dtype, y, y_dtype,
+                   n_rows, n_cols, n_cols, n_cols, eps, flags, act, true, stream);
+}
+
+// --------------------------------------------------------------- rotary --
+
+nsr_status nsr_rope_table_f32(float* host_table, int64_t max_pos, int rotary_dim, float theta) {
+  if (!host_table) return fail(NSR_ERR_BAD_ARG, "rope_table: null table");
+  if (max_pos < 0 || rotary_dim <= 0 || rotary_dim % 2 != 0)
+    return fail(NSR_ERR_BAD_ARG, "rope_table: bad max_pos/rotary_dim");
+  const int half = rotary_dim / 2;
+  // f32 arithmetic, op for op as src/moonshine/gpu_decoder.rs:328-338
+  for (int i = 0; i < half; ++i) {
+    const float e = (2.0f * (float)i) / (float)rotary_dim;
+    const float inv_freq = 1.0f / powf(theta, e);
+    for (int64_t p = 0; p < max_pos; ++p) {
+      const float angle = (float)p * inv_freq;
+      host_table[p * 2 * half + i] = cosf(angle);
+      host_table[p * 2 * half + half + i] = sinf(angle);
+    }
+  }
+  return NSR_OK;
+}
+
+nsr_status nsr_rotary_partial_interleaved_f32(const float* q, const float* k, float* q_out,
+                                              float* k_out, int64_t B, int64_t Hq, int64_t Hk,
+                                              int64_t T, int64_t Dh, int rotary_dim, float theta,
+                                              int64_t pos0, const float* rope_table,
+                                              int64_t table_rows, nsr_stream_t stream) {
+  if (!q || !q_out) return fail(NSR_ERR_BAD_ARG, "rotary: null q/q_out");
+  if (k && !k_out) return fail(NSR_ERR_BAD_ARG, "rotary: k given without k_out");
+  if (B < 0 || Hq < 0 || (k && Hk < 0) || T <= 0 || Dh <= 0 || pos0 < 0)
+    return fail(NSR_ERR_BAD_ARG, "rotary: bad shape");
+  if (rotary_dim < 0 || rotary_dim > Dh || rotary_dim % 2 != 0)
+    return fail(NSR_ERR_BAD_ARG, "rotary: rotary_dim %d must be even and <= head_dim %lld", rotary_dim,
+                (long long)Dh);
+  if (Dh % 4 != 0 || rotary_dim % 4 != 0)
+    return fail(NSR_ERR_UNSUPPORTED, "rotary: head_dim and rotary_dim must be multiples of 4");
+  if (rotary_dim / 2 > NSR_MAX_HALF_ROT) return fail(NSR_ERR_UNSUPPORTED, "rotary: rotary_dim > 256");
+  if (!aligned(q, 16) || !aligned(q_out, 16) || (k && (!aligned(k, 16) || !aligned(k_out, 16))))
+    return fail(NSR_ERR_BAD_ARG, "rotary: q/k/outputs must be 16-byte aligned");
+  if (rope_table && (table_rows < pos0 + T || !aligned(rope_table, 8)))
+    return fail(NSR_ERR_BAD_ARG, "rotary: rope table needs >= pos0+T rows and 8-byte alignment");
+  if (!rope_table && !(theta > 0.0f)) return fail(NSR_ERR_BAD_ARG, "rotary: theta must be > 0");
+
+  nsr_rope_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.src[0] = q;
+  a.dst[0] = q_out;
+  a.src[1] = k ? k : q;
+  a.dst[1] = k ? k_out : q_out;
+  a.rows[0] = B * Hq * T;
+  a.rows[1] = k ? B * Hk * T : 0;
+  a.n4[0] = a.rows[0] * (Dh / 4);
+  a.n4[1] = a.rows[1] * (Dh / 4);
+  const int64_t total = a.n4[0] + a.n4[1];
+  if (total == 0) return NSR_OK;
+  if (total >= (int64_t)1 << 31) return fail(NSR_ERR_UNSUPPORTED, "rotary: tensors too large (>8 GiB)");
+  a.table = rope_table;
+  a.pos0 = pos0;
+  a.T = (int32_t)T;
+  a.dh4 = (int32_t)(Dh / 4);
+  a.rot4 = rotary_dim / 4;
+  a.half = rotary_dim / 2;
+  // inv_freq with the reference's f32 operations (src/moonshine/decoder.rs:90-92)
+  for (int i = 0; i < a.half; ++i) {
+    const float e = (2.0f * (float)i) / (float)rotary_dim;
+    a.inv_freq[i] = 1.0f / powf(theta, e);
+  }
+  void* params[] = {&a};
+  return launch(rope_table ? "nsrk_rope_table_f32" : "nsrk_rope_compute_f32", cdiv_u(total, 256), 1, 256, 0,
+                stream, params);
+}
+
+// -------------------------------------------------------- AdaIN + Snake --
+
+nsr_status nsr_adain_snake_f32(const float* x, const void* gamma, const void* beta, const void* alpha,
+                               nsr_dtype param_dtype, int64_t gamma_bstride, int64_t beta_bstride,
+                               float* out, int64_t B, int64_t C, int64_t T, float eps,
+                               nsr_stream_t stream) {
+  if (!x || !gamma || !beta || !alpha || !out) return fail(NSR_ERR_BAD_ARG, "adain_snake: null pointer");
+  if (param_dtype != NSR_F32 && param_dtype != NSR_F16)
+    return fail(NSR_ERR_BAD_ARG, "adain_snake: params must be F32 or F16");
+  if (B < 0 || C <= 0 || T <= 0 || C > 0x7fffffffLL)
+    return fail(NSR_ERR_BAD_ARG, "adain_snake: bad shape B=%lld C=%lld T=%lld", (long long)B, (long long)C,
+                (long long)T);
+  if (gamma_bstride < 0 || beta_bstride < 0) return fail(NSR_ERR_BAD_ARG, "adain_snake: negative stride");
+  if (!(eps >= 0.0f)) return fail(NSR_ERR_BAD_ARG, "adain_snake: eps must be >= 0");
+  const int64_t n_rows = B * C;
+  if (n_rows == 0) return NSR_OK;
+  if (n_rows > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "adain_snake: too many rows");
+  if (n_rows * T >= (int64_t)1 << 34) return fail(NSR_ERR_UNSUPPORTED, "adain_snake: tensor too large");
+
+  DeviceModule* dm = nullptr;
+  nsr_status st = current_module(&dm);
+  if (st != NSR_OK) return st;
+
+  nsr_adain_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.x = x;
+  a.gamma = gamma;
+  a.beta = beta;
+  a.alpha = alpha;
+  a.out = out;
+  a.n_rows = n_rows;
+  a.T = T;
+  a.gamma_bstride = gamma_bstride;
+  a.beta_bstride = beta_bstride;
+  a.C = (int32_t)C;
+  a.eps = eps;
+  a.inv_t = 1.0f / (float)T;
+  int pdt = param_dtype == NSR_F32 ? 0 : 1;
+
+  const bool is_aligned = aligned(x, 16) && aligned(out, 16) && (T % 4 == 0);
+  // chunks each lane array must cover: all chunks (aligned) or interior ones
+  const int64_t need = is_aligned ? T / 4 : ((T + 6) / 4 - 2 > 0 ? (T + 6) / 4 - 2 : 0);
+  int block = 0, nv = 0, nl = 0;
+  {
+    const int small[] = {1, 2, 3, 4, 5, 6, 8};
+    for (int o : small)
+      if (256LL * o >= need) {
+        block = 256;
+        nv = o;
+        break;
+      }
+    if (!block) {
+      const int large[] = {3, 4, 6, 8, 12, 16, 20};
+      for (int o : large)
+        if (1024LL * o >= need) {
+          block = 1024;
+          nv = o;
+          break;
+        }
+    }
+    if (!block && is_aligned) {
+      const int64_t rest = need - 1024LL * 20;
+      const int64_t lds_slots = (dm->max_lds - 1024) / (1024 * 16);
+      const int64_t m = (rest + 1023) / 1024;
+      if (m <= lds_slots) {
+        block = 1024;
+        nv = 20;
+        nl = (int)m;
+      }
+    }
+  }
+  if (block) {
+    a.lds_chunks = nl;
+    void* params[] = {&a, &pdt};
+    const std::string name = "nsrk_adain_res_b" + std::to_string(block) + "_nv" + std::to_string(nv) +
+                             (is_aligned ? "_a" : "_u");
+    return launch(name, (unsigned)n_rows, 1, block, (unsigned)(nl * block * 16), stream, params);
+  }
+
+  // Split path: stats (one read) + apply (second read), stream-ordered scratch.
+  float* stats = nullptr;
+  hipError_t e = hipMallocAsync((void**)&stats, (size_t)n_rows * 2 * sizeof(float), (hipStream_t)stream);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(NSR_ERR_HIP, "adain_snake: hipMallocAsync: %s", hipGetErrorString(e));
+  }
+  a.stats = stats;
+  void* p1[] = {&a};
+  st = launch("nsrk_adain_stats", (unsigned)n_rows, 1, 1024, 0, stream, p1);
+  if (st == NSR_OK) {
+    void* p2[] = {&a, &pdt};
+    const int64_t gy = (T + 1023) / 1024;
+    if (gy > 65535) {
+      st = fail(NSR_ERR_UNSUPPORTED, "adain_snake: T too long for the split path");
+    } else {
+      st = launch("nsrk_adain_apply", (unsigned)n_rows, (unsigned)gy, 256, 0, stream, p2);
+    }
+  }
+  hipFreeAsync(stats, (hipStream_t)stream);
+  return st;
+}
+
+// --------------------------------------------------------------- Q8_0 --
+
+nsr_status nsr_q8_0_embed_gather(const void* blocks, int64_t vocab, int64_t d, const void* ids,
+                                 nsr_index_dtype id_dtype, int64_t n_ids, float* out, nsr_act act,
+                                 int32_t* err_flag, nsr_stream_t stream) {
+  if (!blocks || !ids || !out) return fail(NSR_ERR_BAD_ARG, "q8_0_embed_gather: null pointer");
+  if (vocab <= 0 || d <= 0 || d % 32 != 0 || n_ids < 0)
+    return fail(NSR_ERR_BAD_ARG, "q8_0_embed_gather: need vocab > 0, d a positive multiple of 32, n_ids >= 0");
+  if (id_dtype != NSR_IDX_U32 && id_dtype != NSR_IDX_I64)
+    return fail(NSR_ERR_BAD_ARG, "q8_0_embed_gather: invalid id dtype");
+  if (!act_valid(act)) return fail(NSR_ERR_BAD_ARG, "q8_0_embed_gather: invalid activation");
+  if (!aligned(blocks, 2) || !aligned(out, 16) || !aligned(ids, id_dtype == NSR_IDX_U32 ? 4 : 8))
+    return fail(NSR_ERR_BAD_ARG, "q8_0_embed_gather: misaligned pointer (blocks 2 B, out 16 B, ids)");
+  if (d / 32 * 34 > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "q8_0_embed_gather: row too long");
+  if (n_ids == 0) return NSR_OK;
+  const int64_t total4 = n_ids * (d / 4);
+  if (total4 >= (int64_t)1 << 32 || (total4 + 255) / 256 > 0x7fffffffLL)
+    return fail(NSR_ERR_UNSUPPORTED, "q8_0_embed_gather: output too large");
+  nsr_q8_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.blocks = (const uint8_t*)blocks;
+  a.ids = ids;
+  a.out = out;
+  a.err_flag = err_flag;
+  a.vocab = vocab;
+  a.n_ids = n_ids;
+  a.total4 = total4;
+  a.d4 = (int32_t)(d / 4);
+  a.row_bytes = (int32_t)(d / 32 * 34);
+  a.act = (int32_t)act;
+  a.ids_i64 = id_dtype == NSR_IDX_I64;
+  const char* an = act == NSR_ACT_SILU ? "silu" : act == NSR_ACT_GELU_ERF ? "gelu" : "none";
+  const std::string name =
+      std::string("nsrk_q8_0_gather_") + an + (id_dtype == NSR_IDX_I64 ? "_i64" : "_u32");
+  void* params[] = {&a};
+  return launch(name, cdiv_u(total4, 256), 1, 256, 0, stream, params);
+}
+
+// ---------------------------------------------------------- elementwise --
+
+static nsr_status ew_launch(const char* op, nsr_dtype dtype, nsr_ew_args& a, bool vec_ok,
+                            nsr_stream_t stream) {
+  const int vec = 16 / dt_size(dtype);
+  int64_t first = 0;
+  if (vec_ok) {
+    const int64_t chunks = a.n / vec;
+    if (chunks > 0) {
+      if ((chunks + 255) / 256 > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "%s: too large", op);
+      void* p[] = {&a};
+      nsr_status st = launch(std::string("nsrk_") + op + "_" + dt_name(dtype) + "_v", cdiv_u(chunks, 256), 1,
+                             256, 0, stream, p);
+      if (st != NSR_OK) return st;
+    }
+    first = chunks * vec;
+  }
+  const int64_t rest = a.n - first;
+  if (rest > 0) {
+    if ((rest + 255) / 256 > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "%s: too large", op);
+    void* p[] = {&a, &first};
+    return launch(std::string("nsrk_") + op + "_" + dt_name(dtype) + "_s", cdiv_u(rest, 256), 1, 256, 0, stream,
+                  p);
+  }
+  return NSR_OK;
+}
+
+nsr_status nsr_activation(const void* x, void* y, nsr_dtype dtype, int64_t n, nsr_act act,
+                          nsr_stream_t stream) {
+  if (!x || !y) return fail(NSR_ERR_BAD_ARG, "activation: null pointer");
+  if (!dt_valid(dtype) || n < 0) return fail(NSR_ERR_BAD_ARG, "activation: bad dtype or n");
+  if (act != NSR_ACT_SILU && act != NSR_ACT_GELU_ERF)
+    return fail(NSR_ERR_BAD_ARG, "activation: act must be SILU or GELU_ERF");
+  if (n == 0) return NSR_OK;
+  nsr_ew_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.a = x;
+  a.out = y;
+  a.n = n;
+  a.act = (int32_t)act;
+  return ew_launch(act == NSR_ACT_SILU ? "silu" : "gelu", dtype, a, aligned(x, 16) && aligned(y, 16), stream);
+}
+
+nsr_status nsr_glu_silu(const void* fc1, void* out, nsr_dtype dtype, int64_t n, nsr_stream_t stream) {
+  if (!fc1 || !out) return fail(NSR_ERR_BAD_ARG, "glu_silu: null pointer");
+  if (!dt_valid(dtype) || n < 0) return fail(NSR_ERR_BAD_ARG, "glu_silu: bad dtype or n");
+  if (n == 0) return NSR_OK;
+  nsr_ew_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.a = fc1;
+  a.out = out;
+  a.n = n;
+  const bool ok = aligned(fc1, 16) && aligned(out, 16) && ((n * dt_size(dtype)) % 16 == 0);
+  return ew_launch("glu", dtype, a, ok, stream);
+}
+
+nsr_status nsr_residual_add(const void* x, const void* res, void* out, nsr_dtype dtype, int64_t n,
+                            nsr_stream_t stream) {
+  if (!x || !res || !out) return fail(NSR_ERR_BAD_ARG, "residual_add: null pointer");
+  if (!dt_valid(dtype) || n < 0) return fail(NSR_ERR_BAD_ARG, "residual_add: bad dtype or n");
+  if (n == 0) return NSR_OK;
+  nsr_ew_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.a = x;
+  a.b = res;
+  a.out = out;
+  a.n = n;
+  return ew_launch("add", dtype, a, aligned(x, 16) && aligned(res, 16) && aligned(out, 16), stream);
+}
+
+}  // extern "C"

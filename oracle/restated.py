@@ -1,0 +1,206 @@
+"""ctypes bindings to oracle/_build/libnsr_oracle.so (TEST INFRASTRUCTURE).
+
+Every function takes and returns numpy arrays. See nsr_oracle.c for the
+reference file:line each restatement follows.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+_LIB_PATH = Path(__file__).resolve().parent / "_build" / "libnsr_oracle.so"
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+_i64p = np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS")
+_I64 = C.c_int64
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            raise FileNotFoundError(f"{_LIB_PATH} missing: run python -m nspeech_amd.build (or oracle/build.py)")
+        L = C.CDLL(str(_LIB_PATH))
+        L.orc_f16_to_f32.argtypes = [_u16p, _f32p, _I64]
+        L.orc_f32_to_bf16.argtypes = [_f32p, _u16p, _I64]
+        L.orc_bf16_to_f32.argtypes = [_u16p, _f32p, _I64]
+        L.orc_q8_0_dequantize.argtypes = [_u8p, _I64, _I64, _f32p]
+        L.orc_index_select_rows.argtypes = [_f32p, _I64, _I64, _i64p, _I64, _f32p]
+        L.orc_index_select_rows.restype = _I64
+        L.orc_q8_0_embedding.argtypes = [_u8p, _I64, _I64, _i64p, _I64, C.c_int, _f32p, _f32p]
+        L.orc_q8_0_embedding.restype = _I64
+        L.orc_silu_f32.argtypes = [_f32p, _f32p, _I64]
+        L.orc_gelu_erf_f32.argtypes = [_f32p, _f32p, _I64]
+        L.orc_glu_silu_f32.argtypes = [_f32p, _f32p, _I64]
+        L.orc_fast_add_f32.argtypes = [_f32p, _f32p, _f32p, _I64]
+        L.orc_layernorm_candle_f32.argtypes = [_f32p, C.c_void_p, C.c_void_p, _f32p, _I64, _I64, C.c_float, C.c_int]
+        L.orc_layernorm_twopass_f32.argtypes = [_f32p, C.c_void_p, C.c_void_p, _f32p, _I64, _I64, C.c_float,
+                                                C.c_int, C.c_int]
+        L.orc_resadd_ln_gelu_bf16.argtypes = [_u16p, _u16p, _u16p, _u16p, C.c_void_p, _u16p, _I64, _I64,
+                                              C.c_float, C.c_int, C.c_int]
+        L.orc_rope_table_f32.argtypes = [_f32p, _I64, C.c_int, C.c_float]
+        L.orc_rotary_f32.argtypes = [_f32p, _f32p, _I64, _I64, _I64, _I64, C.c_int, C.c_float, _I64, _f32p, C.c_int]
+        L.orc_adain_snake_f32.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _I64, _I64, _I64, _I64, _I64,
+                                          C.c_float, C.c_int]
+        _lib = L
+    return _lib
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+# -------------------------------------------------------------- dtypes ---
+
+def f16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    h = _c(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().orc_f16_to_f32(h.ravel(), out.ravel(), h.size)
+    return out
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_bf16(x.ravel(), out.ravel(), x.size)
+    return out
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    b = _c(b, np.uint16)
+    out = np.empty(b.shape, np.float32)
+    lib().orc_bf16_to_f32(b.ravel(), out.ravel(), b.size)
+    return out
+
+
+# ---------------------------------------------------------------- Q8_0 ---
+
+def q8_0_dequantize(blocks: np.ndarray, vocab: int, d: int) -> np.ndarray:
+    blocks = _c(blocks, np.uint8)
+    assert blocks.size == vocab * (d // 32) * 34
+    out = np.empty((vocab, d), np.float32)
+    lib().orc_q8_0_dequantize(blocks.ravel(), vocab, d, out.ravel())
+    return out
+
+
+def q8_0_embedding(blocks: np.ndarray, vocab: int, d: int, ids: np.ndarray, act: int = 0):
+    """QEmbedding::forward (+ silu when act == 1). Returns (out, n_bad_ids)."""
+    blocks = _c(blocks, np.uint8)
+    ids64 = _c(ids, np.int64).ravel()
+    table = np.empty(vocab * d, np.float32)
+    out = np.empty((ids64.size, d), np.float32)
+    bad = lib().orc_q8_0_embedding(blocks.ravel(), vocab, d, ids64, ids64.size, act, table, out.ravel())
+    return out, int(bad)
+
+
+# --------------------------------------------------------- activations ---
+
+def silu(x: np.ndarray) -> np.ndarray:
+    x = _c(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_silu_f32(x.ravel(), y.ravel(), x.size)
+    return y
+
+
+def gelu_erf(x: np.ndarray) -> np.ndarray:
+    x = _c(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_gelu_erf_f32(x.ravel(), y.ravel(), x.size)
+    return y
+
+
+def glu_silu(fc1: np.ndarray) -> np.ndarray:
+    fc1 = _c(fc1, np.float32).ravel()
+    n = fc1.size // 2
+    out = np.empty(n, np.float32)
+    lib().orc_glu_silu_f32(fc1, out, n)
+    return out
+
+
+def fast_add(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    a = _c(a, np.float32)
+    b = _c(b, np.float32)
+    out = np.empty_like(a)
+    lib().orc_fast_add_f32(a.ravel(), b.ravel(), out.ravel(), a.size)
+    return out
+
+
+# ----------------------------------------------------------- LayerNorm ---
+
+def layernorm_candle(x, w=None, b=None, eps=1e-5, nthreads=1):
+    x = _c(x, np.float32)
+    cols = x.shape[-1]
+    rows = x.size // cols
+    w = None if w is None else _c(w, np.float32)
+    b = None if b is None else _c(b, np.float32)
+    y = np.empty_like(x)
+    lib().orc_layernorm_candle_f32(x.ravel(), _ptr(w), _ptr(b), y.ravel(), rows, cols, eps, nthreads)
+    return y
+
+
+def layernorm_twopass(x, w=None, b=None, eps=1e-5, unit_offset=False, nthreads=1):
+    x = _c(x, np.float32)
+    cols = x.shape[-1]
+    rows = x.size // cols
+    w = None if w is None else _c(w, np.float32)
+    b = None if b is None else _c(b, np.float32)
+    y = np.empty_like(x)
+    lib().orc_layernorm_twopass_f32(x.ravel(), _ptr(w), _ptr(b), y.ravel(), rows, cols, eps, int(unit_offset),
+                                    nthreads)
+    return y
+
+
+def resadd_ln_gelu_bf16(x_bits, res_bits, w_bits, b_bits, eps=1e-5, gelu=True, nthreads=1):
+    """bf16 chain (all arguments/outputs are bf16 bit patterns). Returns (h, y)."""
+    x_bits = _c(x_bits, np.uint16)
+    res_bits = _c(res_bits, np.uint16)
+    cols = x_bits.shape[-1]
+    rows = x_bits.size // cols
+    h = np.empty_like(x_bits)
+    y = np.empty_like(x_bits)
+    lib().orc_resadd_ln_gelu_bf16(x_bits.ravel(), res_bits.ravel(), _c(w_bits, np.uint16), _c(b_bits, np.uint16),
+                                  h.ctypes.data_as(C.c_void_p), y.ravel(), rows, cols, eps, int(gelu), nthreads)
+    return h, y
+
+
+# -------------------------------------------------------------- rotary ---
+
+def rope_table(max_pos: int, rot: int, theta: float) -> np.ndarray:
+    t = np.empty((max_pos, rot), np.float32)
+    lib().orc_rope_table_f32(t.ravel(), max_pos, rot, theta)
+    return t
+
+
+def rotary(x, rot: int, theta: float, pos0: int = 0, nthreads=1):
+    """x [B, H, T, Dh] -> rotated copy (apply_rotary_pos_emb on one tensor)."""
+    x = _c(x, np.float32)
+    B, H, T, Dh = x.shape
+    out = np.empty_like(x)
+    cs = np.empty(max(1, T * rot), np.float32)
+    lib().orc_rotary_f32(x.ravel(), out.ravel(), B, H, T, Dh, rot, theta, pos0, cs, nthreads)
+    return out
+
+
+# ------------------------------------------------------ AdaIN + Snake ---
+
+def adain_snake(x, gamma, beta, alpha, eps=1e-5, nthreads=1):
+    """x [B, C, T]; gamma/beta [C] (shared) or [B, C]; alpha [C]."""
+    x = _c(x, np.float32)
+    B, Cc, T = x.shape
+    gamma = _c(gamma, np.float32)
+    beta = _c(beta, np.float32)
+    gs = Cc if gamma.ndim == 2 else 0
+    bs = Cc if beta.ndim == 2 else 0
+    out = np.empty_like(x)
+    lib().orc_adain_snake_f32(x.ravel(), gamma.ravel(), beta.ravel(), _c(alpha, np.float32).ravel(), out.ravel(),
+                              B, Cc, T, gs, bs, eps, nthreads)
+    return out

@@ -1,0 +1,99 @@
+"""The C ABI boundary on the CPU: the library loads, exports exactly what
+include/nspeech_rocm.h declares, validates arguments before touching the GPU,
+and fails loudly (no CPU fallback) when there is no GPU."""
+import ctypes as C
+import re
+import subprocess
+
+import pytest
+import torch
+
+from nspeech_amd import abi
+
+NULL = None
+
+
+def test_library_exports_every_declared_function():
+    L = abi.lib()
+    declared = abi.header_functions()
+    assert len(declared) >= 13
+    for name in declared:
+        assert hasattr(L, name), f"{name} declared in include/nspeech_rocm.h but not exported"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(abi.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r" T (nsr_[a-z0-9_]+)$", out, flags=re.M))
+    assert exported == set(declared), exported ^ set(declared)
+
+
+def test_embedded_code_objects_are_gfx950():
+    out = subprocess.run(["nm", "-D", "--defined-only", str(abi.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    units = re.findall(r" R nsr_co_([a-z0-9_]+)$", out, flags=re.M)
+    assert sorted(units) == sorted(["q8_0_gather", "layernorm", "rotary", "adain_snake", "elementwise"])
+    for u in units:
+        p = abi.LIB_DIR / f"nsr_{u}_gfx950.hsaco"
+        head = p.read_bytes()[:64]
+        assert head[:4] == b"\x7fELF" and head[18] == 0xE0  # EM_AMDGPU
+        assert b"gfx950" in p.read_bytes()
+
+
+def test_version_and_header_is_plain_c():
+    assert "gfx950" in abi.version()
+    text = abi.HEADER.read_text()
+    assert "torch" not in text and "hip_runtime" not in text
+
+
+@pytest.mark.parametrize("call", [
+    lambda L: L.nsr_layernorm(NULL, 0, NULL, NULL, 0, 16, 0, 4, 8, 8, 8, C.c_float(1e-5), 0, 0, NULL),
+    lambda L: L.nsr_layernorm(16, 0, NULL, NULL, 0, 16, 0, 4, 0, 8, 8, C.c_float(1e-5), 0, 0, NULL),
+    lambda L: L.nsr_layernorm(16, 0, NULL, NULL, 0, 16, 0, 4, 8, 4, 8, C.c_float(1e-5), 0, 0, NULL),
+    lambda L: L.nsr_layernorm(16, 7, NULL, NULL, 0, 16, 0, 4, 8, 8, 8, C.c_float(1e-5), 0, 0, NULL),
+    lambda L: L.nsr_layernorm(16, 0, NULL, NULL, 2, 16, 0, 4, 8, 8, 8, C.c_float(1e-5), 0, 0, NULL),
+    lambda L: L.nsr_layernorm(16, 0, NULL, NULL, 0, 16, 0, 4, 8, 8, 8, C.c_float(1e-5), 4, 0, NULL),
+    lambda L: L.nsr_layernorm(16, 0, NULL, NULL, 0, 16, 0, 4, 8, 8, 8, C.c_float(1e-5), 0, 9, NULL),
+    lambda L: L.nsr_residual_add_layernorm(16, 0, NULL, 0, NULL, 0, NULL, NULL, 0, 16, 0, 4, 8, C.c_float(1e-5),
+                                           0, 0, NULL),
+    lambda L: L.nsr_rope_table_f32(NULL, 4, 32, C.c_float(1e4)),
+    lambda L: L.nsr_rope_table_f32(16, 4, 31, C.c_float(1e4)),
+    lambda L: L.nsr_rotary_partial_interleaved_f32(16, 16, 16, 16, 1, 8, 8, 16, 64, 34, C.c_float(1e4), 0, NULL, 0,
+                                                   NULL),
+    lambda L: L.nsr_rotary_partial_interleaved_f32(16, 16, 16, 16, 1, 8, 8, 16, 64, 66, C.c_float(1e4), 0, NULL, 0,
+                                                   NULL),
+    lambda L: L.nsr_rotary_partial_interleaved_f32(16, 16, 16, NULL, 1, 8, 8, 16, 64, 32, C.c_float(1e4), 0, NULL,
+                                                   0, NULL),
+    lambda L: L.nsr_rotary_partial_interleaved_f32(17, NULL, 16, NULL, 1, 8, 8, 16, 64, 32, C.c_float(1e4), 0,
+                                                   NULL, 0, NULL),
+    lambda L: L.nsr_rotary_partial_interleaved_f32(16, NULL, 16, NULL, 1, 8, 8, 16, 64, 32, C.c_float(1e4), 8, 16,
+                                                   20, NULL),
+    lambda L: L.nsr_adain_snake_f32(16, 16, 16, 16, 0, 0, 0, 16, 1, 4, 0, C.c_float(1e-5), NULL),
+    lambda L: L.nsr_adain_snake_f32(16, NULL, 16, 16, 0, 0, 0, 16, 1, 4, 100, C.c_float(1e-5), NULL),
+    lambda L: L.nsr_adain_snake_f32(16, 16, 16, 16, 2, 0, 0, 16, 1, 4, 100, C.c_float(1e-5), NULL),
+    lambda L: L.nsr_q8_0_embed_gather(16, 100, 48, 16, 0, 4, 16, 0, NULL, NULL),
+    lambda L: L.nsr_q8_0_embed_gather(16, 100, 64, 16, 0, 4, 20, 0, NULL, NULL),
+    lambda L: L.nsr_q8_0_embed_gather(17, 100, 64, 16, 0, 4, 16, 0, NULL, NULL),
+    lambda L: L.nsr_q8_0_embed_gather(16, 0, 64, 16, 0, 4, 16, 0, NULL, NULL),
+    lambda L: L.nsr_activation(16, 16, 0, 100, 0, NULL),
+    lambda L: L.nsr_activation(16, 16, 5, 100, 1, NULL),
+    lambda L: L.nsr_glu_silu(NULL, 16, 0, 100, NULL),
+    lambda L: L.nsr_residual_add(16, NULL, 16, 0, 100, NULL),
+])
+def test_invalid_arguments_are_rejected_before_any_launch(call):
+    L = abi.lib()
+    st = call(L)
+    assert st in (abi.NSR_ERR_BAD_ARG, abi.NSR_ERR_UNSUPPORTED), st
+    assert L.nsr_last_error().decode()
+
+
+def test_empty_inputs_are_no_ops():
+    L = abi.lib()
+    assert L.nsr_layernorm(16, 0, NULL, NULL, 0, 16, 0, 0, 8, 8, 8, C.c_float(1e-5), 0, 0, NULL) == abi.NSR_OK
+    assert L.nsr_q8_0_embed_gather(16, 100, 64, 16, 0, 0, 16, 0, NULL, NULL) == abi.NSR_OK
+    assert L.nsr_activation(16, 16, 0, 0, 1, NULL) == abi.NSR_OK
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU error path")
+def test_no_gpu_fails_loudly():
+    with pytest.raises(abi.NsrError) as ei:
+        abi.init()
+    assert ei.value.status in (abi.NSR_ERR_HIP, abi.NSR_ERR_NOT_INIT)
+    assert abi.lib().nsr_kernel_count() == 0

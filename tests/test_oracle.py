@@ -1,0 +1,287 @@
+"""Pin the CPU oracle (oracle/nsr_oracle.c) before trusting it (CPU only).
+
+Every restated function is checked against something it was not written
+from: torch/numpy library routines in float64, numpy's own float16/bfloat16
+conversions, a complex-number formulation of the rotation, the structured
+GGUF block decode, and invariants chosen so that a plausible mistake (a
+dropped eps, a wrong pair sign, a transposed index, n-1 instead of n) fails.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from nspeech_amd import configs
+from oracle import closed_form as CF
+from oracle import restated as R
+
+from ._util import RTOL_F32, assert_bitexact, assert_close, rel_err
+
+
+# ------------------------------------------------------------- dtypes ---
+
+def test_f16_decode_all_patterns():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = R.f16_bits_to_f32(bits)
+    ref = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert_bitexact(got[~nan], ref[~nan], "f16 -> f32")
+
+
+def test_bf16_rounding_matches_torch():
+    g = configs.rng(7)
+    x = np.concatenate([
+        g.standard_normal(100000).astype(np.float32) * 10,
+        np.array([0.0, -0.0, 1.0, 1.00390625, 1.01171875, 3.0e38, -3.0e38, 1e-40, np.inf, -np.inf], np.float32),
+        # exact ties: 1 + k*2^-8 + 2^-9 (round half to even)
+        (1.0 + np.arange(16) / 256.0 + 1.0 / 512.0).astype(np.float32),
+    ])
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert_bitexact(R.f32_to_bf16_bits(x), ref, "oracle f32->bf16")
+    assert_bitexact(configs.f32_to_bf16_bits(x), ref, "configs f32->bf16")
+    back = R.bf16_bits_to_f32(ref)
+    assert_bitexact(back, torch.from_numpy(ref.view(np.int16)).view(torch.bfloat16).float().numpy(), "bf16->f32")
+
+
+# --------------------------------------------------------------- Q8_0 ---
+
+def test_q8_0_dequant_matches_structured_decode():
+    g = configs.rng(11)
+    vocab, d = 257, 96
+    blocks = configs.make_q8_0_table(g, vocab, d)
+    got = R.q8_0_dequantize(blocks, vocab, d)
+    ref = CF.q8_0_decode(blocks, vocab, d)
+    # int8 * f16 is exact in f32, so the f64 decode rounds to the same f32
+    assert_bitexact(got, ref.astype(np.float32), "q8_0 dequant")
+
+
+def test_q8_0_known_blocks():
+    # block 0: d = 0.5, qs = -127..-96 ; block 1: d = smallest f16 subnormal, qs = 127
+    rec = np.zeros(2, dtype=configs.Q8_BLOCK)
+    rec["d"][0] = np.float16(0.5)
+    rec["qs"][0] = np.arange(-127, -95, dtype=np.int8)
+    rec["d"][1] = np.uint16(1).view(np.float16)
+    rec["qs"][1] = 127
+    got = R.q8_0_dequantize(rec.view(np.uint8), 1, 64)
+    exp0 = np.arange(-127, -95, dtype=np.float32) * np.float32(0.5)
+    exp1 = np.full(32, 127 * 2.0 ** -24, np.float32)
+    assert_bitexact(got[0, :32], exp0, "block 0")
+    assert_bitexact(got[0, 32:], exp1, "block 1")
+
+
+def test_q8_0_embedding_is_row_select_of_dequant():
+    g = configs.rng(12)
+    vocab, d = 50, 64
+    blocks = configs.make_q8_0_table(g, vocab, d)
+    ids = np.array([0, 49, 3, 3, 17, 49, 0], np.int64)
+    out, bad = R.q8_0_embedding(blocks, vocab, d, ids)
+    assert bad == 0
+    dense = CF.q8_0_decode(blocks, vocab, d).astype(np.float32)
+    assert_bitexact(out, dense[ids], "embedding rows")
+    out2, bad2 = R.q8_0_embedding(blocks, vocab, d, np.array([1, 50, -1], np.int64))
+    assert bad2 == 2 and not out2[1:].any()
+    silu, _ = R.q8_0_embedding(blocks, vocab, d, ids, act=1)
+    ref = torch.nn.functional.silu(torch.from_numpy(dense[ids].astype(np.float64))).numpy()
+    assert_close(silu, ref, 1e-6, "embedding + silu vs torch f64")
+
+
+# -------------------------------------------------------- activations ---
+
+def _act_inputs():
+    g = configs.rng(13)
+    return np.concatenate([g.standard_normal(20000).astype(np.float32) * 4,
+                           np.linspace(-30, 30, 2001, dtype=np.float32),
+                           np.array([0.0, -0.0, 1e-30, -1e-30, 88.0, -88.0, -104.0], np.float32)])
+
+
+def test_silu_matches_torch_f64():
+    x = _act_inputs()
+    ref = torch.nn.functional.silu(torch.from_numpy(x.astype(np.float64))).numpy()
+    assert_close(R.silu(x), ref, 1e-6, "silu")
+    assert R.silu(np.zeros(1, np.float32))[0] == 0.0
+
+
+def test_gelu_erf_matches_torch_f64():
+    x = _act_inputs()
+    ref = torch.nn.functional.gelu(torch.from_numpy(x.astype(np.float64)), approximate="none").numpy()
+    assert_close(R.gelu_erf(x), ref, 1e-6, "gelu")
+    # odd part of gelu is x/2: gelu(x) - gelu(-x) = x
+    xs = np.linspace(-5, 5, 101).astype(np.float32)
+    assert_close(R.gelu_erf(xs).astype(np.float64) - R.gelu_erf(-xs), xs, 1e-6, "gelu odd part")
+    assert np.array_equal(CF.gelu_erf(x[:50]), CF.gelu_erf(x[:50]))
+
+
+def test_glu_and_fast_add():
+    g = configs.rng(14)
+    fc1 = g.standard_normal(2 * 1000).astype(np.float32)
+    ref = torch.nn.functional.silu(torch.from_numpy(fc1[1000:].astype(np.float64))).numpy() * fc1[:1000]
+    assert_close(R.glu_silu(fc1), ref, 1e-6, "glu")
+    a, b = g.standard_normal(999).astype(np.float32), g.standard_normal(999).astype(np.float32)
+    assert_bitexact(R.fast_add(a, b), a + b, "fast_add")
+
+
+# --------------------------------------------------------- LayerNorm ---
+
+def test_layernorm_candle_matches_torch_f64():
+    c = configs.c0()
+    ref = torch.nn.functional.layer_norm(torch.from_numpy(c["x"].astype(np.float64)), (1024,),
+                                         torch.from_numpy(c["gamma"].astype(np.float64)),
+                                         torch.from_numpy(c["beta"].astype(np.float64)), eps=1e-5).numpy()
+    e1 = assert_close(R.layernorm_candle(c["x"], c["gamma"], c["beta"]), ref, RTOL_F32, "candle LN")
+    e2 = assert_close(R.layernorm_twopass(c["x"], c["gamma"], c["beta"]), ref, RTOL_F32, "two-pass LN")
+    assert e1 < 2e-6 and e2 < 2e-6
+
+
+def test_layernorm_unit_offset_and_invariants():
+    g = configs.rng(15)
+    x = (g.standard_normal((64, 288)) * 3 + 5).astype(np.float32)
+    w = (0.1 * g.standard_normal(288)).astype(np.float32)
+    got = R.layernorm_twopass(x, w, unit_offset=True)
+    assert_close(got, CF.layernorm(x, w, unit_offset=True), RTOL_F32, "unit offset LN")
+    # no affine: per-row mean 0 and variance var/(var+eps)
+    y = R.layernorm_twopass(x).astype(np.float64)
+    var = x.astype(np.float64).var(axis=-1)
+    assert np.abs(y.mean(axis=-1)).max() < 1e-6
+    assert np.abs(y.var(axis=-1) - var / (var + 1e-5)).max() < 1e-5
+    # constant row -> exactly beta (x - mean == 0)
+    xc = np.full((2, 128), 0.5, np.float32)
+    b = g.standard_normal(128).astype(np.float32)
+    assert_bitexact(R.layernorm_candle(xc, np.ones(128, np.float32), b)[0], b, "constant row")
+    assert_bitexact(R.layernorm_twopass(xc, np.ones(128, np.float32), b)[1], b, "constant row")
+
+
+def test_resadd_ln_gelu_bf16_chain():
+    c = configs.c4a(rows=96)
+    wb = configs.f32_to_bf16_bits(c["gamma"])
+    bb = configs.f32_to_bf16_bits(c["beta"])
+    h, y = R.resadd_ln_gelu_bf16(c["x"], c["res"], wb, bb)
+    xf, rf = configs.bf16_bits_to_f32(c["x"]), configs.bf16_bits_to_f32(c["res"])
+    h_ref = torch.from_numpy(xf + rf).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert_bitexact(h, h_ref, "h = bf16(x + res)")
+    hf = configs.bf16_bits_to_f32(h).astype(np.float64)
+    ref = CF.gelu_erf(CF.layernorm(hf, c["gamma"], c["beta"]))
+    yf = configs.bf16_bits_to_f32(y)
+    assert_close(yf, ref, 1e-2, "bf16 chain vs f64")
+    # the chain rounds n = LN(h)*w+b to bf16 (unit roundoff 2^-8 |n|, carried
+    # by gelu' <= 1.13) and then y (2^-8 |y|): bound each element by that
+    n = CF.layernorm(hf, c["gamma"], c["beta"])
+    bound = 1.13 * 2.0 ** -8 * np.abs(n) * 1.01 + 2.0 ** -8 * np.abs(ref) * 1.01 + 1e-6
+    assert np.all(np.abs(yf - ref) <= bound)
+
+
+# ------------------------------------------------------------ rotary ---
+
+def test_rope_table_matches_f64_of_f32_angles():
+    tab = R.rope_table(1024, 32, 10000.0)
+    f = CF.inv_freq_f32(32, 10000.0)
+    ang = (np.arange(1024, dtype=np.float32)[:, None] * f[None, :]).astype(np.float32).astype(np.float64)
+    assert_close(tab[:, :16], np.cos(ang), 1.2e-7, "cos")
+    assert_close(tab[:, 16:], np.sin(ang), 1.2e-7, "sin")
+
+
+def test_rope_table_of_product_equals_oracle():
+    """The library's host-side table builder (CPU only) equals the oracle's."""
+    from nspeech_amd import abi
+
+    for max_pos, rot, theta in [(1024, 32, 10000.0), (17, 64, 500000.0), (3, 4, 10.0)]:
+        assert_bitexact(abi.rope_table(max_pos, rot, theta).numpy(), R.rope_table(max_pos, rot, theta),
+                        f"table {max_pos},{rot},{theta}")
+
+
+def test_rotary_matches_complex_rotation():
+    c = configs.c1(T=256)
+    for pos0 in (0, 700):
+        got = R.rotary(c["q"], c["rot"], c["theta"], pos0)
+        ref = CF.rotary(c["q"], c["rot"], c["theta"], pos0)
+        assert_close(got, ref, 1e-6, f"rotary pos0={pos0}")
+
+
+def test_rotary_invariants():
+    c = configs.c1(T=64)
+    q = c["q"]
+    out = R.rotary(q, 32, 10000.0, 0)
+    assert_bitexact(out[:, :, 0], q[:, :, 0], "position 0 is identity")
+    assert_bitexact(out[..., 32:], q[..., 32:], "pass-through dims")
+    n_in = q[..., :32:2].astype(np.float64) ** 2 + q[..., 1:32:2].astype(np.float64) ** 2
+    n_out = out[..., :32:2].astype(np.float64) ** 2 + out[..., 1:32:2].astype(np.float64) ** 2
+    assert np.max(np.abs(n_out - n_in) / np.maximum(n_in, 1e-3)) < 1e-5
+    # a rotation by +angle (not -angle): pair (1, 0) at pos 1, i=0 goes to (cos 1, sin 1)
+    e = np.zeros((1, 1, 2, 4), np.float32)
+    e[0, 0, 1, 0] = 1.0
+    o = R.rotary(e, 4, 10000.0, 0)
+    assert abs(o[0, 0, 1, 0] - math.cos(1.0)) < 1e-7 and abs(o[0, 0, 1, 1] - math.sin(1.0)) < 1e-7
+
+
+# ----------------------------------------------------- AdaIN + Snake ---
+
+def test_adain_snake_matches_torch_instance_norm():
+    c = configs.c2(C=64)
+    x64 = torch.from_numpy(c["x"].astype(np.float64))
+    xn = torch.nn.functional.instance_norm(x64, eps=1e-5).numpy()
+    y = xn * (1.0 + c["gamma"].astype(np.float64))[None, :, None] + c["beta"].astype(np.float64)[None, :, None]
+    a = c["alpha"].astype(np.float64)[None, :, None]
+    inv_a = (1.0 / (c["alpha"] + np.float32(1e-9))).astype(np.float64)[None, :, None]
+    ref = y + np.sin(a * y) ** 2 * inv_a
+    got = R.adain_snake(c["x"], c["gamma"], c["beta"], c["alpha"])
+    assert_close(got, ref, RTOL_F32, "adain+snake vs torch instance_norm")
+    assert_close(CF.adain_snake(c["x"], c["gamma"], c["beta"], c["alpha"]), ref, 1e-12, "closed form")
+
+
+def test_adain_snake_kokoro_known_answer():
+    """Inputs and expected formula of test_adain_snake_f32_large
+    (src/kokoro/gpu_decoder.rs:78-129): f64 statistics, f32 apply."""
+    for C_, T_ in ((4, 100), (128, 11281)):
+        k = configs.kokoro_kat(C_, T_)
+        g32, b32, a32 = (k[n].astype(np.float32) for n in ("gamma", "beta", "alpha"))
+        got = R.adain_snake(k["x"], g32, b32, a32)
+        x = k["x"][0]
+        mean = (x.astype(np.float64).sum(axis=1) / T_).astype(np.float32)
+        var = ((x.astype(np.float64) - mean.astype(np.float64)[:, None]) ** 2).sum(axis=1) / T_
+        rstd = (np.float32(1.0) / np.sqrt(var.astype(np.float32) + np.float32(1e-5))).astype(np.float32)
+        scale = (g32 + np.float32(1.0)) * rstd
+        inv_a = np.float32(1.0) / (a32 + np.float32(1e-9))
+        styled = scale[:, None] * (x - mean[:, None]) + b32[:, None]
+        s = np.sin(a32[:, None] * styled)
+        expected = styled + s * s * inv_a[:, None]
+        assert_close(got[0], expected, RTOL_F32, f"kokoro KAT C={C_} T={T_}")
+
+
+def test_adain_snake_invariants():
+    g = configs.rng(16)
+    x = (g.standard_normal((2, 3, 500)) * 2 + 3).astype(np.float32)
+    z = np.zeros(3, np.float32)
+    big = np.full(3, 1e6, np.float32)
+    # gamma = beta = 0: y is the plain two-pass LN (same f32 ops), and the
+    # snake term sin^2(alpha y)/alpha lies in [0, 1/alpha]
+    out = R.adain_snake(x, z, z, big).astype(np.float64)
+    y = R.layernorm_twopass(x.reshape(6, 500)).reshape(2, 3, 500).astype(np.float64)
+    assert np.all(out - y >= 0.0) and np.all(out - y <= 1e-6 * (1 + 1e-6) + 1e-6 * np.abs(y))
+    # per-batch gamma/beta index b*C + c
+    gb = g.standard_normal((2, 3)).astype(np.float32) * 0.1
+    assert_close(R.adain_snake(x, gb, gb, np.ones(3, np.float32)), CF.adain_snake(x, gb, gb, np.ones(3)), RTOL_F32,
+                 "per-batch params")
+
+
+def test_adain_snake_large_offset_conditioning():
+    """Rows with |mean| >> std: the reference's sequential f32 mean loses
+    about log2(n |mean| / std) bits, so the restatement is only ~1e-4 from
+    exact here (the GPU kernels are checked against the f64 closed form on
+    such rows)."""
+    g = configs.rng(17)
+    x = (g.standard_normal((2, 3, 500)) * 2 + 100).astype(np.float32)
+    ref = CF.adain_snake(x, np.zeros(3), np.zeros(3), np.ones(3))
+    e = rel_err(R.adain_snake(x, np.zeros(3, np.float32), np.zeros(3, np.float32), np.ones(3, np.float32)), ref)
+    assert 1e-6 < e < 2e-4
+
+
+# ------------------------------------------------------------ golden ---
+
+def test_golden_fixtures_reproduce():
+    from .golden import make_golden
+
+    for name, case in make_golden.load_all().items():
+        fresh = make_golden.compute(name, case)
+        for key, val in fresh.items():
+            assert_bitexact(val, case[key], f"golden {name}:{key}")
