@@ -12,6 +12,8 @@
 #define NSR_DEV __device__ __forceinline__
 
 typedef float nsr_float4 __attribute__((ext_vector_type(4)));
+typedef float nsr_float2 __attribute__((ext_vector_type(2)));
+typedef __bf16 nsr_bf16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t nsr_uint4 __attribute__((ext_vector_type(4)));
 typedef uint32_t nsr_uint2 __attribute__((ext_vector_type(2)));
 
@@ -22,14 +24,15 @@ enum { ACT_NONE = 0, ACT_SILU = 1, ACT_GELU = 2 };
 
 NSR_DEV float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
 
-/* f32 -> bf16 bits, round to nearest even; NaN stays a quiet NaN. Same
- * rounding as the `half` crate's bf16::from_f32 used by Candle. */
-NSR_DEV uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+/* Two f32 -> packed bf16 (lo = a, hi = b), round to nearest even, NaN
+ * quieted: one v_cvt_pk_bf16_f32. Same rounding as the `half` crate's
+ * bf16::from_f32 used by Candle. */
+NSR_DEV uint32_t f32x2_to_bf16x2_bits(float a, float b) {
+  const nsr_float2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, nsr_bf16x2));
 }
+
+NSR_DEV uint32_t f32_to_bf16_bits(float f) { return f32x2_to_bf16x2_bits(f, 0.0f) & 0xffffu; }
 
 NSR_DEV float f16_bits_to_f32(uint32_t h) {
   _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
@@ -92,15 +95,11 @@ template <int DT> NSR_DEV nsr_uint4 pack16(const float* v) {
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      uint32_t lo, hi;
       if constexpr (DT == DT_BF16) {
-        lo = f32_to_bf16_bits(v[2 * i]);
-        hi = f32_to_bf16_bits(v[2 * i + 1]);
+        r[i] = f32x2_to_bf16x2_bits(v[2 * i], v[2 * i + 1]);
       } else {
-        lo = f32_to_f16_bits(v[2 * i]);
-        hi = f32_to_f16_bits(v[2 * i + 1]);
+        r[i] = f32_to_f16_bits(v[2 * i]) | (f32_to_f16_bits(v[2 * i + 1]) << 16);
       }
-      r[i] = lo | (hi << 16);
     }
   }
   return r;
@@ -117,10 +116,14 @@ template <int DT> NSR_DEV float round_to(float v) {
   }
 }
 
-NSR_DEV nsr_uint4 ld16(const void* p) { return *(const nsr_uint4*)p; }
-NSR_DEV void st16(void* p, nsr_uint4 v) { *(nsr_uint4*)p = v; }
-NSR_DEV nsr_float4 ldf4(const float* p) { return *(const nsr_float4*)p; }
-NSR_DEV void stf4(float* p, nsr_float4 v) { *(nsr_float4*)p = v; }
+/* 128-bit global access. Data streamed through a kernel once is loaded and
+ * stored non-temporally (it is not kept in L2 for reuse it will not get). */
+NSR_DEV nsr_uint4 ld16(const void* p) { return __builtin_nontemporal_load((const nsr_uint4*)p); }
+NSR_DEV void st16(void* p, nsr_uint4 v) { __builtin_nontemporal_store(v, (nsr_uint4*)p); }
+NSR_DEV nsr_float4 ldf4(const float* p) { return __builtin_nontemporal_load((const nsr_float4*)p); }
+NSR_DEV void stf4(float* p, nsr_float4 v) { __builtin_nontemporal_store(v, (nsr_float4*)p); }
+/* cached 128-bit load, for small data many lanes re-read (gamma, beta) */
+NSR_DEV nsr_uint4 ld16_cached(const void* p) { return *(const nsr_uint4*)p; }
 
 /* ------------------------------------------------------- wave reductions -- */
 
@@ -200,12 +203,37 @@ NSR_DEV void block_sum2(float& a, float& b, float* red) {
 
 /* ------------------------------------------------------------ activations -- */
 
-/* candle silu: v / (1 + exp(-v)) */
-NSR_DEV float act_silu(float v) { return v / (1.0f + expf(-v)); }
+/* silu(v) = v / (1 + exp(-v)) (candle silu), as v * rcp(1 + 2^(-v log2 e))
+ * with the hardware exp2 and reciprocal: branch-free, a few ulp. */
+NSR_DEV float act_silu(float v) {
+  return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(v * -1.4426950408889634f));
+}
 
-/* candle gelu_erf: v * 0.5 * (1 + erf(v / sqrt(2))) */
+/* gelu_erf(v) = v * Phi(v), Phi(v) = 0.5 * (1 + erf(v / sqrt 2)) (candle
+ * gelu_erf). Branch-free erfc from Abramowitz & Stegun, Handbook of
+ * Mathematical Functions, formula 7.1.26: for z >= 0,
+ *   erfc(z) = (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-z^2),
+ *   t = 1 / (1 + p z),  |error| <= 1.5e-7,
+ * with z = |v| / sqrt 2; Phi = 1 - erfc/2 for v >= 0 and erfc/2 below.
+ * The coefficients below are the published a_k halved and p / sqrt 2. */
+#define NSR_AS_P_SQRT2 0.23164189877f   /* 0.3275911 / sqrt(2) */
+#define NSR_AS_HA1 0.127414796f         /* a1 / 2, a1 = 0.254829592 */
+#define NSR_AS_HA2 -0.142248368f        /* a2 / 2, a2 = -0.284496736 */
+#define NSR_AS_HA3 0.7107068705f        /* a3 / 2, a3 = 1.421413741 */
+#define NSR_AS_HA4 -0.7265760135f       /* a4 / 2, a4 = -1.453152027 */
+#define NSR_AS_HA5 0.5307027145f        /* a5 / 2, a5 = 1.061405429 */
 NSR_DEV float act_gelu_erf(float v) {
-  return v * (0.5f * (1.0f + erff(v * 0.70710678118654752f)));
+  const float av = __builtin_fabsf(v);
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(av, NSR_AS_P_SQRT2, 1.0f));
+  float q = __builtin_fmaf(NSR_AS_HA5, t, NSR_AS_HA4);
+  q = __builtin_fmaf(q, t, NSR_AS_HA3);
+  q = __builtin_fmaf(q, t, NSR_AS_HA2);
+  q = __builtin_fmaf(q, t, NSR_AS_HA1);
+  /* exp(-v^2/2) = 2^(-v^2 log2(e) / 2) */
+  const float e = __builtin_amdgcn_exp2f((av * -0.72134752044448170f) * av);
+  const float h = (q * t) * e; /* erfc(|v|/sqrt 2) / 2 */
+  const float phi = v >= 0.0f ? 1.0f - h : h;
+  return v * phi;
 }
 
 template <int ACT> NSR_DEV float apply_act(float v) {

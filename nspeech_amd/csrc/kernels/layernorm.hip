@@ -27,15 +27,17 @@ struct ln_vec {
   static constexpr int value = all32 ? 4 : 8;
 };
 
-template <int DT, int VEC>
+/* VEC elements of dtype DT at base[elem]; NT: streamed (non-temporal) load,
+ * otherwise a cached load (parameters every row re-reads). */
+template <int DT, int VEC, bool NT = true>
 NSR_DEV void load_vec(const void* base, int64_t elem, float* v) {
   constexpr int BYTES = VEC * dt_size<DT>::value;
   const char* p = (const char*)base + elem * dt_size<DT>::value;
   if constexpr (BYTES == 16) {
-    unpack16<DT>(ld16(p), v);
+    unpack16<DT>(NT ? ld16(p) : ld16_cached(p), v);
   } else if constexpr (BYTES == 32) {
-    unpack16<DT>(ld16(p), v);
-    unpack16<DT>(ld16(p + 16), v + 16 / dt_size<DT>::value);
+    unpack16<DT>(NT ? ld16(p) : ld16_cached(p), v);
+    unpack16<DT>(NT ? ld16(p + 16) : ld16_cached(p + 16), v + 16 / dt_size<DT>::value);
   } else { /* 8 bytes: 4 x 16-bit */
     const nsr_uint2 r = *(const nsr_uint2*)p;
     nsr_uint4 r4 = {r[0], r[1], 0u, 0u};
@@ -73,9 +75,9 @@ NSR_DEV void load_param_vec(const void* p, int pdt, int col0, float* v, float fi
 #pragma unroll
     for (int e = 0; e < VEC; ++e) v[e] = fill;
   } else if (pdt == DT_F32) {
-    load_vec<DT_F32, VEC>(p, col0, v);
+    load_vec<DT_F32, VEC, false>(p, col0, v);
   } else {
-    load_vec<DT_F16, VEC>(p, col0, v);
+    load_vec<DT_F16, VEC, false>(p, col0, v);
   }
 }
 
@@ -92,6 +94,22 @@ NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
   const int nchunk = a.n_cols / VEC;
   const int64_t xrow = row * a.ld_x;
   const int64_t yrow = row * a.ld_y;
+
+  /* gamma/beta do not depend on the row: when they fit in 64 more VGPRs
+   * they are loaded up front, so their latency hides under the row's loads
+   * instead of adding a round trip after the reductions. */
+  constexpr bool PREFETCH = NC * VEC <= 32;
+  float gpre[PREFETCH ? NC : 1][VEC], bpre[PREFETCH ? NC : 1][VEC];
+  if constexpr (PREFETCH) {
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      const int j = lane + 64 * k;
+      if (j < nchunk) {
+        load_param_vec<VEC>(a.gamma, pdt, j * VEC, gpre[k], 1.0f);
+        load_param_vec<VEC>(a.beta, pdt, j * VEC, bpre[k], 0.0f);
+      }
+    }
+  }
 
   float v[NC][VEC];
   float sum = 0.f;
@@ -141,8 +159,16 @@ NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
     if (j < nchunk) {
       const int col0 = j * VEC;
       float g[VEC], b[VEC], o[VEC];
-      load_param_vec<VEC>(a.gamma, pdt, col0, g, 1.0f);
-      load_param_vec<VEC>(a.beta, pdt, col0, b, 0.0f);
+      if constexpr (PREFETCH) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          g[e] = gpre[k][e];
+          b[e] = bpre[k][e];
+        }
+      } else {
+        load_param_vec<VEC>(a.gamma, pdt, col0, g, 1.0f);
+        load_param_vec<VEC>(a.beta, pdt, col0, b, 0.0f);
+      }
       const float goff = a.unit_offset ? 1.0f : 0.0f;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
