@@ -358,7 +358,7 @@ def main():
                "per_config": per_cfg, "host_cores": ncores}
 
     traffic = None
-    tf = ROOT / "profiles" / "pmc_traffic.txt"
+    tf = ROOT / "profiles" / "hbm_traffic_bench_workloads.txt"
     if tf.exists():
         for line in tf.read_text().splitlines():
             parts = line.split()
