@@ -141,7 +141,7 @@ def build_workload(name):
             abi.check(L.nsr_adain_snake_f32(s["x"].data_ptr(), g.data_ptr(), b.data_ptr(), a.data_ptr(), 0, gs, gs,
                                             s["o"].data_ptr(), B, C, TT, 1e-5, stream()))
 
-        kern = "nsrk_adain_res_b256_nv5_a" if name == "c2" else "nsrk_adain_res_b1024_nv20_a"
+        kern = "nsrk_adain_row_b256_v5_l0" if name == "c2" else "nsrk_adain_row_b512_v44_l14"
         return Workload(name, f"AdaIN1d+Snake f32 x[{B},{C},{TT}]", configs.algorithmic_bytes(name),
                         2 * x0.numel() * 4, make_set, launch, kern, "f32")
 
@@ -201,31 +201,50 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms):
         w.launch(sets[i % nsets])
     torch.cuda.synchronize()
 
+    def held(enqueue, n, per_call_ms):
+        """Hold the stream with a spin kernel while `enqueue` issues n calls,
+        so the GPU then runs them back to back. Returns True when the host
+        finished enqueueing before the hold expired (else the timing would
+        include host launch gaps and the caller retries with a longer hold)."""
+        hold_ms = 5.0 + per_call_ms * n
+        torch.cuda.synchronize()
+        torch.cuda._sleep(int(cyc_per_ms * hold_ms))
+        h0 = time.perf_counter()
+        enqueue()
+        host_ms = (time.perf_counter() - h0) * 1e3
+        torch.cuda.synchronize()
+        return host_ms < 0.8 * hold_ms
+
     def run(order):
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in order]
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        # hold the stream while the calls are enqueued (~40 us of host work each)
-        torch.cuda._sleep(int(cyc_per_ms * (5.0 + 0.06 * len(order))))
-        t0.record()
-        for (a, b), i in zip(ev, order):
-            a.record()
-            w.launch(sets[i])
-            b.record()
-        t1.record()
-        torch.cuda.synchronize()
+
+        def enqueue():
+            t0.record()
+            for (a, b), i in zip(ev, order):
+                a.record()
+                w.launch(sets[i])
+                b.record()
+            t1.record()
+
+        for per_call in (0.15, 0.6):
+            if held(enqueue, len(order), per_call):
+                break
         per = [a.elapsed_time(b) * 1e3 for a, b in ev]  # us
         return per, t0.elapsed_time(t1) * 1e3 / len(order)
 
     def run_plain(order):
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        torch.cuda._sleep(int(cyc_per_ms * (5.0 + 0.03 * len(order))))
-        t0.record()
-        for i in order:
-            w.launch(sets[i])
-        t1.record()
-        torch.cuda.synchronize()
+
+        def enqueue():
+            t0.record()
+            for i in order:
+                w.launch(sets[i])
+            t1.record()
+
+        for per_call in (0.1, 0.4):
+            if held(enqueue, len(order), per_call):
+                break
         return t0.elapsed_time(t1) * 1e3 / len(order)
 
     rotating = [i % nsets for i in range(steps)]

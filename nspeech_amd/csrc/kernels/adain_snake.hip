@@ -9,17 +9,26 @@
  * gamma/beta come per (batch, channel) from the style Linear (precomputed and
  * rounded to f16 for the GPU backend, decoder.rs:966-981), alpha per channel.
  *
- * Resident kernel (one workgroup per (b, c) row): the row is read from HBM
- * once into VGPRs (NV float4 per lane) and, for long rows, LDS (filled with
- * global_load_lds_dwordx4, no VGPR staging); mean and centred variance are
- * two passes over on-chip data; the apply pass writes out once. HBM traffic
- * is the algorithmic 8 bytes per element. sin^2 uses a period-pi reduction in
- * y units and a fitted polynomial (device_common.h), about 16 VALU ops per
- * element in total.
+ * Row kernel (aligned rows: x, out 16-byte aligned, T % 4 == 0), one
+ * workgroup per (b, c) row. The row is read from HBM once, as BLOCK-wide
+ * slots of 16-byte chunks: NV slots land in VGPRs (buffer_load_dwordx4 with
+ * the slot offset in an SGPR) and NL more go straight to LDS
+ * (buffer_load_dwordx4 ... lds). Statistics are a single pass about a shift K
+ * (the mean of slot 0, reduced while the other slots are still in flight):
+ * s1 = sum(x - K), s2 = sum((x - K)^2), mean = K + s1/T,
+ * var = s2/T - (s1/T)^2, accurate when |mean| >> std because K is within a
+ * few std of the mean. The apply pass writes out once, so HBM traffic is the
+ * algorithmic 8 bytes per element. Chunks past the row end read as 0 through
+ * the buffer range check and are masked out of the sums; their stores are
+ * dropped by the same check.
  *
- * Split path (rows longer than the on-chip budget, or unaligned pointers):
- * a stats kernel (single read, shifted sums) then an apply kernel (second
- * read): 12 bytes per element.
+ * Measured on MI355X: 512 threads x (44 VGPR + up to 18 LDS slots) beats a
+ * 1024-thread workgroup, whose 128-VGPR budget forces spills, and keeps 8
+ * waves per CU streaming; x[8,128,115200] runs at ~5.3 TB/s.
+ *
+ * Unaligned rows take the register-resident kernel at the end (global loads,
+ * partial edge chunks per element). Rows longer than the on-chip budget take
+ * the split path: a stats kernel (one read) and an apply kernel (second read).
  */
 #include "device_common.h"
 
@@ -29,8 +38,150 @@ NSR_DEV float adain_param(const void* p, int pdt, int64_t i) {
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-/* Element-wise access to a partial chunk (row edge when not ALIGNED):
- * element idx of chunk space belongs to the row iff lo <= idx < hi. */
+NSR_DEV nsr_float4 adain_snake4(nsr_float4 d, float A, float bet, const snake_consts& sc) {
+  nsr_float4 o;
+  o.x = snake_eval(__builtin_fmaf(d.x, A, bet), sc);
+  o.y = snake_eval(__builtin_fmaf(d.y, A, bet), sc);
+  o.z = snake_eval(__builtin_fmaf(d.z, A, bet), sc);
+  o.w = snake_eval(__builtin_fmaf(d.w, A, bet), sc);
+  return o;
+}
+
+NSR_DEV float sumsq4(nsr_float4 d, float sq) {
+  sq = __builtin_fmaf(d.x, d.x, sq);
+  sq = __builtin_fmaf(d.y, d.y, sq);
+  sq = __builtin_fmaf(d.z, d.z, sq);
+  return __builtin_fmaf(d.w, d.w, sq);
+}
+
+NSR_DEV float sum4(nsr_float4 d) { return (d.x + d.y) + (d.z + d.w); }
+
+/* ------------------------------------------------------------ row kernel -- */
+
+template <int BLOCK, int NV, int NL>
+NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
+  constexpr int NW = BLOCK / 64;
+  constexpr int NS = NV + NL;
+  static_assert(NS <= 64, "slot mask is 64 bits");
+  typedef typename std::conditional<(NS <= 32), uint32_t, uint64_t>::type mask_t;
+  constexpr int MB = 8 * (int)sizeof(mask_t);
+  extern __shared__ nsr_float4 lds_x[];
+  __shared__ float red[2 * NW];
+
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  if (row >= a.n_rows) return;
+  const int64_t T = a.T;
+  const int nch = (int)(T >> 2);
+  const uint32_t rbytes = (uint32_t)(T * 4);
+  const uint32_t voff = (uint32_t)tid * 16u;
+
+  /* per-row parameters first: their loads are then the oldest outstanding */
+  const int64_t bi = row / a.C;
+  const int64_t ci = row - bi * a.C;
+  const float gam = adain_param(a.gamma, pdt, bi * a.gamma_bstride + ci);
+  const float bet = adain_param(a.beta, pdt, bi * a.beta_bstride + ci);
+  const float alp = adain_param(a.alpha, pdt, ci);
+
+  const nsr_rsrc xr = make_rsrc(a.x + row * T, rbytes);
+  nsr_float4 v[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) v[k] = buf_load4(xr, voff, (uint32_t)(k * BLOCK * 16));
+  /* LDS slots of this wave: base address wave-uniform (an SGPR, M0 per load);
+   * lane i of the wave lands at base + 16 i, i.e. at lds_x[m * BLOCK + tid] */
+  lds_void* const lw = (lds_void*)(lds_x + __builtin_amdgcn_readfirstlane(tid & ~63));
+#pragma unroll
+  for (int m = 0; m < NL; ++m)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)((char*)lw + m * BLOCK * 16), 16, voff,
+                                             (uint32_t)((NV + m) * BLOCK * 16), 0, 0);
+
+  /* bit k: slot k of this lane lies inside the row */
+  const int nvalid = nch > tid ? (nch - tid + BLOCK - 1) / BLOCK : 0;
+  const mask_t valid = nvalid >= MB ? (mask_t)~(mask_t)0 : (mask_t)(((mask_t)1 << nvalid) - 1);
+  const nsr_float4 zero4 = {0.f, 0.f, 0.f, 0.f};
+
+  /* shift K: mean of slot 0 (the first min(T, 4 BLOCK) elements) */
+  const float n0 = (float)(nch < BLOCK ? 4 * nch : 4 * BLOCK);
+  const float K = block_sum<NW>(sum4(v[0]), red) / n0;
+
+  float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const nsr_float4 d = v[k] - K;
+    v[k] = ((valid >> k) & 1) ? d : zero4;
+    s1 += sum4(v[k]);
+    s2 = sumsq4(v[k], s2);
+  }
+  static_for<0, NL>([&](auto mc) {
+    constexpr int m = decltype(mc)::value;
+    NSR_WAIT_VMCNT(NL - 1 - m); /* LDS slot m has landed */
+    nsr_float4 d = lds_x[m * BLOCK + tid] - K;
+    d = ((valid >> (NV + m)) & 1) ? d : zero4;
+    s1 += sum4(d);
+    s2 = sumsq4(d, s2);
+  });
+  block_sum2<NW>(s1, s2, red);
+  const float c = s1 * a.inv_t; /* mean - K */
+  const float var = fmaxf(__builtin_fmaf(-c, c, s2 * a.inv_t), 0.0f);
+  const float rstd = 1.0f / sqrtf(var + a.eps);
+  const float A = (gam + 1.0f) * rstd;
+  const float Bc = __builtin_fmaf(-c, A, bet); /* (d - c) A + beta = d A + Bc */
+  const snake_consts sc = make_snake_consts(alp);
+
+  const nsr_rsrc orr = make_rsrc(a.out + row * T, rbytes);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) buf_store4(orr, voff, (uint32_t)(k * BLOCK * 16), adain_snake4(v[k], A, Bc, sc));
+#pragma unroll 1
+  for (int m = 0; m < NL; ++m) {
+    const nsr_float4 d = lds_x[m * BLOCK + tid] - K;
+    buf_store4(orr, voff, (uint32_t)((NV + m) * BLOCK * 16), adain_snake4(d, A, Bc, sc));
+  }
+}
+
+#define NSR_ADAIN_ROW(BLOCK, NV, NL)                                                        \
+  extern "C" __global__ void __launch_bounds__(BLOCK)                                      \
+      nsrk_adain_row_b##BLOCK##_v##NV##_l##NL(const nsr_adain_args a, const int pdt) {     \
+    adain_row<BLOCK, NV, NL>(a, pdt);                                                      \
+  }
+
+/* short rows: 256 threads, 1..8 VGPR slots (T <= 8192) */
+NSR_ADAIN_ROW(256, 1, 0)
+NSR_ADAIN_ROW(256, 2, 0)
+NSR_ADAIN_ROW(256, 3, 0)
+NSR_ADAIN_ROW(256, 4, 0)
+NSR_ADAIN_ROW(256, 5, 0)
+NSR_ADAIN_ROW(256, 6, 0)
+NSR_ADAIN_ROW(256, 7, 0)
+NSR_ADAIN_ROW(256, 8, 0)
+/* medium rows: 512 threads, VGPR slots only (T <= 90112) */
+NSR_ADAIN_ROW(512, 5, 0)
+NSR_ADAIN_ROW(512, 6, 0)
+NSR_ADAIN_ROW(512, 8, 0)
+NSR_ADAIN_ROW(512, 10, 0)
+NSR_ADAIN_ROW(512, 12, 0)
+NSR_ADAIN_ROW(512, 16, 0)
+NSR_ADAIN_ROW(512, 20, 0)
+NSR_ADAIN_ROW(512, 24, 0)
+NSR_ADAIN_ROW(512, 28, 0)
+NSR_ADAIN_ROW(512, 32, 0)
+NSR_ADAIN_ROW(512, 36, 0)
+NSR_ADAIN_ROW(512, 40, 0)
+NSR_ADAIN_ROW(512, 44, 0)
+/* long rows: 44 VGPR slots + 2..18 LDS slots (T <= 126976; 18 slots = 144 KiB of LDS) */
+NSR_ADAIN_ROW(512, 44, 2)
+NSR_ADAIN_ROW(512, 44, 4)
+NSR_ADAIN_ROW(512, 44, 6)
+NSR_ADAIN_ROW(512, 44, 8)
+NSR_ADAIN_ROW(512, 44, 10)
+NSR_ADAIN_ROW(512, 44, 12)
+NSR_ADAIN_ROW(512, 44, 14)
+NSR_ADAIN_ROW(512, 44, 16)
+NSR_ADAIN_ROW(512, 44, 18)
+
+/* ------------------------------------------------ unaligned resident rows -- */
+
+/* Element-wise access to a partial chunk (row edge): element idx of chunk
+ * space belongs to the row iff lo <= idx < hi. */
 NSR_DEV nsr_float4 load_chunk_masked(const float* xb, int j, int lo, int64_t hi) {
   nsr_float4 r = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -58,33 +209,16 @@ NSR_DEV void store_chunk_masked(float* ob, int j, int lo, int64_t hi, nsr_float4
   }
 }
 
-NSR_DEV nsr_float4 adain_snake4(nsr_float4 d, float A, float bet, const snake_consts& sc) {
-  nsr_float4 o;
-  o.x = snake_eval(__builtin_fmaf(d.x, A, bet), sc);
-  o.y = snake_eval(__builtin_fmaf(d.y, A, bet), sc);
-  o.z = snake_eval(__builtin_fmaf(d.z, A, bet), sc);
-  o.w = snake_eval(__builtin_fmaf(d.w, A, bet), sc);
-  return o;
-}
-
-NSR_DEV float sumsq4(nsr_float4 d, float sq) {
-  sq = __builtin_fmaf(d.x, d.x, sq);
-  sq = __builtin_fmaf(d.y, d.y, sq);
-  sq = __builtin_fmaf(d.z, d.z, sq);
-  return __builtin_fmaf(d.w, d.w, sq);
-}
-
-/* ALIGNED: x and out 16-byte aligned and T % 4 == 0, so every row is a whole
- * number of float4 chunks j = 0..nch-1, chunk j held by lane j % BLOCK.
- * Otherwise chunks lie on the float4 grid of the tensor: the row's first and
- * last chunk are partial and held by lane 0 (element access, e0/e1), the
- * interior chunks 1..nch-2 are full and spread as j = 1 + tid + BLOCK*k.
- * All loads of the chunk array are branch-free (index clamped in bounds,
- * out-of-row slots zeroed by a select), which keeps the array in VGPRs. */
-template <int BLOCK, int NV, bool ALIGNED>
-NSR_DEV void adain_resident(const nsr_adain_args& a, int pdt) {
+/* Rows whose start is not 16-byte aligned (misaligned views, T % 4 != 0).
+ * Chunks lie on the float4 grid of the tensor: the row's first and last chunk
+ * are partial and held by lane 0 (element access, e0/e1), the interior chunks
+ * 1..nch-2 are full and spread as j = 1 + tid + BLOCK*k. Loads of the chunk
+ * array are branch-free (index clamped in bounds, out-of-row slots zeroed by
+ * a select), which keeps the array in VGPRs. Two-pass statistics over the
+ * registers (mean, then centred sums with the corrected two-pass term). */
+template <int BLOCK, int NV>
+NSR_DEV void adain_resident_u(const nsr_adain_args& a, int pdt) {
   constexpr int NW = BLOCK / 64;
-  extern __shared__ nsr_float4 lds_x[];
   __shared__ float red[2 * NW];
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
@@ -97,7 +231,7 @@ NSR_DEV void adain_resident(const nsr_adain_args& a, int pdt) {
   const float alp = adain_param(a.alpha, pdt, ci);
 
   const int64_t s = row * T;
-  const int64_t a0 = ALIGNED ? s : (s & ~(int64_t)3);
+  const int64_t a0 = s & ~(int64_t)3;
   const int lo = (int)(s - a0);        /* first row element in chunk space */
   const int64_t hi = (int64_t)lo + T;  /* one past the last */
   const int nch = (int)((hi + 3) >> 2);
@@ -105,26 +239,11 @@ NSR_DEV void adain_resident(const nsr_adain_args& a, int pdt) {
   const float* xb = a.x + a0;
   float* ob = a.out + a0;
   const nsr_float4 zero4 = {0.f, 0.f, 0.f, 0.f};
-
-  /* chunk held in slot k of this lane, and the last valid chunk index */
-  const int jbase = ALIGNED ? tid : 1 + tid;
-  const int jmax = ALIGNED ? jlast : nch - 2;
-
-  int nl = 0;
-  if constexpr (ALIGNED) {
-    /* LDS part first: chunks tid + BLOCK*(NV+m), straight from HBM into LDS
-     * (lane i of a wave lands at wave base + 16*i). */
-    nl = a.lds_chunks;
-#pragma unroll 1
-    for (int m = 0; m < nl; ++m) {
-      const int j = min(tid + BLOCK * (NV + m), jlast);
-      __builtin_amdgcn_global_load_lds((const void*)(xb + 4 * (int64_t)j),
-                                       (lds_void*)(lds_x + m * BLOCK + (tid & ~63)), 16, 0, 0);
-    }
-  }
+  const int jbase = 1 + tid;
+  const int jmax = nch - 2;
 
   nsr_float4 v[NV];
-  if (jmax >= jbase - tid) { /* at least one full chunk in the array (uniform) */
+  if (jmax >= 1) { /* at least one interior chunk (uniform) */
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       const int j = jbase + BLOCK * k;
@@ -135,35 +254,17 @@ NSR_DEV void adain_resident(const nsr_adain_args& a, int pdt) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) v[k] = zero4;
   }
-  nsr_float4 e0 = zero4, e1 = zero4; /* partial edge chunks (unaligned, lane 0) */
-  if constexpr (!ALIGNED) {
-    if (tid == 0) {
-      e0 = load_chunk_masked(xb, 0, lo, hi);
-      if (jlast > 0) e1 = load_chunk_masked(xb, jlast, lo, hi);
-    }
+  nsr_float4 e0 = zero4, e1 = zero4;
+  if (tid == 0) {
+    e0 = load_chunk_masked(xb, 0, lo, hi);
+    if (jlast > 0) e1 = load_chunk_masked(xb, jlast, lo, hi);
   }
 
-  float sum = 0.f;
+  float sum = sum4(e0) + sum4(e1);
 #pragma unroll
-  for (int k = 0; k < NV; ++k) sum += (v[k].x + v[k].y) + (v[k].z + v[k].w);
-  if constexpr (!ALIGNED) sum += ((e0.x + e0.y) + (e0.z + e0.w)) + ((e1.x + e1.y) + (e1.z + e1.w));
-  if constexpr (ALIGNED) {
-    if (nl > 0) {
-      /* each lane reads back only the LDS slots its own wave filled */
-      __builtin_amdgcn_s_waitcnt(0);
-#pragma unroll 1
-      for (int m = 0; m < nl; ++m) {
-        const int j = tid + BLOCK * (NV + m);
-        const nsr_float4 t = lds_x[m * BLOCK + tid];
-        sum += j < nch ? (t.x + t.y) + (t.z + t.w) : 0.f;
-      }
-    }
-  }
+  for (int k = 0; k < NV; ++k) sum += sum4(v[k]);
   const float mean = block_sum<NW>(sum, red) * a.inv_t;
 
-  /* Centred pass: d = x - mean, with sum(d^2) and sum(d). The second sum
-   * corrects the f32 mean (corrected two-pass algorithm), which keeps rows
-   * whose |mean| >> std accurate; the correction c is folded into the bias. */
   float sq = 0.f, sd = 0.f;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
@@ -171,32 +272,20 @@ NSR_DEV void adain_resident(const nsr_adain_args& a, int pdt) {
     const nsr_float4 d = v[k] - mean;
     v[k] = j <= jmax ? d : zero4;
     sq = sumsq4(v[k], sq);
-    sd += (v[k].x + v[k].y) + (v[k].z + v[k].w);
+    sd += sum4(v[k]);
   }
-  if constexpr (!ALIGNED) {
-    if (tid == 0) {
-      e0 = mask_chunk(e0 - mean, 0, lo, hi);
-      e1 = jlast > 0 ? mask_chunk(e1 - mean, jlast, lo, hi) : zero4;
-    }
-    sq = sumsq4(e0, sumsq4(e1, sq));
-    sd += ((e0.x + e0.y) + (e0.z + e0.w)) + ((e1.x + e1.y) + (e1.z + e1.w));
+  if (tid == 0) {
+    e0 = mask_chunk(e0 - mean, 0, lo, hi);
+    e1 = jlast > 0 ? mask_chunk(e1 - mean, jlast, lo, hi) : zero4;
   }
-  if constexpr (ALIGNED) {
-#pragma unroll 1
-    for (int m = 0; m < nl; ++m) {
-      const int j = tid + BLOCK * (NV + m);
-      nsr_float4 d = lds_x[m * BLOCK + tid] - mean;
-      d = j < nch ? d : zero4;
-      sq = sumsq4(d, sq);
-      sd += (d.x + d.y) + (d.z + d.w);
-    }
-  }
+  sq = sumsq4(e0, sumsq4(e1, sq));
+  sd += sum4(e0) + sum4(e1);
   block_sum2<NW>(sq, sd, red);
   const float c = sd * a.inv_t;
   const float var = fmaxf(__builtin_fmaf(-c, sd, sq) * a.inv_t, 0.0f);
   const float rstd = 1.0f / sqrtf(var + a.eps);
   const float A = (gam + 1.0f) * rstd;
-  const float Bc = __builtin_fmaf(-c, A, bet); /* (d - c) * A + beta = d * A + Bc */
+  const float Bc = __builtin_fmaf(-c, A, bet);
   const snake_consts sc = make_snake_consts(alp);
 
 #pragma unroll
@@ -205,46 +294,29 @@ NSR_DEV void adain_resident(const nsr_adain_args& a, int pdt) {
     const nsr_float4 o = adain_snake4(v[k], A, Bc, sc);
     if (j <= jmax) stf4(ob + 4 * (int64_t)j, o);
   }
-  if constexpr (!ALIGNED) {
-    if (tid == 0) {
-      store_chunk_masked(ob, 0, lo, hi, adain_snake4(e0, A, Bc, sc));
-      if (jlast > 0) store_chunk_masked(ob, jlast, lo, hi, adain_snake4(e1, A, Bc, sc));
-    }
-  }
-  if constexpr (ALIGNED) {
-#pragma unroll 1
-    for (int m = 0; m < nl; ++m) {
-      const int j = tid + BLOCK * (NV + m);
-      const nsr_float4 o = adain_snake4(lds_x[m * BLOCK + tid] - mean, A, Bc, sc);
-      if (j < nch) stf4(ob + 4 * (int64_t)j, o);
-    }
+  if (tid == 0) {
+    store_chunk_masked(ob, 0, lo, hi, adain_snake4(e0, A, Bc, sc));
+    if (jlast > 0) store_chunk_masked(ob, jlast, lo, hi, adain_snake4(e1, A, Bc, sc));
   }
 }
 
-#define NSR_ADAIN_RES(BLOCK, NV)                                                  \
-  extern "C" __global__ void __launch_bounds__(BLOCK)                            \
-      nsrk_adain_res_b##BLOCK##_nv##NV##_a(const nsr_adain_args a, const int pdt) { \
-    adain_resident<BLOCK, NV, true>(a, pdt);                                     \
-  }                                                                              \
-  extern "C" __global__ void __launch_bounds__(BLOCK)                            \
-      nsrk_adain_res_b##BLOCK##_nv##NV##_u(const nsr_adain_args a, const int pdt) { \
-    adain_resident<BLOCK, NV, false>(a, pdt);                                    \
+#define NSR_ADAIN_RES_U(BLOCK, NV)                                                      \
+  extern "C" __global__ void __launch_bounds__(BLOCK)                                  \
+      nsrk_adain_res_b##BLOCK##_nv##NV##_u(const nsr_adain_args a, const int pdt) {    \
+    adain_resident_u<BLOCK, NV>(a, pdt);                                               \
   }
 
-NSR_ADAIN_RES(256, 1)
-NSR_ADAIN_RES(256, 2)
-NSR_ADAIN_RES(256, 3)
-NSR_ADAIN_RES(256, 4)
-NSR_ADAIN_RES(256, 5)
-NSR_ADAIN_RES(256, 6)
-NSR_ADAIN_RES(256, 8)
-NSR_ADAIN_RES(1024, 3)
-NSR_ADAIN_RES(1024, 4)
-NSR_ADAIN_RES(1024, 6)
-NSR_ADAIN_RES(1024, 8)
-NSR_ADAIN_RES(1024, 12)
-NSR_ADAIN_RES(1024, 16)
-NSR_ADAIN_RES(1024, 20)
+NSR_ADAIN_RES_U(256, 1)
+NSR_ADAIN_RES_U(256, 2)
+NSR_ADAIN_RES_U(256, 3)
+NSR_ADAIN_RES_U(256, 4)
+NSR_ADAIN_RES_U(256, 5)
+NSR_ADAIN_RES_U(256, 6)
+NSR_ADAIN_RES_U(256, 8)
+NSR_ADAIN_RES_U(512, 12)
+NSR_ADAIN_RES_U(512, 16)
+NSR_ADAIN_RES_U(512, 24)
+NSR_ADAIN_RES_U(512, 32)
 
 /* ------------------------------------------------------------ split path -- */
 

@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../nsr_kargs.h"
 
 #define NSR_DEV __device__ __forceinline__
@@ -246,63 +248,96 @@ template <int ACT> NSR_DEV float apply_act(float v) {
   }
 }
 
-/* ------------------------------------------------------------- snake sin^2 -- */
+/* ------------------------------------------------------------------ snake -- */
 
-/* sin^2(t) = u * P(u), u = t^2, |t| <= pi/2. P fitted (weighted least squares
- * on Chebyshev nodes) to sin^2(sqrt(u))/u on [0, (pi/2)^2]; f32 Horner error
- * below 3e-7 relative. */
-#define NSR_S2_C0 1.0f
-#define NSR_S2_C1 -0.3333333432674408f
-#define NSR_S2_C2 0.04444441944360733f
-#define NSR_S2_C3 -0.0031745436135679483f
-#define NSR_S2_C4 0.0001410240220138803f
-#define NSR_S2_C5 -4.233750587445684e-06f
-#define NSR_S2_C6 8.134502849088676e-08f
+/* snake(t) = t + sin^2(alpha t) * (1 / (alpha + 1e-9)), the reference's form
+ * (src/kokoro/decoder.rs:1471-1476), evaluated as:
+ *   q = t * alpha/pi,  f = q - rint(q)  (exact: |f| <= 1/2, Sterbenz),
+ *   sin^2(alpha t) = sin^2(pi f) = w Q(w),  w = f^2 in [0, 1/4],
+ * sin^2 having period pi. Q is a degree-6 polynomial fitted to
+ * sin^2(pi sqrt(w)) / w on [0, 1/4] by Lawson's iteratively reweighted least
+ * squares (minimax) on Chebyshev nodes: relative error 5.4e-8 with the f32
+ * coefficients below. The per-row factor 1/(alpha + 1e-9) is folded into the
+ * coefficients, so one element costs 11 VALU operations:
+ *   mul, rndne, sub, mul, 6 fma (Horner), fma (t + p*w).
+ * Worst error over t in [-200, 200], alpha in {0, 1e-9, 1e-4, 0.5 .. 10, -0.7}:
+ * 3.9e-7 of max(|out|, 1) in f32. */
+#define NSR_SNAKE_Q0 9.869604110717773f
+#define NSR_SNAKE_Q1 -32.469696044921875f
+#define NSR_SNAKE_Q2 42.72837829589844f
+#define NSR_SNAKE_Q3 -30.121654510498047f
+#define NSR_SNAKE_Q4 13.205862045288086f
+#define NSR_SNAKE_Q5 -3.910468578338623f
+#define NSR_SNAKE_Q6 0.7385572195053101f
 
-NSR_DEV float sin2_poly(float u) {
-  float p = NSR_S2_C6;
-  p = __builtin_fmaf(p, u, NSR_S2_C5);
-  p = __builtin_fmaf(p, u, NSR_S2_C4);
-  p = __builtin_fmaf(p, u, NSR_S2_C3);
-  p = __builtin_fmaf(p, u, NSR_S2_C2);
-  p = __builtin_fmaf(p, u, NSR_S2_C1);
-  p = __builtin_fmaf(p, u, NSR_S2_C0);
-  return p;
-}
-
-/* Per-row constants for snake(y) = y + sin^2(alpha*y) * inv_alpha evaluated
- * in y units: alpha*y = k*pi + alpha*r, k = rint(y*alpha/pi),
- * r = y - k*(pi/alpha) (two-term split), sin^2(alpha*y) = sin^2(alpha*r)
- * because sin^2 has period pi. */
 struct snake_consts {
-  float a_over_pi;   /* alpha / pi */
-  float p_hi, p_lo;  /* pi / alpha = p_hi + p_lo (0, 0 when alpha == 0) */
-  float a2;          /* alpha^2 */
-  float k2;          /* alpha^2 * inv_alpha */
+  float a_pi; /* alpha / pi */
+  float c[7]; /* Q coefficients times 1 / (alpha + 1e-9) */
 };
 
 NSR_DEV snake_consts make_snake_consts(float alpha) {
   snake_consts s;
-  const float inv_alpha = 1.0f / (alpha + 1e-9f); /* as decoder.rs:1474 */
-  s.a_over_pi = (float)((double)alpha * 0.31830988618379067154);
-  if (alpha != 0.0f) {
-    const double pa = 3.14159265358979323846 / (double)alpha;
-    s.p_hi = (float)pa;
-    s.p_lo = (float)(pa - (double)s.p_hi);
-  } else {
-    s.p_hi = 0.f;
-    s.p_lo = 0.f;
-  }
-  s.a2 = alpha * alpha;
-  s.k2 = s.a2 * inv_alpha;
+  const float inv_a = 1.0f / (alpha + 1e-9f); /* recip(alpha + 1e-9), decoder.rs:1474 */
+  s.a_pi = (float)((double)alpha * 0.31830988618379067154);
+  s.c[0] = NSR_SNAKE_Q0 * inv_a;
+  s.c[1] = NSR_SNAKE_Q1 * inv_a;
+  s.c[2] = NSR_SNAKE_Q2 * inv_a;
+  s.c[3] = NSR_SNAKE_Q3 * inv_a;
+  s.c[4] = NSR_SNAKE_Q4 * inv_a;
+  s.c[5] = NSR_SNAKE_Q5 * inv_a;
+  s.c[6] = NSR_SNAKE_Q6 * inv_a;
   return s;
 }
 
-NSR_DEV float snake_eval(float y, const snake_consts& s) {
-  const float k = __builtin_rintf(y * s.a_over_pi);
-  float r = __builtin_fmaf(-k, s.p_hi, y);
-  r = __builtin_fmaf(-k, s.p_lo, r);
-  const float v = r * r;
-  const float p = sin2_poly(v * s.a2);
-  return __builtin_fmaf(p, v * s.k2, y);
+NSR_DEV float snake_eval(float t, const snake_consts& s) {
+  const float q = t * s.a_pi;
+  const float f = q - __builtin_rintf(q);
+  const float w = f * f;
+  float p = __builtin_fmaf(s.c[6], w, s.c[5]);
+  p = __builtin_fmaf(p, w, s.c[4]);
+  p = __builtin_fmaf(p, w, s.c[3]);
+  p = __builtin_fmaf(p, w, s.c[2]);
+  p = __builtin_fmaf(p, w, s.c[1]);
+  p = __builtin_fmaf(p, w, s.c[0]);
+  return __builtin_fmaf(p, w, t);
+}
+
+/* ------------------------------------------------------- buffer access -- */
+
+/* Raw buffer resource over [base, base + bytes): loads past the end return
+ * 0 and stores past the end are dropped by the hardware range check. */
+typedef __amdgpu_buffer_rsrc_t nsr_rsrc;
+#define NSR_RSRC_WORD3 0x00020000 /* gfx9 data format 32, raw (stride 0) */
+#define NSR_AUX_NT 2              /* non-temporal (streamed) access */
+
+NSR_DEV nsr_rsrc make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)bytes, NSR_RSRC_WORD3);
+}
+
+/* 16-byte load at voff + soff (soff wave-uniform, kept in an SGPR). */
+NSR_DEV nsr_float4 buf_load4(nsr_rsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(nsr_float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, NSR_AUX_NT));
+}
+
+/* 16-byte store at voff + off with soffset 0. Stores carry their offset in
+ * the VGPR address, never in soffset: the compiler exempts MUBUF stores with
+ * an SGPR soffset from the wait state that a VALU write of the store's data
+ * registers needs right after a >64-bit store, and on gfx950 such stores were
+ * observed to write the overwritten values. */
+NSR_DEV void buf_store4(nsr_rsrc r, uint32_t voff, uint32_t off, nsr_float4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(nsr_uint4, v), r, voff + off, 0, NSR_AUX_NT);
+}
+
+/* s_waitcnt vmcnt(n) alone (gfx9 encoding: vmcnt[3:0], vmcnt[5:4] at bit 14,
+ * expcnt and lgkmcnt left at their maxima). */
+#define NSR_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt((((n)&15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8)))
+
+/* Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E). */
+template <int B, int E, typename F>
+NSR_DEV void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
 }

@@ -209,8 +209,8 @@ int nsr_kernel_count(void) {
   // Count kernels by probing the names this runtime launches.
   static const char* probe[] = {"nsrk_q8_0_gather_none_u32", "nsrk_ln_f32_f32_nc4",
                                 "nsrk_resln_bf16_nc2",       "nsrk_rope_table_f32",
-                                "nsrk_rope_compute_f32",     "nsrk_adain_res_b256_nv5_a",
-                                "nsrk_adain_res_b1024_nv20_a", "nsrk_adain_stats",
+                                "nsrk_rope_compute_f32",     "nsrk_adain_row_b256_v5_l0",
+                                "nsrk_adain_row_b512_v44_l14", "nsrk_adain_stats",
                                 "nsrk_adain_apply",          "nsrk_gelu_f32_v"};
   int n = 0;
   for (const char* p : probe) {
@@ -425,11 +425,38 @@ nsr_status nsr_adain_snake_f32(const float* x, const void* gamma, const void* be
   int pdt = param_dtype == NSR_F32 ? 0 : 1;
 
   const bool is_aligned = aligned(x, 16) && aligned(out, 16) && (T % 4 == 0);
-  // chunks each lane array must cover: all chunks (aligned) or interior ones
-  const int64_t need = is_aligned ? T / 4 : ((T + 6) / 4 - 2 > 0 ? (T + 6) / 4 - 2 : 0);
-  int block = 0, nv = 0, nl = 0;
-  {
-    const int small[] = {1, 2, 3, 4, 5, 6, 8};
+  std::string name;
+  unsigned block = 0, lds = 0;
+  if (is_aligned) {
+    // Row kernel: BLOCK-wide slots of 16-byte chunks, NV in VGPRs + NL in LDS.
+    const int64_t nch = T / 4;
+    int nv = 0, nl = 0;
+    if (nch <= 256 * 8) {
+      block = 256;
+      nv = (int)((nch + 255) / 256);
+    } else if (nch <= 512 * 44) {
+      block = 512;
+      static const int opts[] = {5, 6, 8, 10, 12, 16, 20, 24, 28, 32, 36, 40, 44};
+      for (int o : opts)
+        if (512LL * o >= nch) {
+          nv = o;
+          break;
+        }
+    } else if (nch <= 512 * (44 + 18)) {
+      block = 512;
+      nv = 44;
+      const int64_t m = (nch - 512 * 44 + 511) / 512;
+      nl = (int)((m + 1) / 2 * 2);  // built for even NL 2..18
+      lds = (unsigned)(nl * 512 * 16);
+      if (lds + 1024 > (unsigned)dm->max_lds) block = 0;
+    }
+    if (block)
+      name = "nsrk_adain_row_b" + std::to_string(block) + "_v" + std::to_string(nv) + "_l" + std::to_string(nl);
+  } else {
+    // Unaligned rows: interior chunks 1..nch-2 resident in VGPRs, edges by element.
+    const int64_t need = (T + 6) / 4 - 2 > 0 ? (T + 6) / 4 - 2 : 0;
+    int nv = 0;
+    static const int small[] = {1, 2, 3, 4, 5, 6, 8};
     for (int o : small)
       if (256LL * o >= need) {
         block = 256;
@@ -437,31 +464,20 @@ nsr_status nsr_adain_snake_f32(const float* x, const void* gamma, const void* be
         break;
       }
     if (!block) {
-      const int large[] = {3, 4, 6, 8, 12, 16, 20};
+      static const int large[] = {12, 16, 24, 32};
       for (int o : large)
-        if (1024LL * o >= need) {
-          block = 1024;
+        if (512LL * o >= need) {
+          block = 512;
           nv = o;
           break;
         }
     }
-    if (!block && is_aligned) {
-      const int64_t rest = need - 1024LL * 20;
-      const int64_t lds_slots = (dm->max_lds - 1024) / (1024 * 16);
-      const int64_t m = (rest + 1023) / 1024;
-      if (m <= lds_slots) {
-        block = 1024;
-        nv = 20;
-        nl = (int)m;
-      }
-    }
+    if (block) name = "nsrk_adain_res_b" + std::to_string(block) + "_nv" + std::to_string(nv) + "_u";
   }
   if (block) {
-    a.lds_chunks = nl;
+    a.lds_chunks = (int32_t)(lds / (16u * block));
     void* params[] = {&a, &pdt};
-    const std::string name = "nsrk_adain_res_b" + std::to_string(block) + "_nv" + std::to_string(nv) +
-                             (is_aligned ? "_a" : "_u");
-    return launch(name, (unsigned)n_rows, 1, block, (unsigned)(nl * block * 16), stream, params);
+    return launch(name, (unsigned)n_rows, 1, block, lds, stream, params);
   }
 
   // Split path: stats (one read) + apply (second read), stream-ordered scratch.

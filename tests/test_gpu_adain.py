@@ -58,13 +58,35 @@ def test_config4b_full_size(dev):
     assert np.all(np.isfinite(got))
 
 
+def _bucket_lengths():
+    """Row lengths at both edges of every kernel variant the runtime selects:
+    aligned rows (T % 4 == 0) in 16-byte chunks: 256 threads x 1..8 slots,
+    512 threads x {5..44} VGPR slots, 512 x (44 + 2..18 LDS slots), then the
+    split path; unaligned rows (T % 4 != 0) by interior-chunk count."""
+    Ts = set()
+    for nv in range(1, 9):                                       # b256 row kernels
+        Ts |= {4 * 256 * nv, 4 * (256 * (nv - 1) + 1)}
+    prev = 2048
+    for nv in (5, 6, 8, 10, 12, 16, 20, 24, 28, 32, 36, 40, 44):  # b512 VGPR-only
+        Ts |= {4 * 512 * nv, 4 * (prev + 1)}
+        prev = 512 * nv
+    for nl in range(2, 19, 2):                                    # b512 + LDS slots
+        Ts |= {4 * 512 * (44 + nl), 4 * (512 * (44 + nl - 2) + 1)}
+    Ts |= {4 * (512 * 62 + 1), 150000}                            # split path
+    for need in (1, 256, 257, 1536, 1537, 2048, 2049, 6144, 8192, 8193, 12288, 16384, 16385):  # unaligned
+        Ts.add(4 * need + 5)
+    return sorted(Ts)
+
+
 @pytest.mark.parametrize("B,C,T", [(1, 3, 1), (1, 2, 2), (1, 2, 3), (1, 5, 5), (2, 3, 7), (1, 4, 100), (1, 3, 1023),
                                    (1, 3, 1025), (2, 2, 4097), (1, 2, 8191), (1, 2, 8200), (1, 2, 20481),
                                    (1, 2, 81920), (1, 2, 81921), (1, 2, 100000), (1, 2, 118784), (1, 2, 118785),
-                                   (1, 2, 150000), (1, 2, 150002)])
+                                   (1, 2, 150000), (1, 2, 150002)]
+                         + [(1, 2, t) for t in _bucket_lengths()])
 def test_shapes(dev, B, C, T):
-    """Every kernel variant: resident (aligned and unaligned), VGPR+LDS,
-    and the split path (T beyond the on-chip budget, or unaligned and long)."""
+    """Every kernel variant: row kernels (VGPR slots, VGPR + LDS slots), the
+    unaligned resident kernel and the split path (T beyond the on-chip
+    budget, or unaligned and long)."""
     g = configs.rng(B * 13 + C * 7 + T)
     x = (g.standard_normal((B, C, T)) * 1.3 + 0.2).astype(np.float32)
     gamma = (0.1 * g.standard_normal((B, C))).astype(np.float32)
