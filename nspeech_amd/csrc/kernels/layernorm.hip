@@ -14,7 +14,9 @@
  * 16 bytes per lane (128-bit coalesced loads), statistics in two passes over
  * the registers (mean, then centred sum of squares) with DPP wave reductions,
  * so x (and res) are read from HBM exactly once and y (and h) written once.
- * Four rows per 256-thread workgroup; no LDS and no block barriers.
+ * Four waves per 256-thread workgroup, no LDS and no block barriers; the grid
+ * is capped and each wave walks rows with the grid's wave count as stride,
+ * loading its next row while it reduces the current one.
  * Rows that are not 16-byte aligned or longer than 4096 columns take the
  * generic kernel at the bottom (one workgroup per row, scalar access).
  */
@@ -81,23 +83,44 @@ NSR_DEV void load_param_vec(const void* p, int pdt, int col0, float* v, float fi
   }
 }
 
+/* Raw 16-byte words of one VEC-element chunk of dtype DT (1 or 2 words). */
+template <int DT, int VEC> struct chunk_words { static constexpr int value = VEC * dt_size<DT>::value / 16; };
+
+template <int DT, int VEC>
+NSR_DEV void load_raw(const void* base, int64_t elem, nsr_uint4* w) {
+  const char* p = (const char*)base + elem * dt_size<DT>::value;
+#pragma unroll
+  for (int i = 0; i < chunk_words<DT, VEC>::value; ++i) w[i] = ld16(p + 16 * i);
+}
+
+template <int DT, int VEC>
+NSR_DEV void unpack_raw(const nsr_uint4* w, float* v) {
+#pragma unroll
+  for (int i = 0; i < chunk_words<DT, VEC>::value; ++i) unpack16<DT>(w[i], v + i * (16 / dt_size<DT>::value));
+}
+
 /*
- * FUSED = false: h = x.  FUSED = true: h = round_H(x + res), stored if a.h.
- * PDT runtime (gamma/beta are read once per chunk), ACT compile time.
+ * One wave64 per row, rows visited persistently: wave w of the grid takes
+ * rows w, w + W, w + 2W, ... (W = waves in the grid), so gamma/beta are
+ * loaded once per wave, and the next row's x (and res) chunks are loaded
+ * while the current row is reduced and written. FUSED = false: h = x.
+ * FUSED = true: h = round_H(x + res), stored (if a.h) as soon as it is
+ * formed. PDT runtime, ACT compile time.
  */
-template <int X, int R, int H, int Y, int NC, bool FUSED, int ACT>
+template <int X, int R, int H, int Y, int NC, bool FUSED, int ACT, bool FULL = false>
 NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
   constexpr int VEC = ln_vec<X, R, H, Y>::value;
+  constexpr int XW = chunk_words<X, VEC>::value;
+  constexpr int RW = FUSED ? chunk_words<R, VEC>::value : 1;
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= a.n_rows) return; /* whole wave leaves; no barriers below */
-  const int nchunk = a.n_cols / VEC;
-  const int64_t xrow = row * a.ld_x;
-  const int64_t yrow = row * a.ld_y;
+  /* FULL: n_cols == 64 * NC * VEC, every chunk guard below is true */
+  const int nchunk = FULL ? 64 * NC : a.n_cols / VEC;
 
   /* gamma/beta do not depend on the row: when they fit in 64 more VGPRs
-   * they are loaded up front, so their latency hides under the row's loads
-   * instead of adding a round trip after the reductions. */
+   * they are loaded once per wave, before the first row's loads */
   constexpr bool PREFETCH = NC * VEC <= 32;
   float gpre[PREFETCH ? NC : 1][VEC], bpre[PREFETCH ? NC : 1][VEC];
   if constexpr (PREFETCH) {
@@ -110,84 +133,123 @@ NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
       }
     }
   }
+  const float goff = a.unit_offset ? 1.0f : 0.0f;
 
-  float v[NC][VEC];
-  float sum = 0.f;
+  /* raw chunks of the row being worked on; refilled with the next row's
+   * chunks while this one is reduced, when they fit in 32 VGPRs */
+  constexpr bool PIPE = NC * (XW + (FUSED ? RW : 0)) * 4 <= 32;
+  nsr_uint4 rx[NC][XW], rr[NC][RW];
+  auto load_row = [&](int64_t r) {
 #pragma unroll
-  for (int k = 0; k < NC; ++k) {
-    const int j = lane + 64 * k;
-    if (j < nchunk) {
-      load_vec<X, VEC>(a.x, xrow + (int64_t)j * VEC, v[k]);
-      if constexpr (FUSED) {
-        float r[VEC];
-        load_vec<R, VEC>(a.res, xrow + (int64_t)j * VEC, r);
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) v[k][e] = round_to<H>(v[k][e] + r[e]);
-        if (a.h) store_vec<H, VEC>(a.h, xrow + (int64_t)j * VEC, v[k]);
-      }
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) sum += v[k][e];
-    }
-  }
-  const float mean = wave_sum(sum) * a.inv_n;
-
-  /* centred pass; sum(d) corrects the f32 mean (corrected two-pass), which
-   * keeps rows with |mean| >> std accurate */
-  float sq = 0.f, sd = 0.f;
-#pragma unroll
-  for (int k = 0; k < NC; ++k) {
-    const int j = lane + 64 * k;
-    if (j < nchunk) {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        v[k][e] -= mean;
-        sq = __builtin_fmaf(v[k][e], v[k][e], sq);
-        sd += v[k][e];
+    for (int k = 0; k < NC; ++k) {
+      const int j = lane + 64 * k;
+      if (j < nchunk) {
+        load_raw<X, VEC>(a.x, r * a.ld_x + (int64_t)j * VEC, rx[k]);
+        if constexpr (FUSED) load_raw<R, VEC>(a.res, r * a.ld_x + (int64_t)j * VEC, rr[k]);
       }
     }
-  }
-  sq = wave_sum(sq);
-  sd = wave_sum(sd);
-  const float c = sd * a.inv_n;
-  const float var = fmaxf(__builtin_fmaf(-c, sd, sq) * a.inv_n, 0.0f);
-  const float rstd = 1.0f / sqrtf(var + a.eps);
-  const float crs = -c * rstd; /* (d - c) * rstd = d * rstd + crs */
+  };
+  load_row(row);
 
+  while (true) {
+    const int64_t xrow = row * a.ld_x;
+    const int64_t yrow = row * a.ld_y;
+    const int64_t next = row + stride;
+    const bool more = next < a.n_rows;
+
+    float v[NC][VEC];
+    float sum = 0.f;
 #pragma unroll
-  for (int k = 0; k < NC; ++k) {
-    const int j = lane + 64 * k;
-    if (j < nchunk) {
-      const int col0 = j * VEC;
-      float g[VEC], b[VEC], o[VEC];
-      if constexpr (PREFETCH) {
+    for (int k = 0; k < NC; ++k) {
+      const int j = lane + 64 * k;
+      if (j < nchunk) {
+        unpack_raw<X, VEC>(rx[k], v[k]);
+        if constexpr (FUSED) {
+          float r[VEC];
+          unpack_raw<R, VEC>(rr[k], r);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) v[k][e] = round_to<H>(v[k][e] + r[e]);
+          if (a.h) store_vec<H, VEC>(a.h, xrow + (int64_t)j * VEC, v[k]);
+        }
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) sum += v[k][e];
+      }
+    }
+    if constexpr (PIPE) {
+      if (more) load_row(next);
+    }
+    const float mean = wave_sum(sum) * a.inv_n;
+
+    /* centred pass; sum(d) corrects the f32 mean (corrected two-pass), which
+     * keeps rows with |mean| >> std accurate */
+    float sq = 0.f, sd = 0.f;
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      const int j = lane + 64 * k;
+      if (j < nchunk) {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
-          g[e] = gpre[k][e];
-          b[e] = bpre[k][e];
+          v[k][e] -= mean;
+          sq = __builtin_fmaf(v[k][e], v[k][e], sq);
+          sd += v[k][e];
         }
-      } else {
-        load_param_vec<VEC>(a.gamma, pdt, col0, g, 1.0f);
-        load_param_vec<VEC>(a.beta, pdt, col0, b, 0.0f);
       }
-      const float goff = a.unit_offset ? 1.0f : 0.0f;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        o[e] = apply_act<ACT>(__builtin_fmaf(__builtin_fmaf(v[k][e], rstd, crs), g[e] + goff, b[e]));
-      }
-      store_vec<Y, VEC>(a.y, yrow + col0, o);
     }
+    sq = wave_sum(sq);
+    sd = wave_sum(sd);
+    const float c = sd * a.inv_n;
+    const float var = fmaxf(__builtin_fmaf(-c, sd, sq) * a.inv_n, 0.0f);
+    const float rstd = 1.0f / sqrtf(var + a.eps);
+    const float crs = -c * rstd; /* (d - c) * rstd = d * rstd + crs */
+
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      const int j = lane + 64 * k;
+      if (j < nchunk) {
+        const int col0 = j * VEC;
+        float g[VEC], b[VEC], o[VEC];
+        if constexpr (PREFETCH) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            g[e] = gpre[k][e];
+            b[e] = bpre[k][e];
+          }
+        } else {
+          load_param_vec<VEC>(a.gamma, pdt, col0, g, 1.0f);
+          load_param_vec<VEC>(a.beta, pdt, col0, b, 0.0f);
+        }
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          o[e] = apply_act<ACT>(__builtin_fmaf(__builtin_fmaf(v[k][e], rstd, crs), g[e] + goff, b[e]));
+        }
+        store_vec<Y, VEC>(a.y, yrow + col0, o);
+      }
+    }
+    if (!more) break;
+    row = next;
+    if constexpr (!PIPE) load_row(row);
   }
 }
 
-/* Kernel: PDT and ACT switch uniformly outside the row body. */
-template <int X, int R, int H, int Y, int NC, bool FUSED>
-NSR_DEV void ln_wave_entry(const nsr_ln_args& a, int pdt, int act) {
+/* Kernel: PDT, ACT and FULL switch uniformly outside the row body. FULL
+ * (n_cols == 64 * NC * VEC) drops the per-chunk column guards. */
+template <int X, int R, int H, int Y, int NC, bool FUSED, bool FULL>
+NSR_DEV void ln_wave_act(const nsr_ln_args& a, int pdt, int act) {
   if (act == ACT_GELU) {
-    ln_row_wave<X, R, H, Y, NC, FUSED, ACT_GELU>(a, pdt);
+    ln_row_wave<X, R, H, Y, NC, FUSED, ACT_GELU, FULL>(a, pdt);
   } else if (act == ACT_SILU) {
-    ln_row_wave<X, R, H, Y, NC, FUSED, ACT_SILU>(a, pdt);
+    ln_row_wave<X, R, H, Y, NC, FUSED, ACT_SILU, FULL>(a, pdt);
   } else {
-    ln_row_wave<X, R, H, Y, NC, FUSED, ACT_NONE>(a, pdt);
+    ln_row_wave<X, R, H, Y, NC, FUSED, ACT_NONE, FULL>(a, pdt);
+  }
+}
+
+template <int X, int R, int H, int Y, int NC, bool FUSED>
+NSR_DEV void ln_wave_entry(const nsr_ln_args& a, int pdt, int act, int full) {
+  if (full) {
+    ln_wave_act<X, R, H, Y, NC, FUSED, true>(a, pdt, act);
+  } else {
+    ln_wave_act<X, R, H, Y, NC, FUSED, false>(a, pdt, act);
   }
 }
 
@@ -244,18 +306,20 @@ NSR_DEV void ln_row_generic(const nsr_ln_args& a, int pdt, int act) {
 }
 
 /* ------------------------------------------------------------ instances -- */
-/* Kernel argument tail: pdt and act are packed into one int (pdt | act<<8). */
+/* Kernel argument tail: pdt, act and full packed into one int
+ * (pdt | act << 8 | full << 16). */
 
 #define NSR_LN_WAVE(NAME, X, R, H, Y, NC, FUSED)                                \
   extern "C" __global__ void __launch_bounds__(256)                            \
       NAME(const nsr_ln_args a, const int mode) {                              \
-    ln_wave_entry<X, R, H, Y, NC, FUSED>(a, mode & 0xff, mode >> 8);            \
+    ln_wave_entry<X, R, H, Y, NC, FUSED>(a, mode & 0xff, (mode >> 8) & 0xff,    \
+                                         mode >> 16);                          \
   }
 
 #define NSR_LN_GENERIC(NAME, X, R, H, Y, FUSED)                                 \
   extern "C" __global__ void __launch_bounds__(256)                            \
       NAME(const nsr_ln_args a, const int mode) {                              \
-    ln_row_generic<X, R, H, Y, FUSED>(a, mode & 0xff, mode >> 8);               \
+    ln_row_generic<X, R, H, Y, FUSED>(a, mode & 0xff, (mode >> 8) & 0xff);      \
   }
 
 /* Plain LayerNorm: x dtype -> y dtype, NC chunks per lane. */

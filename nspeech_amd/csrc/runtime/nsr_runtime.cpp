@@ -288,11 +288,16 @@ static nsr_status ln_common(const void* x, nsr_dtype xd, const void* res, nsr_dt
   a.eps = eps;
   a.inv_n = 1.0f / (float)n_cols;
   int mode = (pd == NSR_F32 ? 0 : 1) | ((int)act << 8);
+  if (nc > 0 && n_cols == 64LL * nc * vec) mode |= 1 << 16;  // every chunk of every lane in the row
   void* params[] = {&a, &mode};
   if (nc > 0) {
-    if (cdiv_u(n_rows, 4) == 0 || (n_rows + 3) / 4 > 0x7fffffffLL)
-      return fail(NSR_ERR_UNSUPPORTED, "layernorm: too many rows");
-    return launch(prefix + "_nc" + std::to_string(nc), cdiv_u(n_rows, 4), 1, 256, 0, stream, params);
+    // Four rows (waves) per workgroup; past kLnMaxGrid workgroups each wave
+    // walks rows with the grid's wave count as stride (measured best on
+    // gfx950 for [24000, 1024] bf16: 4096 workgroups).
+    constexpr int64_t kLnMaxGrid = 4096;
+    const int64_t groups = (n_rows + 3) / 4;
+    return launch(prefix + "_nc" + std::to_string(nc), (unsigned)(groups < kLnMaxGrid ? groups : kLnMaxGrid), 1,
+                  256, 0, stream, params);
   }
   if (n_rows > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "layernorm: too many rows");
   return launch(prefix + "_generic", (unsigned)n_rows, 1, 256, 0, stream, params);
