@@ -7,6 +7,9 @@ tree):
   nspeech_amd/lib/nsr_<unit>_gfx950.hsaco   one code object per kernel unit
   nspeech_amd/lib/libnspeech_rocm.so        C ABI (include/nspeech_rocm.h),
                                             code objects embedded
+  nspeech_amd/lib/libnspeech_rocm_host.so   C++ host side (nspeech_amd/host/
+                                            rocm_kernels.h) over the C ABI
+  tests/host/_build/test_host_mirror        C++ tests of the host side
   oracle/_build/libnsr_oracle.so            CPU oracle (test infrastructure)
 """
 from __future__ import annotations
@@ -86,6 +89,35 @@ def build_library() -> Path:
     return out
 
 
+HOST_CXX = ["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__"]
+
+
+def build_host_library() -> Path:
+    """C++ host side (namespace nspeech::rocm) linked against the C ABI."""
+    out = LIB / "libnspeech_rocm_host.so"
+    tmp = LIB / "libnspeech_rocm_host.so.tmp"
+    _run([*HOST_CXX, "-shared", f"-I{ROOT / 'include'}", f"-I{ROCM / 'include'}",
+          str(PKG / "host" / "rocm_kernels.cpp"),
+          f"-L{LIB}", "-lnspeech_rocm", f"-L{ROCM / 'lib'}", "-lamdhip64",
+          "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM / 'lib'}", "-Wl,--no-undefined", "-o", str(tmp)])
+    os.replace(tmp, out)
+    return out
+
+
+def build_host_tests() -> Path:
+    """tests/host/test_host_mirror.cpp -> tests/host/_build/test_host_mirror."""
+    src = ROOT / "tests" / "host" / "test_host_mirror.cpp"
+    out_dir = ROOT / "tests" / "host" / "_build"
+    out_dir.mkdir(parents=True, exist_ok=True)
+    out = out_dir / "test_host_mirror"
+    tmp = out_dir / "test_host_mirror.tmp"
+    _run([*HOST_CXX, f"-I{PKG / 'host'}", f"-I{ROOT / 'include'}", f"-I{ROCM / 'include'}", str(src),
+          f"-L{LIB}", "-lnspeech_rocm_host", "-lnspeech_rocm", f"-L{ROCM / 'lib'}", "-lamdhip64",
+          "-Wl,-rpath,$ORIGIN/../../../nspeech_amd/lib", f"-Wl,-rpath,{ROCM / 'lib'}", "-o", str(tmp)])
+    os.replace(tmp, out)
+    return out
+
+
 def build_oracle() -> Path:
     sys.path.insert(0, str(ROOT))
     from oracle import build as oracle_build  # noqa: E402
@@ -96,6 +128,8 @@ def build_oracle() -> Path:
 def build_all() -> None:
     build_code_objects()
     build_library()
+    build_host_library()
+    build_host_tests()
     build_oracle()
 
 

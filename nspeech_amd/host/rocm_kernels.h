@@ -1,0 +1,219 @@
+// nspeech::rocm — C++ host side of the MI355X fused layer kernels.
+//
+// Mirrors the host interface nspeech uses for these ops, over the C ABI of
+// libnspeech_rocm.so (include/nspeech_rocm.h):
+//   * the Tensor-level triton_* functions and buffer-level enc_* functions of
+//     src/triton_kernels.rs (same names, argument order and meaning; the
+//     Metal device/pipeline pair becomes RocmDevice/RocmKernels and a
+//     ComputeCommandEncoder becomes an Encoder = the device's HIP stream);
+//   * KokoroGpuBackend::adain_snake_f32 (src/kokoro/gpu_backend.rs:181-185);
+//   * QEmbedding::forward (src/parakeet/quantized_layers.rs:65-71);
+//   * RotaryEmbedding + apply_rotary_pos_emb (src/moonshine/decoder.rs:85-183).
+//
+// Error behaviour follows the reference's anyhow::Result: every fallible
+// call throws nspeech::rocm::Error with a message (the reference bails with
+// "All tensors must be on Metal device" on a storage mismatch,
+// src/triton_kernels.rs:138; here "... on the ROCm device"). Launches are
+// asynchronous on the device's stream, as Candle's pooled command buffer is;
+// RocmDevice::synchronize() is the wait_until_completed() equivalent.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace nspeech {
+namespace rocm {
+
+class Error : public std::runtime_error {
+ public:
+  explicit Error(const std::string& msg) : std::runtime_error(msg) {}
+};
+
+enum class DType { F32, F16, BF16, U8, U32, I64 };
+size_t dtype_size(DType d);
+const char* dtype_name(DType d);
+
+// One GPU and its stream (candle's MetalDevice + pooled command buffer).
+class RocmDevice {
+ public:
+  // Device `ordinal`, with a default-priority stream of its own.
+  static RocmDevice create(int ordinal = 0);
+  int ordinal() const { return ordinal_; }
+  hipStream_t stream() const { return stream_->s; }
+  void synchronize() const;  // wait_until_completed()
+
+ private:
+  struct Stream {
+    hipStream_t s = nullptr;
+    ~Stream();
+  };
+  int ordinal_ = 0;
+  std::shared_ptr<Stream> stream_;
+};
+
+// Device buffer + byte offset (candle_core::GpuBuffer, src/triton_kernels.rs:9).
+struct GpuBuffer {
+  void* ptr = nullptr;
+  size_t offset = 0;
+  void* at() const { return static_cast<char*>(ptr) + offset; }
+};
+
+// Contiguous tensor in device memory (or, for the error paths, host memory).
+class Tensor {
+ public:
+  static Tensor empty(const RocmDevice& dev, std::vector<size_t> shape, DType dtype);
+  static Tensor from_host(const RocmDevice& dev, const void* data, std::vector<size_t> shape, DType dtype);
+  // A host-resident tensor: passing it to a kernel entry point is an error.
+  static Tensor cpu(const void* data, std::vector<size_t> shape, DType dtype);
+
+  DType dtype() const { return dtype_; }
+  const std::vector<size_t>& shape() const { return shape_; }
+  size_t dim(int i) const;
+  size_t elem_count() const;
+  size_t size_bytes() const { return elem_count() * dtype_size(dtype_); }
+  bool on_device() const { return storage_ && storage_->device; }
+  GpuBuffer buffer() const;  // the enc_* view of a device tensor
+  std::vector<uint8_t> to_host_bytes() const;
+  template <class T>
+  std::vector<T> to_vec() const {
+    std::vector<uint8_t> b = to_host_bytes();
+    std::vector<T> v(b.size() / sizeof(T));
+    std::copy(b.data(), b.data() + v.size() * sizeof(T), reinterpret_cast<uint8_t*>(v.data()));
+    return v;
+  }
+
+ private:
+  struct Storage {
+    void* ptr = nullptr;
+    bool device = false;
+    std::vector<uint8_t> host;
+    ~Storage();
+  };
+  std::shared_ptr<Storage> storage_;
+  std::vector<size_t> shape_;
+  DType dtype_ = DType::F32;
+};
+
+// The loaded kernel set (TritonKernels::load / DecoderKernels::load /
+// KokoroKernels::load, kernels/out/generated/triton_metal_gen.rs:39-106).
+class RocmKernels {
+ public:
+  static RocmKernels load(const RocmDevice& dev);
+  int kernel_count() const { return kernel_count_; }
+
+ private:
+  int kernel_count_ = 0;
+};
+
+// The encoder of the enc_* API: launches go onto this stream.
+using Encoder = hipStream_t;
+
+// ---- Tensor-level API (src/triton_kernels.rs) ------------------------------
+
+// out = LN(x) * (gamma + 1), f16 out [n_rows, n_cols] (:312).
+Tensor triton_layernorm_unit_offset(const RocmDevice& device, const RocmKernels& kernels, const Tensor& x,
+                                    const Tensor& gamma, size_t n_rows, size_t n_cols);
+// out = (x - mean) / sqrt(var + eps), f16 out (:345).
+Tensor triton_layernorm_bare(const RocmDevice& device, const RocmKernels& kernels, const Tensor& x, size_t n_rows,
+                             size_t n_cols);
+// out = x + residual, f16 (:383).
+Tensor triton_residual_add(const RocmDevice& device, const RocmKernels& kernels, const Tensor& x,
+                           const Tensor& residual, size_t n_elements);
+// out = gelu(x), f16 (:412).
+Tensor triton_gelu(const RocmDevice& device, const RocmKernels& kernels, const Tensor& x, size_t n_elements);
+// out = LN(x) * weight: f32 x, f16 weight, f16 out (:598).
+void triton_layernorm_std_f32in(const RocmDevice& device, const RocmKernels& kernels, const Tensor& x,
+                                const Tensor& weight, const Tensor& out, size_t n_rows, size_t n_cols);
+// out = x + residual, f32 (:625).
+void triton_residual_add_f32(const RocmDevice& device, const RocmKernels& kernels, const Tensor& x,
+                             const Tensor& residual, const Tensor& out, size_t n_elements);
+// out[i] = silu(fc1[n + i]) * fc1[i], f16 (:713).
+void triton_glu_silu(const RocmDevice& device, const RocmKernels& kernels, const Tensor& fc1, const Tensor& out,
+                     size_t n_elements);
+// f32_out = f16_proj + f32_residual; f16_norm = LN(f32_out) * weight (:742).
+void triton_residual_add_layernorm(const RocmDevice& device, const RocmKernels& kernels, const Tensor& f16_proj,
+                                   const Tensor& f32_residual, const Tensor& f32_out, const Tensor& weight,
+                                   const Tensor& f16_norm, size_t n_rows, size_t dim);
+
+// ---- Buffer-level API (src/triton_kernels.rs:862-1423) ----------------------
+
+void enc_layernorm_std_f32in(Encoder enc, const RocmKernels& kernels, const GpuBuffer& x, const GpuBuffer& weight,
+                             const GpuBuffer& out, size_t n_rows, size_t n_cols);
+void enc_residual_add_layernorm(Encoder enc, const RocmKernels& kernels, const GpuBuffer& f16_proj,
+                                const GpuBuffer& f32_residual, const GpuBuffer& f32_out, const GpuBuffer& weight,
+                                const GpuBuffer& f16_norm, size_t n_rows, size_t dim);
+void enc_layernorm_bare(Encoder enc, const RocmKernels& kernels, const GpuBuffer& x, const GpuBuffer& out,
+                        size_t n_rows, size_t n_cols);
+void enc_layernorm_unit_offset(Encoder enc, const RocmKernels& kernels, const GpuBuffer& x, const GpuBuffer& gamma,
+                               const GpuBuffer& out, size_t n_rows, size_t n_cols);
+void enc_gelu(Encoder enc, const RocmKernels& kernels, const GpuBuffer& x, const GpuBuffer& out, size_t n_elements);
+void enc_residual_add(Encoder enc, const RocmKernels& kernels, const GpuBuffer& x, const GpuBuffer& residual,
+                      const GpuBuffer& out, size_t n_elements);
+
+// ---- Kokoro backend (src/kokoro/gpu_backend.rs) ------------------------------
+
+// The AdaIN+Snake part of KokoroGpuBackend for the ROCm device: Buf = GpuBuffer.
+class RocmKokoroBackend {
+ public:
+  RocmKokoroBackend(const RocmDevice& device, const RocmKernels& kernels) : device_(device), kernels_(kernels) {}
+  // out = snake(AdaIN(x)) over x [channels, seq_len] f32; gamma, beta, alpha
+  // [channels] f16 (the precomputed style parameters, decoder.rs:966-981).
+  void adain_snake_f32(const GpuBuffer& x, const GpuBuffer& gamma, const GpuBuffer& beta, const GpuBuffer& alpha,
+                       const GpuBuffer& out, size_t channels, size_t seq_len) const;
+  // The f16-activation variant (gpu_backend.rs:55-57) is not built for this
+  // device: it throws, as the trait's unsupported methods return Err.
+  void adain_snake(const GpuBuffer& x, const GpuBuffer& gamma, const GpuBuffer& beta, const GpuBuffer& alpha,
+                   const GpuBuffer& out, size_t channels, size_t seq_len) const;
+
+ private:
+  RocmDevice device_;
+  RocmKernels kernels_;
+};
+
+// ---- Embedding and rotary (model-side entry points the GPU also serves) ------
+
+// GGUF Q8_0 embedding table on the device (QEmbedding, quantized_layers.rs).
+class QEmbedding {
+ public:
+  // table: U8 bytes of vocab rows x hidden/32 blocks {f16 d; i8 qs[32]}.
+  QEmbedding(const RocmDevice& device, const RocmKernels& kernels, Tensor table, size_t vocab, size_t hidden);
+  size_t hidden_size() const { return hidden_; }
+  // indexes: U32 or I64 device tensor of any shape -> f32 [..., hidden].
+  // An index outside [0, vocab) is an error (as Candle's index_select).
+  Tensor forward(const Tensor& indexes) const;
+
+ private:
+  RocmDevice device_;
+  RocmKernels kernels_;
+  Tensor table_;
+  size_t vocab_, hidden_;
+};
+
+// inv_freq and the f32 cos/sin table of RotaryEmbedding::new, built on the
+// host with the reference's f32 operations (decoder.rs:85-95).
+class RotaryEmbedding {
+ public:
+  RotaryEmbedding(const RocmDevice& device, const RocmKernels& kernels, size_t rotary_dim, size_t max_positions,
+                  float theta);
+  size_t rotary_dim() const { return rotary_dim_; }
+  const Tensor& table() const { return table_; }  // [max_positions, rotary_dim]: cos | sin
+  // apply_rotary_pos_emb for q [B, Hq, T, Dh], k [B, Hk, T, Dh] f32 at
+  // positions pos0 .. pos0 + T - 1; dims >= rotary_dim pass through.
+  std::pair<Tensor, Tensor> apply(const Tensor& q, const Tensor& k, size_t pos0) const;
+
+ private:
+  RocmDevice device_;
+  RocmKernels kernels_;
+  size_t rotary_dim_, max_positions_;
+  float theta_;
+  Tensor table_;
+};
+
+}  // namespace rocm
+}  // namespace nspeech

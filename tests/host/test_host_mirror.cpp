@@ -1,0 +1,345 @@
+// Host-side tests of the nspeech::rocm mirror (nspeech_amd/host/rocm_kernels.h),
+// written the way the reference's Kokoro GPU self-tests are
+// (src/kokoro/gpu_decoder.rs:64-456): deterministic known-answer inputs, the
+// expected values from inline float64 formulas, a max-error report per test,
+// plus a tolerance the reference's self-tests do not assert. Returns 0 when
+// every test passes. Run on a GPU by tests/test_gpu_host_mirror.py.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "rocm_kernels.h"
+
+using namespace nspeech::rocm;
+
+namespace {
+
+int g_failed = 0;
+
+void report(const char* name, double err, double tol) {
+  const bool ok = err <= tol;
+  std::printf("%-34s max scaled error %.3e (tol %.0e) %s\n", name, err, tol, ok ? "ok" : "FAIL");
+  if (!ok) ++g_failed;
+}
+
+void expect_throw(const char* name, const std::function<void()>& f, const char* needle) {
+  try {
+    f();
+  } catch (const Error& e) {
+    const bool ok = std::strstr(e.what(), needle) != nullptr;
+    std::printf("%-34s threw \"%s\" %s\n", name, e.what(), ok ? "ok" : "FAIL");
+    if (!ok) ++g_failed;
+    return;
+  }
+  std::printf("%-34s did not throw FAIL\n", name);
+  ++g_failed;
+}
+
+// IEEE half <-> float (round to nearest even), host side.
+uint16_t f2h(float f) {
+  uint32_t x;
+  std::memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  int32_t e = (int32_t)((x >> 23) & 0xff) - 127 + 15;
+  uint32_t m = x & 0x7fffffu;
+  if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+  if (e <= 0) {
+    if (e < -10) return (uint16_t)sign;
+    m |= 0x800000u;
+    const int shift = 14 - e;
+    uint32_t h = m >> shift;
+    const uint32_t rem = m & ((1u << shift) - 1), half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (h & 1))) ++h;
+    return (uint16_t)(sign | h);
+  }
+  uint32_t h = ((uint32_t)e << 10) | (m >> 13);
+  const uint32_t rem = m & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1))) ++h;
+  return (uint16_t)(sign | h);
+}
+
+float h2f(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1f, m = h & 0x3ff;
+  uint32_t x;
+  if (e == 0) {
+    float v = (float)m * 5.9604644775390625e-08f;
+    std::memcpy(&x, &v, 4);
+    x |= sign;
+  } else if (e == 31) {
+    x = sign | 0x7f800000u | (m << 13);
+  } else {
+    x = sign | ((e + 112) << 23) | (m << 13);
+  }
+  float f;
+  std::memcpy(&f, &x, 4);
+  return f;
+}
+
+double scaled(double got, double ref) { return std::fabs(got - ref) / std::max(std::fabs(ref), 1.0); }
+
+// Kokoro self-test inputs (gpu_decoder.rs:84-87): x[i] = sin(0.001 i) * 3,
+// gamma_c = f16(sin(0.01c) * 0.5), beta_c = f16(cos(0.02c) * 0.3),
+// alpha_c = f16(1 + sin(0.005c)).
+void test_adain_snake_f32(const RocmDevice& dev, const RocmKernels& k, size_t C, size_t T, const char* name) {
+  std::vector<float> x(C * T);
+  for (size_t i = 0; i < x.size(); ++i) x[i] = std::sin(0.001f * (float)i) * 3.0f;
+  std::vector<uint16_t> g(C), b(C), a(C);
+  for (size_t c = 0; c < C; ++c) {
+    g[c] = f2h(std::sin(0.01f * (float)c) * 0.5f);
+    b[c] = f2h(std::cos(0.02f * (float)c) * 0.3f);
+    a[c] = f2h(1.0f + std::sin(0.005f * (float)c));
+  }
+  Tensor X = Tensor::from_host(dev, x.data(), {C, T}, DType::F32);
+  Tensor G = Tensor::from_host(dev, g.data(), {C}, DType::F16);
+  Tensor B = Tensor::from_host(dev, b.data(), {C}, DType::F16);
+  Tensor A = Tensor::from_host(dev, a.data(), {C}, DType::F16);
+  Tensor O = Tensor::empty(dev, {C, T}, DType::F32);
+  RocmKokoroBackend be(dev, k);
+  be.adain_snake_f32(X.buffer(), G.buffer(), B.buffer(), A.buffer(), O.buffer(), C, T);
+  dev.synchronize();
+  std::vector<float> o = O.to_vec<float>();
+  double err = 0;
+  for (size_t c = 0; c < C; ++c) {
+    double mean = 0, var = 0;
+    for (size_t t = 0; t < T; ++t) mean += x[c * T + t];
+    mean /= (double)T;
+    for (size_t t = 0; t < T; ++t) var += (x[c * T + t] - mean) * (x[c * T + t] - mean);
+    var /= (double)T;
+    const double al = h2f(a[c]);
+    const double inv_a = (double)(1.0f / (h2f(a[c]) + 1e-9f));
+    for (size_t t = 0; t < T; ++t) {
+      const double y = (x[c * T + t] - mean) / std::sqrt(var + 1e-5) * (1.0 + h2f(g[c])) + h2f(b[c]);
+      const double s = std::sin(al * y);
+      err = std::max(err, scaled(o[c * T + t], y + s * s * inv_a));
+    }
+  }
+  report(name, err, 1e-5);
+}
+
+void test_layernorm_std_f32in(const RocmDevice& dev, const RocmKernels& k) {
+  const size_t R = 17, N = 640;  // decoder width of layernorm_standard_f32in_640
+  std::vector<float> x(R * N);
+  std::vector<uint16_t> w(N);
+  for (size_t i = 0; i < x.size(); ++i) x[i] = std::sin(0.1f * (float)i) * 3.0f + 0.5f;
+  for (size_t c = 0; c < N; ++c) w[c] = f2h(1.0f + 0.1f * std::cos(0.03f * (float)c));
+  Tensor X = Tensor::from_host(dev, x.data(), {R, N}, DType::F32);
+  Tensor W = Tensor::from_host(dev, w.data(), {N}, DType::F16);
+  Tensor O = Tensor::empty(dev, {R, N}, DType::F16);
+  triton_layernorm_std_f32in(dev, k, X, W, O, R, N);
+  dev.synchronize();
+  std::vector<uint16_t> o = O.to_vec<uint16_t>();
+  double err = 0;
+  for (size_t r = 0; r < R; ++r) {
+    double m = 0, v = 0;
+    for (size_t c = 0; c < N; ++c) m += x[r * N + c];
+    m /= N;
+    for (size_t c = 0; c < N; ++c) v += (x[r * N + c] - m) * (x[r * N + c] - m);
+    v /= N;
+    for (size_t c = 0; c < N; ++c)
+      err = std::max(err, scaled(h2f(o[r * N + c]), (x[r * N + c] - m) / std::sqrt(v + 1e-5) * h2f(w[c])));
+  }
+  report("triton_layernorm_std_f32in", err, 2e-3);
+}
+
+void test_layernorm_unit_offset_and_bare(const RocmDevice& dev, const RocmKernels& k) {
+  const size_t R = 9, N = 768;  // encoder width of layernorm_unit_offset_768
+  std::vector<uint16_t> x(R * N), g(N);
+  for (size_t i = 0; i < x.size(); ++i) x[i] = f2h(std::sin(0.37f * (float)i) * 2.0f);
+  for (size_t c = 0; c < N; ++c) g[c] = f2h(0.05f * std::sin(0.11f * (float)c));
+  Tensor X = Tensor::from_host(dev, x.data(), {R, N}, DType::F16);
+  Tensor G = Tensor::from_host(dev, g.data(), {N}, DType::F16);
+  Tensor U = triton_layernorm_unit_offset(dev, k, X, G, R, N);
+  Tensor Bo = triton_layernorm_bare(dev, k, X, R, N);
+  dev.synchronize();
+  std::vector<uint16_t> u = U.to_vec<uint16_t>(), bo = Bo.to_vec<uint16_t>();
+  double eu = 0, eb = 0;
+  for (size_t r = 0; r < R; ++r) {
+    double m = 0, v = 0;
+    for (size_t c = 0; c < N; ++c) m += h2f(x[r * N + c]);
+    m /= N;
+    for (size_t c = 0; c < N; ++c) v += (h2f(x[r * N + c]) - m) * (h2f(x[r * N + c]) - m);
+    v /= N;
+    for (size_t c = 0; c < N; ++c) {
+      const double n = (h2f(x[r * N + c]) - m) / std::sqrt(v + 1e-5);
+      eu = std::max(eu, scaled(h2f(u[r * N + c]), n * (h2f(g[c]) + 1.0)));
+      eb = std::max(eb, scaled(h2f(bo[r * N + c]), n));
+    }
+  }
+  report("triton_layernorm_unit_offset", eu, 2e-3);
+  report("triton_layernorm_bare", eb, 2e-3);
+}
+
+void test_elementwise(const RocmDevice& dev, const RocmKernels& k) {
+  const size_t n = 3000;
+  std::vector<uint16_t> x(n), r(n), fc1(2 * n);
+  for (size_t i = 0; i < n; ++i) {
+    x[i] = f2h(std::sin(0.05f * (float)i) * 4.0f);
+    r[i] = f2h(std::cos(0.07f * (float)i));
+  }
+  for (size_t i = 0; i < 2 * n; ++i) fc1[i] = f2h(std::sin(0.013f * (float)i) * 3.0f);
+  Tensor X = Tensor::from_host(dev, x.data(), {n}, DType::F16);
+  Tensor Rr = Tensor::from_host(dev, r.data(), {n}, DType::F16);
+  Tensor F = Tensor::from_host(dev, fc1.data(), {2 * n}, DType::F16);
+  Tensor Gl = triton_gelu(dev, k, X, n);
+  Tensor Ad = triton_residual_add(dev, k, X, Rr, n);
+  Tensor Gs = Tensor::empty(dev, {n}, DType::F16);
+  triton_glu_silu(dev, k, F, Gs, n);
+  dev.synchronize();
+  std::vector<uint16_t> gl = Gl.to_vec<uint16_t>(), ad = Ad.to_vec<uint16_t>(), gs = Gs.to_vec<uint16_t>();
+  double eg = 0, ea = 0, es = 0;
+  for (size_t i = 0; i < n; ++i) {
+    const double v = h2f(x[i]);
+    eg = std::max(eg, scaled(h2f(gl[i]), v * 0.5 * (1.0 + std::erf(v / std::sqrt(2.0)))));
+    ea = std::max(ea, scaled(h2f(ad[i]), (double)h2f(x[i]) + h2f(r[i])));
+    const double gate = h2f(fc1[n + i]);
+    es = std::max(es, scaled(h2f(gs[i]), gate / (1.0 + std::exp(-gate)) * h2f(fc1[i])));
+  }
+  report("triton_gelu", eg, 2e-3);
+  report("triton_residual_add", ea, 2e-3);
+  report("triton_glu_silu", es, 2e-3);
+}
+
+void test_residual_add_layernorm(const RocmDevice& dev, const RocmKernels& k) {
+  const size_t R = 5, D = 640;
+  std::vector<uint16_t> proj(R * D), w(D);
+  std::vector<float> res(R * D);
+  for (size_t i = 0; i < R * D; ++i) {
+    proj[i] = f2h(std::sin(0.21f * (float)i));
+    res[i] = std::cos(0.017f * (float)i) * 2.0f;
+  }
+  for (size_t c = 0; c < D; ++c) w[c] = f2h(1.0f + 0.2f * std::sin(0.05f * (float)c));
+  Tensor P = Tensor::from_host(dev, proj.data(), {R, D}, DType::F16);
+  Tensor Rs = Tensor::from_host(dev, res.data(), {R, D}, DType::F32);
+  Tensor W = Tensor::from_host(dev, w.data(), {D}, DType::F16);
+  Tensor H = Tensor::empty(dev, {R, D}, DType::F32);
+  Tensor N = Tensor::empty(dev, {R, D}, DType::F16);
+  triton_residual_add_layernorm(dev, k, P, Rs, H, W, N, R, D);
+  dev.synchronize();
+  std::vector<float> h = H.to_vec<float>();
+  std::vector<uint16_t> nn = N.to_vec<uint16_t>();
+  double eh = 0, en = 0;
+  for (size_t r = 0; r < R; ++r) {
+    std::vector<double> hv(D);
+    double m = 0, v = 0;
+    for (size_t c = 0; c < D; ++c) {
+      hv[c] = (double)(h2f(proj[r * D + c]) + res[r * D + c]);
+      eh = std::max(eh, scaled(h[r * D + c], hv[c]));
+      m += hv[c];
+    }
+    m /= D;
+    for (size_t c = 0; c < D; ++c) v += (hv[c] - m) * (hv[c] - m);
+    v /= D;
+    for (size_t c = 0; c < D; ++c)
+      en = std::max(en, scaled(h2f(nn[r * D + c]), (hv[c] - m) / std::sqrt(v + 1e-5) * h2f(w[c])));
+  }
+  report("triton_residual_add_layernorm h", eh, 1e-6);
+  report("triton_residual_add_layernorm y", en, 2e-3);
+}
+
+void test_q8_embedding(const RocmDevice& dev, const RocmKernels& k) {
+  const size_t vocab = 97, hidden = 416, nb = hidden / 32;
+  std::vector<uint8_t> table(vocab * nb * 34);
+  for (size_t blk = 0; blk < vocab * nb; ++blk) {
+    const uint16_t d = f2h(0.001f + 0.0001f * (float)(blk % 97));
+    std::memcpy(&table[blk * 34], &d, 2);
+    for (int j = 0; j < 32; ++j) table[blk * 34 + 2 + j] = (uint8_t)(int8_t)((int)((blk * 31 + j * 7) % 255) - 127);
+  }
+  std::vector<uint32_t> ids = {0, 96, 5, 5, 42, 17, 96, 1};
+  QEmbedding emb(dev, k, Tensor::from_host(dev, table.data(), {table.size()}, DType::U8), vocab, hidden);
+  Tensor I = Tensor::from_host(dev, ids.data(), {2, 4}, DType::U32);
+  Tensor O = emb.forward(I);
+  std::vector<float> o = O.to_vec<float>();
+  long bad = 0;
+  for (size_t n = 0; n < ids.size(); ++n)
+    for (size_t j = 0; j < hidden; ++j) {
+      const uint8_t* bp = &table[(ids[n] * nb + j / 32) * 34];
+      uint16_t d;
+      std::memcpy(&d, bp, 2);
+      const float ref = (float)(int8_t)bp[2 + j % 32] * h2f(d);  // exact in f32
+      if (std::memcmp(&ref, &o[n * hidden + j], 4) != 0) ++bad;
+    }
+  std::printf("%-34s %ld elements differ (shape [%zu, %zu, %zu]) %s\n", "QEmbedding::forward bit-exact", bad,
+              O.dim(0), O.dim(1), O.dim(2), bad == 0 ? "ok" : "FAIL");
+  if (bad) ++g_failed;
+  std::vector<uint32_t> badids = {3, 97};
+  Tensor BI = Tensor::from_host(dev, badids.data(), {2}, DType::U32);
+  expect_throw("QEmbedding::forward out of range", [&] { emb.forward(BI); }, "out of range");
+}
+
+void test_rotary(const RocmDevice& dev, const RocmKernels& k) {
+  const size_t B = 1, Hq = 4, Hk = 2, T = 37, Dh = 64, rot = 32, pos0 = 11;
+  RotaryEmbedding re(dev, k, rot, 4096, 10000.0f);
+  std::vector<float> q(B * Hq * T * Dh), kk(B * Hk * T * Dh);
+  for (size_t i = 0; i < q.size(); ++i) q[i] = std::sin(0.3f * (float)i);
+  for (size_t i = 0; i < kk.size(); ++i) kk[i] = std::cos(0.7f * (float)i);
+  Tensor Q = Tensor::from_host(dev, q.data(), {B, Hq, T, Dh}, DType::F32);
+  Tensor K = Tensor::from_host(dev, kk.data(), {B, Hk, T, Dh}, DType::F32);
+  auto [QO, KO] = re.apply(Q, K, pos0);
+  dev.synchronize();
+  double err = 0;
+  auto check = [&](const std::vector<float>& in, const std::vector<float>& out, size_t H) {
+    for (size_t h = 0; h < B * H; ++h)
+      for (size_t t = 0; t < T; ++t)
+        for (size_t i = 0; i < Dh; ++i) {
+          const size_t o = (h * T + t) * Dh;
+          double ref = in[o + i];
+          if (i < rot) {
+            const size_t p = i / 2;
+            const float inv_freq = 1.0f / std::pow(10000.0f, (2.0f * (float)p) / (float)rot);
+            const double ang = (double)((float)(pos0 + t) * inv_freq);
+            ref = (i % 2 == 0) ? in[o + i] * std::cos(ang) - in[o + i + 1] * std::sin(ang)
+                               : in[o + i] * std::cos(ang) + in[o + i - 1] * std::sin(ang);
+          }
+          err = std::max(err, scaled(out[o + i], ref));
+        }
+  };
+  check(q, QO.to_vec<float>(), Hq);
+  check(kk, KO.to_vec<float>(), Hk);
+  report("apply_rotary_pos_emb (RoPE table)", err, 1e-5);
+}
+
+void test_errors(const RocmDevice& dev, const RocmKernels& k) {
+  float host[8] = {0};
+  Tensor C = Tensor::cpu(host, {2, 4}, DType::F32);
+  Tensor D = Tensor::empty(dev, {2, 4}, DType::F16);
+  expect_throw("host tensor is rejected", [&] { triton_layernorm_std_f32in(dev, k, C, D, D, 2, 4); },
+               "must be on the ROCm device");
+  Tensor X = Tensor::empty(dev, {2, 4}, DType::F16);
+  expect_throw("wrong dtype is rejected", [&] { triton_layernorm_std_f32in(dev, k, X, D, D, 2, 4); },
+               "expected f32");
+  Tensor Xf = Tensor::empty(dev, {2, 4}, DType::F32);
+  expect_throw("short tensor is rejected", [&] { triton_layernorm_std_f32in(dev, k, Xf, D, D, 4, 4); },
+               "need 16");
+  RocmKokoroBackend be(dev, k);
+  expect_throw("adain_snake f16 unsupported",
+               [&] { be.adain_snake(X.buffer(), X.buffer(), X.buffer(), X.buffer(), X.buffer(), 2, 4); },
+               "not supported");
+}
+
+}  // namespace
+
+int main() {
+  try {
+    RocmDevice dev = RocmDevice::create(0);
+    RocmKernels k = RocmKernels::load(dev);
+    std::printf("kernels loaded: %d probed\n", k.kernel_count());
+    test_adain_snake_f32(dev, k, 4, 100, "adain_snake_f32 C=4 T=100");
+    test_adain_snake_f32(dev, k, 128, 11281, "adain_snake_f32 C=128 T=11281");
+    test_layernorm_std_f32in(dev, k);
+    test_layernorm_unit_offset_and_bare(dev, k);
+    test_elementwise(dev, k);
+    test_residual_add_layernorm(dev, k);
+    test_q8_embedding(dev, k);
+    test_rotary(dev, k);
+    test_errors(dev, k);
+  } catch (const Error& e) {
+    std::printf("unexpected error: %s\n", e.what());
+    return 2;
+  }
+  std::printf("%s: %d failed\n", g_failed ? "FAILED" : "PASSED", g_failed);
+  return g_failed ? 1 : 0;
+}
