@@ -46,8 +46,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workloads", default="c0,c1,c1t,c2,c3,c4a,c4b",
-                    help="comma list of c0,c1,c1t,c2,c3,c4a,c4b,copy")
+    ap.add_argument("--workloads", default="c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2",
+                    help="comma list of c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,copy")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline (0 = skip)")
     ap.add_argument("--no-rotate", action="store_true", help="one buffer set (warm MALL) for all timings")
     return ap.parse_args()
@@ -161,6 +161,38 @@ def build_workload(name):
         return Workload(name, "GGUF Q8_0 gather-dequant + SiLU, table 32768x416, 4096 ids -> f32 [4096,416]",
                         configs.algorithmic_bytes("c3"), blocks0.numel() + 4096 * 416 * 4, make_set, launch,
                         "nsrk_q8_0_gather_silu_u32", "i8xf16->f32")
+
+    if name in ("dec", "dec2"):
+        # Moonshine decoder step per layer (kernel_configs.py:102-104): q,k,v f16 [10, 64], rot 32,
+        # caches [10, 448, 64]; "dec" = one launch, "dec2" = the reference's two dispatches
+        # (rope_qk_cache_fused, then kv_cache_append).
+        g = configs.rng(1006)
+        Hq = Hk = 10
+        Dh, rot, Lc, pos = 64, 32, 448, 300
+        tab = abi.rope_table(Lc, rot, 10000.0).to(dev)
+        mk = lambda *sh: torch.from_numpy(g.standard_normal(sh).astype(np.float16)).to(dev)  # noqa: E731
+
+        def make_set(_):
+            z = lambda: torch.zeros((Hk, Lc, Dh), dtype=torch.float16, device=dev)  # noqa: E731
+            return {"q": mk(Hq, Dh), "k": mk(Hk, Dh), "v": mk(Hk, Dh), "ck": z(), "cv": z()}
+
+        def launch(s):
+            if name == "dec":
+                abi.check(L.nsr_rope_qk_cache_append(s["q"].data_ptr(), s["k"].data_ptr(), s["v"].data_ptr(), 1,
+                                                      tab.data_ptr(), Lc, s["ck"].data_ptr(), s["cv"].data_ptr(),
+                                                      Hq, Hk, Dh, rot, pos, Lc, stream()))
+            else:
+                abi.check(L.nsr_rope_qk_cache_append(s["q"].data_ptr(), s["k"].data_ptr(), None, 1,
+                                                      tab.data_ptr(), Lc, s["ck"].data_ptr(), None,
+                                                      Hq, Hk, Dh, rot, pos, Lc, stream()))
+                abi.check(L.nsr_kv_cache_append(s["v"].data_ptr(), s["cv"].data_ptr(), 1, Hk, Dh, Lc, pos,
+                                                  stream()))
+
+        alg = 2 * (2 * Hq * Dh + 2 * Hk * Dh) + 2 * (2 * Hk * Dh) + 2 * Hk * Dh + 4 * rot
+        return Workload(name, "decode step RoPE(q,k) + K/V cache append f16, 10 heads x 64, rot 32"
+                        + (" (one launch)" if name == "dec" else " (two launches, as the reference)"), alg,
+                        2 * Hk * Lc * Dh * 2, make_set, launch,
+                        "nsrk_rope_cache_f16", "f16")
 
     if name == "c4a":
         c = configs.c4a()

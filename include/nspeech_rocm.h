@@ -156,6 +156,35 @@ nsr_status nsr_rotary_partial_interleaved_f32(const float* q, const float* k,
                                               int64_t table_rows,
                                               nsr_stream_t stream);
 
+/* Decode step, one position: rotate q [n_q_heads, head_dim] and k
+ * [n_kv_heads, head_dim] IN PLACE on the interleaved pairs < rotary_dim with
+ * row `pos` of a DEVICE RoPE table (layout of nsr_rope_table_f32, at least
+ * pos + 1 rows), write the rotated k row to cache_k[h, pos, :] and, when v is
+ * given, the v row to cache_v[h, pos, :]. Caches are [n_kv_heads,
+ * max_kv_len, head_dim]. dtype F16 (the reference decoder's) or F32; each
+ * rotated value is rounded to dtype from f32 products. head_dim and
+ * rotary_dim even; q/k/v/caches 4-byte (F16) or 8-byte (F32) aligned.
+ * One launch replaces the reference's two dispatches per layer and token:
+ * enc_rope_qk_cache_fused (src/triton_kernels.rs:975;
+ * kernels/moonshine_kernels.py:1372-1454) and enc_kv_cache_append (:993;
+ * moonshine_kernels.py:865-883), issued together by
+ * MetalBackend::rope_kv_cache (src/moonshine/gpu_decoder_metal.rs:144-156).
+ * v == NULL (and cache_v == NULL) is exactly enc_rope_qk_cache_fused. */
+nsr_status nsr_rope_qk_cache_append(void* q, void* k, const void* v, nsr_dtype dtype,
+                                    const float* rope_table, int64_t table_rows,
+                                    void* cache_k, void* cache_v,
+                                    int64_t n_q_heads, int64_t n_kv_heads, int64_t head_dim,
+                                    int rotary_dim, int64_t pos, int64_t max_kv_len,
+                                    nsr_stream_t stream);
+
+/* cache[h, pos, :] = new_kv[h, :] for h < n_kv_heads; cache [n_kv_heads,
+ * max_kv_len, head_dim], head_dim even, dtype F16 or F32.
+ * Replaces enc_kv_cache_append (src/triton_kernels.rs:993) and
+ * triton_kv_cache_append (:680); kernels/moonshine_kernels.py:865-883. */
+nsr_status nsr_kv_cache_append(const void* new_kv, void* cache, nsr_dtype dtype,
+                               int64_t n_kv_heads, int64_t head_dim, int64_t max_kv_len,
+                               int64_t pos, nsr_stream_t stream);
+
 /* ---- AdaIN1d + Snake ------------------------------------------------------ */
 
 /* For x [B, C, T] f32, per (b, c) row:

@@ -56,6 +56,9 @@ def lib() -> C.CDLL:
         L.nsr_rope_table_f32.argtypes = [_P, _I64, C.c_int, C.c_float]
         L.nsr_rotary_partial_interleaved_f32.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, C.c_int,
                                                          C.c_float, _I64, _P, _I64, _P]
+        L.nsr_rope_qk_cache_append.argtypes = [_P, _P, _P, C.c_int, _P, _I64, _P, _P, _I64, _I64, _I64, C.c_int,
+                                                _I64, _I64, _P]
+        L.nsr_kv_cache_append.argtypes = [_P, _P, C.c_int, _I64, _I64, _I64, _I64, _P]
         L.nsr_adain_snake_f32.argtypes = [_P, _P, _P, _P, C.c_int, _I64, _I64, _P, _I64, _I64, _I64, C.c_float,
                                           _P]
         L.nsr_q8_0_embed_gather.argtypes = [_P, _I64, _I64, _P, C.c_int, _I64, _P, C.c_int, _P, _P]
@@ -63,6 +66,7 @@ def lib() -> C.CDLL:
         L.nsr_glu_silu.argtypes = [_P, _P, C.c_int, _I64, _P]
         L.nsr_residual_add.argtypes = [_P, _P, _P, C.c_int, _I64, _P]
         for name in ("nsr_init", "nsr_layernorm", "nsr_residual_add_layernorm", "nsr_rope_table_f32",
+                     "nsr_rope_qk_cache_append", "nsr_kv_cache_append",
                      "nsr_rotary_partial_interleaved_f32", "nsr_adain_snake_f32", "nsr_q8_0_embed_gather",
                      "nsr_activation", "nsr_glu_silu", "nsr_residual_add"):
             getattr(L, name).restype = C.c_int
@@ -168,6 +172,22 @@ def rotary(q, k, rotary_dim, theta=10000.0, pos0=0, *, table=None, q_out=None, k
     check(lib().nsr_rotary_partial_interleaved_f32(_ptr(q), _ptr(k), _ptr(q_out), _ptr(k_out), B, Hq, Hk, T, Dh,
                                                    rotary_dim, theta, pos0, _ptr(table), rows, _stream(stream)))
     return q_out, k_out
+
+
+def rope_qk_cache_append(q, k, v, table, cache_k, cache_v, pos, rotary_dim, *, stream=None):
+    """Decode step, in place: q [Hq, Dh], k [Hk, Dh] rotated with table row pos;
+    rotated k and v (or v None) written to the caches [Hk, L, Dh] at pos."""
+    Hq, Dh = q.shape
+    Hk = k.shape[0]
+    check(lib().nsr_rope_qk_cache_append(_ptr(q), _ptr(k), _ptr(v), _dt(q), _ptr(table), table.shape[0],
+                                         _ptr(cache_k), _ptr(cache_v), Hq, Hk, Dh, rotary_dim, pos, cache_k.shape[1],
+                                         _stream(stream)))
+
+
+def kv_cache_append(new_kv, cache, pos, *, stream=None):
+    """cache[h, pos, :] = new_kv[h, :]; cache [Hk, L, Dh]."""
+    Hk, L, Dh = cache.shape
+    check(lib().nsr_kv_cache_append(_ptr(new_kv), _ptr(cache), _dt(cache), Hk, Dh, L, pos, _stream(stream)))
 
 
 def adain_snake(x, gamma, beta, alpha, *, eps=1e-5, out=None, stream=None):

@@ -70,3 +70,93 @@ extern "C" __global__ void __launch_bounds__(256) nsrk_rope_table_f32(const nsr_
 extern "C" __global__ void __launch_bounds__(256) nsrk_rope_compute_f32(const nsr_rope_args a) {
   rope_body<false>(a);
 }
+
+/* ------------------------------------------------- decode step: RoPE + cache -- */
+
+/*
+ * One decode position: q [Hq, Dh] and k [Hk, Dh] rotated in place on the
+ * interleaved pairs < rotary_dim with the RoPE table row pos, the rotated k
+ * row and the v row appended to the caches [Hk, max_kv_len, Dh] at pos.
+ * Reference: rope_qk_cache_fused (kernels/moonshine_kernels.py:1372-1454,
+ * enc_rope_qk_cache_fused src/triton_kernels.rs:975) and kv_cache_append
+ * (:865-883, enc_kv_cache_append :993), which the reference's decoder
+ * dispatches back to back (src/moonshine/gpu_decoder_metal.rs:144-156); here
+ * one launch. One lane per element pair, four disjoint lane ranges (q pairs,
+ * k pairs, k pass-through pairs, v pairs): no lane reads what another writes.
+ * Each rotated value is the storage dtype of x0*c - x1*s / x1*c + x0*s with
+ * the f32 products rounded separately.
+ */
+template <int DT>
+NSR_DEV void load_pair(const void* p, int64_t e, float& a, float& b) {
+  if constexpr (DT == DT_F32) {
+    const float2 v = *((const float2*)p + (e >> 1));
+    a = v.x;
+    b = v.y;
+  } else {
+    const uint32_t w = *((const uint32_t*)p + (e >> 1));
+    a = f16_bits_to_f32(w & 0xffffu);
+    b = f16_bits_to_f32(w >> 16);
+  }
+}
+
+template <int DT>
+NSR_DEV void store_pair(void* p, int64_t e, float a, float b) {
+  if constexpr (DT == DT_F32) {
+    *((float2*)p + (e >> 1)) = make_float2(a, b);
+  } else {
+    *((uint32_t*)p + (e >> 1)) = f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
+  }
+}
+
+template <int DT>
+NSR_DEV void copy_pair(const void* src, int64_t es, void* dst, int64_t ed) {
+  if constexpr (DT == DT_F32) {
+    *((float2*)dst + (ed >> 1)) = *((const float2*)src + (es >> 1));
+  } else {
+    *((uint32_t*)dst + (ed >> 1)) = *((const uint32_t*)src + (es >> 1));
+  }
+}
+
+template <int DT>
+NSR_DEV void rope_cache_body(const nsr_rope_cache_args& a) {
+#pragma clang fp contract(off)
+  int p = (int)(blockIdx.x * 256u + threadIdx.x);
+  const int Dh = a.Dh, half = a.half;
+  const float* cs = a.table + a.pos * (int64_t)(2 * half);
+  if (p < a.nq + a.nk) {
+    const bool isk = p >= a.nq;
+    if (isk) p -= a.nq;
+    const int h = p / half, i = p - h * half;
+    void* x = isk ? a.k : a.q;
+    const int64_t e = (int64_t)h * Dh + 2 * i;
+    float x0, x1;
+    load_pair<DT>(x, e, x0, x1);
+    const float c = cs[i], s = cs[half + i];
+    const float y0 = round_to<DT>(x0 * c - x1 * s);
+    const float y1 = round_to<DT>(x1 * c + x0 * s);
+    store_pair<DT>(x, e, y0, y1);
+    if (isk) store_pair<DT>(a.cache_k, ((int64_t)h * a.max_kv_len + a.pos) * Dh + 2 * i, y0, y1);
+    return;
+  }
+  p -= a.nq + a.nk;
+  if (p < a.nkp) {
+    const int npp = (Dh - 2 * half) / 2;
+    const int h = p / npp, j = 2 * half + 2 * (p - h * npp);
+    copy_pair<DT>(a.k, (int64_t)h * Dh + j, a.cache_k, ((int64_t)h * a.max_kv_len + a.pos) * Dh + j);
+    return;
+  }
+  p -= a.nkp;
+  if (p < a.nv) {
+    const int nh = Dh / 2;
+    const int h = p / nh, j = 2 * (p - h * nh);
+    copy_pair<DT>(a.v, (int64_t)h * Dh + j, a.cache_v, ((int64_t)h * a.max_kv_len + a.pos) * Dh + j);
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256) nsrk_rope_cache_f16(const nsr_rope_cache_args a) {
+  rope_cache_body<DT_F16>(a);
+}
+
+extern "C" __global__ void __launch_bounds__(256) nsrk_rope_cache_f32(const nsr_rope_cache_args a) {
+  rope_cache_body<DT_F32>(a);
+}

@@ -56,6 +56,23 @@ typedef struct nsr_rope_args {
   float inv_freq[NSR_MAX_HALF_ROT];
 } nsr_rope_args;
 
+typedef struct nsr_rope_cache_args {
+  void* q;                 /* [Hq, Dh], rotated in place (may be NULL when nq == 0) */
+  void* k;                 /* [Hk, Dh], rotated in place */
+  const void* v;           /* [Hk, Dh] */
+  const float* table;      /* RoPE table row pos: cos[half] then sin[half] */
+  void* cache_k;           /* [Hk, max_kv_len, Dh] */
+  void* cache_v;           /* [Hk, max_kv_len, Dh] */
+  int64_t pos;
+  int64_t max_kv_len;
+  int32_t Dh;
+  int32_t half;            /* rotary_dim / 2 */
+  int32_t nq;              /* lanes (element pairs) of each region: q pairs, */
+  int32_t nk;              /*   k pairs, */
+  int32_t nkp;             /*   k pass-through pairs, */
+  int32_t nv;              /*   v pairs */
+} nsr_rope_cache_args;
+
 typedef struct nsr_adain_args {
   const float* x;          /* [B, C, T] */
   const void* gamma;       /* [B?, C] */

@@ -390,6 +390,66 @@ nsr_status nsr_rotary_partial_interleaved_f32(const float* q, const float* k, fl
                 stream, params);
 }
 
+// --------------------------------------------------- decode RoPE + cache --
+
+static nsr_status rope_cache_launch(void* q, void* k, const void* v, nsr_dtype dtype, const float* table,
+                                    int64_t table_rows, void* cache_k, void* cache_v, int64_t Hq, int64_t Hk,
+                                    int64_t Dh, int rot, int64_t pos, int64_t L, bool k_required,
+                                    nsr_stream_t stream, const char* what) {
+  if (dtype != NSR_F16 && dtype != NSR_F32) return fail(NSR_ERR_UNSUPPORTED, "%s: dtype must be F16 or F32", what);
+  if (Hq < 0 || Hk < 0 || Dh <= 0 || Dh % 2 != 0 || rot < 0 || rot % 2 != 0 || rot > Dh)
+    return fail(NSR_ERR_BAD_ARG, "%s: need even head_dim > 0 and even rotary_dim <= head_dim", what);
+  if (pos < 0 || L <= 0 || pos >= L) return fail(NSR_ERR_BAD_ARG, "%s: pos %lld outside the cache of %lld", what,
+                                                 (long long)pos, (long long)L);
+  if (Hq > 0x7fff || Hk > 0x7fff || Dh > 0x7fff) return fail(NSR_ERR_UNSUPPORTED, "%s: too many heads", what);
+  const uintptr_t al = dtype == NSR_F16 ? 4 : 8;
+  const int half = rot / 2;
+  const bool use_k = k_required && Hk > 0;  // kv_cache_append passes no k
+  const bool need_q = Hq > 0 && half > 0;
+  if ((need_q && (!q || !aligned(q, al))) || (use_k && (!k || !aligned(k, al) || !cache_k || !aligned(cache_k, al))))
+    return fail(NSR_ERR_BAD_ARG, "%s: null or misaligned q/k/cache_k", what);
+  if ((v == nullptr) != (cache_v == nullptr)) return fail(NSR_ERR_BAD_ARG, "%s: v and cache_v go together", what);
+  if (v && (!aligned(v, al) || !aligned(cache_v, al))) return fail(NSR_ERR_BAD_ARG, "%s: misaligned v/cache_v", what);
+  if (half > 0 && (!table || table_rows <= pos || !aligned(table, 4)))
+    return fail(NSR_ERR_BAD_ARG, "%s: RoPE table needs more than pos = %lld rows", what, (long long)pos);
+  nsr_rope_cache_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.table = table;
+  a.cache_k = cache_k;
+  a.cache_v = cache_v;
+  a.pos = pos;
+  a.max_kv_len = L;
+  a.Dh = (int32_t)Dh;
+  a.half = half;
+  a.nq = need_q ? (int32_t)(Hq * half) : 0;
+  a.nk = use_k ? (int32_t)(Hk * half) : 0;
+  a.nkp = use_k ? (int32_t)(Hk * (Dh - rot) / 2) : 0;
+  a.nv = v ? (int32_t)(Hk * Dh / 2) : 0;
+  const int64_t total = (int64_t)a.nq + a.nk + a.nkp + a.nv;
+  if (total == 0) return NSR_OK;
+  void* params[] = {&a};
+  return launch(dtype == NSR_F16 ? "nsrk_rope_cache_f16" : "nsrk_rope_cache_f32", cdiv_u(total, 256), 1, 256, 0,
+                stream, params);
+}
+
+nsr_status nsr_rope_qk_cache_append(void* q, void* k, const void* v, nsr_dtype dtype, const float* rope_table,
+                                    int64_t table_rows, void* cache_k, void* cache_v, int64_t n_q_heads,
+                                    int64_t n_kv_heads, int64_t head_dim, int rotary_dim, int64_t pos,
+                                    int64_t max_kv_len, nsr_stream_t stream) {
+  return rope_cache_launch(q, k, v, dtype, rope_table, table_rows, cache_k, cache_v, n_q_heads, n_kv_heads,
+                           head_dim, rotary_dim, pos, max_kv_len, true, stream, "rope_qk_cache_append");
+}
+
+nsr_status nsr_kv_cache_append(const void* new_kv, void* cache, nsr_dtype dtype, int64_t n_kv_heads,
+                               int64_t head_dim, int64_t max_kv_len, int64_t pos, nsr_stream_t stream) {
+  if (!new_kv || !cache) return fail(NSR_ERR_BAD_ARG, "kv_cache_append: null pointer");
+  return rope_cache_launch(nullptr, nullptr, new_kv, dtype, nullptr, 0, nullptr, cache, 0, n_kv_heads, head_dim, 0,
+                           pos, max_kv_len, false, stream, "kv_cache_append");
+}
+
 // -------------------------------------------------------- AdaIN + Snake --
 
 nsr_status nsr_adain_snake_f32(const float* x, const void* gamma, const void* beta, const void* alpha,

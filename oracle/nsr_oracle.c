@@ -89,6 +89,34 @@ static uint16_t f64_to_bf16(double d) {
   return f32_to_bf16(f);
 }
 
+/* f32 -> IEEE binary16, round to nearest even (half crate f16::from_f32;
+ * Triton's .to(tl.float16)); overflow to inf, NaN kept quiet. */
+static uint16_t f32_to_f16(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t ax = x & 0x7fffffffu;
+  if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((ax >> 13) & 0x3ffu));
+  if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* rounds to >= 65520: inf */
+  if (ax < 0x38800000u) {                                  /* |f| < 2^-14: subnormal or zero */
+    if (ax < 0x33000000u) return (uint16_t)sign;           /* < 2^-25: rounds to 0 */
+    const uint32_t e = ax >> 23, m = (ax & 0x7fffffu) | 0x800000u;
+    const uint32_t shift = 126u - e;                       /* 14 - (e - 127) + 13 - 1 ... */
+    uint32_t h = m >> shift;
+    const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (h & 1u))) ++h;
+    return (uint16_t)(sign | h);
+  }
+  uint32_t h = ((ax >> 13) - (112u << 10));
+  const uint32_t rem = ax & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
+  return (uint16_t)(sign | h);
+}
+
+ORC_API void orc_f32_to_f16(const float* x, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = f32_to_f16(x[i]);
+}
+
 ORC_API void orc_f16_to_f32(const uint16_t* h, float* out, int64_t n) {
   for (int64_t i = 0; i < n; ++i) out[i] = f16_to_f32(h[i]);
 }
@@ -379,5 +407,41 @@ ORC_API void orc_adain_snake_f32(const float* x, const float* gamma, const float
       const float sin_sq = s * s;
       orow[t] = y + sin_sq * inv_a;
     }
+  }
+}
+
+/* ------------------------------------------- decode-step RoPE + KV cache --- */
+
+/* rope_qk_cache_fused (kernels/moonshine_kernels.py:1372-1454, dispatched by
+ * enc_rope_qk_cache_fused src/triton_kernels.rs:975) followed by
+ * kv_cache_append of v (:865-883, enc_kv_cache_append :993), one decode
+ * position, f16 tensors:
+ *   q [Hq, Dh], k [Hk, Dh] rotated in place on dims < rot (interleaved pairs,
+ *   cos/sin = table[pos][i], table[pos][half + i]); each rotated value is
+ *   f16(x0 * c - x1 * s) / f16(x1 * c + x0 * s) with f32 products;
+ *   cache_k[h, pos, :] = rotated k row (pass-through dims copied);
+ *   cache_v[h, pos, :] = v row (when v and cache_v are given).
+ * Caches are [Hk, max_kv_len, Dh]. */
+ORC_API void orc_rope_qk_cache_f16(uint16_t* q, uint16_t* k, const uint16_t* v, const float* table, int64_t Hq,
+                                   int64_t Hk, int64_t Dh, int rot, int64_t pos, int64_t max_kv_len,
+                                   uint16_t* cache_k, uint16_t* cache_v) {
+  const int half = rot / 2;
+  const float* cs = table + pos * 2 * half;
+  for (int64_t pass = 0; pass < 2; ++pass) {
+    uint16_t* x = pass == 0 ? q : k;
+    const int64_t H = pass == 0 ? Hq : Hk;
+    for (int64_t h = 0; h < H; ++h) {
+      for (int i = 0; i < half; ++i) {
+        const float c = cs[i], sn = cs[half + i];
+        const float x0 = f16_to_f32(x[h * Dh + 2 * i]), x1 = f16_to_f32(x[h * Dh + 2 * i + 1]);
+        const float p0 = x0 * c, q0 = x1 * sn, p1 = x1 * c, q1 = x0 * sn;
+        x[h * Dh + 2 * i] = f32_to_f16(p0 - q0);
+        x[h * Dh + 2 * i + 1] = f32_to_f16(p1 + q1);
+      }
+    }
+  }
+  for (int64_t h = 0; h < Hk; ++h) {
+    memcpy(cache_k + (h * max_kv_len + pos) * Dh, k + h * Dh, (size_t)Dh * 2);
+    if (v && cache_v) memcpy(cache_v + (h * max_kv_len + pos) * Dh, v + h * Dh, (size_t)Dh * 2);
   }
 }

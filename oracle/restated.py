@@ -27,6 +27,9 @@ def lib() -> C.CDLL:
             raise FileNotFoundError(f"{_LIB_PATH} missing: run python -m nspeech_amd.build (or oracle/build.py)")
         L = C.CDLL(str(_LIB_PATH))
         L.orc_f16_to_f32.argtypes = [_u16p, _f32p, _I64]
+        L.orc_f32_to_f16.argtypes = [_f32p, _u16p, _I64]
+        L.orc_rope_qk_cache_f16.argtypes = [_u16p, _u16p, C.c_void_p, _f32p, _I64, _I64, _I64, C.c_int, _I64, _I64,
+                                            _u16p, C.c_void_p]
         L.orc_f32_to_bf16.argtypes = [_f32p, _u16p, _I64]
         L.orc_bf16_to_f32.argtypes = [_u16p, _f32p, _I64]
         L.orc_q8_0_dequantize.argtypes = [_u8p, _I64, _I64, _f32p]
@@ -204,3 +207,29 @@ def adain_snake(x, gamma, beta, alpha, eps=1e-5, nthreads=1):
     lib().orc_adain_snake_f32(x.ravel(), gamma.ravel(), beta.ravel(), _c(alpha, np.float32).ravel(), out.ravel(),
                               B, Cc, T, gs, bs, eps, nthreads)
     return out
+
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    """f32 -> IEEE half bits, round to nearest even (orc_f32_to_f16)."""
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_f16(x.ravel(), out.ravel(), x.size)
+    return out
+
+
+def rope_qk_cache_f16(q_bits, k_bits, v_bits, table, pos, rot, cache_k_bits, cache_v_bits=None):
+    """Decode-step RoPE(q, k) + K (and V) cache append on f16 bit patterns
+    (orc_rope_qk_cache_f16). q [Hq, Dh], k/v [Hk, Dh], caches [Hk, L, Dh];
+    returns (q, k, cache_k, cache_v) as new arrays."""
+    q = _c(q_bits, np.uint16).copy()
+    k = _c(k_bits, np.uint16).copy()
+    ck = _c(cache_k_bits, np.uint16).copy()
+    cv = None if cache_v_bits is None else _c(cache_v_bits, np.uint16).copy()
+    v = None if v_bits is None else _c(v_bits, np.uint16)
+    Hq, Dh = q.shape
+    Hk = k.shape[0]
+    L = ck.shape[1]
+    t = _c(table, np.float32)
+    lib().orc_rope_qk_cache_f16(q.ravel(), k.ravel(), _ptr(v), t.ravel(), Hq, Hk, Dh, rot, pos, L, ck.ravel(),
+                                _ptr(cv))
+    return q, k, ck, cv

@@ -76,6 +76,17 @@ def test_version_and_header_is_plain_c():
     lambda L: L.nsr_activation(16, 16, 5, 100, 1, NULL),
     lambda L: L.nsr_glu_silu(NULL, 16, 0, 100, NULL),
     lambda L: L.nsr_residual_add(16, NULL, 16, 0, 100, NULL),
+    # decode RoPE + cache: odd head_dim, rotary_dim > head_dim, pos outside the cache, bf16, v without cache_v,
+    # misaligned f16 q, table too short
+    lambda L: L.nsr_rope_qk_cache_append(16, 16, NULL, 1, 16, 8, 16, NULL, 2, 2, 63, 32, 0, 8, NULL),
+    lambda L: L.nsr_rope_qk_cache_append(16, 16, NULL, 1, 16, 8, 16, NULL, 2, 2, 64, 66, 0, 8, NULL),
+    lambda L: L.nsr_rope_qk_cache_append(16, 16, NULL, 1, 16, 8, 16, NULL, 2, 2, 64, 32, 8, 8, NULL),
+    lambda L: L.nsr_rope_qk_cache_append(16, 16, NULL, 2, 16, 8, 16, NULL, 2, 2, 64, 32, 0, 8, NULL),
+    lambda L: L.nsr_rope_qk_cache_append(16, 16, 16, 1, 16, 8, 16, NULL, 2, 2, 64, 32, 0, 8, NULL),
+    lambda L: L.nsr_rope_qk_cache_append(18, 16, NULL, 1, 16, 8, 16, NULL, 2, 2, 64, 32, 0, 8, NULL),
+    lambda L: L.nsr_rope_qk_cache_append(16, 16, NULL, 1, 16, 3, 16, NULL, 2, 2, 64, 32, 5, 8, NULL),
+    lambda L: L.nsr_kv_cache_append(NULL, 16, 1, 2, 64, 8, 0, NULL),
+    lambda L: L.nsr_kv_cache_append(16, 16, 1, 2, 64, 8, -1, NULL),
 ])
 def test_invalid_arguments_are_rejected_before_any_launch(call):
     L = abi.lib()
@@ -89,6 +100,7 @@ def test_empty_inputs_are_no_ops():
     assert L.nsr_layernorm(16, 0, NULL, NULL, 0, 16, 0, 0, 8, 8, 8, C.c_float(1e-5), 0, 0, NULL) == abi.NSR_OK
     assert L.nsr_q8_0_embed_gather(16, 100, 64, 16, 0, 0, 16, 0, NULL, NULL) == abi.NSR_OK
     assert L.nsr_activation(16, 16, 0, 0, 1, NULL) == abi.NSR_OK
+    assert L.nsr_kv_cache_append(16, 16, 1, 0, 64, 8, 0, NULL) == abi.NSR_OK
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU error path")

@@ -285,3 +285,50 @@ def test_golden_fixtures_reproduce():
         fresh = make_golden.compute(name, case)
         for key, val in fresh.items():
             assert_bitexact(val, case[key], f"golden {name}:{key}")
+
+
+# ------------------------------------------------- decode RoPE + cache ---
+
+def test_f32_to_f16_rounding_matches_numpy():
+    g = configs.rng(31)
+    x = np.concatenate([g.standard_normal(100000).astype(np.float32) * 300,
+                        g.standard_normal(100000).astype(np.float32) * 1e-5,
+                        np.array([65504, 65519, 65520, 6e-8, 2.9802322e-08, -0.0, np.inf, -np.inf], np.float32)])
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    assert_bitexact(R.f32_to_f16_bits(x), ref, "f32 -> f16 RNE")
+
+
+def test_rope_qk_cache_f16_against_f64_rotation_and_copies():
+    """rope_qk_cache_fused + kv_cache_append restated: each rotated value is
+    the f16 rounding of its f32 expression, which lies within half an f16
+    ulp (plus f32 rounding) of the f64 rotation; the caches hold exact
+    copies of the rotated k and of v at row pos, nothing else changes."""
+    g = configs.rng(32)
+    Hq, Hk, Dh, rot, L, pos = 10, 4, 64, 32, 50, 37
+    q = g.standard_normal((Hq, Dh)).astype(np.float16).view(np.uint16)
+    k = g.standard_normal((Hk, Dh)).astype(np.float16).view(np.uint16)
+    v = g.standard_normal((Hk, Dh)).astype(np.float16).view(np.uint16)
+    ck0 = g.standard_normal((Hk, L, Dh)).astype(np.float16).view(np.uint16)
+    cv0 = g.standard_normal((Hk, L, Dh)).astype(np.float16).view(np.uint16)
+    tab = R.rope_table(64, rot, 1e4)
+    qo, ko, ck, cv = R.rope_qk_cache_f16(q, k, v, tab, pos, rot, ck0, cv0)
+    ang = tab[pos, :rot // 2].astype(np.float64), tab[pos, rot // 2:].astype(np.float64)
+    for x_in, x_out in ((q, qo), (k, ko)):
+        xi = x_in.view(np.float16).astype(np.float64)
+        xo = x_out.view(np.float16).astype(np.float64)
+        c, s = ang
+        e0 = xi[:, 0:rot:2] * c - xi[:, 1:rot:2] * s
+        e1 = xi[:, 1:rot:2] * c + xi[:, 0:rot:2] * s
+        for got, exp in ((xo[:, 0:rot:2], e0), (xo[:, 1:rot:2], e1)):
+            assert np.all(np.abs(got - exp) <= np.abs(exp) * 2.0 ** -11 * 1.01 + 2.0 ** -24 * 4)
+        assert_bitexact(x_out[:, rot:], x_in[:, rot:], "pass-through dims untouched")
+    assert_bitexact(ck[:, pos], ko, "k cache row = rotated k")
+    assert_bitexact(cv[:, pos], v, "v cache row = v")
+    others = np.arange(L) != pos
+    assert_bitexact(ck[:, others], ck0[:, others], "other k cache rows")
+    assert_bitexact(cv[:, others], cv0[:, others], "other v cache rows")
+    # position 0: cos = 1, sin = 0 -> identity
+    q0, k0, _, _ = R.rope_qk_cache_f16(q, k, None, tab, 0, rot, ck0)
+    assert_bitexact(q0, q, "pos 0 identity q")
+    assert_bitexact(k0, k, "pos 0 identity k")
