@@ -248,6 +248,51 @@ nsr_status nsr_glu_silu(const void* fc1, void* out, nsr_dtype dtype, int64_t n,
 nsr_status nsr_residual_add(const void* x, const void* res, void* out,
                             nsr_dtype dtype, int64_t n, nsr_stream_t stream);
 
+/* ---- Repacked-Q8 GEMV (decoder projections at M = 1) ---------------------- */
+
+/* Weights W [K, NW] in the repacked Q8 layout of the reference's decoder
+ * kernels: qs u32 [K, NW/4] with the int8 weight of column c in byte c % 4
+ * (lowest byte first) of word c / 4, and scales f16 [K/32, NW], one per
+ * 32-row block and column: W[k, c] = int8 * f32(scale[k / 32, c]). x [K] is
+ * F16 or F32. Accumulation is f32; the sum is split over K across the GPU
+ * and the partial sums are added in a fixed order, so results do not depend
+ * on timing. Split-K scratch is owned by the library, one buffer per
+ * (device, stream): the first call on a stream allocates it (and may
+ * synchronise the device); calls on the same stream are ordered, and calls
+ * on different streams do not share it.
+ * Requirements: K % 32 == 0 and K > 0, N % 16 == 0, qs and scales 16-byte
+ * aligned. N == 0 is a no-op. */
+
+/* out[N] = x @ W (+ bias[N] f32 when bias != NULL); out F16 or F32.
+ * Replaces gemv_q8 / gemv_q8_bias (kernels/moonshine_kernels.py:616-644,
+ * 647-677). */
+nsr_status nsr_gemv_q8(const void* x, nsr_dtype x_dtype, const uint32_t* qs,
+                       const uint16_t* scales, const float* bias, void* out,
+                       nsr_dtype out_dtype, int64_t K, int64_t N,
+                       nsr_stream_t stream);
+
+/* W is [K, 2N]: x-half in columns [0, N), gate-half in [N, 2N); bias [2N]
+ * f32 or NULL. out[i] = silu(x@Wg[i] + bg[i]) * (x@Wx[i] + bx[i]), i < N.
+ * Replaces gemv_q8_bias_glu (kernels/moonshine_kernels.py:1721-1772), the
+ * fused fc1 + GLU of DecoderMLP::forward (src/moonshine/decoder.rs:403-411). */
+nsr_status nsr_gemv_q8_bias_glu(const void* x, nsr_dtype x_dtype, const uint32_t* qs,
+                                const uint16_t* scales, const float* bias, void* out,
+                                nsr_dtype out_dtype, int64_t K, int64_t N,
+                                nsr_stream_t stream);
+
+/* proj = f16-rounded x @ W (W [K, dim]); out_f32 = proj + residual (f32;
+ * out_f32 may be residual itself); norm = (out_f32 - mean) / sqrt(var + eps)
+ * * ln_weight (biased variance over dim; ln_weight F16 or F32; norm F16 or
+ * F32). Replaces gemv_q8_resadd_ln (kernels/moonshine_kernels.py:1775-1819),
+ * the fused out-projection + residual + next LayerNorm of the decoder step
+ * (triton_residual_add_layernorm src/triton_kernels.rs:742 after the
+ * projection). */
+nsr_status nsr_gemv_q8_resadd_ln(const void* x, nsr_dtype x_dtype, const uint32_t* qs,
+                                 const uint16_t* scales, const float* residual,
+                                 float* out_f32, const void* ln_weight, nsr_dtype w_dtype,
+                                 void* norm, nsr_dtype norm_dtype, int64_t K, int64_t dim,
+                                 float eps, nsr_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -65,10 +65,15 @@ def lib() -> C.CDLL:
         L.nsr_activation.argtypes = [_P, _P, C.c_int, _I64, C.c_int, _P]
         L.nsr_glu_silu.argtypes = [_P, _P, C.c_int, _I64, _P]
         L.nsr_residual_add.argtypes = [_P, _P, _P, C.c_int, _I64, _P]
+        L.nsr_gemv_q8.argtypes = [_P, C.c_int, _P, _P, _P, _P, C.c_int, _I64, _I64, _P]
+        L.nsr_gemv_q8_bias_glu.argtypes = [_P, C.c_int, _P, _P, _P, _P, C.c_int, _I64, _I64, _P]
+        L.nsr_gemv_q8_resadd_ln.argtypes = [_P, C.c_int, _P, _P, _P, _P, _P, C.c_int, _P, C.c_int, _I64, _I64,
+                                            C.c_float, _P]
         for name in ("nsr_init", "nsr_layernorm", "nsr_residual_add_layernorm", "nsr_rope_table_f32",
                      "nsr_rope_qk_cache_append", "nsr_kv_cache_append",
                      "nsr_rotary_partial_interleaved_f32", "nsr_adain_snake_f32", "nsr_q8_0_embed_gather",
-                     "nsr_activation", "nsr_glu_silu", "nsr_residual_add"):
+                     "nsr_activation", "nsr_glu_silu", "nsr_residual_add", "nsr_gemv_q8",
+                     "nsr_gemv_q8_bias_glu", "nsr_gemv_q8_resadd_ln"):
             getattr(L, name).restype = C.c_int
         _lib = L
     return _lib
@@ -233,3 +238,49 @@ def residual_add(x, res, *, out=None, stream=None):
         out = torch.empty_like(x)
     check(lib().nsr_residual_add(_ptr(x), _ptr(res), _ptr(out), _dt(x), x.numel(), _stream(stream)))
     return out
+
+
+def _q8_shape(qs, scales):
+    """K and weight columns of a repacked Q8 weight: qs int32/uint32 [K, NW/4],
+    scales f16 [K/32, NW]."""
+    if qs.dim() != 2 or scales.dim() != 2 or scales.dtype != torch.float16:
+        raise ValueError("qs must be [K, NW/4] 32-bit words and scales [K/32, NW] f16")
+    K, nw = qs.shape[0], 4 * qs.shape[1]
+    if scales.shape[1] != nw or scales.shape[0] * 32 != K:
+        raise ValueError(f"scales {tuple(scales.shape)} do not match qs {tuple(qs.shape)}")
+    return K, nw
+
+
+def gemv_q8(x, qs, scales, bias=None, *, out=None, out_dtype=torch.float16, stream=None):
+    """out[N] = x[K] @ dequant(W) (+ bias); W in the repacked Q8 layout."""
+    K, N = _q8_shape(qs, scales)
+    if out is None:
+        out = torch.empty(N, dtype=out_dtype, device=x.device)
+    check(lib().nsr_gemv_q8(_ptr(x), _dt(x), _ptr(qs), _ptr(scales), _ptr(bias), _ptr(out), _dt(out), K, N,
+                            _stream(stream)))
+    return out
+
+
+def gemv_q8_bias_glu(x, qs, scales, bias=None, *, out=None, out_dtype=torch.float16, stream=None):
+    """out[N] = silu(x @ Wg + bg) * (x @ Wx + bx); W [K, 2N]: x half, then gate half."""
+    K, nw = _q8_shape(qs, scales)
+    N = nw // 2
+    if out is None:
+        out = torch.empty(N, dtype=out_dtype, device=x.device)
+    check(lib().nsr_gemv_q8_bias_glu(_ptr(x), _dt(x), _ptr(qs), _ptr(scales), _ptr(bias), _ptr(out), _dt(out), K,
+                                     N, _stream(stream)))
+    return out
+
+
+def gemv_q8_resadd_ln(x, qs, scales, residual, ln_weight, *, eps=1e-5, out_f32=None, norm=None,
+                      norm_dtype=torch.float16, stream=None):
+    """h = f16(x @ W) + residual (f32), norm = LN(h) * ln_weight. Returns (h, norm)."""
+    K, dim = _q8_shape(qs, scales)
+    if out_f32 is None:
+        out_f32 = torch.empty(dim, dtype=torch.float32, device=x.device)
+    if norm is None:
+        norm = torch.empty(dim, dtype=norm_dtype, device=x.device)
+    check(lib().nsr_gemv_q8_resadd_ln(_ptr(x), _dt(x), _ptr(qs), _ptr(scales), _ptr(residual), _ptr(out_f32),
+                                      _ptr(ln_weight), _dt(ln_weight), _ptr(norm), _dt(norm), K, dim, eps,
+                                      _stream(stream)))
+    return out_f32, norm

@@ -90,6 +90,27 @@ typedef struct nsr_adain_args {
   float inv_t;             /* 1 / T */
 } nsr_adain_args;
 
+typedef struct nsr_gemv_args {
+  const void* x;           /* [K], f16 or f32 */
+  const uint32_t* qs;      /* [K, NW/4] packed int8, column c in byte c % 4 of word c / 4 */
+  const uint16_t* scales;  /* [K/32, NW] f16 */
+  const float* bias;       /* [NW] or NULL */
+  void* out;               /* [N] (modes 0, 1) or the f16/f32 norm output (mode 2) */
+  const float* residual;   /* [N] (mode 2) */
+  float* out_f32;          /* [N] residual + projection (mode 2) */
+  const void* ln_w;        /* [N] layernorm weight (mode 2) */
+  float* partial;          /* [S, NW] split-K partial sums (S > 1) */
+  uint32_t* counters;      /* [tiles] (modes 0, 1) or [1] (mode 2); zero between calls */
+  int32_t K;
+  int32_t NW;              /* weight columns: N, or 2N for the GLU form */
+  int32_t N;               /* output columns */
+  int32_t S;               /* K chunks (grid.y) */
+  int32_t kc;              /* rows per K chunk, multiple of 32 */
+  int32_t ln_w_f16;        /* mode 2: 1 = f16 weight, 0 = f32 */
+  float eps;
+  int32_t pad_;
+} nsr_gemv_args;
+
 typedef struct nsr_ew_args {
   const void* a;
   const void* b;

@@ -18,5 +18,6 @@ NSR_EMBED(layernorm)
 NSR_EMBED(rotary)
 NSR_EMBED(adain_snake)
 NSR_EMBED(elementwise)
+NSR_EMBED(gemv_q8)
 
     .section .note.GNU-stack, "", @progbits

@@ -12,10 +12,12 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -28,6 +30,7 @@ extern "C" const unsigned char nsr_co_layernorm[];
 extern "C" const unsigned char nsr_co_rotary[];
 extern "C" const unsigned char nsr_co_adain_snake[];
 extern "C" const unsigned char nsr_co_elementwise[];
+extern "C" const unsigned char nsr_co_gemv_q8[];
 
 namespace {
 
@@ -39,7 +42,8 @@ const Unit kUnits[] = {{"q8_0_gather", nsr_co_q8_0_gather},
                        {"layernorm", nsr_co_layernorm},
                        {"rotary", nsr_co_rotary},
                        {"adain_snake", nsr_co_adain_snake},
-                       {"elementwise", nsr_co_elementwise}};
+                       {"elementwise", nsr_co_elementwise},
+                       {"gemv_q8", nsr_co_gemv_q8}};
 constexpr int kNumUnits = sizeof(kUnits) / sizeof(kUnits[0]);
 
 constexpr int kMaxDevices = 64;
@@ -130,7 +134,7 @@ int unit_of(const std::string& name) {
   };
   static const P map[] = {{"nsrk_q8_0_", 0}, {"nsrk_ln_", 1},    {"nsrk_resln_", 1}, {"nsrk_rope_", 2},
                           {"nsrk_adain_", 3}, {"nsrk_silu_", 4}, {"nsrk_gelu_", 4},  {"nsrk_glu_", 4},
-                          {"nsrk_add_", 4}};
+                          {"nsrk_add_", 4},  {"nsrk_gemv_", 5}};
   for (const P& p : map)
     if (name.compare(0, std::strlen(p.prefix), p.prefix) == 0) return p.unit;
   return -1;
@@ -211,7 +215,9 @@ int nsr_kernel_count(void) {
                                 "nsrk_resln_bf16_nc2",       "nsrk_rope_table_f32",
                                 "nsrk_rope_compute_f32",     "nsrk_adain_row_b256_v5_l0",
                                 "nsrk_adain_row_b512_v44_l14", "nsrk_adain_stats",
-                                "nsrk_adain_apply",          "nsrk_gelu_f32_v"};
+                                "nsrk_adain_apply",          "nsrk_gelu_f32_v",
+                                "nsrk_gemv_q8_f16_f16",      "nsrk_gemv_q8_glu_f16_f16",
+                                "nsrk_gemv_q8_resln_f16_f16"};
   int n = 0;
   for (const char* p : probe) {
     hipFunction_t f;
@@ -674,6 +680,156 @@ nsr_status nsr_residual_add(const void* x, const void* res, void* out, nsr_dtype
   a.out = out;
   a.n = n;
   return ew_launch("add", dtype, a, aligned(x, 16) && aligned(res, 16) && aligned(out, 16), stream);
+}
+
+}  // extern "C"
+
+// ----------------------------------------------------------- Q8 GEMV --
+
+namespace {
+
+// Split-K scratch of one (device, stream): f32 partial sums [S, NW] and the
+// per-tile arrival counters, which every launch leaves at zero.
+struct GemvScratch {
+  float* partial = nullptr;
+  size_t partial_cap = 0;  // floats
+  uint32_t* counters = nullptr;
+  size_t counter_cap = 0;  // u32
+};
+std::mutex g_gemv_mu;
+std::map<std::pair<int, void*>, GemvScratch> g_gemv_scratch;
+
+nsr_status gemv_scratch(nsr_stream_t stream, size_t n_partial, size_t n_counters, GemvScratch* out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(NSR_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  std::lock_guard<std::mutex> lk(g_gemv_mu);
+  GemvScratch& sc = g_gemv_scratch[{dev, stream}];
+  if (sc.partial_cap < n_partial || sc.counter_cap < n_counters) {
+    // Work already queued on this stream may still use the old buffers.
+    e = hipStreamSynchronize((hipStream_t)stream);
+    if (e != hipSuccess) return fail(NSR_ERR_HIP, "gemv scratch: hipStreamSynchronize: %s", hipGetErrorString(e));
+    const size_t np = std::max({n_partial, sc.partial_cap, (size_t)1 << 20});
+    const size_t nc = std::max({n_counters, sc.counter_cap, (size_t)4096});
+    if (sc.partial) (void)hipFree(sc.partial);
+    if (sc.counters) (void)hipFree(sc.counters);
+    sc = GemvScratch();
+    float* p = nullptr;
+    uint32_t* c = nullptr;
+    e = hipMalloc((void**)&p, np * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void**)&c, nc * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(c, 0, nc * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+      if (p) (void)hipFree(p);
+      if (c) (void)hipFree(c);
+      (void)hipGetLastError();
+      return fail(NSR_ERR_HIP, "gemv scratch allocation (%zu floats): %s", np, hipGetErrorString(e));
+    }
+    sc.partial = p;
+    sc.partial_cap = np;
+    sc.counters = c;
+    sc.counter_cap = nc;
+  }
+  *out = sc;
+  return NSR_OK;
+}
+
+enum GemvMode { kGemvPlain = 0, kGemvGlu = 1, kGemvResLn = 2 };
+
+// Workgroups a launch aims for: ~2 per CU keeps every CU's load queue busy
+// at M = 1 without making the partial sums outweigh the weights.
+constexpr int64_t kGemvTargetGroups = 512;
+
+nsr_status gemv_launch(GemvMode mode, const void* x, nsr_dtype xd, const uint32_t* qs, const uint16_t* scales,
+                       const float* bias, void* out, nsr_dtype od, const float* residual, float* out_f32,
+                       const void* ln_w, nsr_dtype wd, int64_t K, int64_t N, float eps, nsr_stream_t stream,
+                       const char* what) {
+  if (!x || !qs || !scales || !out || (mode == kGemvResLn && (!residual || !out_f32 || !ln_w)))
+    return fail(NSR_ERR_BAD_ARG, "%s: null pointer", what);
+  if ((xd != NSR_F16 && xd != NSR_F32) || (od != NSR_F16 && od != NSR_F32))
+    return fail(xd == NSR_BF16 || od == NSR_BF16 ? NSR_ERR_UNSUPPORTED : NSR_ERR_BAD_ARG,
+                "%s: x and output dtypes must be F16 or F32", what);
+  if (mode == kGemvResLn && wd != NSR_F16 && wd != NSR_F32)
+    return fail(NSR_ERR_BAD_ARG, "%s: ln_weight dtype must be F16 or F32", what);
+  if (K < 0 || N < 0 || K > (1LL << 30) || N > (1LL << 28))
+    return fail(NSR_ERR_BAD_ARG, "%s: bad shape K=%lld N=%lld", what, (long long)K, (long long)N);
+  if (K % 32 != 0) return fail(NSR_ERR_BAD_ARG, "%s: K=%lld must be a multiple of 32", what, (long long)K);
+  if (N % 16 != 0) return fail(NSR_ERR_BAD_ARG, "%s: N=%lld must be a multiple of 16", what, (long long)N);
+  if (!aligned(qs, 16) || !aligned(scales, 16)) return fail(NSR_ERR_BAD_ARG, "%s: qs and scales need 16-byte alignment", what);
+  if (!aligned(x, dt_size(xd)) || !aligned(out, dt_size(od)) || (bias && !aligned(bias, 4)) ||
+      (residual && !aligned(residual, 4)) || (out_f32 && !aligned(out_f32, 4)) ||
+      (ln_w && !aligned(ln_w, dt_size(wd))))
+    return fail(NSR_ERR_BAD_ARG, "%s: misaligned pointer", what);
+  if (!(eps >= 0.0f)) return fail(NSR_ERR_BAD_ARG, "%s: eps must be >= 0", what);
+  if (N == 0) return NSR_OK;
+  if (K == 0) return fail(NSR_ERR_BAD_ARG, "%s: K must be > 0", what);
+
+  const int64_t NW = mode == kGemvGlu ? 2 * N : N;
+  const int64_t tiles = mode == kGemvGlu ? (N + 127) / 128 : (NW + 255) / 256;
+  const int64_t blocks = K / 32;
+  int64_t S = kGemvTargetGroups / tiles;
+  if (S < 1) S = 1;
+  if (S > blocks) S = blocks;
+  const int64_t bpc = (blocks + S - 1) / S;
+  S = (blocks + bpc - 1) / bpc;
+  if (tiles > 0x7fffffffLL || S > 65535) return fail(NSR_ERR_UNSUPPORTED, "%s: grid too large", what);
+
+  nsr_gemv_args a;
+  std::memset(&a, 0, sizeof(a));
+  const bool need_scratch = S > 1 || (mode == kGemvResLn && tiles > 1);
+  if (need_scratch) {
+    GemvScratch sc;
+    nsr_status st = gemv_scratch(stream, S > 1 ? (size_t)(S * NW) : 0, (size_t)tiles + 1, &sc);
+    if (st != NSR_OK) return st;
+    a.partial = sc.partial;
+    a.counters = sc.counters;
+  }
+  a.x = x;
+  a.qs = qs;
+  a.scales = scales;
+  a.bias = bias;
+  a.out = out;
+  a.residual = residual;
+  a.out_f32 = out_f32;
+  a.ln_w = ln_w;
+  a.K = (int32_t)K;
+  a.NW = (int32_t)NW;
+  a.N = (int32_t)N;
+  a.S = (int32_t)S;
+  a.kc = (int32_t)(bpc * 32);
+  a.ln_w_f16 = wd == NSR_F16 ? 1 : 0;
+  a.eps = eps;
+  static const char* kind[] = {"nsrk_gemv_q8_", "nsrk_gemv_q8_glu_", "nsrk_gemv_q8_resln_"};
+  const std::string name = std::string(kind[mode]) + dt_name(xd) + "_" + dt_name(od);
+  void* params[] = {&a};
+  return launch(name, (unsigned)tiles, (unsigned)S, 256, 0, stream, params);
+}
+
+}  // namespace
+
+extern "C" {
+
+nsr_status nsr_gemv_q8(const void* x, nsr_dtype x_dtype, const uint32_t* qs, const uint16_t* scales,
+                       const float* bias, void* out, nsr_dtype out_dtype, int64_t K, int64_t N,
+                       nsr_stream_t stream) {
+  return gemv_launch(kGemvPlain, x, x_dtype, qs, scales, bias, out, out_dtype, nullptr, nullptr, nullptr,
+                     NSR_F32, K, N, 0.0f, stream, "gemv_q8");
+}
+
+nsr_status nsr_gemv_q8_bias_glu(const void* x, nsr_dtype x_dtype, const uint32_t* qs, const uint16_t* scales,
+                                const float* bias, void* out, nsr_dtype out_dtype, int64_t K, int64_t N,
+                                nsr_stream_t stream) {
+  return gemv_launch(kGemvGlu, x, x_dtype, qs, scales, bias, out, out_dtype, nullptr, nullptr, nullptr,
+                     NSR_F32, K, N, 0.0f, stream, "gemv_q8_bias_glu");
+}
+
+nsr_status nsr_gemv_q8_resadd_ln(const void* x, nsr_dtype x_dtype, const uint32_t* qs, const uint16_t* scales,
+                                 const float* residual, float* out_f32, const void* ln_weight, nsr_dtype w_dtype,
+                                 void* norm, nsr_dtype norm_dtype, int64_t K, int64_t dim, float eps,
+                                 nsr_stream_t stream) {
+  return gemv_launch(kGemvResLn, x, x_dtype, qs, scales, nullptr, norm, norm_dtype, residual, out_f32, ln_weight,
+                     w_dtype, K, dim, eps, stream, "gemv_q8_resadd_ln");
 }
 
 }  // extern "C"

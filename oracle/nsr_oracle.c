@@ -22,6 +22,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #ifdef _OPENMP
@@ -444,4 +445,69 @@ ORC_API void orc_rope_qk_cache_f16(uint16_t* q, uint16_t* k, const uint16_t* v, 
     memcpy(cache_k + (h * max_kv_len + pos) * Dh, k + h * Dh, (size_t)Dh * 2);
     if (v && cache_v) memcpy(cache_v + (h * max_kv_len + pos) * Dh, v + h * Dh, (size_t)Dh * 2);
   }
+}
+
+/* ------------------------------------------------------- Q8 GEMV (M = 1) --- */
+
+/* gemv_q8 / gemv_q8_bias / gemv_q8_bias_glu / gemv_q8_resadd_ln
+ * (kernels/moonshine_kernels.py:616-677, 1721-1819), repacked Q8 weights:
+ * qs u32 [K, NW/4], the int8 weight of column c in byte c % 4 of word c / 4;
+ * scales f16 [K/32, NW]. x f32 [K] (f16 inputs widened exactly). For every
+ * column, in k order: acc += (x[k] * q[k, c]) * scale[k / 32, c], in f32.
+ * mode 0: out[c] = acc[c] (+ bias[c] when bias != NULL), NW = N columns.
+ * mode 1 (GLU, NW = 2N): out[c] = silu(acc[N + c] + bias[N + c]) * (acc[c] + bias[c]),
+ *   silu(g) = g * sigmoid(g) in f32 (bias may be NULL).
+ * Outputs are f32 before the kernels' final rounding to the output dtype. */
+ORC_API void orc_gemv_q8_f32(const float* x, const uint32_t* qs, const uint16_t* scales, const float* bias,
+                             float* out, int64_t K, int64_t N, int mode) {
+  const int64_t NW = mode == 1 ? 2 * N : N;
+  float* acc = mode == 1 ? (float*)malloc((size_t)NW * sizeof(float)) : out; /* mode 0 sums in place */
+  for (int64_t c = 0; c < NW; ++c) acc[c] = 0.0f;
+  for (int64_t k = 0; k < K; ++k) {
+    const float xk = x[k];
+    for (int64_t c = 0; c < NW; ++c) {
+      const uint32_t w = qs[k * (NW / 4) + c / 4];
+      const float q = (float)(int8_t)((w >> (8 * (c % 4))) & 0xffu);
+      const float s = f16_to_f32(scales[(k / 32) * NW + c]);
+      acc[c] += (xk * q) * s;
+    }
+  }
+  if (mode == 0) {
+    if (bias) for (int64_t c = 0; c < N; ++c) out[c] = acc[c] + bias[c];
+  } else {
+    for (int64_t c = 0; c < N; ++c) {
+      const float xv = acc[c] + (bias ? bias[c] : 0.0f);
+      const float g = acc[N + c] + (bias ? bias[N + c] : 0.0f);
+      const float sg = g * (1.0f / (1.0f + expf(-g)));
+      out[c] = sg * xv;
+    }
+    free(acc);
+  }
+}
+
+/* gemv_q8_resadd_ln (kernels/moonshine_kernels.py:1775-1819): proj = f16(x @ W),
+ * h = proj + residual (f32, written to out_f32), norm = f16(LN(h) * w) with
+ * mean, centred variance over dim, eps; returns norm as f16 bits. */
+ORC_API void orc_gemv_q8_resadd_ln(const float* x, const uint32_t* qs, const uint16_t* scales,
+                                   const float* residual, const uint16_t* ln_w_f16, float* out_f32,
+                                   uint16_t* norm_f16, int64_t K, int64_t dim, float eps) {
+  float* acc = (float*)malloc((size_t)dim * sizeof(float));
+  orc_gemv_q8_f32(x, qs, scales, NULL, acc, K, dim, 0);
+  /* mode 0 without bias leaves the sums in acc */
+  for (int64_t c = 0; c < dim; ++c) {
+    const float proj = f16_to_f32(f32_to_f16(acc[c]));
+    out_f32[c] = proj + residual[c];
+  }
+  float sum = 0.0f;
+  for (int64_t c = 0; c < dim; ++c) sum += out_f32[c];
+  const float mean = sum / (float)dim;
+  float sq = 0.0f;
+  for (int64_t c = 0; c < dim; ++c) {
+    const float d = out_f32[c] - mean;
+    sq += d * d;
+  }
+  const float inv_std = 1.0f / sqrtf(sq / (float)dim + eps);
+  for (int64_t c = 0; c < dim; ++c)
+    norm_f16[c] = f32_to_f16((out_f32[c] - mean) * inv_std * f16_to_f32(ln_w_f16[c]));
+  free(acc);
 }

@@ -28,6 +28,9 @@ def lib() -> C.CDLL:
         L = C.CDLL(str(_LIB_PATH))
         L.orc_f16_to_f32.argtypes = [_u16p, _f32p, _I64]
         L.orc_f32_to_f16.argtypes = [_f32p, _u16p, _I64]
+        _u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
+        L.orc_gemv_q8_f32.argtypes = [_f32p, _u32p, _u16p, C.c_void_p, _f32p, _I64, _I64, C.c_int]
+        L.orc_gemv_q8_resadd_ln.argtypes = [_f32p, _u32p, _u16p, _f32p, _u16p, _f32p, _u16p, _I64, _I64, C.c_float]
         L.orc_rope_qk_cache_f16.argtypes = [_u16p, _u16p, C.c_void_p, _f32p, _I64, _I64, _I64, C.c_int, _I64, _I64,
                                             _u16p, C.c_void_p]
         L.orc_f32_to_bf16.argtypes = [_f32p, _u16p, _I64]
@@ -233,3 +236,32 @@ def rope_qk_cache_f16(q_bits, k_bits, v_bits, table, pos, rot, cache_k_bits, cac
     lib().orc_rope_qk_cache_f16(q.ravel(), k.ravel(), _ptr(v), t.ravel(), Hq, Hk, Dh, rot, pos, L, ck.ravel(),
                                 _ptr(cv))
     return q, k, ck, cv
+
+
+def gemv_q8(x, qs, scales_bits, bias=None, glu=False):
+    """Q8 GEMV (M = 1) as gemv_q8 / gemv_q8_bias / gemv_q8_bias_glu compute it, f32
+    result before the output rounding. qs u32 [K, NW/4], scales f16 bits [K/32, NW]."""
+    x = _c(x, np.float32)
+    qs = _c(qs, np.uint32)
+    sc = _c(scales_bits, np.uint16)
+    K = x.shape[0]
+    NW = sc.shape[1]
+    N = NW // 2 if glu else NW
+    out = np.empty(N, np.float32)
+    b = None if bias is None else _c(bias, np.float32)
+    lib().orc_gemv_q8_f32(x, qs.ravel(), sc.ravel(), _ptr(b), out, K, N, 1 if glu else 0)
+    return out
+
+
+def gemv_q8_resadd_ln(x, qs, scales_bits, residual, ln_w_bits, eps=1e-5):
+    """gemv_q8_resadd_ln: returns (h f32 [dim], norm f16 bits [dim])."""
+    x = _c(x, np.float32)
+    qs = _c(qs, np.uint32)
+    sc = _c(scales_bits, np.uint16)
+    res = _c(residual, np.float32)
+    w = _c(ln_w_bits, np.uint16)
+    K, dim = x.shape[0], sc.shape[1]
+    h = np.empty(dim, np.float32)
+    norm = np.empty(dim, np.uint16)
+    lib().orc_gemv_q8_resadd_ln(x, qs.ravel(), sc.ravel(), res, w, h, norm, K, dim, eps)
+    return h, norm

@@ -29,7 +29,9 @@ def test_embedded_code_objects_are_gfx950():
     out = subprocess.run(["nm", "-D", "--defined-only", str(abi.LIB_PATH)], capture_output=True, text=True,
                          check=True).stdout
     units = re.findall(r" R nsr_co_([a-z0-9_]+)$", out, flags=re.M)
-    assert sorted(units) == sorted(["q8_0_gather", "layernorm", "rotary", "adain_snake", "elementwise"])
+    from nspeech_amd import build
+
+    assert sorted(units) == sorted(build.UNITS)
     for u in units:
         p = abi.LIB_DIR / f"nsr_{u}_gfx950.hsaco"
         head = p.read_bytes()[:64]
@@ -87,6 +89,17 @@ def test_version_and_header_is_plain_c():
     lambda L: L.nsr_rope_qk_cache_append(16, 16, NULL, 1, 16, 3, 16, NULL, 2, 2, 64, 32, 5, 8, NULL),
     lambda L: L.nsr_kv_cache_append(NULL, 16, 1, 2, 64, 8, 0, NULL),
     lambda L: L.nsr_kv_cache_append(16, 16, 1, 2, 64, 8, -1, NULL),
+    # Q8 GEMV: K not a multiple of 32, N not a multiple of 16, misaligned qs, bf16 output, null x, K == 0,
+    # GLU with misaligned scales, resadd_ln without residual, bf16 LN weight
+    lambda L: L.nsr_gemv_q8(16, 1, 16, 16, NULL, 16, 1, 40, 64, NULL),
+    lambda L: L.nsr_gemv_q8(16, 1, 16, 16, NULL, 16, 1, 64, 40, NULL),
+    lambda L: L.nsr_gemv_q8(16, 1, 24, 16, NULL, 16, 1, 64, 64, NULL),
+    lambda L: L.nsr_gemv_q8(16, 1, 16, 16, NULL, 16, 2, 64, 64, NULL),
+    lambda L: L.nsr_gemv_q8(NULL, 1, 16, 16, NULL, 16, 1, 64, 64, NULL),
+    lambda L: L.nsr_gemv_q8(16, 1, 16, 16, NULL, 16, 1, 0, 64, NULL),
+    lambda L: L.nsr_gemv_q8_bias_glu(16, 1, 16, 40, 16, 16, 1, 64, 64, NULL),
+    lambda L: L.nsr_gemv_q8_resadd_ln(16, 1, 16, 16, NULL, 16, 16, 1, 16, 1, 64, 64, C.c_float(1e-5), NULL),
+    lambda L: L.nsr_gemv_q8_resadd_ln(16, 1, 16, 16, 16, 16, 16, 2, 16, 1, 64, 64, C.c_float(1e-5), NULL),
 ])
 def test_invalid_arguments_are_rejected_before_any_launch(call):
     L = abi.lib()
@@ -101,6 +114,7 @@ def test_empty_inputs_are_no_ops():
     assert L.nsr_q8_0_embed_gather(16, 100, 64, 16, 0, 0, 16, 0, NULL, NULL) == abi.NSR_OK
     assert L.nsr_activation(16, 16, 0, 0, 1, NULL) == abi.NSR_OK
     assert L.nsr_kv_cache_append(16, 16, 1, 0, 64, 8, 0, NULL) == abi.NSR_OK
+    assert L.nsr_gemv_q8(16, 1, 16, 16, NULL, 16, 1, 64, 0, NULL) == abi.NSR_OK
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU error path")

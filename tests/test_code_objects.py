@@ -12,7 +12,11 @@ LLVM tools:
   gfx950 a buffer store whose offset sits in an SGPR soffset gets no wait
   state there from the compiler, and such stores were observed to write the
   overwritten values; the kernels keep store offsets in the VGPR address, and
-  this test keeps it that way.
+  this test keeps it that way;
+* no int -> float conversion reads a sign-extended sub-dword operand as
+  unsigned (v_cvt_f32_u32 with an SDWA sext source). This compiler folds
+  __builtin_amdgcn_sbfe(w, off, 8) followed by an int -> float conversion
+  into that form, which turns every negative byte into ~4.29e9.
 """
 import re
 import shutil
@@ -24,7 +28,7 @@ import pytest
 ROOT = Path(__file__).resolve().parent.parent
 LIB = ROOT / "nspeech_amd" / "lib"
 LLVM = Path("/opt/rocm/llvm/bin")
-UNITS = ["q8_0_gather", "layernorm", "rotary", "adain_snake", "elementwise"]
+UNITS = ["q8_0_gather", "layernorm", "rotary", "adain_snake", "elementwise", "gemv_q8"]
 
 
 def _co(unit):
@@ -122,3 +126,20 @@ def test_no_store_data_hazard(unit):
     assert "s_endpgm" in out, "disassembly produced no kernel code"
     hits = store_data_hazards(out)
     assert not hits, f"{len(hits)} wide stores with data overwritten by the next VALU op, e.g. {hits[:2]}"
+
+
+_UNSIGNED_CVT_OF_SEXT = re.compile(r"v_cvt_f32_u32_sdwa\s+v\d+,\s*sext\(")
+
+
+def test_sext_unsigned_convert_pattern_matches_planted_line():
+    planted = ("v_cvt_f32_u32_sdwa v0, sext(v2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0\n"
+               "v_cvt_f32_i32_sdwa v1, sext(v2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1\n")
+    assert len(_UNSIGNED_CVT_OF_SEXT.findall(planted)) == 1
+
+
+@pytest.mark.parametrize("unit", UNITS)
+def test_no_unsigned_convert_of_sign_extended_bytes(unit):
+    out = subprocess.run([_tool("llvm-objdump"), "-d", "--mcpu=gfx950", str(_co(unit))], capture_output=True,
+                         text=True, check=True).stdout
+    hits = _UNSIGNED_CVT_OF_SEXT.findall(out)
+    assert not hits, f"{unit}: {len(hits)} unsigned converts of sign-extended bytes"

@@ -332,3 +332,108 @@ def test_rope_qk_cache_f16_against_f64_rotation_and_copies():
     q0, k0, _, _ = R.rope_qk_cache_f16(q, k, None, tab, 0, rot, ck0)
     assert_bitexact(q0, q, "pos 0 identity q")
     assert_bitexact(k0, k, "pos 0 identity k")
+
+
+# -------------------------------------------------------------- Q8 GEMV ---
+
+def _q8_weight(g, K, NW, scale=0.02):
+    """Random repacked-Q8 weight: qs u32 [K, NW/4], scales f16 bits [K/32, NW],
+    and its dequantisation in float64, decoded independently of the oracle
+    (little-endian int8 view of the packed words: column c = byte c % 4 of
+    word c / 4)."""
+    qs = g.integers(0, 2 ** 32, size=(K, NW // 4), dtype=np.uint64).astype(np.uint32)
+    sc = (g.standard_normal((K // 32, NW)) * scale).astype(np.float16)
+    q = qs.view(np.int8).reshape(K, NW).astype(np.float64)
+    W = q * np.repeat(sc.astype(np.float64), 32, axis=0)
+    return qs, sc.view(np.uint16), W
+
+
+def _acc_bound(x, W):
+    """Forward error bound of an f32 dot product of length K (Higham's
+    gamma_K), applied to |x| @ |W|."""
+    K = x.shape[0]
+    u = 2.0 ** -24
+    gam = (K + 2) * u / (1 - (K + 2) * u)
+    return gam * (np.abs(x.astype(np.float64)) @ np.abs(W))
+
+
+def test_gemv_q8_matches_f64_matmul_of_dequant():
+    g = configs.rng(41)
+    for K, N in ((32, 16), (256, 96), (640, 640)):
+        qs, sc, W = _q8_weight(g, K, N)
+        x = g.standard_normal(K).astype(np.float16).astype(np.float32)
+        bias = g.standard_normal(N).astype(np.float32)
+        for b in (None, bias):
+            got = R.gemv_q8(x, qs, sc, b)
+            ref = x.astype(np.float64) @ W + (0 if b is None else b.astype(np.float64))
+            bound = _acc_bound(x, W) + np.abs(ref) * 2.0 ** -23
+            assert np.all(np.abs(got - ref) <= bound), (K, N, float(np.max(np.abs(got - ref) - bound)))
+
+
+def test_gemv_q8_one_hot_selects_a_dequantised_row():
+    """x = e_k: every product is exact, so out = f32(q[k, c] * scale) (+ bias
+    rounded once) bit for bit."""
+    g = configs.rng(42)
+    K, N = 96, 48
+    qs, sc, W = _q8_weight(g, K, N)
+    bias = g.standard_normal(N).astype(np.float32)
+    for k in (0, 31, 32, 95):
+        x = np.zeros(K, np.float32)
+        x[k] = 1.0
+        # + 0.0: the accumulator starts at +0, so a zero weight gives +0
+        assert_bitexact(R.gemv_q8(x, qs, sc), (W[k] + 0.0).astype(np.float32), f"row {k}")
+        assert_bitexact(R.gemv_q8(x, qs, sc, bias), (W[k] + bias.astype(np.float64)).astype(np.float32),
+                        f"row {k} + bias")
+
+
+def test_gemv_q8_glu_matches_f64_silu_gate():
+    g = configs.rng(43)
+    K, N = 320, 80
+    qs, sc, W = _q8_weight(g, K, 2 * N)
+    x = g.standard_normal(K).astype(np.float16).astype(np.float32)
+    bias = g.standard_normal(2 * N).astype(np.float32)
+    got = R.gemv_q8(x, qs, sc, bias, glu=True)
+    pre = x.astype(np.float64) @ W + bias
+    xa, ga = pre[:N], pre[N:]
+    sil = ga / (1 + np.exp(-ga))
+    ref = sil * xa
+    e = _acc_bound(x, W) + np.abs(pre) * 2.0 ** -23
+    # |d silu / dg| <= 1.1; silu and the product add a few f32 roundings
+    bound = 1.1 * e[N:] * np.abs(xa) + np.abs(sil) * e[:N] + np.abs(ref) * 2.0 ** -20
+    assert np.all(np.abs(got - ref) <= bound)
+    # the halves are not interchangeable: swapping them changes the result
+    swapped = xa / (1 + np.exp(-xa)) * ga
+    assert np.max(np.abs(swapped - ref)) > 1e-2
+
+
+def test_gemv_q8_resadd_ln_against_f64():
+    """h = f16(x @ W) + residual: the f16-rounded f32 sum lies within the
+    accumulation bound plus one f16 ulp of the f64 projection's f16 rounding;
+    norm is LN(h) * w rounded to f16 once, within one f16 ulp of
+    the f64 LN of the oracle's own h."""
+    g = configs.rng(44)
+    for K, dim in ((2560, 640), (288, 288)):
+        qs, sc, W = _q8_weight(g, K, dim)
+        x = g.standard_normal(K).astype(np.float16).astype(np.float32)
+        res = g.standard_normal(dim).astype(np.float32)
+        w = (1 + 0.1 * g.standard_normal(dim)).astype(np.float16)
+        h, norm = R.gemv_q8_resadd_ln(x, qs, sc, res, w.view(np.uint16), 1e-5)
+        proj64 = x.astype(np.float64) @ W
+        p16 = proj64.astype(np.float16).astype(np.float64)
+        e = _acc_bound(x, W)
+        # f16 rounding is monotone: |f16(acc) - f16(proj)| <= e + one f16 ulp at |proj| + e
+        ulp = np.spacing((np.abs(proj64) + e).astype(np.float16)).astype(np.float64)
+        hr = p16 + res
+        assert np.all(np.abs(h - hr) <= e + ulp + np.abs(hr) * 2.0 ** -23)
+        # with a zero residual h is the projection itself, an f16 value, and
+        # the f16 rounding of the plain GEMV's f32 result
+        h0, _ = R.gemv_q8_resadd_ln(x, qs, sc, np.zeros(dim, np.float32), w.view(np.uint16), 1e-5)
+        assert_bitexact(h0, h0.astype(np.float16).astype(np.float32), "projection is rounded to f16")
+        assert_bitexact(h0, R.gemv_q8(x, qs, sc).astype(np.float16).astype(np.float32), "same sums as gemv_q8")
+        h64 = h.astype(np.float64)
+        mu = h64.mean()
+        var = ((h64 - mu) ** 2).mean()
+        n64 = (h64 - mu) / np.sqrt(var + 1e-5) * w.astype(np.float64)
+        got = norm.view(np.float16).astype(np.float64)
+        ulpn = np.spacing(np.abs(n64).astype(np.float16)).astype(np.float64)
+        assert np.all(np.abs(got - n64) <= ulpn + 1e-6)
