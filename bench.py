@@ -46,8 +46,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workloads", default="c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,q8fc1,q8fc2",
-                    help="comma list of c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,q8fc1,q8fc2,copy")
+    ap.add_argument("--workloads", default="c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,q8fc1,q8fc2,q8fc1r,q8fc2r",
+                    help="comma list of c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,q8fc1,q8fc2,q8fc1r,q8fc2r,copy")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline (0 = skip)")
     ap.add_argument("--no-rotate", action="store_true", help="one buffer set (warm MALL) for all timings")
     return ap.parse_args()
@@ -194,14 +194,18 @@ def build_workload(name):
                         2 * Hk * Lc * Dh * 2, make_set, launch,
                         "nsrk_rope_cache_f16", "f16")
 
-    if name in ("q8fc1", "q8fc2"):
-        # Moonshine decoder MLP at M = 1 (dim 640, intermediate 2560; f16 activations, repacked Q8 weights):
+    if name in ("q8fc1", "q8fc2", "q8fc1r", "q8fc2r"):
+        # Moonshine decoder MLP at M = 1 (dim 640, intermediate 2560; f16 activations, Q8 weights):
         # q8fc1 = fc1 + bias + GLU-SiLU (gemv_q8_bias_glu), q8fc2 = fc2 + residual + next LayerNorm
-        # (gemv_q8_resadd_ln). Every buffer set holds its own weight copy, so the timed calls stream the
-        # weights from HBM as a real decode step over many layers does.
+        # (gemv_q8_resadd_ln, two launches). q8fc1/q8fc2 read t4 tiles (nsr_q8_pack_t4, packed once per
+        # buffer set outside the timed region); the "r" variants read the reference's [K, N/4] layout.
+        # Every buffer set holds its own weight copy, so the timed calls stream the weights from HBM as a
+        # decode step over many layers does.
         g = configs.rng(1007)
         dim, inter = 640, 2560
-        K, NW = (dim, 2 * inter) if name == "q8fc1" else (inter, dim)
+        fc1 = name.startswith("q8fc1")
+        t4 = not name.endswith("r")
+        K, NW = (dim, 2 * inter) if fc1 else (inter, dim)
         qs0 = torch.from_numpy(g.integers(0, 2 ** 32, size=(K, NW // 4), dtype=np.uint64).astype(np.uint32)
                                .view(np.int32)).to(dev)
         sc0 = torch.from_numpy((g.standard_normal((K // 32, NW)) * 0.02).astype(np.float16)).to(dev)
@@ -211,28 +215,36 @@ def build_workload(name):
         lnw = torch.ones(dim, dtype=torch.float16, device=dev)
 
         def make_set(_):
-            return {"q": qs0.clone(), "s": sc0.clone(), "o": torch.empty(inter if name == "q8fc1" else dim,
-                                                                         dtype=torch.float16, device=dev),
+            if t4:
+                w = abi.Q8T4(qs0, sc0, glu=fc1)
+                q, s_ = w.qs, w.scales
+            else:
+                q, s_ = qs0.clone(), sc0.clone()
+            return {"q": q, "s": s_, "o": torch.empty(inter if fc1 else dim, dtype=torch.float16, device=dev),
                     "h": torch.empty(dim, dtype=torch.float32, device=dev)}
 
+        f_glu = L.nsr_gemv_q8_t4_bias_glu if t4 else L.nsr_gemv_q8_bias_glu
+        f_rln = L.nsr_gemv_q8_t4_resadd_ln if t4 else L.nsr_gemv_q8_resadd_ln
+
         def launch(s):
-            if name == "q8fc1":
-                abi.check(L.nsr_gemv_q8_bias_glu(x.data_ptr(), 1, s["q"].data_ptr(), s["s"].data_ptr(),
-                                                 bias.data_ptr(), s["o"].data_ptr(), 1, K, inter, stream()))
+            if fc1:
+                abi.check(f_glu(x.data_ptr(), 1, s["q"].data_ptr(), s["s"].data_ptr(), bias.data_ptr(),
+                                s["o"].data_ptr(), 1, K, inter, stream()))
             else:
-                abi.check(L.nsr_gemv_q8_resadd_ln(x.data_ptr(), 1, s["q"].data_ptr(), s["s"].data_ptr(),
-                                                  res.data_ptr(), s["h"].data_ptr(), lnw.data_ptr(), 1,
-                                                  s["o"].data_ptr(), 1, K, dim, 1e-5, stream()))
+                abi.check(f_rln(x.data_ptr(), 1, s["q"].data_ptr(), s["s"].data_ptr(), res.data_ptr(),
+                                s["h"].data_ptr(), lnw.data_ptr(), 1, s["o"].data_ptr(), 1, K, dim, 1e-5, stream()))
 
         wbytes = K * NW + (K // 32) * NW * 2
-        if name == "q8fc1":
+        lay = "t4 tiles" if t4 else "reference [K,N/4] layout"
+        if fc1:
             alg = wbytes + 2 * K + 4 * NW + 2 * inter
-            desc = f"Q8 GEMV fc1 + bias + GLU-SiLU, x f16 [{K}] @ W [{K},{NW}] -> f16 [{inter}]"
-            kern = "nsrk_gemv_q8_glu_f16_f16"
+            desc = f"Q8 GEMV fc1 + bias + GLU-SiLU, x f16 [{K}] @ W [{K},{NW}] ({lay}) -> f16 [{inter}]"
+            kern = "nsrk_gemv_q8t4_glu_f16_f16_b256" if t4 else "nsrk_gemv_q8_glu_f16_f16"
         else:
             alg = wbytes + 2 * K + 4 * dim + 4 * dim + 2 * dim + 2 * dim
-            desc = f"Q8 GEMV fc2 + residual + LayerNorm, x f16 [{K}] @ W [{K},{NW}] -> f32 h, f16 norm [{dim}]"
-            kern = "nsrk_gemv_q8_resln_f16_f16"
+            desc = (f"Q8 GEMV fc2 + residual + LayerNorm, x f16 [{K}] @ W [{K},{NW}] ({lay}) -> f32 h, "
+                    f"f16 norm [{dim}] (two launches)")
+            kern = "nsrk_gemv_q8t4_h_f16_b1024" if t4 else "nsrk_gemv_q8_h_f16"
         return Workload(name, desc, alg, wbytes, make_set, launch, kern, "i8xf16->f32")
 
     if name == "c4a":
@@ -402,23 +414,23 @@ def cpu_baseline(budget_s, names):
             f1 = lambda: R.resadd_ln_gelu_bf16(c["x"], c["res"], wb, bb)  # noqa: E731
             fn = lambda: R.resadd_ln_gelu_bf16(c["x"], c["res"], wb, bb, nthreads=ncores)  # noqa: E731
             sample = "750 of the 24000 rows, scaled"
-        elif nm in ("q8fc1", "q8fc2"):
+        elif nm in ("q8fc1", "q8fc2"):  # the "r" variants have the same CPU path
             g = configs.rng(1007)
-            K, NW = (640, 5120) if nm == "q8fc1" else (2560, 640)
+            K, NW = (640, 5120) if nm.startswith("q8fc1") else (2560, 640)
             qs = g.integers(0, 2 ** 32, size=(K, NW // 4), dtype=np.uint64).astype(np.uint32)
             sc = (g.standard_normal((K // 32, NW)) * 0.02).astype(np.float16).view(np.uint16)
             xx = g.standard_normal(K).astype(np.float16).astype(np.float32)
             bb = g.standard_normal(NW).astype(np.float32)
             rr = g.standard_normal(640).astype(np.float32)
             ww = np.ones(640, np.float16).view(np.uint16)
-            if nm == "q8fc1":
+            if nm.startswith("q8fc1"):
                 f1 = lambda: R.gemv_q8(xx, qs, sc, bb, glu=True)  # noqa: E731
             else:
                 f1 = lambda: R.gemv_q8_resadd_ln(xx, qs, sc, rr, ww)  # noqa: E731
             fn = None
             sample = "full config (scalar restatement of the Triton kernel, 1 thread)"
             wb = K * NW + (K // 32) * NW * 2
-            galg = wb + 2 * K + (4 * NW + 2 * 2560 if nm == "q8fc1" else 12 * 640)
+            galg = wb + 2 * K + (4 * NW + 2 * 2560 if nm.startswith("q8fc1") else 12 * 640)
             r1 = timed(f1, galg, per)
             out[nm] = {"sample": sample, "threads_1": {"us_per_call": r1["us_per_call"], "GBs": r1["GBs"]}}
             continue

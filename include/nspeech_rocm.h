@@ -254,12 +254,8 @@ nsr_status nsr_residual_add(const void* x, const void* res, void* out,
  * kernels: qs u32 [K, NW/4] with the int8 weight of column c in byte c % 4
  * (lowest byte first) of word c / 4, and scales f16 [K/32, NW], one per
  * 32-row block and column: W[k, c] = int8 * f32(scale[k / 32, c]). x [K] is
- * F16 or F32. Accumulation is f32; the sum is split over K across the GPU
- * and the partial sums are added in a fixed order, so results do not depend
- * on timing. Split-K scratch is owned by the library, one buffer per
- * (device, stream): the first call on a stream allocates it (and may
- * synchronise the device); calls on the same stream are ordered, and calls
- * on different streams do not share it.
+ * F16 or F32. Accumulation is f32 in a fixed order (no atomics, no scratch):
+ * results are reproducible run to run.
  * Requirements: K % 32 == 0 and K > 0, N % 16 == 0, qs and scales 16-byte
  * aligned. N == 0 is a no-op. */
 
@@ -283,8 +279,9 @@ nsr_status nsr_gemv_q8_bias_glu(const void* x, nsr_dtype x_dtype, const uint32_t
 /* proj = f16-rounded x @ W (W [K, dim]); out_f32 = proj + residual (f32;
  * out_f32 may be residual itself); norm = (out_f32 - mean) / sqrt(var + eps)
  * * ln_weight (biased variance over dim; ln_weight F16 or F32; norm F16 or
- * F32). Replaces gemv_q8_resadd_ln (kernels/moonshine_kernels.py:1775-1819),
- * the fused out-projection + residual + next LayerNorm of the decoder step
+ * F32). Two launches on `stream`: the projection, then the row LayerNorm.
+ * Replaces gemv_q8_resadd_ln (kernels/moonshine_kernels.py:1775-1819), the
+ * fused out-projection + residual + next LayerNorm of the decoder step
  * (triton_residual_add_layernorm src/triton_kernels.rs:742 after the
  * projection). */
 nsr_status nsr_gemv_q8_resadd_ln(const void* x, nsr_dtype x_dtype, const uint32_t* qs,
@@ -292,6 +289,40 @@ nsr_status nsr_gemv_q8_resadd_ln(const void* x, nsr_dtype x_dtype, const uint32_
                                  float* out_f32, const void* ln_weight, nsr_dtype w_dtype,
                                  void* norm, nsr_dtype norm_dtype, int64_t K, int64_t dim,
                                  float eps, nsr_stream_t stream);
+
+/* ---- t4 tiles: the same weights packed for coalesced reads --------------- */
+
+/* Packs a repacked-Q8 weight (qs u32 [K, NW/4], scales f16 [K/32, NW], as
+ * above) into t4 tiles, once, at load time: tile t holds 4 weight columns
+ * for all K rows contiguously (t4_qs [NW/4][K] u32, one int8 per byte) and
+ * their scales (t4_scales [NW/4][K/32][4] f16). glu != 0 packs a GLU weight
+ * ([K, 2N], NW = 2N): tile t holds x-half columns 2t, 2t+1 and gate-half
+ * columns 2t, 2t+1. The packing is a byte permutation: dequantised values
+ * are unchanged. t4_qs takes K*NW bytes, t4_scales K/32*NW*2 bytes, both
+ * 16-byte aligned. Requirements: K % 32 == 0, NW % 16 == 0 (NW % 32 == 0
+ * for GLU). Has no counterpart in the reference, which defines only the
+ * [K, N/4] layout (kernels/moonshine_kernels.py:611-614) and reads it with
+ * one thread per column; on gfx950 a workgroup that owns a few columns of
+ * that layout scatters its reads over all K rows. */
+nsr_status nsr_q8_pack_t4(const uint32_t* qs, const uint16_t* scales, int64_t K,
+                          int64_t NW, int glu, uint32_t* t4_qs, uint16_t* t4_scales,
+                          nsr_stream_t stream);
+
+/* nsr_gemv_q8 / nsr_gemv_q8_bias_glu / nsr_gemv_q8_resadd_ln over t4 tiles
+ * (same results up to f32 summation order; x additionally aligned to 4
+ * elements). Replace the same reference kernels as the functions above. */
+nsr_status nsr_gemv_q8_t4(const void* x, nsr_dtype x_dtype, const uint32_t* t4_qs,
+                          const uint16_t* t4_scales, const float* bias, void* out,
+                          nsr_dtype out_dtype, int64_t K, int64_t N, nsr_stream_t stream);
+nsr_status nsr_gemv_q8_t4_bias_glu(const void* x, nsr_dtype x_dtype, const uint32_t* t4_qs,
+                                   const uint16_t* t4_scales, const float* bias, void* out,
+                                   nsr_dtype out_dtype, int64_t K, int64_t N,
+                                   nsr_stream_t stream);
+nsr_status nsr_gemv_q8_t4_resadd_ln(const void* x, nsr_dtype x_dtype, const uint32_t* t4_qs,
+                                    const uint16_t* t4_scales, const float* residual,
+                                    float* out_f32, const void* ln_weight, nsr_dtype w_dtype,
+                                    void* norm, nsr_dtype norm_dtype, int64_t K, int64_t dim,
+                                    float eps, nsr_stream_t stream);
 
 #ifdef __cplusplus
 }

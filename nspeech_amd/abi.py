@@ -69,11 +69,17 @@ def lib() -> C.CDLL:
         L.nsr_gemv_q8_bias_glu.argtypes = [_P, C.c_int, _P, _P, _P, _P, C.c_int, _I64, _I64, _P]
         L.nsr_gemv_q8_resadd_ln.argtypes = [_P, C.c_int, _P, _P, _P, _P, _P, C.c_int, _P, C.c_int, _I64, _I64,
                                             C.c_float, _P]
+        L.nsr_q8_pack_t4.argtypes = [_P, _P, _I64, _I64, C.c_int, _P, _P, _P]
+        L.nsr_gemv_q8_t4.argtypes = [_P, C.c_int, _P, _P, _P, _P, C.c_int, _I64, _I64, _P]
+        L.nsr_gemv_q8_t4_bias_glu.argtypes = [_P, C.c_int, _P, _P, _P, _P, C.c_int, _I64, _I64, _P]
+        L.nsr_gemv_q8_t4_resadd_ln.argtypes = [_P, C.c_int, _P, _P, _P, _P, _P, C.c_int, _P, C.c_int, _I64, _I64,
+                                               C.c_float, _P]
         for name in ("nsr_init", "nsr_layernorm", "nsr_residual_add_layernorm", "nsr_rope_table_f32",
                      "nsr_rope_qk_cache_append", "nsr_kv_cache_append",
                      "nsr_rotary_partial_interleaved_f32", "nsr_adain_snake_f32", "nsr_q8_0_embed_gather",
                      "nsr_activation", "nsr_glu_silu", "nsr_residual_add", "nsr_gemv_q8",
-                     "nsr_gemv_q8_bias_glu", "nsr_gemv_q8_resadd_ln"):
+                     "nsr_gemv_q8_bias_glu", "nsr_gemv_q8_resadd_ln", "nsr_q8_pack_t4", "nsr_gemv_q8_t4",
+                     "nsr_gemv_q8_t4_bias_glu", "nsr_gemv_q8_t4_resadd_ln"):
             getattr(L, name).restype = C.c_int
         _lib = L
     return _lib
@@ -283,4 +289,47 @@ def gemv_q8_resadd_ln(x, qs, scales, residual, ln_weight, *, eps=1e-5, out_f32=N
     check(lib().nsr_gemv_q8_resadd_ln(_ptr(x), _dt(x), _ptr(qs), _ptr(scales), _ptr(residual), _ptr(out_f32),
                                       _ptr(ln_weight), _dt(ln_weight), _ptr(norm), _dt(norm), K, dim, eps,
                                       _stream(stream)))
+    return out_f32, norm
+
+
+class Q8T4:
+    """A repacked-Q8 weight packed into t4 tiles on the device (nsr_q8_pack_t4)."""
+
+    def __init__(self, qs, scales, *, glu=False, stream=None):
+        K, nw = _q8_shape(qs, scales)
+        self.K, self.NW, self.glu = K, nw, glu
+        self.qs = torch.empty(K * nw // 4, dtype=torch.int32, device=qs.device)
+        self.scales = torch.empty((K // 32) * nw, dtype=torch.float16, device=qs.device)
+        check(lib().nsr_q8_pack_t4(_ptr(qs), _ptr(scales), K, nw, 1 if glu else 0, _ptr(self.qs),
+                                   _ptr(self.scales), _stream(stream)))
+
+
+def gemv_q8_t4(x, w: Q8T4, bias=None, *, out=None, out_dtype=torch.float16, stream=None):
+    N = w.NW
+    if out is None:
+        out = torch.empty(N, dtype=out_dtype, device=x.device)
+    check(lib().nsr_gemv_q8_t4(_ptr(x), _dt(x), _ptr(w.qs), _ptr(w.scales), _ptr(bias), _ptr(out), _dt(out), w.K,
+                               N, _stream(stream)))
+    return out
+
+
+def gemv_q8_t4_bias_glu(x, w: Q8T4, bias=None, *, out=None, out_dtype=torch.float16, stream=None):
+    N = w.NW // 2
+    if out is None:
+        out = torch.empty(N, dtype=out_dtype, device=x.device)
+    check(lib().nsr_gemv_q8_t4_bias_glu(_ptr(x), _dt(x), _ptr(w.qs), _ptr(w.scales), _ptr(bias), _ptr(out),
+                                        _dt(out), w.K, N, _stream(stream)))
+    return out
+
+
+def gemv_q8_t4_resadd_ln(x, w: Q8T4, residual, ln_weight, *, eps=1e-5, out_f32=None, norm=None,
+                         norm_dtype=torch.float16, stream=None):
+    dim = w.NW
+    if out_f32 is None:
+        out_f32 = torch.empty(dim, dtype=torch.float32, device=x.device)
+    if norm is None:
+        norm = torch.empty(dim, dtype=norm_dtype, device=x.device)
+    check(lib().nsr_gemv_q8_t4_resadd_ln(_ptr(x), _dt(x), _ptr(w.qs), _ptr(w.scales), _ptr(residual),
+                                         _ptr(out_f32), _ptr(ln_weight), _dt(ln_weight), _ptr(norm), _dt(norm),
+                                         w.K, dim, eps, _stream(stream)))
     return out_f32, norm

@@ -1,190 +1,270 @@
 /*
- * Q8 GEMV at M = 1 (decoder projections) over the repacked Q8 layout:
- * qs u32 [K, NW/4] (the int8 weight of column c in byte c % 4 of word c / 4),
- * scales f16 [K/32, NW]. Forms (kernels/moonshine_kernels.py):
- *   mode 0  out = x @ W (+ bias)                       gemv_q8 / gemv_q8_bias :616-677
- *   mode 1  out = silu(x @ Wg + bg) * (x @ Wx + bx)    gemv_q8_bias_glu :1721-1772
- *           (W [K, 2N]: x half in columns [0, N), gate half in [N, 2N))
- *   mode 2  h = f16(x @ W) + residual (written f32), out = LN(h) * w
- *                                                      gemv_q8_resadd_ln :1775-1819
+ * Q8 GEMV at M = 1 (decoder projections), three forms
+ * (kernels/moonshine_kernels.py):
+ *   plain  out = x @ W (+ bias)                       gemv_q8 / gemv_q8_bias :616-677
+ *   glu    out = silu(x @ Wg + bg) * (x @ Wx + bx)    gemv_q8_bias_glu :1721-1772
+ *          (W [K, 2N]: x half in columns [0, N), gate half in [N, 2N))
+ *   h      h = f16(x @ W) + residual (f32)            first half of gemv_q8_resadd_ln
+ *          :1775-1819; the LayerNorm of h is a second launch (the row
+ *          LayerNorm kernels), since it needs every column of h
+ * over two weight layouts:
  *
- * Design (gfx950, memory-bound on the weights): split-K over a 2-D grid so
- * that even a 640 x 2560 projection spreads over ~200-400 workgroups. A
- * workgroup (256 threads = 16 column lanes x 16 row lanes) covers a tile of
- * 256 weight columns (16 per lane, one 16-byte word of qs per row) and a
- * chunk of K. Per 32-row Q8 block a lane reads its 16 scales and 2 rows
- * and applies the scale once to the two-row sum. The 16 row lanes are
- * reduced through LDS in a fixed order. With one K chunk the epilogue follows directly; otherwise
- * each workgroup stores its f32 partial sums, and the last workgroup of a
- * tile to finish (a device-scope atomic count; no workgroup ever waits on
- * another) adds the partials in chunk order, applies the epilogue and resets
- * the count for the next call. Results do not depend on arrival order.
+ * - the reference's repacked Q8: qs u32 [K, NW/4] (the int8 weight of column
+ *   c in byte c % 4 of word c / 4), scales f16 [K/32, NW]. A workgroup owns 8
+ *   weight columns (plain, h) or 8 x-half + 8 gate-half columns (glu) over
+ *   all of K; its 256 lanes take row pairs (2 rows of one 32-row block, so
+ *   one scale per column) and are reduced through LDS in a fixed order. Each
+ *   row contributes only 8 bytes per workgroup, so neighbouring tiles share
+ *   cache lines: tiles are ordered so that consecutive tiles run on the same
+ *   XCD (workgroups are dealt round-robin to the 8 XCDs) and meet in its L2.
+ *
+ * - t4 tiles (nsr_q8_pack_t4): tile t holds 4 weight columns for all K rows
+ *   contiguously, [K][4] int8, with its scales [K/32][4] f16. A workgroup
+ *   reads its tile as consecutive 16-byte chunks (4 rows x 4 columns per
+ *   lane), so every wave load is one contiguous 1 KB span: the weight
+ *   stream runs at the coalesced-read rate. GLU tiles hold x-half columns
+ *   2t, 2t+1 and gate-half columns 2t, 2t+1.
+ *
+ * No workgroup depends on another (no split-K, no scratch, no atomics);
+ * every column's sum is formed in a fixed order, so results are
+ * reproducible run to run.
  */
 #include "device_common.h"
 
-enum { GEMV_PLAIN = 0, GEMV_GLU = 1, GEMV_RESLN = 2 };
+enum { GEMV_PLAIN = 0, GEMV_GLU = 1, GEMV_H = 2 };
 
-template <int XDT>
-NSR_DEV float gemv_x(const void* x, int64_t k) {
-  return load_scalar<XDT>(x, k);
+/* Tile order that puts consecutive tiles on one XCD: workgroup b runs on XCD
+ * b % 8; XCD x takes the x-th contiguous run of tiles. A bijection of
+ * [0, n). */
+NSR_DEV int xcd_tile(int b, int n) {
+  const int per = (n + 7) >> 3, x = b & 7, i = b >> 3;
+  const int full = n - 8 * (per - 1); /* XCDs that take `per` tiles */
+  return (x < full ? x * per : full * per + (x - full) * (per - 1)) + i;
 }
 
-/* One 32-row block for this lane's 16 columns: rows 2*kl and 2*kl + 1 of
- * the block, summed in f32, times the block scale, added to acc. */
-template <int XDT>
-NSR_DEV void gemv_block(const nsr_gemv_args& a, int64_t b, int kl, int64_t w0, float* acc) {
-  const int64_t r0 = b * 32 + 2 * kl;
-  const int64_t nw4 = a.NW >> 2;
-  const nsr_uint4 q0 = ld16(a.qs + r0 * nw4 + w0);
-  const nsr_uint4 q1 = ld16(a.qs + (r0 + 1) * nw4 + w0);
-  const nsr_uint4 s01 = ld16_cached(a.scales + b * a.NW + 4 * w0);
-  const nsr_uint4 s23 = ld16_cached(a.scales + b * a.NW + 4 * w0 + 8);
-  const float x0 = gemv_x<XDT>(a.x, r0), x1 = gemv_x<XDT>(a.x, r0 + 1);
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    /* signed byte j % 4 of word j / 4 -> f32: one v_cvt_f32_i32 with a
-     * sign-extended byte select. (Written as an int8_t cast: the same value
-     * through __builtin_amdgcn_sbfe is folded by this compiler into an
-     * unsigned convert of the sign-extended byte, wrong for negatives.) */
-    const int sh = 8 * (j & 3);
-    const float v0 = (float)(int)(int8_t)(q0[j >> 2] >> sh);
-    const float v1 = (float)(int)(int8_t)(q1[j >> 2] >> sh);
-    const float blk = __builtin_fmaf(x1, v1, x0 * v0);
-    const uint32_t sw = j < 8 ? s01[j >> 1] : s23[(j - 8) >> 1];
-    const float sc = f16_bits_to_f32((j & 1) ? (sw >> 16) : (sw & 0xffffu));
-    acc[j] = __builtin_fmaf(blk, sc, acc[j]);
-  }
+NSR_DEV float silu_f(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
 }
 
-/* Device-scope "am I the last of `total` arrivals on counter c": every
- * thread's prior global writes are released before the count, and the last
- * arrival acquires all of them. The last arrival resets the counter. */
-NSR_DEV bool gemv_arrive_last(uint32_t* c, uint32_t total, uint32_t* flag) {
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t prev = atomicAdd(c, 1u);
-    *flag = prev == total - 1u ? 1u : 0u;
-    if (prev == total - 1u) atomicExch(c, 0u);
-  }
-  __syncthreads();
-  const bool last = *flag != 0u;
-  if (last) __threadfence();
-  return last;
-}
+NSR_DEV float s8(uint32_t w, int byte) { return (float)(int)(int8_t)(w >> (8 * byte)); }
+
+/* ------------------------------------------------ reference layout -- */
 
 template <int XDT, int ODT, int MODE>
-NSR_DEV void gemv_q8_body(const nsr_gemv_args& a) {
-  __shared__ float red[16][257];
-  __shared__ float fin[256];
-  __shared__ float redl[8];
-  __shared__ uint32_t flag;
+NSR_DEV void gemv_ref(const nsr_gemv_args& a) {
+  /* columns per workgroup: 8 (plain, h) or 8 x-half + 8 gate-half (glu) */
+  constexpr int NC = MODE == GEMV_GLU ? 16 : 8;
+  __shared__ float red[256][NC + 1];
+  __shared__ float red2[256];
+  __shared__ float fin[NC];
   const int tid = threadIdx.x;
-  const int cl = tid & 15, kl = tid >> 4;
-  const int t = blockIdx.x, s = blockIdx.y;
+  const int t = xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t nw4 = a.NW >> 2;
+  /* first word (per row) of each 8-column group */
+  const int64_t g0 = 2 * (int64_t)t;
+  const int64_t g1 = (a.N >> 2) + 2 * (int64_t)t; /* gate half (glu only) */
 
-  /* this lane's first weight column; GLU tiles pair 128 x-half columns with
-   * the matching 128 gate-half columns */
-  int64_t c0;
-  bool cvalid;
-  if constexpr (MODE == GEMV_GLU) {
-    const int64_t oc = (int64_t)t * 128 + 16 * (cl & 7);
-    c0 = oc + (cl >= 8 ? a.N : 0);
-    cvalid = oc < a.N;
-  } else {
-    c0 = (int64_t)t * 256 + 16 * cl;
-    cvalid = c0 < a.NW;
-  }
-
-  float acc[16];
+  float acc[NC];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) acc[j] = 0.f;
-  if (cvalid) {
-    const int64_t bpc = a.kc >> 5;
-    const int64_t b0 = (int64_t)s * bpc;
-    const int64_t b1 = min(b0 + bpc, (int64_t)(a.K >> 5));
-    for (int64_t b = b0; b < b1; ++b) gemv_block<XDT>(a, b, kl, c0 >> 2, acc);
-  }
+  for (int j = 0; j < NC; ++j) acc[j] = 0.f;
+  const int npairs = a.K >> 1;
+  for (int p = tid; p < npairs; p += 256) {
+    const int64_t r0 = 2 * (int64_t)p, b = p >> 4;
+    const uint32_t* q0 = a.qs + r0 * nw4;
+    const uint32_t* q1 = q0 + nw4;
+    uint32_t w0[NC / 4], w1[NC / 4], sw[NC / 2];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) red[kl][16 * cl + j] = acc[j];
+    for (int h = 0; h < NC / 8; ++h) {
+      const int64_t g = h ? g1 : g0;
+      const nsr_uint2 a0 = *(const nsr_uint2*)(q0 + g), a1 = *(const nsr_uint2*)(q1 + g);
+      w0[2 * h] = a0.x;
+      w0[2 * h + 1] = a0.y;
+      w1[2 * h] = a1.x;
+      w1[2 * h + 1] = a1.y;
+      const nsr_uint4 s4 = ld16_cached(a.scales + b * a.NW + 4 * g);
+      sw[4 * h] = s4.x;
+      sw[4 * h + 1] = s4.y;
+      sw[4 * h + 2] = s4.z;
+      sw[4 * h + 3] = s4.w;
+    }
+    const float x0 = load_scalar<XDT>(a.x, r0), x1 = load_scalar<XDT>(a.x, r0 + 1);
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const float blk = __builtin_fmaf(x1, s8(w1[j >> 2], j & 3), x0 * s8(w0[j >> 2], j & 3));
+      const float sc = f16_bits_to_f32((j & 1) ? (sw[j >> 1] >> 16) : (sw[j >> 1] & 0xffffu));
+      acc[j] = __builtin_fmaf(blk, sc, acc[j]);
+    }
+  }
+  /* fixed-order reduction over the 256 lanes: 256/NC strided groups, then NC partials each */
+  constexpr int G = 256 / NC;
+#pragma unroll
+  for (int j = 0; j < NC; ++j) red[tid][j] = acc[j];
   __syncthreads();
-  /* thread tid owns tile column tid: the 16 row lanes summed in order */
-  float v = 0.f;
+  {
+    const int col = tid % NC, g = tid / NC;
+    float v = 0.f;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) v += red[r][tid];
-
-  int64_t col; /* weight column of tile column tid */
-  bool valid;
-  if constexpr (MODE == GEMV_GLU) {
-    const int64_t oc = (int64_t)t * 128 + (tid & 127);
-    col = oc + (tid >= 128 ? a.N : 0);
-    valid = oc < a.N;
-  } else {
-    col = (int64_t)t * 256 + tid;
-    valid = col < a.NW;
+    for (int k = 0; k < NC; ++k) v += red[g + G * k][col];
+    red2[tid] = v;
   }
-
-  if (a.S > 1) {
-    /* split K: the last chunk of this tile to arrive adds all chunks' partial
-     * sums in chunk order */
-    if (valid) a.partial[(int64_t)s * a.NW + col] = v;
-    if (!gemv_arrive_last(a.counters + t, (uint32_t)a.S, &flag)) return;
-    if (valid) {
-      v = 0.f;
-      for (int i = 0; i < a.S; ++i) v += a.partial[(int64_t)i * a.NW + col];
-    }
-  }
-
-  if constexpr (MODE == GEMV_PLAIN) {
-    if (valid) store_scalar<ODT>(a.out, col, a.bias ? v + a.bias[col] : v);
-  } else if constexpr (MODE == GEMV_GLU) {
-    fin[tid] = valid ? (a.bias ? v + a.bias[col] : v) : 0.f;
-    __syncthreads();
-    if (tid < 128 && valid) {
-      const float g = fin[tid + 128];
-      const float sg = g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
-      store_scalar<ODT>(a.out, col, sg * fin[tid]);
-    }
-  } else {
-    /* h = f16(projection) + residual for this tile's columns; the last tile
-     * to finish normalises all N columns */
-    if (valid) a.out_f32[col] = round_to<DT_F16>(v) + a.residual[col];
-    if (gridDim.x > 1) {
-      if (!gemv_arrive_last(a.counters + gridDim.x, gridDim.x, &flag)) return;
+  __syncthreads();
+  if (tid < NC) {
+    float v = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) v += red2[NC * g + tid];
+    const int64_t col = 4 * ((tid < 8) ? g0 : g1) + (tid & 7);
+    if constexpr (MODE == GEMV_PLAIN) {
+      store_scalar<ODT>(a.out, col, a.bias ? v + a.bias[col] : v);
+    } else if constexpr (MODE == GEMV_H) {
+      a.out_f32[col] = round_to<DT_F16>(v) + a.residual[col];
     } else {
-      __syncthreads();
+      fin[tid] = a.bias ? v + a.bias[col] : v;
     }
-    float sum = 0.f;
-    for (int64_t c = tid; c < a.N; c += 256) sum += a.out_f32[c];
-    const float mean = block_sum<4>(sum, redl) / (float)a.N;
-    float sq = 0.f;
-    for (int64_t c = tid; c < a.N; c += 256) {
-      const float d = a.out_f32[c] - mean;
-      sq = __builtin_fmaf(d, d, sq);
+  }
+  if constexpr (MODE == GEMV_GLU) {
+    __syncthreads();
+    if (tid < 8) store_scalar<ODT>(a.out, 4 * g0 + tid, silu_f(fin[8 + tid]) * fin[tid]);
+  }
+}
+
+/* ------------------------------------------------------- t4 tiles -- */
+
+template <int XDT, int ODT, int MODE, int BLOCK>
+NSR_DEV void gemv_t4(const nsr_gemv_args& a) {
+  constexpr int NWV = BLOCK / 64;
+  __shared__ float red[NWV][4];
+  const int tid = threadIdx.x;
+  const int t = blockIdx.x;
+  const nsr_uint4* tile = (const nsr_uint4*)a.qs + (int64_t)t * (a.K >> 2);
+  const nsr_uint2* tsc = (const nsr_uint2*)a.scales + (int64_t)t * (a.K >> 5);
+  const int nchunk = a.K >> 2;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int j = tid; j < nchunk; j += BLOCK) {
+    const nsr_uint4 q = ld16(tile + j); /* rows 4j .. 4j+3, 4 columns each */
+    const nsr_uint2 sw = tsc[j >> 3];
+    float xs[4];
+    if constexpr (XDT == DT_F16) {
+      const nsr_uint2 xw = *((const nsr_uint2*)a.x + j);
+      xs[0] = f16_bits_to_f32(xw.x & 0xffffu);
+      xs[1] = f16_bits_to_f32(xw.x >> 16);
+      xs[2] = f16_bits_to_f32(xw.y & 0xffffu);
+      xs[3] = f16_bits_to_f32(xw.y >> 16);
+    } else {
+      const nsr_float4 xv = *((const nsr_float4*)a.x + j);
+      xs[0] = xv.x;
+      xs[1] = xv.y;
+      xs[2] = xv.z;
+      xs[3] = xv.w;
     }
-    const float var = block_sum<4>(sq, redl) / (float)a.N;
-    const float rstd = 1.0f / sqrtf(var + a.eps);
-    for (int64_t c = tid; c < a.N; c += 256) {
-      const float w = a.ln_w_f16 ? f16_bits_to_f32(((const uint16_t*)a.ln_w)[c]) : ((const float*)a.ln_w)[c];
-      store_scalar<ODT>(a.out, c, (a.out_f32[c] - mean) * rstd * w);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float blk = xs[0] * s8(q[0], c);
+#pragma unroll
+      for (int i = 1; i < 4; ++i) blk = __builtin_fmaf(xs[i], s8(q[i], c), blk);
+      const float sc = f16_bits_to_f32((c & 1) ? (sw[c >> 1] >> 16) : (sw[c >> 1] & 0xffffu));
+      acc[c] = __builtin_fmaf(blk, sc, acc[c]);
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const float w = wave_sum(acc[c]);
+    if ((tid & 63) == 0) red[tid >> 6][c] = w;
+  }
+  __syncthreads();
+  if (tid < 4) {
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < NWV; ++w) v += red[w][tid];
+    if constexpr (MODE == GEMV_PLAIN) {
+      const int64_t col = 4 * (int64_t)t + tid;
+      store_scalar<ODT>(a.out, col, a.bias ? v + a.bias[col] : v);
+    } else if constexpr (MODE == GEMV_H) {
+      const int64_t col = 4 * (int64_t)t + tid;
+      a.out_f32[col] = round_to<DT_F16>(v) + a.residual[col];
+    } else {
+      red[0][tid] = v; /* every wave's partials were read above */
+    }
+  }
+  if constexpr (MODE == GEMV_GLU) {
+    __syncthreads();
+    if (tid < 2) {
+      const int64_t col = 2 * (int64_t)t + tid;
+      const float xv = red[0][tid] + (a.bias ? a.bias[col] : 0.f);
+      const float gv = red[0][2 + tid] + (a.bias ? a.bias[a.N + col] : 0.f);
+      store_scalar<ODT>(a.out, col, silu_f(gv) * xv);
     }
   }
 }
 
-#define NSR_GEMV(XN, XDT, ON, ODT)                                                              \
-  extern "C" __global__ void __launch_bounds__(256) nsrk_gemv_q8_##XN##_##ON(const nsr_gemv_args a) { \
-    gemv_q8_body<XDT, ODT, GEMV_PLAIN>(a);                                                     \
-  }                                                                                             \
-  extern "C" __global__ void __launch_bounds__(256)                                             \
-      nsrk_gemv_q8_glu_##XN##_##ON(const nsr_gemv_args a) {                                     \
-    gemv_q8_body<XDT, ODT, GEMV_GLU>(a);                                                       \
-  }                                                                                             \
-  extern "C" __global__ void __launch_bounds__(256)                                             \
-      nsrk_gemv_q8_resln_##XN##_##ON(const nsr_gemv_args a) {                                   \
-    gemv_q8_body<XDT, ODT, GEMV_RESLN>(a);                                                     \
+/* t4 packing: one thread per (tile, row) word, then one per (tile, block)
+ * scale quad. Source column of tile t, slot c: 4t + c (plain); 2t + c for
+ * c < 2 and N + 2t + c - 2 otherwise (GLU). */
+NSR_DEV int64_t t4_src_col(int64_t t, int c, int N) {
+  if (N == 0) return 4 * t + c;
+  return c < 2 ? 2 * t + c : (int64_t)N + 2 * t + (c - 2);
+}
+
+extern "C" __global__ void __launch_bounds__(256) nsrk_gemv_q8t4_pack(const nsr_q8_pack_args a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t tiles = a.NW >> 2;
+  const int64_t nq = tiles * a.K;
+  if (i < nq) {
+    const int64_t t = i / a.K, r = i - t * a.K;
+    const uint8_t* row = a.qs + r * a.NW;
+    uint32_t w = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) w |= (uint32_t)row[t4_src_col(t, c, a.N)] << (8 * c);
+    a.tq[i] = w;
+  } else if (i < nq + tiles * (a.K >> 5)) {
+    const int64_t k = i - nq, nb = a.K >> 5;
+    const int64_t t = k / nb, b = k - t * nb;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) a.ts[4 * k + c] = a.scales[b * a.NW + t4_src_col(t, c, a.N)];
+  }
+}
+
+#define NSR_GEMV_REF(XN, XDT, ON, ODT)                                                                  \
+  extern "C" __global__ void __launch_bounds__(256) nsrk_gemv_q8_##XN##_##ON(const nsr_gemv_args a) {   \
+    gemv_ref<XDT, ODT, GEMV_PLAIN>(a);                                                                  \
+  }                                                                                                     \
+  extern "C" __global__ void __launch_bounds__(256) nsrk_gemv_q8_glu_##XN##_##ON(const nsr_gemv_args a) { \
+    gemv_ref<XDT, ODT, GEMV_GLU>(a);                                                                    \
   }
 
-NSR_GEMV(f16, DT_F16, f16, DT_F16)
-NSR_GEMV(f16, DT_F16, f32, DT_F32)
-NSR_GEMV(f32, DT_F32, f16, DT_F16)
-NSR_GEMV(f32, DT_F32, f32, DT_F32)
+#define NSR_GEMV_T4(XN, XDT, ON, ODT, B)                                                   \
+  extern "C" __global__ void __launch_bounds__(B)                                          \
+      nsrk_gemv_q8t4_##XN##_##ON##_b##B(const nsr_gemv_args a) {                           \
+    gemv_t4<XDT, ODT, GEMV_PLAIN, B>(a);                                                   \
+  }                                                                                        \
+  extern "C" __global__ void __launch_bounds__(B)                                          \
+      nsrk_gemv_q8t4_glu_##XN##_##ON##_b##B(const nsr_gemv_args a) {                       \
+    gemv_t4<XDT, ODT, GEMV_GLU, B>(a);                                                     \
+  }
+
+#define NSR_GEMV_ALL(XN, XDT, ON, ODT) \
+  NSR_GEMV_REF(XN, XDT, ON, ODT)       \
+  NSR_GEMV_T4(XN, XDT, ON, ODT, 256)   \
+  NSR_GEMV_T4(XN, XDT, ON, ODT, 512)   \
+  NSR_GEMV_T4(XN, XDT, ON, ODT, 1024)
+
+NSR_GEMV_ALL(f16, DT_F16, f16, DT_F16)
+NSR_GEMV_ALL(f16, DT_F16, f32, DT_F32)
+NSR_GEMV_ALL(f32, DT_F32, f16, DT_F16)
+NSR_GEMV_ALL(f32, DT_F32, f32, DT_F32)
+
+#define NSR_GEMV_H(XN, XDT)                                                                       \
+  extern "C" __global__ void __launch_bounds__(256) nsrk_gemv_q8_h_##XN(const nsr_gemv_args a) {   \
+    gemv_ref<XDT, DT_F32, GEMV_H>(a);                                                             \
+  }                                                                                               \
+  extern "C" __global__ void __launch_bounds__(256) nsrk_gemv_q8t4_h_##XN##_b256(const nsr_gemv_args a) { \
+    gemv_t4<XDT, DT_F32, GEMV_H, 256>(a);                                                         \
+  }                                                                                               \
+  extern "C" __global__ void __launch_bounds__(512) nsrk_gemv_q8t4_h_##XN##_b512(const nsr_gemv_args a) { \
+    gemv_t4<XDT, DT_F32, GEMV_H, 512>(a);                                                         \
+  }                                                                                               \
+  extern "C" __global__ void __launch_bounds__(1024) nsrk_gemv_q8t4_h_##XN##_b1024(const nsr_gemv_args a) { \
+    gemv_t4<XDT, DT_F32, GEMV_H, 1024>(a);                                                        \
+  }
+
+NSR_GEMV_H(f16, DT_F16)
+NSR_GEMV_H(f32, DT_F32)

@@ -92,24 +92,28 @@ typedef struct nsr_adain_args {
 
 typedef struct nsr_gemv_args {
   const void* x;           /* [K], f16 or f32 */
-  const uint32_t* qs;      /* [K, NW/4] packed int8, column c in byte c % 4 of word c / 4 */
-  const uint16_t* scales;  /* [K/32, NW] f16 */
+  const uint32_t* qs;      /* weights: repacked Q8 [K, NW/4] words, or t4 tiles */
+  const uint16_t* scales;  /* f16: [K/32, NW], or t4 tiles [NW/4][K/32][4] */
   const float* bias;       /* [NW] or NULL */
-  void* out;               /* [N] (modes 0, 1) or the f16/f32 norm output (mode 2) */
-  const float* residual;   /* [N] (mode 2) */
-  float* out_f32;          /* [N] residual + projection (mode 2) */
-  const void* ln_w;        /* [N] layernorm weight (mode 2) */
-  float* partial;          /* [S, NW] split-K partial sums (S > 1) */
-  uint32_t* counters;      /* [tiles] (modes 0, 1) or [1] (mode 2); zero between calls */
+  void* out;               /* [N] */
+  const float* residual;   /* [N] (h form) */
+  float* out_f32;          /* [N] h = f16(x @ W) + residual (h form) */
   int32_t K;
   int32_t NW;              /* weight columns: N, or 2N for the GLU form */
   int32_t N;               /* output columns */
-  int32_t S;               /* K chunks (grid.y) */
-  int32_t kc;              /* rows per K chunk, multiple of 32 */
-  int32_t ln_w_f16;        /* mode 2: 1 = f16 weight, 0 = f32 */
-  float eps;
   int32_t pad_;
 } nsr_gemv_args;
+
+typedef struct nsr_q8_pack_args {
+  const uint8_t* qs;       /* [K, NW] int8 bytes (the repacked Q8 words, little-endian) */
+  const uint16_t* scales;  /* [K/32, NW] f16 */
+  uint32_t* tq;            /* [NW/4][K] words: tile t, row r = 4 int8 */
+  uint16_t* ts;            /* [NW/4][K/32][4] f16 */
+  int32_t K;
+  int32_t NW;
+  int32_t N;               /* GLU: output columns (NW = 2N); 0 = plain */
+  int32_t pad_;
+} nsr_q8_pack_args;
 
 typedef struct nsr_ew_args {
   const void* a;

@@ -17,7 +17,6 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
-#include <map>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -688,63 +687,20 @@ nsr_status nsr_residual_add(const void* x, const void* res, void* out, nsr_dtype
 
 namespace {
 
-// Split-K scratch of one (device, stream): f32 partial sums [S, NW] and the
-// per-tile arrival counters, which every launch leaves at zero.
-struct GemvScratch {
-  float* partial = nullptr;
-  size_t partial_cap = 0;  // floats
-  uint32_t* counters = nullptr;
-  size_t counter_cap = 0;  // u32
-};
-std::mutex g_gemv_mu;
-std::map<std::pair<int, void*>, GemvScratch> g_gemv_scratch;
-
-nsr_status gemv_scratch(nsr_stream_t stream, size_t n_partial, size_t n_counters, GemvScratch* out) {
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return fail(NSR_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
-  std::lock_guard<std::mutex> lk(g_gemv_mu);
-  GemvScratch& sc = g_gemv_scratch[{dev, stream}];
-  if (sc.partial_cap < n_partial || sc.counter_cap < n_counters) {
-    // Work already queued on this stream may still use the old buffers.
-    e = hipStreamSynchronize((hipStream_t)stream);
-    if (e != hipSuccess) return fail(NSR_ERR_HIP, "gemv scratch: hipStreamSynchronize: %s", hipGetErrorString(e));
-    const size_t np = std::max({n_partial, sc.partial_cap, (size_t)1 << 20});
-    const size_t nc = std::max({n_counters, sc.counter_cap, (size_t)4096});
-    if (sc.partial) (void)hipFree(sc.partial);
-    if (sc.counters) (void)hipFree(sc.counters);
-    sc = GemvScratch();
-    float* p = nullptr;
-    uint32_t* c = nullptr;
-    e = hipMalloc((void**)&p, np * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc((void**)&c, nc * sizeof(uint32_t));
-    if (e == hipSuccess) e = hipMemset(c, 0, nc * sizeof(uint32_t));
-    if (e == hipSuccess) e = hipDeviceSynchronize();
-    if (e != hipSuccess) {
-      if (p) (void)hipFree(p);
-      if (c) (void)hipFree(c);
-      (void)hipGetLastError();
-      return fail(NSR_ERR_HIP, "gemv scratch allocation (%zu floats): %s", np, hipGetErrorString(e));
-    }
-    sc.partial = p;
-    sc.partial_cap = np;
-    sc.counters = c;
-    sc.counter_cap = nc;
-  }
-  *out = sc;
-  return NSR_OK;
-}
-
 enum GemvMode { kGemvPlain = 0, kGemvGlu = 1, kGemvResLn = 2 };
 
-// Workgroups a launch aims for: ~2 per CU keeps every CU's load queue busy
-// at M = 1 without making the partial sums outweigh the weights.
-constexpr int64_t kGemvTargetGroups = 512;
+// Workgroup size for t4 tiles: about one 16-byte chunk (4 rows) per lane,
+// between 256 and 1024 lanes (measured on gfx950: K = 640 -> 256,
+// K = 2560 -> 1024).
+int t4_block(int64_t K) {
+  const int64_t chunks = K / 4;
+  return chunks <= 256 ? 256 : chunks <= 512 ? 512 : 1024;
+}
 
-nsr_status gemv_launch(GemvMode mode, const void* x, nsr_dtype xd, const uint32_t* qs, const uint16_t* scales,
-                       const float* bias, void* out, nsr_dtype od, const float* residual, float* out_f32,
-                       const void* ln_w, nsr_dtype wd, int64_t K, int64_t N, float eps, nsr_stream_t stream,
-                       const char* what) {
+nsr_status gemv_launch(GemvMode mode, bool t4, const void* x, nsr_dtype xd, const uint32_t* qs,
+                       const uint16_t* scales, const float* bias, void* out, nsr_dtype od, const float* residual,
+                       float* out_f32, const void* ln_w, nsr_dtype wd, int64_t K, int64_t N, float eps,
+                       nsr_stream_t stream, const char* what) {
   if (!x || !qs || !scales || !out || (mode == kGemvResLn && (!residual || !out_f32 || !ln_w)))
     return fail(NSR_ERR_BAD_ARG, "%s: null pointer", what);
   if ((xd != NSR_F16 && xd != NSR_F32) || (od != NSR_F16 && od != NSR_F32))
@@ -756,8 +712,11 @@ nsr_status gemv_launch(GemvMode mode, const void* x, nsr_dtype xd, const uint32_
     return fail(NSR_ERR_BAD_ARG, "%s: bad shape K=%lld N=%lld", what, (long long)K, (long long)N);
   if (K % 32 != 0) return fail(NSR_ERR_BAD_ARG, "%s: K=%lld must be a multiple of 32", what, (long long)K);
   if (N % 16 != 0) return fail(NSR_ERR_BAD_ARG, "%s: N=%lld must be a multiple of 16", what, (long long)N);
-  if (!aligned(qs, 16) || !aligned(scales, 16)) return fail(NSR_ERR_BAD_ARG, "%s: qs and scales need 16-byte alignment", what);
-  if (!aligned(x, dt_size(xd)) || !aligned(out, dt_size(od)) || (bias && !aligned(bias, 4)) ||
+  if (!aligned(qs, 16) || !aligned(scales, 16))
+    return fail(NSR_ERR_BAD_ARG, "%s: qs and scales need 16-byte alignment", what);
+  // t4 kernels read x 4 elements at a time
+  const uintptr_t xa = t4 ? 4 * dt_size(xd) : dt_size(xd);
+  if (!aligned(x, xa) || !aligned(out, dt_size(od)) || (bias && !aligned(bias, 4)) ||
       (residual && !aligned(residual, 4)) || (out_f32 && !aligned(out_f32, 4)) ||
       (ln_w && !aligned(ln_w, dt_size(wd))))
     return fail(NSR_ERR_BAD_ARG, "%s: misaligned pointer", what);
@@ -766,25 +725,8 @@ nsr_status gemv_launch(GemvMode mode, const void* x, nsr_dtype xd, const uint32_
   if (K == 0) return fail(NSR_ERR_BAD_ARG, "%s: K must be > 0", what);
 
   const int64_t NW = mode == kGemvGlu ? 2 * N : N;
-  const int64_t tiles = mode == kGemvGlu ? (N + 127) / 128 : (NW + 255) / 256;
-  const int64_t blocks = K / 32;
-  int64_t S = kGemvTargetGroups / tiles;
-  if (S < 1) S = 1;
-  if (S > blocks) S = blocks;
-  const int64_t bpc = (blocks + S - 1) / S;
-  S = (blocks + bpc - 1) / bpc;
-  if (tiles > 0x7fffffffLL || S > 65535) return fail(NSR_ERR_UNSUPPORTED, "%s: grid too large", what);
-
   nsr_gemv_args a;
   std::memset(&a, 0, sizeof(a));
-  const bool need_scratch = S > 1 || (mode == kGemvResLn && tiles > 1);
-  if (need_scratch) {
-    GemvScratch sc;
-    nsr_status st = gemv_scratch(stream, S > 1 ? (size_t)(S * NW) : 0, (size_t)tiles + 1, &sc);
-    if (st != NSR_OK) return st;
-    a.partial = sc.partial;
-    a.counters = sc.counters;
-  }
   a.x = x;
   a.qs = qs;
   a.scales = scales;
@@ -792,18 +734,29 @@ nsr_status gemv_launch(GemvMode mode, const void* x, nsr_dtype xd, const uint32_
   a.out = out;
   a.residual = residual;
   a.out_f32 = out_f32;
-  a.ln_w = ln_w;
   a.K = (int32_t)K;
   a.NW = (int32_t)NW;
   a.N = (int32_t)N;
-  a.S = (int32_t)S;
-  a.kc = (int32_t)(bpc * 32);
-  a.ln_w_f16 = wd == NSR_F16 ? 1 : 0;
-  a.eps = eps;
-  static const char* kind[] = {"nsrk_gemv_q8_", "nsrk_gemv_q8_glu_", "nsrk_gemv_q8_resln_"};
-  const std::string name = std::string(kind[mode]) + dt_name(xd) + "_" + dt_name(od);
   void* params[] = {&a};
-  return launch(name, (unsigned)tiles, (unsigned)S, 256, 0, stream, params);
+  std::string name;
+  unsigned groups, block;
+  if (t4) {
+    static const char* kind[] = {"nsrk_gemv_q8t4_", "nsrk_gemv_q8t4_glu_", "nsrk_gemv_q8t4_h_"};
+    block = (unsigned)t4_block(K);
+    name = std::string(kind[mode]) + dt_name(xd) + (mode == kGemvResLn ? "" : std::string("_") + dt_name(od)) +
+           "_b" + std::to_string(block);
+    groups = (unsigned)(NW / 4);
+  } else {
+    static const char* kind[] = {"nsrk_gemv_q8_", "nsrk_gemv_q8_glu_", "nsrk_gemv_q8_h_"};
+    block = 256;
+    name = std::string(kind[mode]) + dt_name(xd) + (mode == kGemvResLn ? "" : std::string("_") + dt_name(od));
+    groups = (unsigned)(mode == kGemvGlu ? N / 8 : NW / 8);
+  }
+  nsr_status st = launch(name, groups, 1, block, 0, stream, params);
+  if (st != NSR_OK || mode != kGemvResLn) return st;
+  // LayerNorm of the dim columns of h, weight only (one row)
+  return ln_common(out_f32, NSR_F32, nullptr, NSR_F32, nullptr, NSR_F32, ln_w, nullptr, wd, out, od, 1, N, N, N, eps,
+                   0, NSR_ACT_NONE, false, stream);
 }
 
 }  // namespace
@@ -813,14 +766,14 @@ extern "C" {
 nsr_status nsr_gemv_q8(const void* x, nsr_dtype x_dtype, const uint32_t* qs, const uint16_t* scales,
                        const float* bias, void* out, nsr_dtype out_dtype, int64_t K, int64_t N,
                        nsr_stream_t stream) {
-  return gemv_launch(kGemvPlain, x, x_dtype, qs, scales, bias, out, out_dtype, nullptr, nullptr, nullptr,
+  return gemv_launch(kGemvPlain, false, x, x_dtype, qs, scales, bias, out, out_dtype, nullptr, nullptr, nullptr,
                      NSR_F32, K, N, 0.0f, stream, "gemv_q8");
 }
 
 nsr_status nsr_gemv_q8_bias_glu(const void* x, nsr_dtype x_dtype, const uint32_t* qs, const uint16_t* scales,
                                 const float* bias, void* out, nsr_dtype out_dtype, int64_t K, int64_t N,
                                 nsr_stream_t stream) {
-  return gemv_launch(kGemvGlu, x, x_dtype, qs, scales, bias, out, out_dtype, nullptr, nullptr, nullptr,
+  return gemv_launch(kGemvGlu, false, x, x_dtype, qs, scales, bias, out, out_dtype, nullptr, nullptr, nullptr,
                      NSR_F32, K, N, 0.0f, stream, "gemv_q8_bias_glu");
 }
 
@@ -828,8 +781,53 @@ nsr_status nsr_gemv_q8_resadd_ln(const void* x, nsr_dtype x_dtype, const uint32_
                                  const float* residual, float* out_f32, const void* ln_weight, nsr_dtype w_dtype,
                                  void* norm, nsr_dtype norm_dtype, int64_t K, int64_t dim, float eps,
                                  nsr_stream_t stream) {
-  return gemv_launch(kGemvResLn, x, x_dtype, qs, scales, nullptr, norm, norm_dtype, residual, out_f32, ln_weight,
-                     w_dtype, K, dim, eps, stream, "gemv_q8_resadd_ln");
+  return gemv_launch(kGemvResLn, false, x, x_dtype, qs, scales, nullptr, norm, norm_dtype, residual, out_f32,
+                     ln_weight, w_dtype, K, dim, eps, stream, "gemv_q8_resadd_ln");
+}
+
+nsr_status nsr_q8_pack_t4(const uint32_t* qs, const uint16_t* scales, int64_t K, int64_t NW, int glu,
+                          uint32_t* t4_qs, uint16_t* t4_scales, nsr_stream_t stream) {
+  if (!qs || !scales || !t4_qs || !t4_scales) return fail(NSR_ERR_BAD_ARG, "q8_pack_t4: null pointer");
+  if (K <= 0 || NW <= 0 || K % 32 != 0 || NW % 16 != 0 || (glu && NW % 32 != 0) || K > (1LL << 30) ||
+      NW > (1LL << 28) || K * NW > (1LL << 40))
+    return fail(NSR_ERR_BAD_ARG, "q8_pack_t4: bad shape K=%lld NW=%lld (K %% 32 == 0, NW %% 16 == 0%s)",
+                (long long)K, (long long)NW, glu ? ", NW % 32 == 0 for GLU" : "");
+  if (!aligned(qs, 4) || !aligned(scales, 2) || !aligned(t4_qs, 16) || !aligned(t4_scales, 16))
+    return fail(NSR_ERR_BAD_ARG, "q8_pack_t4: misaligned pointer (outputs need 16 bytes)");
+  nsr_q8_pack_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.qs = (const uint8_t*)qs;
+  a.scales = scales;
+  a.tq = t4_qs;
+  a.ts = t4_scales;
+  a.K = (int32_t)K;
+  a.NW = (int32_t)NW;
+  a.N = glu ? (int32_t)(NW / 2) : 0;
+  const int64_t total = (NW / 4) * K + (NW / 4) * (K / 32);
+  void* params[] = {&a};
+  return launch("nsrk_gemv_q8t4_pack", cdiv_u(total, 256), 1, 256, 0, stream, params);
+}
+
+nsr_status nsr_gemv_q8_t4(const void* x, nsr_dtype x_dtype, const uint32_t* t4_qs, const uint16_t* t4_scales,
+                          const float* bias, void* out, nsr_dtype out_dtype, int64_t K, int64_t N,
+                          nsr_stream_t stream) {
+  return gemv_launch(kGemvPlain, true, x, x_dtype, t4_qs, t4_scales, bias, out, out_dtype, nullptr, nullptr, nullptr,
+                     NSR_F32, K, N, 0.0f, stream, "gemv_q8_t4");
+}
+
+nsr_status nsr_gemv_q8_t4_bias_glu(const void* x, nsr_dtype x_dtype, const uint32_t* t4_qs,
+                                   const uint16_t* t4_scales, const float* bias, void* out, nsr_dtype out_dtype,
+                                   int64_t K, int64_t N, nsr_stream_t stream) {
+  return gemv_launch(kGemvGlu, true, x, x_dtype, t4_qs, t4_scales, bias, out, out_dtype, nullptr, nullptr, nullptr,
+                     NSR_F32, K, N, 0.0f, stream, "gemv_q8_t4_bias_glu");
+}
+
+nsr_status nsr_gemv_q8_t4_resadd_ln(const void* x, nsr_dtype x_dtype, const uint32_t* t4_qs,
+                                    const uint16_t* t4_scales, const float* residual, float* out_f32,
+                                    const void* ln_weight, nsr_dtype w_dtype, void* norm, nsr_dtype norm_dtype,
+                                    int64_t K, int64_t dim, float eps, nsr_stream_t stream) {
+  return gemv_launch(kGemvResLn, true, x, x_dtype, t4_qs, t4_scales, nullptr, norm, norm_dtype, residual, out_f32,
+                     ln_weight, w_dtype, K, dim, eps, stream, "gemv_q8_t4_resadd_ln");
 }
 
 }  // extern "C"

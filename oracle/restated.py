@@ -265,3 +265,25 @@ def gemv_q8_resadd_ln(x, qs, scales_bits, residual, ln_w_bits, eps=1e-5):
     norm = np.empty(dim, np.uint16)
     lib().orc_gemv_q8_resadd_ln(x, qs.ravel(), sc.ravel(), res, w, h, norm, K, dim, eps)
     return h, norm
+
+
+def q8_pack_t4(qs, scales_bits, glu=False):
+    """t4 tile packing of a repacked-Q8 weight (the layout nsr_q8_pack_t4
+    writes): tiles [NW/4][K][4] int8 (returned as u32 words, byte c = slot c)
+    and scales [NW/4][K/32][4] f16 bits. Slot c of tile t is weight column
+    4t + c, or for a GLU weight [K, 2N] x-half column 2t + c (c < 2) and
+    gate-half column N + 2t + c - 2. A byte permutation of the input; the
+    GEMV over the tiles is the GEMV over the original columns."""
+    qs = np.ascontiguousarray(qs, np.uint32)
+    sc = np.ascontiguousarray(scales_bits, np.uint16)
+    K, NW = qs.shape[0], 4 * qs.shape[1]
+    q8 = qs.view(np.uint8).reshape(K, NW)
+    t = np.arange(NW // 4)
+    if glu:
+        N = NW // 2
+        cols = np.stack([2 * t, 2 * t + 1, N + 2 * t, N + 2 * t + 1], axis=1)
+    else:
+        cols = 4 * t[:, None] + np.arange(4)[None, :]
+    tiles = np.ascontiguousarray(q8[:, cols].transpose(1, 0, 2))        # [T, K, 4]
+    tsc = np.ascontiguousarray(sc[:, cols].transpose(1, 0, 2))          # [T, K/32, 4]
+    return tiles.reshape(-1).view(np.uint32).copy(), tsc.reshape(-1).copy()

@@ -100,6 +100,14 @@ def test_version_and_header_is_plain_c():
     lambda L: L.nsr_gemv_q8_bias_glu(16, 1, 16, 40, 16, 16, 1, 64, 64, NULL),
     lambda L: L.nsr_gemv_q8_resadd_ln(16, 1, 16, 16, NULL, 16, 16, 1, 16, 1, 64, 64, C.c_float(1e-5), NULL),
     lambda L: L.nsr_gemv_q8_resadd_ln(16, 1, 16, 16, 16, 16, 16, 2, 16, 1, 64, 64, C.c_float(1e-5), NULL),
+    # t4 packing: K not a multiple of 32, GLU with NW not a multiple of 32, misaligned output; t4 GEMV with x
+    # not aligned to 4 elements
+    lambda L: L.nsr_q8_pack_t4(16, 16, 40, 64, 0, 16, 16, NULL),
+    lambda L: L.nsr_q8_pack_t4(16, 16, 64, 48, 1, 16, 16, NULL),
+    lambda L: L.nsr_q8_pack_t4(16, 16, 64, 64, 0, 24, 16, NULL),
+    lambda L: L.nsr_gemv_q8_t4(18, 1, 16, 16, NULL, 16, 1, 64, 64, NULL),
+    lambda L: L.nsr_gemv_q8_t4_bias_glu(16, 1, 16, 16, NULL, 16, 1, 64, 40, NULL),
+    lambda L: L.nsr_gemv_q8_t4_resadd_ln(16, 1, 16, 16, NULL, 16, 16, 1, 16, 1, 64, 64, C.c_float(1e-5), NULL),
 ])
 def test_invalid_arguments_are_rejected_before_any_launch(call):
     L = abi.lib()

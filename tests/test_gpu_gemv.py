@@ -1,14 +1,17 @@
 """Repacked-Q8 GEMV family on the GPU vs the oracle's restatement of
 gemv_q8 / gemv_q8_bias / gemv_q8_bias_glu / gemv_q8_resadd_ln
-(kernels/moonshine_kernels.py:616-677, 1721-1819).
+(kernels/moonshine_kernels.py:616-677, 1721-1819), over the reference's
+repacked-Q8 layout ("ref") and over the t4 tiles nsr_q8_pack_t4 makes
+("t4"; the packing itself is checked bit for bit against the oracle's
+restatement).
 
 The GPU adds the same f32 products in another order (split over K), so the
 bar is the f32 accumulation error bound rather than bit equality: two f32
 sums of the same K products each lie within gamma_K * sum|x_k w_k| of the
 exact sum, so they differ by at most twice that. f16 outputs add one f16 ulp
 (the two sums may round to neighbouring f16 values); every result also meets
-the f16 tolerance of the parity bar. Repeated calls are bit-identical (the
-partial sums are added in a fixed order, whatever the arrival order)."""
+the f16 tolerance of the parity bar. Repeated calls are bit-identical (every
+sum is formed in a fixed order)."""
 import numpy as np
 import pytest
 import torch
@@ -32,6 +35,14 @@ def _weight(g, K, NW):
 
 def _dev_w(qs, sc):
     return (torch.from_numpy(qs.view(np.int32)).cuda(), torch.from_numpy(sc).cuda())
+
+
+def _run(layout, fn, xt, q_t, s_t, *args, glu=False, **kw):
+    """Call the reference-layout entry point, or pack to t4 and call its twin."""
+    if layout == "ref":
+        return getattr(abi, fn)(xt, q_t, s_t, *args, **kw)
+    w = abi.Q8T4(q_t, s_t, glu=glu)
+    return getattr(abi, fn.replace("gemv_q8", "gemv_q8_t4"))(xt, w, *args, **kw)
 
 
 def _bound(x, W):
@@ -61,6 +72,7 @@ def _check(got_t, ref, e, odt, what):
     assert not bad.any(), f"{what}: {bad.sum()} outside the bound, first {np.flatnonzero(bad)[:5]}"
 
 
+@pytest.mark.parametrize("layout", ["ref", "t4"])
 @pytest.mark.parametrize("K,N,xd,od,with_bias", [
     (288, 288, "f16", "f16", True),      # Moonshine tiny decoder dim (kernel_configs.py)
     (416, 416, "f16", "f16", False),     # Moonshine base decoder dim
@@ -72,36 +84,38 @@ def _check(got_t, ref, e, odt, what):
     (96, 272, "f32", "f16", True),       # a 16-column second tile
     (32, 16, "f32", "f32", True),        # smallest legal shape, one K chunk
 ])
-def test_gemv_q8(dev, K, N, xd, od, with_bias):
-    say("gemv_q8", K, N, xd, od, with_bias)
+def test_gemv_q8(dev, layout, K, N, xd, od, with_bias):
+    say("gemv_q8", layout, K, N, xd, od, with_bias)
     g = configs.rng(K * 3 + N)
     qs, sc, W = _weight(g, K, N)
     x, xt = _x(g, K, xd)
     bias = g.standard_normal(N).astype(np.float32) if with_bias else None
     bt = torch.from_numpy(bias).cuda() if with_bias else None
     q_t, s_t = _dev_w(qs, sc)
-    out = abi.gemv_q8(xt, q_t, s_t, bt, out_dtype=_TD[od])
-    out2 = abi.gemv_q8(xt, q_t, s_t, bt, out_dtype=_TD[od])
+    out = _run(layout, "gemv_q8", xt, q_t, s_t, bt, out_dtype=_TD[od])
+    out2 = _run(layout, "gemv_q8", xt, q_t, s_t, bt, out_dtype=_TD[od])
     torch.cuda.synchronize()
     ref = R.gemv_q8(x, qs, sc.view(np.uint16), bias).astype(np.float64)
     _check(out, ref, _bound(x, W), od, f"gemv_q8 K={K} N={N}")
     assert_bitexact(out2.cpu().numpy(), out.cpu().numpy(), "repeat call")
 
 
+@pytest.mark.parametrize("layout", ["ref", "t4"])
 @pytest.mark.parametrize("K,N,xd,od", [
     (640, 2560, "f16", "f16"),   # Moonshine decoder fc1 + GLU (dim 640, intermediate 2560)
     (288, 1152, "f16", "f16"),
     (96, 144, "f32", "f32"),     # a 16-column second tile
     (32, 16, "f16", "f32"),
 ])
-def test_gemv_q8_bias_glu(dev, K, N, xd, od):
-    say("gemv_q8_bias_glu", K, N, xd, od)
+def test_gemv_q8_bias_glu(dev, layout, K, N, xd, od):
+    say("gemv_q8_bias_glu", layout, K, N, xd, od)
     g = configs.rng(K * 5 + N)
     qs, sc, W = _weight(g, K, 2 * N)
     x, xt = _x(g, K, xd)
     bias = g.standard_normal(2 * N).astype(np.float32)
     q_t, s_t = _dev_w(qs, sc)
-    out = abi.gemv_q8_bias_glu(xt, q_t, s_t, torch.from_numpy(bias).cuda(), out_dtype=_TD[od])
+    out = _run(layout, "gemv_q8_bias_glu", xt, q_t, s_t, torch.from_numpy(bias).cuda(), out_dtype=_TD[od],
+               glu=True)
     torch.cuda.synchronize()
     ref = R.gemv_q8(x, qs, sc.view(np.uint16), bias, glu=True).astype(np.float64)
     pre = x.astype(np.float64) @ W + bias
@@ -114,6 +128,7 @@ def test_gemv_q8_bias_glu(dev, K, N, xd, od):
     _check(out, ref, e / 2, od, f"gemv_q8_bias_glu K={K} N={N}")
 
 
+@pytest.mark.parametrize("layout", ["ref", "t4"])
 @pytest.mark.parametrize("K,dim,xd,wd,nd,in_place", [
     (2560, 640, "f16", "f16", "f16", False),  # decoder fc2 + residual + next LN (dim 640)
     (640, 640, "f16", "f16", "f16", True),    # attention out-projection, residual updated in place
@@ -121,8 +136,8 @@ def test_gemv_q8_bias_glu(dev, K, N, xd, od):
     (1152, 288, "f32", "f32", "f32", False),
     (32, 16, "f16", "f16", "f16", False),
 ])
-def test_gemv_q8_resadd_ln(dev, K, dim, xd, wd, nd, in_place):
-    say("gemv_q8_resadd_ln", K, dim, xd, wd, nd, in_place)
+def test_gemv_q8_resadd_ln(dev, layout, K, dim, xd, wd, nd, in_place):
+    say("gemv_q8_resadd_ln", layout, K, dim, xd, wd, nd, in_place)
     g = configs.rng(K * 7 + dim)
     qs, sc, W = _weight(g, K, dim)
     x, xt = _x(g, K, xd)
@@ -131,8 +146,8 @@ def test_gemv_q8_resadd_ln(dev, K, dim, xd, wd, nd, in_place):
     q_t, s_t = _dev_w(qs, sc)
     res_t = torch.from_numpy(res).cuda()
     w_t = torch.from_numpy(w16).cuda().to(_TD[wd])
-    h, norm = abi.gemv_q8_resadd_ln(xt, q_t, s_t, res_t, w_t, eps=1e-5, out_f32=res_t if in_place else None,
-                                    norm_dtype=_TD[nd])
+    h, norm = _run(layout, "gemv_q8_resadd_ln", xt, q_t, s_t, res_t, w_t, eps=1e-5,
+                   out_f32=res_t if in_place else None, norm_dtype=_TD[nd])
     torch.cuda.synchronize()
     h_ref, _ = R.gemv_q8_resadd_ln(x, qs, sc.view(np.uint16), res, w16.view(np.uint16), 1e-5)
     proj = x.astype(np.float64) @ W
@@ -149,26 +164,41 @@ def test_gemv_q8_resadd_ln(dev, K, dim, xd, wd, nd, in_place):
     assert np.all(np.abs(ng - n64) <= tol), float(np.max(np.abs(ng - n64) - tol))
 
 
+@pytest.mark.parametrize("K,NW,glu", [(640, 5120, True), (2560, 640, False), (32, 16, False), (96, 288, True)])
+def test_q8_pack_t4_bitexact(dev, K, NW, glu):
+    say("q8_pack_t4", K, NW, glu)
+    g = configs.rng(K + NW + glu)
+    qs, sc, _ = _weight(g, K, NW)
+    q_t, s_t = _dev_w(qs, sc)
+    w = abi.Q8T4(q_t, s_t, glu=glu)
+    torch.cuda.synchronize()
+    tq, ts = R.q8_pack_t4(qs, sc.view(np.uint16), glu=glu)
+    assert_bitexact(w.qs.cpu().numpy().view(np.uint32), tq, "t4 words")
+    assert_bitexact(w.scales.cpu().numpy().view(np.uint16), ts, "t4 scales")
+
+
 def test_gemv_q8_streams_and_repeats_agree(dev):
-    """Two streams hold separate split-K scratch: the same call on each, and
-    again after a different shape, gives bit-identical results."""
+    """The same call on two streams, and again after other shapes ran, gives
+    bit-identical results on both layouts."""
     g = configs.rng(77)
     K, N = 2560, 640
     qs, sc, _ = _weight(g, K, N)
     x, xt = _x(g, K, "f16")
     q_t, s_t = _dev_w(qs, sc)
-    say("gemv_q8 streams", K, N)
-    base = abi.gemv_q8(xt, q_t, s_t)
-    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
-    outs = []
-    for s in (s1, s2, s1):
-        with torch.cuda.stream(s):
-            outs.append(abi.gemv_q8(xt, q_t, s_t, stream=s))
-    qs2, sc2, _ = _weight(g, 640, 5120)
-    q2, s2t = _dev_w(qs2, sc2)
-    _, x2 = _x(g, 640, "f16")
-    abi.gemv_q8(x2, q2, s2t)
-    again = abi.gemv_q8(xt, q_t, s_t)
-    torch.cuda.synchronize()
-    for o in outs + [again]:
-        assert_bitexact(o.cpu().numpy(), base.cpu().numpy(), "same result on every stream and call")
+    for layout in ("ref", "t4"):
+        say("gemv_q8 streams", layout, K, N)
+        base = _run(layout, "gemv_q8", xt, q_t, s_t)
+        torch.cuda.synchronize()
+        s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+        outs = []
+        for s in (s1, s2, s1):
+            with torch.cuda.stream(s):
+                outs.append(_run(layout, "gemv_q8", xt, q_t, s_t, stream=s))
+        qs2, sc2, _ = _weight(g, 640, 5120)
+        q2, s2t = _dev_w(qs2, sc2)
+        _, x2 = _x(g, 640, "f16")
+        _run(layout, "gemv_q8", x2, q2, s2t)
+        again = _run(layout, "gemv_q8", xt, q_t, s_t)
+        torch.cuda.synchronize()
+        for o in outs + [again]:
+            assert_bitexact(o.cpu().numpy(), base.cpu().numpy(), f"{layout}: same result on every stream and call")

