@@ -308,6 +308,25 @@ nsr_status nsr_q8_pack_t4(const uint32_t* qs, const uint16_t* scales, int64_t K,
                           int64_t NW, int glu, uint32_t* t4_qs, uint16_t* t4_scales,
                           nsr_stream_t stream);
 
+/* From a GGUF Q8_0 weight, on the device: `blocks` is an nn::Linear weight
+ * W [N, K] (out, in) as the reference's GGUF files store it (N rows of K/32
+ * blocks {f16 d; int8 qs[32]}, 34 bytes each; tools/quantize-moonshine/src/
+ * main.rs:63-150), for example uploaded by nsr_gguf_upload. These write the
+ * GEMV layouts of W^T (x[K] @ W^T = the layer's output): the repacked Q8
+ * qs [K, N/4] + scales [K/32, N] of nsr_gemv_q8*, or t4 tiles (glu != 0:
+ * rows [0, N/2) are the x half and [N/2, N) the gate half, as
+ * DecoderMLP::forward chunks fc1's output, src/moonshine/decoder.rs:
+ * 403-411). A transpose of the stored int8 values and f16 scales: the
+ * dequantised weights are unchanged. Replaces the reference's host-side
+ * dequantise + transpose of decoder weights (dequant_2d,
+ * src/moonshine/gpu_decoder.rs:180-184). Requirements: K % 32 == 0,
+ * N % 16 == 0 (N % 32 == 0 for GLU), blocks 2-byte and outputs 16-byte
+ * aligned. */
+nsr_status nsr_q8_0_to_gemv_q8(const void* blocks, int64_t N, int64_t K, uint32_t* qs,
+                               uint16_t* scales, nsr_stream_t stream);
+nsr_status nsr_q8_0_to_t4(const void* blocks, int64_t N, int64_t K, int glu, uint32_t* t4_qs,
+                          uint16_t* t4_scales, nsr_stream_t stream);
+
 /* nsr_gemv_q8 / nsr_gemv_q8_bias_glu / nsr_gemv_q8_resadd_ln over t4 tiles
  * (same results up to f32 summation order; x additionally aligned to 4
  * elements). Replace the same reference kernels as the functions above. */

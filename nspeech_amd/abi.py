@@ -70,6 +70,8 @@ def lib() -> C.CDLL:
         L.nsr_gemv_q8_resadd_ln.argtypes = [_P, C.c_int, _P, _P, _P, _P, _P, C.c_int, _P, C.c_int, _I64, _I64,
                                             C.c_float, _P]
         L.nsr_q8_pack_t4.argtypes = [_P, _P, _I64, _I64, C.c_int, _P, _P, _P]
+        L.nsr_q8_0_to_gemv_q8.argtypes = [_P, _I64, _I64, _P, _P, _P]
+        L.nsr_q8_0_to_t4.argtypes = [_P, _I64, _I64, C.c_int, _P, _P, _P]
         L.nsr_gemv_q8_t4.argtypes = [_P, C.c_int, _P, _P, _P, _P, C.c_int, _I64, _I64, _P]
         L.nsr_gemv_q8_t4_bias_glu.argtypes = [_P, C.c_int, _P, _P, _P, _P, C.c_int, _I64, _I64, _P]
         L.nsr_gemv_q8_t4_resadd_ln.argtypes = [_P, C.c_int, _P, _P, _P, _P, _P, C.c_int, _P, C.c_int, _I64, _I64,
@@ -78,7 +80,7 @@ def lib() -> C.CDLL:
                      "nsr_rope_qk_cache_append", "nsr_kv_cache_append",
                      "nsr_rotary_partial_interleaved_f32", "nsr_adain_snake_f32", "nsr_q8_0_embed_gather",
                      "nsr_activation", "nsr_glu_silu", "nsr_residual_add", "nsr_gemv_q8",
-                     "nsr_gemv_q8_bias_glu", "nsr_gemv_q8_resadd_ln", "nsr_q8_pack_t4", "nsr_gemv_q8_t4",
+                     "nsr_gemv_q8_bias_glu", "nsr_gemv_q8_resadd_ln", "nsr_q8_pack_t4", "nsr_gemv_q8_t4", "nsr_q8_0_to_gemv_q8", "nsr_q8_0_to_t4",
                      "nsr_gemv_q8_t4_bias_glu", "nsr_gemv_q8_t4_resadd_ln"):
             getattr(L, name).restype = C.c_int
         _lib = L
@@ -293,15 +295,38 @@ def gemv_q8_resadd_ln(x, qs, scales, residual, ln_weight, *, eps=1e-5, out_f32=N
 
 
 class Q8T4:
-    """A repacked-Q8 weight packed into t4 tiles on the device (nsr_q8_pack_t4)."""
+    """A repacked-Q8 weight packed into t4 tiles on the device (nsr_q8_pack_t4),
+    or built from a GGUF Q8_0 weight with Q8T4.from_q8_0."""
 
     def __init__(self, qs, scales, *, glu=False, stream=None):
+        if qs is None:
+            return
         K, nw = _q8_shape(qs, scales)
-        self.K, self.NW, self.glu = K, nw, glu
-        self.qs = torch.empty(K * nw // 4, dtype=torch.int32, device=qs.device)
-        self.scales = torch.empty((K // 32) * nw, dtype=torch.float16, device=qs.device)
+        self._alloc(K, nw, glu, qs.device)
         check(lib().nsr_q8_pack_t4(_ptr(qs), _ptr(scales), K, nw, 1 if glu else 0, _ptr(self.qs),
                                    _ptr(self.scales), _stream(stream)))
+
+    def _alloc(self, K, nw, glu, device):
+        self.K, self.NW, self.glu = K, nw, glu
+        self.qs = torch.empty(K * nw // 4, dtype=torch.int32, device=device)
+        self.scales = torch.empty((K // 32) * nw, dtype=torch.float16, device=device)
+
+    @classmethod
+    def from_q8_0(cls, blocks, N, K, *, glu=False, stream=None):
+        """blocks: uint8 device tensor of a GGUF Q8_0 weight [N, K] (nn::Linear [out, in])."""
+        w = cls(None, None)
+        w._alloc(K, N, glu, blocks.device)
+        check(lib().nsr_q8_0_to_t4(_ptr(blocks), N, K, 1 if glu else 0, _ptr(w.qs), _ptr(w.scales),
+                                   _stream(stream)))
+        return w
+
+
+def q8_0_to_gemv_q8(blocks, N, K, *, stream=None):
+    """GGUF Q8_0 weight [N, K] on the device -> (qs int32 [K, N/4], scales f16 [K/32, N]) of W^T."""
+    qs = torch.empty((K, N // 4), dtype=torch.int32, device=blocks.device)
+    sc = torch.empty((K // 32, N), dtype=torch.float16, device=blocks.device)
+    check(lib().nsr_q8_0_to_gemv_q8(_ptr(blocks), N, K, _ptr(qs), _ptr(sc), _stream(stream)))
+    return qs, sc
 
 
 def gemv_q8_t4(x, w: Q8T4, bias=None, *, out=None, out_dtype=torch.float16, stream=None):

@@ -97,7 +97,7 @@ def build_host_library() -> Path:
     out = LIB / "libnspeech_rocm_host.so"
     tmp = LIB / "libnspeech_rocm_host.so.tmp"
     _run([*HOST_CXX, "-shared", f"-I{ROOT / 'include'}", f"-I{ROCM / 'include'}",
-          str(PKG / "host" / "rocm_kernels.cpp"),
+          str(PKG / "host" / "rocm_kernels.cpp"), str(PKG / "host" / "gguf.cpp"),
           f"-L{LIB}", "-lnspeech_rocm", f"-L{ROCM / 'lib'}", "-lamdhip64",
           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM / 'lib'}", "-Wl,--no-undefined", "-o", str(tmp)])
     os.replace(tmp, out)
@@ -115,6 +115,15 @@ def build_host_tests() -> Path:
           f"-L{LIB}", "-lnspeech_rocm_host", "-lnspeech_rocm", f"-L{ROCM / 'lib'}", "-lamdhip64",
           "-Wl,-rpath,$ORIGIN/../../../nspeech_amd/lib", f"-Wl,-rpath,{ROCM / 'lib'}", "-o", str(tmp)])
     os.replace(tmp, out)
+    # the GGUF reader built with AddressSanitizer (host code only, g++), for
+    # the malformed-file tests
+    asan = out_dir / "test_gguf_asan"
+    _run(["g++", "-O1", "-g", "-std=c++17", "-fsanitize=address,undefined", "-fno-omit-frame-pointer",
+          "-D__HIP_PLATFORM_AMD__", f"-I{ROOT / 'include'}", f"-I{ROCM / 'include'}", f"-I{PKG / 'host'}",
+          str(ROOT / "tests" / "host" / "test_gguf_asan.cpp"), str(PKG / "host" / "gguf.cpp"),
+          str(PKG / "host" / "rocm_kernels.cpp"), f"-L{LIB}", "-lnspeech_rocm", f"-L{ROCM / 'lib'}", "-lamdhip64",
+          "-Wl,-rpath,$ORIGIN/../../../nspeech_amd/lib", f"-Wl,-rpath,{ROCM / 'lib'}", "-o", str(asan) + ".tmp"])
+    os.replace(str(asan) + ".tmp", asan)
     return out
 
 

@@ -223,6 +223,43 @@ extern "C" __global__ void __launch_bounds__(256) nsrk_gemv_q8t4_pack(const nsr_
   }
 }
 
+/* GGUF Q8_0 weight W [N, K] (N rows of K/32 34-byte blocks, the layout of
+ * an nn::Linear [out, in] weight in the reference's GGUF files) -> the
+ * GEMV layouts of W^T: a transpose of the int8 values and of the f16 block
+ * scales, no arithmetic. One thread per output word (k fastest, so the
+ * reads of a weight row are consecutive), then one per scale quad. */
+extern "C" __global__ void __launch_bounds__(256) nsrk_gemv_q8_from_q8_0(const nsr_q8_0_conv_args a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t K = a.K, nb = K >> 5, quads = (int64_t)a.N >> 2;
+  const int64_t nw = quads * K;
+  const int64_t rowb = nb * 34; /* bytes per weight row */
+  if (i < nw) {
+    const int64_t q = i / K, k = i - q * K; /* column quad q, row k of W^T */
+    uint32_t w = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int64_t n = a.t4 ? t4_src_col(q, c, a.glu_n) : 4 * q + c;
+      w |= (uint32_t)a.blocks[n * rowb + (k >> 5) * 34 + 2 + (k & 31)] << (8 * c);
+    }
+    if (a.t4)
+      a.qs[i] = w;
+    else
+      a.qs[k * quads + q] = w;
+  } else if (i < nw + quads * nb) {
+    const int64_t j = i - nw;
+    const int64_t q = j / nb, b = j - q * nb;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int64_t n = a.t4 ? t4_src_col(q, c, a.glu_n) : 4 * q + c;
+      const uint16_t d = *(const uint16_t*)(a.blocks + n * rowb + b * 34);
+      if (a.t4)
+        a.scales[4 * j + c] = d;
+      else
+        a.scales[b * a.N + n] = d;
+    }
+  }
+}
+
 #define NSR_GEMV_REF(XN, XDT, ON, ODT)                                                                  \
   extern "C" __global__ void __launch_bounds__(256) nsrk_gemv_q8_##XN##_##ON(const nsr_gemv_args a) {   \
     gemv_ref<XDT, ODT, GEMV_PLAIN>(a);                                                                  \

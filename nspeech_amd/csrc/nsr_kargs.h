@@ -115,6 +115,16 @@ typedef struct nsr_q8_pack_args {
   int32_t pad_;
 } nsr_q8_pack_args;
 
+typedef struct nsr_q8_0_conv_args {
+  const uint8_t* blocks;   /* GGUF Q8_0 weight [N rows][K/32 blocks] of {f16 d; int8 qs[32]} */
+  uint32_t* qs;            /* repacked [K, N/4] words, or t4 tiles [N/4][K] */
+  uint16_t* scales;        /* repacked [K/32, N], or t4 [N/4][K/32][4] */
+  int32_t N;
+  int32_t K;
+  int32_t t4;              /* 0: repacked layout, 1: t4 tiles */
+  int32_t glu_n;           /* t4 GLU: output columns (N = 2 glu_n); 0 = plain */
+} nsr_q8_0_conv_args;
+
 typedef struct nsr_ew_args {
   const void* a;
   const void* b;

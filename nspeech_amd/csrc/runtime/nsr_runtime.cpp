@@ -808,6 +808,39 @@ nsr_status nsr_q8_pack_t4(const uint32_t* qs, const uint16_t* scales, int64_t K,
   return launch("nsrk_gemv_q8t4_pack", cdiv_u(total, 256), 1, 256, 0, stream, params);
 }
 
+static nsr_status q8_0_convert(const void* blocks, int64_t N, int64_t K, int t4, int glu, uint32_t* qs,
+                               uint16_t* scales, nsr_stream_t stream, const char* what) {
+  if (!blocks || !qs || !scales) return fail(NSR_ERR_BAD_ARG, "%s: null pointer", what);
+  if (N <= 0 || K <= 0 || K % 32 != 0 || N % 16 != 0 || (glu && N % 32 != 0) || K > (1LL << 30) ||
+      N > (1LL << 28) || N * K > (1LL << 40))
+    return fail(NSR_ERR_BAD_ARG, "%s: bad shape N=%lld K=%lld (K %% 32 == 0, N %% 16 == 0%s)", what, (long long)N,
+                (long long)K, glu ? ", N % 32 == 0 for GLU" : "");
+  if (!aligned(blocks, 2) || !aligned(qs, 16) || !aligned(scales, 16))
+    return fail(NSR_ERR_BAD_ARG, "%s: misaligned pointer (blocks 2 bytes, outputs 16 bytes)", what);
+  nsr_q8_0_conv_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.blocks = (const uint8_t*)blocks;
+  a.qs = qs;
+  a.scales = scales;
+  a.N = (int32_t)N;
+  a.K = (int32_t)K;
+  a.t4 = t4;
+  a.glu_n = glu ? (int32_t)(N / 2) : 0;
+  const int64_t total = (N / 4) * K + (N / 4) * (K / 32);
+  void* params[] = {&a};
+  return launch("nsrk_gemv_q8_from_q8_0", cdiv_u(total, 256), 1, 256, 0, stream, params);
+}
+
+nsr_status nsr_q8_0_to_gemv_q8(const void* blocks, int64_t N, int64_t K, uint32_t* qs, uint16_t* scales,
+                               nsr_stream_t stream) {
+  return q8_0_convert(blocks, N, K, 0, 0, qs, scales, stream, "q8_0_to_gemv_q8");
+}
+
+nsr_status nsr_q8_0_to_t4(const void* blocks, int64_t N, int64_t K, int glu, uint32_t* t4_qs, uint16_t* t4_scales,
+                          nsr_stream_t stream) {
+  return q8_0_convert(blocks, N, K, 1, glu ? 1 : 0, t4_qs, t4_scales, stream, "q8_0_to_t4");
+}
+
 nsr_status nsr_gemv_q8_t4(const void* x, nsr_dtype x_dtype, const uint32_t* t4_qs, const uint16_t* t4_scales,
                           const float* bias, void* out, nsr_dtype out_dtype, int64_t K, int64_t N,
                           nsr_stream_t stream) {

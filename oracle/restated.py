@@ -287,3 +287,37 @@ def q8_pack_t4(qs, scales_bits, glu=False):
     tiles = np.ascontiguousarray(q8[:, cols].transpose(1, 0, 2))        # [T, K, 4]
     tsc = np.ascontiguousarray(sc[:, cols].transpose(1, 0, 2))          # [T, K/32, 4]
     return tiles.reshape(-1).view(np.uint32).copy(), tsc.reshape(-1).copy()
+
+
+def q8_0_quantize(x):
+    """GGUF Q8_0 quantisation of a float32 matrix [rows, cols] (cols % 32 == 0)
+    as the reference's quantizer calls it (QTensor::quantize(.., Q8_0),
+    tools/quantize-moonshine/src/main.rs:118), following ggml's published
+    quantize_row_q8_0 (candle's BlockQ8_0::from_float): per 32 values,
+    d = max|x| / 127 (f32), q = round(x / d) half away from zero (0 when d is
+    0), stored as {f16 d; int8 q[32]}. Returns uint8 [rows, cols/32*34]."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, cols = x.shape
+    xb = x.reshape(rows, cols // 32, 32)
+    amax = np.max(np.abs(xb), axis=2)
+    d = (amax / np.float32(127.0)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        idv = np.where(d != 0, np.float32(1.0) / d, np.float32(0.0)).astype(np.float32)
+    v = (xb * idv[:, :, None]).astype(np.float32)
+    q = (np.sign(v) * np.floor(np.abs(v) + np.float32(0.5))).astype(np.int8)   # round half away from zero
+    out = np.empty((rows, cols // 32, 34), np.uint8)
+    out[:, :, 0:2] = d.astype(np.float16).view(np.uint8).reshape(rows, cols // 32, 2)
+    out[:, :, 2:] = q.view(np.uint8)
+    return out.reshape(rows, cols // 32 * 34)
+
+
+def q8_0_to_gemv_q8(blocks, N, K):
+    """A GGUF Q8_0 weight W [N, K] (rows of 34-byte blocks) as the repacked
+    Q8 layout of W^T: qs u32 [K, N/4] (qs[k] byte c of word w = int8 of
+    W[4w + c, k]) and scales f16 bits [K/32, N] (W's block scales,
+    transposed)."""
+    b = np.ascontiguousarray(blocks, np.uint8).reshape(N, K // 32, 34)
+    d = np.ascontiguousarray(b[:, :, 0:2]).view(np.uint16).reshape(N, K // 32)
+    q = np.ascontiguousarray(b[:, :, 2:]).reshape(N, K)
+    qs = np.ascontiguousarray(q.T).view(np.uint32).reshape(K, N // 4)
+    return qs, np.ascontiguousarray(d.T)

@@ -108,6 +108,12 @@ def test_version_and_header_is_plain_c():
     lambda L: L.nsr_gemv_q8_t4(18, 1, 16, 16, NULL, 16, 1, 64, 64, NULL),
     lambda L: L.nsr_gemv_q8_t4_bias_glu(16, 1, 16, 16, NULL, 16, 1, 64, 40, NULL),
     lambda L: L.nsr_gemv_q8_t4_resadd_ln(16, 1, 16, 16, NULL, 16, 16, 1, 16, 1, 64, 64, C.c_float(1e-5), NULL),
+    # GGUF Q8_0 -> GEMV layouts: N not a multiple of 16, GLU with N not a multiple of 32, odd blocks pointer,
+    # K not a multiple of 32
+    lambda L: L.nsr_q8_0_to_gemv_q8(16, 40, 64, 16, 16, NULL),
+    lambda L: L.nsr_q8_0_to_t4(16, 48, 64, 1, 16, 16, NULL),
+    lambda L: L.nsr_q8_0_to_gemv_q8(17, 64, 64, 16, 16, NULL),
+    lambda L: L.nsr_q8_0_to_t4(16, 64, 48, 0, 16, 16, NULL),
 ])
 def test_invalid_arguments_are_rejected_before_any_launch(call):
     L = abi.lib()
