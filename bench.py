@@ -46,8 +46,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workloads", default="c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,q8fc1,q8fc2,q8fc1r,q8fc2r",
-                    help="comma list of c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,q8fc1,q8fc2,q8fc1r,q8fc2r,copy")
+    ap.add_argument("--workloads", default="c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,q8fc1,q8fc2,q8fc1r,q8fc2r,q8conv",
+                    help="comma list of c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,q8fc1,q8fc2,q8fc1r,q8fc2r,q8conv,copy")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline (0 = skip)")
     ap.add_argument("--no-rotate", action="store_true", help="one buffer set (warm MALL) for all timings")
     return ap.parse_args()
@@ -246,6 +246,25 @@ def build_workload(name):
                     f"f16 norm [{dim}] (two launches)")
             kern = "nsrk_gemv_q8t4_h_f16_b1024" if t4 else "nsrk_gemv_q8_h_f16"
         return Workload(name, desc, alg, wbytes, make_set, launch, kern, "i8xf16->f32")
+
+    if name == "q8conv":
+        # Load-time conversion of a GGUF Q8_0 nn::Linear weight (the decoder fc1 [2*2560, 640] as the file
+        # stores it: 5120 rows of 20 34-byte blocks) to t4 GLU tiles on the device (nsr_q8_0_to_t4): a byte
+        # transpose, HBM-bound. Random block bytes stand in for the quantised weight (the kernel moves bytes).
+        g = configs.rng(1008)
+        N, K = 5120, 640
+        src = torch.from_numpy(g.integers(0, 256, N * K // 32 * 34, dtype=np.uint8)).to(dev)
+
+        def make_set(_):
+            return {"b": src.clone(), "q": torch.empty(N * K // 4, dtype=torch.int32, device=dev),
+                    "s": torch.empty(N * K // 32, dtype=torch.float16, device=dev)}
+
+        def launch(s):
+            abi.check(L.nsr_q8_0_to_t4(s["b"].data_ptr(), N, K, 1, s["q"].data_ptr(), s["s"].data_ptr(), stream()))
+
+        alg = N * K // 32 * 34 + N * K + N * K // 32 * 2
+        return Workload(name, f"GGUF Q8_0 weight [{N},{K}] -> t4 GLU tiles (load-time conversion)", alg, alg,
+                        make_set, launch, "nsrk_gemv_q8_from_q8_0", "u8")
 
     if name == "c4a":
         c = configs.c4a()
