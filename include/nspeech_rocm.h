@@ -248,6 +248,57 @@ nsr_status nsr_glu_silu(const void* fc1, void* out, nsr_dtype dtype, int64_t n,
 nsr_status nsr_residual_add(const void* x, const void* res, void* out,
                             nsr_dtype dtype, int64_t n, nsr_stream_t stream);
 
+/* ---- Kokoro resblock conv1d (MFMA) ----------------------------------------- */
+
+/* out [B, C_out, T_out] f32 = conv1d(x [B, C_in, T_in] f32, w [C_out, C_in, K]
+ * f16) + bias [C_out] f16 (or NULL), stride 1, zero padding `padding` on both
+ * sides, dilation `dilation`: T_out = T_in + 2 padding - dilation (K - 1).
+ * f32 accuracy on f16 matrix cores (each activation is split into two f16
+ * halves; f32 accumulation). Requirements: C_in % 16 == 0; (K - 1) *
+ * dilation within the LDS budget (about 200 columns of halo at C_in chunks
+ * of 128); stride != 1 returns NSR_ERR_UNSUPPORTED. Packs the weights into
+ * stream-ordered scratch on every call; callers that convolve repeatedly
+ * pack once with nsr_conv1d_pack_f16 and call nsr_conv1d_f16w_packed.
+ * Replaces conv1d_f32io (kernels/kokoro_kernels.py:773-816; one batch per
+ * call there) and Candle's conv1d + bias broadcast_add in
+ * ResBlock::forward (src/kokoro/decoder.rs:1368-1376). */
+nsr_status nsr_conv1d_f32io(const float* x, const void* w, const void* bias, float* out, int64_t B,
+                            int64_t C_in, int64_t C_out, int64_t T_in, int64_t K, int64_t stride,
+                            int64_t padding, int64_t dilation, nsr_stream_t stream);
+
+/* Weights [C_out, C_in, K] f16 -> the packed [C_out, K, C_in] f16 layout the
+ * conv kernels read (16-byte aligned output, C_out*C_in*K halfs). No
+ * counterpart in the reference; done once at load. */
+nsr_status nsr_conv1d_pack_f16(const void* w, int64_t C_out, int64_t C_in, int64_t K, void* w_packed,
+                               nsr_stream_t stream);
+
+/* nsr_conv1d_f32io over packed weights, plus an optional residual [B, C_out,
+ * T_out] f32 added in the epilogue (NULL = none; the `h + residual` that ends
+ * each ResBlock iteration, src/kokoro/decoder.rs:1378). */
+nsr_status nsr_conv1d_f16w_packed(const float* x, const void* w_packed, const void* bias,
+                                  const float* residual, float* out, int64_t B, int64_t C_in,
+                                  int64_t C_out, int64_t T_in, int64_t K, int64_t padding,
+                                  int64_t dilation, nsr_stream_t stream);
+
+/* One ResBlock stage with the AdaIN1d + Snake of the conv input fused into
+ * the conv's load (src/kokoro/decoder.rs:1364-1376):
+ *   y   = snake((1 + gamma) * (x - mean) / sqrt(var + eps) + beta, alpha)
+ *         (per (b, ci) row statistics over T, as nsr_adain_snake_f32)
+ *   out = conv1d(y, w_packed) + bias (+ residual)
+ * x [B, C_in, T] f32; gamma/beta/alpha as nsr_adain_snake_f32 (F32 or F16,
+ * batch strides); y is never written to memory. Two launches (row
+ * statistics, then the fused conv) and 8 bytes per row of stream-ordered
+ * scratch. Replaces adain + snake_activation_tensor + conv1d + bias of
+ * ResBlock::forward (:1364-1376; Metal: adain_snake then conv1d_f32io,
+ * src/kokoro/gpu_decoder.rs:886-950). */
+nsr_status nsr_adain_snake_conv1d_f32(const float* x, const void* gamma, const void* beta,
+                                      const void* alpha, nsr_dtype param_dtype,
+                                      int64_t gamma_bstride, int64_t beta_bstride,
+                                      const void* w_packed, const void* bias,
+                                      const float* residual, float* out, int64_t B, int64_t C_in,
+                                      int64_t C_out, int64_t T, int64_t K, int64_t padding,
+                                      int64_t dilation, float eps, nsr_stream_t stream);
+
 /* ---- Repacked-Q8 GEMV (decoder projections at M = 1) ---------------------- */
 
 /* Weights W [K, NW] in the repacked Q8 layout of the reference's decoder

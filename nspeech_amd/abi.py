@@ -71,6 +71,11 @@ def lib() -> C.CDLL:
                                             C.c_float, _P]
         L.nsr_q8_pack_t4.argtypes = [_P, _P, _I64, _I64, C.c_int, _P, _P, _P]
         L.nsr_q8_0_to_gemv_q8.argtypes = [_P, _I64, _I64, _P, _P, _P]
+        L.nsr_conv1d_f32io.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]
+        L.nsr_conv1d_pack_f16.argtypes = [_P, _I64, _I64, _I64, _P, _P]
+        L.nsr_conv1d_f16w_packed.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]
+        L.nsr_adain_snake_conv1d_f32.argtypes = [_P, _P, _P, _P, C.c_int, _I64, _I64, _P, _P, _P, _P, _I64, _I64,
+                                                 _I64, _I64, _I64, _I64, _I64, C.c_float, _P]
         L.nsr_q8_0_to_t4.argtypes = [_P, _I64, _I64, C.c_int, _P, _P, _P]
         L.nsr_gemv_q8_t4.argtypes = [_P, C.c_int, _P, _P, _P, _P, C.c_int, _I64, _I64, _P]
         L.nsr_gemv_q8_t4_bias_glu.argtypes = [_P, C.c_int, _P, _P, _P, _P, C.c_int, _I64, _I64, _P]
@@ -81,6 +86,8 @@ def lib() -> C.CDLL:
                      "nsr_rotary_partial_interleaved_f32", "nsr_adain_snake_f32", "nsr_q8_0_embed_gather",
                      "nsr_activation", "nsr_glu_silu", "nsr_residual_add", "nsr_gemv_q8",
                      "nsr_gemv_q8_bias_glu", "nsr_gemv_q8_resadd_ln", "nsr_q8_pack_t4", "nsr_gemv_q8_t4", "nsr_q8_0_to_gemv_q8", "nsr_q8_0_to_t4",
+                     "nsr_conv1d_f32io", "nsr_conv1d_pack_f16", "nsr_conv1d_f16w_packed",
+                     "nsr_adain_snake_conv1d_f32",
                      "nsr_gemv_q8_t4_bias_glu", "nsr_gemv_q8_t4_resadd_ln"):
             getattr(L, name).restype = C.c_int
         _lib = L
@@ -358,3 +365,54 @@ def gemv_q8_t4_resadd_ln(x, w: Q8T4, residual, ln_weight, *, eps=1e-5, out_f32=N
                                          _ptr(out_f32), _ptr(ln_weight), _dt(ln_weight), _ptr(norm), _dt(norm),
                                          w.K, dim, eps, _stream(stream)))
     return out_f32, norm
+
+
+# ------------------------------------------------------ Kokoro conv1d ---
+
+def _conv_tout(T, K, padding, dilation):
+    return T + 2 * padding - dilation * (K - 1)
+
+
+def conv1d_f32io(x, w, bias=None, *, padding=0, dilation=1, out=None, stream=None):
+    """x f32 [B, C_in, T]; w f16 [C_out, C_in, K]; bias f16 [C_out] or None."""
+    B, C_in, T = x.shape
+    C_out, _, K = w.shape
+    if out is None:
+        out = torch.empty((B, C_out, _conv_tout(T, K, padding, dilation)), dtype=torch.float32, device=x.device)
+    check(lib().nsr_conv1d_f32io(_ptr(x), _ptr(w), _ptr(bias), _ptr(out), B, C_in, C_out, T, K, 1, padding,
+                                 dilation, _stream(stream)))
+    return out
+
+
+def conv1d_pack_f16(w, *, stream=None):
+    """[C_out, C_in, K] f16 -> packed [C_out, K, C_in] f16."""
+    C_out, C_in, K = w.shape
+    wp = torch.empty((C_out, K, C_in), dtype=torch.float16, device=w.device)
+    check(lib().nsr_conv1d_pack_f16(_ptr(w), C_out, C_in, K, _ptr(wp), _stream(stream)))
+    return wp
+
+
+def conv1d_f16w_packed(x, wp, bias=None, residual=None, *, padding=0, dilation=1, out=None, stream=None):
+    B, C_in, T = x.shape
+    C_out, K, _ = wp.shape
+    if out is None:
+        out = torch.empty((B, C_out, _conv_tout(T, K, padding, dilation)), dtype=torch.float32, device=x.device)
+    check(lib().nsr_conv1d_f16w_packed(_ptr(x), _ptr(wp), _ptr(bias), _ptr(residual), _ptr(out), B, C_in, C_out, T,
+                                       K, padding, dilation, _stream(stream)))
+    return out
+
+
+def adain_snake_conv1d(x, gamma, beta, alpha, wp, bias=None, residual=None, *, padding=0, dilation=1, eps=1e-5,
+                       out=None, stream=None):
+    """conv1d(snake(AdaIN(x))) + bias (+ residual); x f32 [B, C_in, T]; gamma/beta [C_in] or [B, C_in];
+    alpha [C_in] (f32 or f16); wp packed f16 [C_out, K, C_in]."""
+    B, C_in, T = x.shape
+    C_out, K, _ = wp.shape
+    if out is None:
+        out = torch.empty((B, C_out, _conv_tout(T, K, padding, dilation)), dtype=torch.float32, device=x.device)
+    gs = C_in if gamma.dim() == 2 else 0
+    bs = C_in if beta.dim() == 2 else 0
+    check(lib().nsr_adain_snake_conv1d_f32(_ptr(x), _ptr(gamma), _ptr(beta), _ptr(alpha), _dt(gamma), gs, bs,
+                                           _ptr(wp), _ptr(bias), _ptr(residual), _ptr(out), B, C_in, C_out, T, K,
+                                           padding, dilation, eps, _stream(stream)))
+    return out

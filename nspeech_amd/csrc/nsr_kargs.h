@@ -125,6 +125,27 @@ typedef struct nsr_q8_0_conv_args {
   int32_t glu_n;           /* t4 GLU: output columns (N = 2 glu_n); 0 = plain */
 } nsr_q8_0_conv_args;
 
+typedef struct nsr_conv_args {
+  const float* x;          /* [B, C_in, T_in] */
+  const uint16_t* w;       /* packed f16 [C_out][K][C_in] */
+  const uint16_t* bias;    /* f16 [C_out] or NULL */
+  const float* residual;   /* [B, C_out, T_out] or NULL */
+  float* out;              /* [B, C_out, T_out] */
+  const float* stats;      /* [B*C_in][2] mean, rstd (AdaIN+Snake input) */
+  const void* gamma;       /* AdaIN+Snake parameters, as nsr_adain_args */
+  const void* beta;
+  const void* alpha;
+  int64_t gamma_bstride;
+  int64_t beta_bstride;
+  int32_t B, C_in, C_out, T_in, T_out, K, padding, dilation, pdt, pad_;
+} nsr_conv_args;
+
+typedef struct nsr_conv_pack_args {
+  const uint16_t* w;       /* f16 [C_out][C_in][K] */
+  uint16_t* wp;            /* f16 [C_out][K][C_in] */
+  int64_t C_out, C_in, K;
+} nsr_conv_pack_args;
+
 typedef struct nsr_ew_args {
   const void* a;
   const void* b;

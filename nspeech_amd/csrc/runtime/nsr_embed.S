@@ -19,5 +19,6 @@ NSR_EMBED(rotary)
 NSR_EMBED(adain_snake)
 NSR_EMBED(elementwise)
 NSR_EMBED(gemv_q8)
+NSR_EMBED(conv1d)
 
     .section .note.GNU-stack, "", @progbits

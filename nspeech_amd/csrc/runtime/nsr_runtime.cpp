@@ -30,6 +30,7 @@ extern "C" const unsigned char nsr_co_rotary[];
 extern "C" const unsigned char nsr_co_adain_snake[];
 extern "C" const unsigned char nsr_co_elementwise[];
 extern "C" const unsigned char nsr_co_gemv_q8[];
+extern "C" const unsigned char nsr_co_conv1d[];
 
 namespace {
 
@@ -42,7 +43,8 @@ const Unit kUnits[] = {{"q8_0_gather", nsr_co_q8_0_gather},
                        {"rotary", nsr_co_rotary},
                        {"adain_snake", nsr_co_adain_snake},
                        {"elementwise", nsr_co_elementwise},
-                       {"gemv_q8", nsr_co_gemv_q8}};
+                       {"gemv_q8", nsr_co_gemv_q8},
+                       {"conv1d", nsr_co_conv1d}};
 constexpr int kNumUnits = sizeof(kUnits) / sizeof(kUnits[0]);
 
 constexpr int kMaxDevices = 64;
@@ -133,7 +135,8 @@ int unit_of(const std::string& name) {
   };
   static const P map[] = {{"nsrk_q8_0_", 0}, {"nsrk_ln_", 1},    {"nsrk_resln_", 1}, {"nsrk_rope_", 2},
                           {"nsrk_adain_", 3}, {"nsrk_silu_", 4}, {"nsrk_gelu_", 4},  {"nsrk_glu_", 4},
-                          {"nsrk_add_", 4},  {"nsrk_gemv_", 5}};
+                          {"nsrk_add_", 4},  {"nsrk_gemv_", 5},
+                          {"nsrk_conv1d_", 6}};
   for (const P& p : map)
     if (name.compare(0, std::strlen(p.prefix), p.prefix) == 0) return p.unit;
   return -1;
@@ -180,6 +183,26 @@ nsr_status launch(const std::string& name, unsigned gx, unsigned gy, unsigned bl
   return NSR_OK;
 }
 
+// 3-D grid launch (grid.z = batch).
+nsr_status launch3(const std::string& name, unsigned gx, unsigned gy, unsigned gz, unsigned block, unsigned shmem,
+                   nsr_stream_t stream, void** params) {
+  DeviceModule* dm = nullptr;
+  nsr_status st = current_module(&dm);
+  if (st != NSR_OK) return st;
+  hipFunction_t f;
+  st = get_function(dm, name, &f);
+  if (st != NSR_OK) return st;
+  if (shmem > (unsigned)dm->max_lds)
+    return fail(NSR_ERR_UNSUPPORTED, "%s needs %u bytes of LDS, device allows %d", name.c_str(), shmem,
+                dm->max_lds);
+  hipError_t e = hipModuleLaunchKernel(f, gx, gy, gz, block, 1, 1, shmem, (hipStream_t)stream, params, nullptr);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(NSR_ERR_HIP, "launch %s: %s", name.c_str(), hipGetErrorString(e));
+  }
+  return NSR_OK;
+}
+
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
 int dt_size(nsr_dtype d) { return d == NSR_F32 ? 4 : 2; }
@@ -215,8 +238,8 @@ int nsr_kernel_count(void) {
                                 "nsrk_rope_compute_f32",     "nsrk_adain_row_b256_v5_l0",
                                 "nsrk_adain_row_b512_v44_l14", "nsrk_adain_stats",
                                 "nsrk_adain_apply",          "nsrk_gelu_f32_v",
-                                "nsrk_gemv_q8_f16_f16",      "nsrk_gemv_q8_glu_f16_f16",
-                                "nsrk_gemv_q8_resln_f16_f16"};
+                                "nsrk_gemv_q8_f16_f16",      "nsrk_gemv_q8t4_glu_f16_f16_b256",
+                                "nsrk_conv1d_f16x2",         "nsrk_conv1d_adain_snake_f16x2"};
   int n = 0;
   for (const char* p : probe) {
     hipFunction_t f;
@@ -861,6 +884,184 @@ nsr_status nsr_gemv_q8_t4_resadd_ln(const void* x, nsr_dtype x_dtype, const uint
                                     int64_t K, int64_t dim, float eps, nsr_stream_t stream) {
   return gemv_launch(kGemvResLn, true, x, x_dtype, t4_qs, t4_scales, nullptr, norm, norm_dtype, residual, out_f32,
                      ln_weight, w_dtype, K, dim, eps, stream, "gemv_q8_t4_resadd_ln");
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------- Kokoro conv1d --
+
+namespace {
+
+constexpr int kCvTT = 128, kCvCO = 128, kCvCI = 128, kCvS = kCvCI + 8, kCvNcoef = 12;
+
+nsr_status conv_validate(const float* x, const void* w, uintptr_t w_align, float* out, int64_t B, int64_t C_in,
+                         int64_t C_out, int64_t T_in, int64_t K, int64_t padding, int64_t dilation, int64_t* T_out,
+                         const char* what) {
+  if (!x || !w || !out) return fail(NSR_ERR_BAD_ARG, "%s: null pointer", what);
+  if (B < 0 || C_in <= 0 || C_out <= 0 || T_in < 0 || K <= 0 || padding < 0 || dilation <= 0 || B > 65535 ||
+      C_out > 65535LL * kCvCO || C_in > (1 << 20) || K > 4096 || dilation > (1 << 20) || padding > (1 << 24) ||
+      T_in > 0x3fffffffLL)
+    return fail(NSR_ERR_BAD_ARG, "%s: bad shape B=%lld C_in=%lld C_out=%lld T=%lld K=%lld pad=%lld dil=%lld", what,
+                (long long)B, (long long)C_in, (long long)C_out, (long long)T_in, (long long)K, (long long)padding,
+                (long long)dilation);
+  if (C_in % 16 != 0) return fail(NSR_ERR_UNSUPPORTED, "%s: C_in=%lld must be a multiple of 16", what, (long long)C_in);
+  *T_out = T_in + 2 * padding - dilation * (K - 1);
+  if (*T_out <= 0 && T_in > 0)
+    return fail(NSR_ERR_BAD_ARG, "%s: empty output (T_in + 2 padding < dilation (K - 1) + 1)", what);
+  if (!aligned(x, 4) || !aligned(out, 4) || !aligned(w, w_align))
+    return fail(NSR_ERR_BAD_ARG, "%s: misaligned pointer (weights need %u bytes)", what, (unsigned)w_align);
+  return NSR_OK;
+}
+
+nsr_status conv_launch(bool fused, nsr_conv_args& a, nsr_stream_t stream, const char* what) {
+  DeviceModule* dm = nullptr;
+  nsr_status st = current_module(&dm);
+  if (st != NSR_OK) return st;
+  const int64_t TL = kCvTT + (int64_t)(a.K - 1) * a.dilation;
+  const int64_t lds = 2 * TL * kCvS * 2 + (fused ? kCvCI * kCvNcoef * 4 : 0);
+  if (lds > dm->max_lds)
+    return fail(NSR_ERR_UNSUPPORTED, "%s: (K - 1) * dilation = %lld needs %lld bytes of LDS, device allows %d", what,
+                (long long)((a.K - 1) * (int64_t)a.dilation), (long long)lds, dm->max_lds);
+  void* params[] = {&a};
+  const unsigned gx = cdiv_u(a.T_out, kCvTT), gy = cdiv_u(a.C_out, kCvCO);
+  return launch3(fused ? "nsrk_conv1d_adain_snake_f16x2" : "nsrk_conv1d_f16x2", gx, gy, (unsigned)a.B, 256,
+                 (unsigned)lds, stream, params);
+}
+
+}  // namespace
+
+extern "C" {
+
+nsr_status nsr_conv1d_pack_f16(const void* w, int64_t C_out, int64_t C_in, int64_t K, void* w_packed,
+                               nsr_stream_t stream) {
+  if (!w || !w_packed) return fail(NSR_ERR_BAD_ARG, "conv1d_pack_f16: null pointer");
+  if (C_out <= 0 || C_in <= 0 || K <= 0 || C_out * C_in * K > (1LL << 34))
+    return fail(NSR_ERR_BAD_ARG, "conv1d_pack_f16: bad shape");
+  if (!aligned(w, 2) || !aligned(w_packed, 16)) return fail(NSR_ERR_BAD_ARG, "conv1d_pack_f16: misaligned pointer");
+  nsr_conv_pack_args a;
+  a.w = (const uint16_t*)w;
+  a.wp = (uint16_t*)w_packed;
+  a.C_out = C_out;
+  a.C_in = C_in;
+  a.K = K;
+  void* params[] = {&a};
+  return launch("nsrk_conv1d_pack", cdiv_u(C_out * C_in * K, 256), 1, 256, 0, stream, params);
+}
+
+nsr_status nsr_conv1d_f16w_packed(const float* x, const void* w_packed, const void* bias, const float* residual,
+                                  float* out, int64_t B, int64_t C_in, int64_t C_out, int64_t T_in, int64_t K,
+                                  int64_t padding, int64_t dilation, nsr_stream_t stream) {
+  int64_t T_out = 0;
+  nsr_status st = conv_validate(x, w_packed, 16, out, B, C_in, C_out, T_in, K, padding, dilation, &T_out,
+                                "conv1d_f16w_packed");
+  if (st != NSR_OK) return st;
+  if ((bias && !aligned(bias, 2)) || (residual && !aligned(residual, 4)))
+    return fail(NSR_ERR_BAD_ARG, "conv1d_f16w_packed: misaligned bias or residual");
+  if (B == 0 || T_out <= 0) return NSR_OK;  // T_in == 0 with T_out > 0: output = bias (+ residual)
+  nsr_conv_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.x = x;
+  a.w = (const uint16_t*)w_packed;
+  a.bias = (const uint16_t*)bias;
+  a.residual = residual;
+  a.out = out;
+  a.B = (int32_t)B;
+  a.C_in = (int32_t)C_in;
+  a.C_out = (int32_t)C_out;
+  a.T_in = (int32_t)T_in;
+  a.T_out = (int32_t)T_out;
+  a.K = (int32_t)K;
+  a.padding = (int32_t)padding;
+  a.dilation = (int32_t)dilation;
+  return conv_launch(false, a, stream, "conv1d_f16w_packed");
+}
+
+nsr_status nsr_conv1d_f32io(const float* x, const void* w, const void* bias, float* out, int64_t B, int64_t C_in,
+                            int64_t C_out, int64_t T_in, int64_t K, int64_t stride, int64_t padding,
+                            int64_t dilation, nsr_stream_t stream) {
+  if (stride != 1) return fail(NSR_ERR_UNSUPPORTED, "conv1d_f32io: stride %lld (only stride 1 is built)",
+                               (long long)stride);
+  int64_t T_out = 0;
+  nsr_status st = conv_validate(x, w, 2, out, B, C_in, C_out, T_in, K, padding, dilation, &T_out, "conv1d_f32io");
+  if (st != NSR_OK) return st;
+  if (bias && !aligned(bias, 2)) return fail(NSR_ERR_BAD_ARG, "conv1d_f32io: misaligned bias");
+  if (B == 0 || T_out <= 0) return NSR_OK;
+  // pack the weights into stream-ordered scratch, convolve, free
+  uint16_t* wp = nullptr;
+  const size_t bytes = (size_t)(C_out * C_in * K) * 2;
+  hipError_t e = hipMallocAsync((void**)&wp, bytes, (hipStream_t)stream);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(NSR_ERR_HIP, "conv1d_f32io: hipMallocAsync: %s", hipGetErrorString(e));
+  }
+  st = nsr_conv1d_pack_f16(w, C_out, C_in, K, wp, stream);
+  if (st == NSR_OK) st = nsr_conv1d_f16w_packed(x, wp, bias, nullptr, out, B, C_in, C_out, T_in, K, padding, dilation, stream);
+  (void)hipFreeAsync(wp, (hipStream_t)stream);
+  return st;
+}
+
+nsr_status nsr_adain_snake_conv1d_f32(const float* x, const void* gamma, const void* beta, const void* alpha,
+                                      nsr_dtype param_dtype, int64_t gamma_bstride, int64_t beta_bstride,
+                                      const void* w_packed, const void* bias, const float* residual, float* out,
+                                      int64_t B, int64_t C_in, int64_t C_out, int64_t T, int64_t K, int64_t padding,
+                                      int64_t dilation, float eps, nsr_stream_t stream) {
+  const char* what = "adain_snake_conv1d";
+  if (!gamma || !beta || !alpha) return fail(NSR_ERR_BAD_ARG, "%s: null parameter pointer", what);
+  if (param_dtype != NSR_F32 && param_dtype != NSR_F16) return fail(NSR_ERR_BAD_ARG, "%s: params must be F32 or F16", what);
+  if (gamma_bstride < 0 || beta_bstride < 0) return fail(NSR_ERR_BAD_ARG, "%s: negative batch stride", what);
+  if (!(eps >= 0.0f)) return fail(NSR_ERR_BAD_ARG, "%s: eps must be >= 0", what);
+  int64_t T_out = 0;
+  nsr_status st = conv_validate(x, w_packed, 16, out, B, C_in, C_out, T, K, padding, dilation, &T_out, what);
+  if (st != NSR_OK) return st;
+  if ((bias && !aligned(bias, 2)) || (residual && !aligned(residual, 4)))
+    return fail(NSR_ERR_BAD_ARG, "%s: misaligned bias or residual", what);
+  if (B == 0 || T_out <= 0) return NSR_OK;
+  if (T == 0) return fail(NSR_ERR_BAD_ARG, "%s: T == 0 (an empty row has no statistics)", what);
+  // per-(b, ci) mean and 1/sqrt(var + eps) of x in stream-ordered scratch
+  float* stats = nullptr;
+  hipError_t e = hipMallocAsync((void**)&stats, (size_t)(B * C_in) * 2 * sizeof(float), (hipStream_t)stream);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(NSR_ERR_HIP, "%s: hipMallocAsync: %s", what, hipGetErrorString(e));
+  }
+  nsr_adain_args s;
+  std::memset(&s, 0, sizeof(s));
+  s.x = x;
+  s.stats = stats;
+  s.n_rows = B * C_in;
+  s.T = T;
+  s.C = (int32_t)C_in;
+  s.eps = eps;
+  s.inv_t = 1.0f / (float)T;
+  void* p1[] = {&s};
+  st = launch("nsrk_adain_stats", (unsigned)(B * C_in), 1, 1024, 0, stream, p1);
+  if (st == NSR_OK) {
+    nsr_conv_args a;
+    std::memset(&a, 0, sizeof(a));
+    a.x = x;
+    a.w = (const uint16_t*)w_packed;
+    a.bias = (const uint16_t*)bias;
+    a.residual = residual;
+    a.out = out;
+    a.stats = stats;
+    a.gamma = gamma;
+    a.beta = beta;
+    a.alpha = alpha;
+    a.gamma_bstride = gamma_bstride;
+    a.beta_bstride = beta_bstride;
+    a.B = (int32_t)B;
+    a.C_in = (int32_t)C_in;
+    a.C_out = (int32_t)C_out;
+    a.T_in = (int32_t)T;
+    a.T_out = (int32_t)T_out;
+    a.K = (int32_t)K;
+    a.padding = (int32_t)padding;
+    a.dilation = (int32_t)dilation;
+    a.pdt = param_dtype == NSR_F32 ? 0 : 1;
+    st = conv_launch(true, a, stream, what);
+  }
+  (void)hipFreeAsync(stats, (hipStream_t)stream);
+  return st;
 }
 
 }  // extern "C"

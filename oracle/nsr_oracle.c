@@ -511,3 +511,33 @@ ORC_API void orc_gemv_q8_resadd_ln(const float* x, const uint32_t* qs, const uin
     norm_f16[c] = f32_to_f16((out_f32[c] - mean) * inv_std * f16_to_f32(ln_w_f16[c]));
   free(acc);
 }
+
+/* ------------------------------------------------- Kokoro resblock conv --- */
+
+/* conv1d_f32io (kernels/kokoro_kernels.py:773-816) over a batch: x f32
+ * [B, C_in, T_in], w f16 [C_out, C_in, K], bias f16 [C_out] (or NULL),
+ * out f32 [B, C_out, T_out]; per output acc = 0, then for ck in
+ * 0 .. C_in*K-1 (c = ck / K, k = ck % K): t_in = t*stride - padding +
+ * k*dilation, acc += x[c, t_in] * w[co, c, k] (x = 0 outside [0, T_in)),
+ * then acc += bias[co]. f32 arithmetic in that order. */
+ORC_API void orc_conv1d_f32io(const float* x, const uint16_t* w, const uint16_t* bias, float* out, int64_t B,
+                              int64_t C_in, int64_t C_out, int64_t T_in, int64_t T_out, int64_t K, int64_t stride,
+                              int64_t padding, int64_t dilation, int nthreads) {
+#pragma omp parallel for num_threads(nthreads) schedule(static) collapse(2)
+  for (int64_t b = 0; b < B; ++b)
+    for (int64_t co = 0; co < C_out; ++co) {
+      const uint16_t* wr = w + co * C_in * K;
+      float* orow = out + (b * C_out + co) * T_out;
+      const float bv = bias ? f16_to_f32(bias[co]) : 0.0f;
+      for (int64_t t = 0; t < T_out; ++t) {
+        float acc = 0.0f;
+        for (int64_t ck = 0; ck < C_in * K; ++ck) {
+          const int64_t c = ck / K, k = ck % K;
+          const int64_t ti = t * stride - padding + k * dilation;
+          if (ti < 0 || ti >= T_in) continue;
+          acc = acc + x[(b * C_in + c) * T_in + ti] * f16_to_f32(wr[ck]);
+        }
+        orow[t] = acc + bv;
+      }
+    }
+}

@@ -53,6 +53,8 @@ def lib() -> C.CDLL:
         L.orc_rotary_f32.argtypes = [_f32p, _f32p, _I64, _I64, _I64, _I64, C.c_int, C.c_float, _I64, _f32p, C.c_int]
         L.orc_adain_snake_f32.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _I64, _I64, _I64, _I64, _I64,
                                           C.c_float, C.c_int]
+        L.orc_conv1d_f32io.argtypes = [_f32p, _u16p, C.c_void_p, _f32p, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                                       _I64, _I64, C.c_int]
         _lib = L
     return _lib
 
@@ -321,3 +323,20 @@ def q8_0_to_gemv_q8(blocks, N, K):
     q = np.ascontiguousarray(b[:, :, 2:]).reshape(N, K)
     qs = np.ascontiguousarray(q.T).view(np.uint32).reshape(K, N // 4)
     return qs, np.ascontiguousarray(d.T)
+
+
+def conv1d_f32io(x, w_bits, bias_bits=None, stride=1, padding=0, dilation=1, nthreads=1):
+    """conv1d_f32io over a batch: x f32 [B, C_in, T_in], w f16 bits [C_out, C_in, K],
+    bias f16 bits [C_out] or None -> f32 [B, C_out, T_out]."""
+    x = _c(x, np.float32)
+    if x.ndim == 2:
+        x = x[None]
+    w = _c(w_bits, np.uint16)
+    B, C_in, T_in = x.shape
+    C_out, _, K = w.shape
+    T_out = (T_in + 2 * padding - dilation * (K - 1) - 1) // stride + 1
+    out = np.empty((B, C_out, T_out), np.float32)
+    b = None if bias_bits is None else _c(bias_bits, np.uint16)
+    lib().orc_conv1d_f32io(x.ravel(), w.ravel(), _ptr(b), out.ravel(), B, C_in, C_out, T_in, T_out, K, stride,
+                           padding, dilation, nthreads)
+    return out

@@ -466,3 +466,57 @@ def test_q8_pack_t4_is_a_column_permutation():
         scu = np.empty_like(sc)
         scu[:, order] = tsc.transpose(1, 0, 2).reshape(K // 32, NW)
         assert np.array_equal(q8u, q8) and np.array_equal(scu, sc)
+
+
+# ------------------------------------------------ Kokoro resblock conv1d ---
+
+def _conv_f64(x, w, bias, stride, padding, dilation):
+    B, C_in, T_in = x.shape
+    C_out, _, K = w.shape
+    T_out = (T_in + 2 * padding - dilation * (K - 1) - 1) // stride + 1
+    xp = np.zeros((B, C_in, T_in + 2 * padding + stride * T_out + dilation * K), np.float64)
+    xp[:, :, padding:padding + T_in] = x
+    out = np.zeros((B, C_out, T_out))
+    for k in range(K):
+        cols = xp[:, :, k * dilation: k * dilation + stride * (T_out - 1) + 1: stride]   # [B, C_in, T_out]
+        out += np.einsum("oc,bct->bot", w[:, :, k].astype(np.float64), cols)
+    absum = np.zeros_like(out)
+    for k in range(K):
+        cols = np.abs(xp[:, :, k * dilation: k * dilation + stride * (T_out - 1) + 1: stride])
+        absum += np.einsum("oc,bct->bot", np.abs(w[:, :, k].astype(np.float64)), cols)
+    if bias is not None:
+        out += bias.astype(np.float64)[None, :, None]
+    return out, absum
+
+
+@pytest.mark.parametrize("C_in,C_out,T,K,stride,padding,dilation", [
+    (16, 8, 50, 3, 1, 1, 1), (8, 12, 40, 7, 1, 9, 3), (12, 4, 33, 11, 1, 25, 5), (6, 6, 31, 4, 2, 3, 1)])
+def test_conv1d_f32io_matches_f64(C_in, C_out, T, K, stride, padding, dilation):
+    g = configs.rng(80 + K)
+    x = g.standard_normal((2, C_in, T)).astype(np.float32)
+    w = (g.standard_normal((C_out, C_in, K)) * 0.2).astype(np.float16)
+    b = g.standard_normal(C_out).astype(np.float16)
+    got = R.conv1d_f32io(x, w.view(np.uint16), b.view(np.uint16), stride, padding, dilation)
+    ref, absum = _conv_f64(x, w, b, stride, padding, dilation)
+    assert got.shape == ref.shape
+    n = C_in * K + 1
+    gam = n * 2.0 ** -24 / (1 - n * 2.0 ** -24)
+    assert np.all(np.abs(got - ref) <= gam * (absum + np.abs(b.astype(np.float64))[None, :, None]) + 1e-30)
+
+
+def test_conv1d_f32io_identity_and_delta():
+    g = configs.rng(85)
+    x = g.standard_normal((1, 8, 20)).astype(np.float32)
+    eye = np.eye(8, dtype=np.float16)[:, :, None]
+    assert_bitexact(R.conv1d_f32io(x, eye.view(np.uint16)), x, "K=1 identity")
+    # delta input: out[co, t] = w[co, c*, k] where t - padding + k*dilation = t*
+    w = (g.standard_normal((5, 3, 7)) * 0.3).astype(np.float16)
+    d = np.zeros((1, 3, 40), np.float32)
+    d[0, 1, 17] = 1.0
+    out = R.conv1d_f32io(d, w.view(np.uint16), None, 1, 9, 3)
+    exp = np.zeros((1, 5, 40), np.float32)
+    for k in range(7):
+        t = 17 + 9 - 3 * k
+        if 0 <= t < 40:
+            exp[0, :, t] = w[:, 1, k].astype(np.float32)
+    assert_bitexact(out, exp, "delta response")
