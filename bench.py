@@ -46,8 +46,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workloads", default="c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,q8fc1,q8fc2,q8fc1r,q8fc2r,q8conv",
-                    help="comma list of c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,q8fc1,q8fc2,q8fc1r,q8fc2r,q8conv,copy")
+    ap.add_argument("--workloads", default="c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,q8fc1,q8fc2,q8fc1r,q8fc2r,q8conv,kconv3,kconv11,kconv3u",
+                    help="comma list of c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,q8fc1,q8fc2,q8fc1r,q8fc2r,q8conv,kconv3,kconv11,kconv3u,copy")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline (0 = skip)")
     ap.add_argument("--no-rotate", action="store_true", help="one buffer set (warm MALL) for all timings")
     return ap.parse_args()
@@ -58,10 +58,10 @@ def parse():
 class Workload:
     """Buffer sets and a launch(i) closure for one config."""
 
-    def __init__(self, name, desc, alg_bytes, set_bytes, make_set, launch, kernel, dtype):
+    def __init__(self, name, desc, alg_bytes, set_bytes, make_set, launch, kernel, dtype, flops=0):
         self.name, self.desc, self.alg_bytes = name, desc, alg_bytes
         self.set_bytes, self.make_set, self.launch = set_bytes, make_set, launch
-        self.kernel, self.dtype = kernel, dtype
+        self.kernel, self.dtype, self.flops = kernel, dtype, flops
 
 
 def build_workload(name):
@@ -266,6 +266,44 @@ def build_workload(name):
         return Workload(name, f"GGUF Q8_0 weight [{N},{K}] -> t4 GLU tiles (load-time conversion)", alg, alg,
                         make_set, launch, "nsrk_gemv_q8_from_q8_0", "u8")
 
+    if name in ("kconv3", "kconv11", "kconv3u"):
+        # One Kokoro ResBlock stage at the final upsample shape (x [8, 128, 115200], as config c4b):
+        # conv1(snake(AdaIN(x))) + bias, K = 3 dilation 1 (kconv3) or K = 11 dilation 5 (kconv11), fused
+        # (row statistics + the fused conv); kconv3u = the same stage unfused (AdaIN+Snake kernel, then the conv).
+        c = configs.c4b()
+        x0 = T(c["x"])
+        B, C, TT = c["x"].shape
+        g_, b_, a_ = T(c["gamma"]), T(c["beta"]), T(c["alpha"])
+        K, dil = (11, 5) if name == "kconv11" else (3, 1)
+        pad = (K - 1) * dil // 2
+        g = configs.rng(1009)
+        wp = abi.conv1d_pack_f16(torch.from_numpy((g.standard_normal((C, C, K)) * 0.05).astype(np.float16)).to(dev))
+        bias = torch.from_numpy(g.standard_normal(C).astype(np.float16)).to(dev)
+        gs = C if c["gamma"].ndim == 2 else 0
+        y = torch.empty_like(x0) if name == "kconv3u" else None
+
+        def make_set(_):
+            return {"x": x0, "o": torch.empty_like(x0)}
+
+        def launch(s):
+            if name == "kconv3u":
+                abi.check(L.nsr_adain_snake_f32(s["x"].data_ptr(), g_.data_ptr(), b_.data_ptr(), a_.data_ptr(), 0, gs,
+                                                gs, y.data_ptr(), B, C, TT, 1e-5, stream()))
+                abi.check(L.nsr_conv1d_f16w_packed(y.data_ptr(), wp.data_ptr(), bias.data_ptr(), None,
+                                                   s["o"].data_ptr(), B, C, C, TT, K, pad, dil, stream()))
+            else:
+                abi.check(L.nsr_adain_snake_conv1d_f32(s["x"].data_ptr(), g_.data_ptr(), b_.data_ptr(), a_.data_ptr(),
+                                                       0, gs, gs, wp.data_ptr(), bias.data_ptr(), None,
+                                                       s["o"].data_ptr(), B, C, C, TT, K, pad, dil, 1e-5, stream()))
+
+        alg = 2 * x0.numel() * 4
+        flops = 2 * C * C * K * TT * B
+        return Workload(name, f"ResBlock stage AdaIN+Snake -> conv1d K={K} dil={dil} f32 x[{B},{C},{TT}]"
+                        + (" (unfused: two kernels + y round trip)" if name == "kconv3u" else " (fused)"),
+                        alg, x0.numel() * 4, make_set, launch,
+                        "nsrk_conv1d_f16x2" if name == "kconv3u" else "nsrk_conv1d_adain_snake_f16x2", "f32",
+                        flops=flops)
+
     if name == "c4a":
         c = configs.c4a()
         x0, r0 = T(c["x"]), T(c["res"])
@@ -373,6 +411,7 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms):
         "frac_of_peak": round(gbs(cold_us) / HBM_PEAK_GBS, 4),
         "warm_us_per_call": round(warm_us, 3),
         "warm_GBs": round(gbs(warm_us), 1),
+        **({"TFLOPs": round(w.flops / (cold_us * 1e-6) / 1e12, 2)} if w.flops else {}),
         # an event pair around each single call adds the runtime's event
         # overhead (a few us) to small kernels; reported for reference only
         "event_pair_us_median": round(statistics.median(ev_per), 3),

@@ -892,7 +892,7 @@ nsr_status nsr_gemv_q8_t4_resadd_ln(const void* x, nsr_dtype x_dtype, const uint
 
 namespace {
 
-constexpr int kCvTT = 128, kCvCO = 128, kCvCI = 128, kCvS = kCvCI + 8, kCvNcoef = 12;
+constexpr int kCvTT = 64, kCvCO = 128, kCvCI = 128, kCvS = kCvCI + 8, kCvJT = 2;
 
 nsr_status conv_validate(const float* x, const void* w, uintptr_t w_align, float* out, int64_t B, int64_t C_in,
                          int64_t C_out, int64_t T_in, int64_t K, int64_t padding, int64_t dilation, int64_t* T_out,
@@ -918,8 +918,8 @@ nsr_status conv_launch(bool fused, nsr_conv_args& a, nsr_stream_t stream, const 
   nsr_status st = current_module(&dm);
   if (st != NSR_OK) return st;
   const int64_t TL = kCvTT + (int64_t)(a.K - 1) * a.dilation;
-  const int64_t lds = 2 * TL * kCvS * 2 + (fused ? kCvCI * kCvNcoef * 4 : 0);
-  if (lds > dm->max_lds)
+  const int64_t lds = (2 * TL + kCvCO) * kCvS * 2; /* y hi, y lo, one tap's weights */
+  if (TL > 64 * kCvJT || lds > dm->max_lds)
     return fail(NSR_ERR_UNSUPPORTED, "%s: (K - 1) * dilation = %lld needs %lld bytes of LDS, device allows %d", what,
                 (long long)((a.K - 1) * (int64_t)a.dilation), (long long)lds, dm->max_lds);
   void* params[] = {&a};
