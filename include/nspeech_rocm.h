@@ -259,9 +259,11 @@ nsr_status nsr_residual_add(const void* x, const void* res, void* out,
  * of 128); stride != 1 returns NSR_ERR_UNSUPPORTED. Packs the weights into
  * stream-ordered scratch on every call; callers that convolve repeatedly
  * pack once with nsr_conv1d_pack_f16 and call nsr_conv1d_f16w_packed.
- * Replaces conv1d_f32io (kernels/kokoro_kernels.py:773-816; one batch per
- * call there) and Candle's conv1d + bias broadcast_add in
- * ResBlock::forward (src/kokoro/decoder.rs:1368-1376). */
+ * Replaces KokoroGpuBackend::conv1d_f32 (src/kokoro/gpu_backend.rs:165-167;
+ * Metal impl src/kokoro/gpu_decoder.rs:840, which runs conv1d_f32io,
+ * kernels/kokoro_kernels.py:773-816, or an im2col + f16 matmul that rounds
+ * x to f16) and Candle's conv1d + bias broadcast_add in ResBlock::forward
+ * (src/kokoro/decoder.rs:1366-1367, 1373-1374). */
 nsr_status nsr_conv1d_f32io(const float* x, const void* w, const void* bias, float* out, int64_t B,
                             int64_t C_in, int64_t C_out, int64_t T_in, int64_t K, int64_t stride,
                             int64_t padding, int64_t dilation, nsr_stream_t stream);
