@@ -14,9 +14,11 @@
  * input channels it stages y for the 128 columns plus the (K-1)*dilation
  * halo in LDS, transposed to [t][ci] so a B fragment is one 16-byte LDS
  * read, then runs the K * 8 reduction steps of v_mfma_f32_32x32x16_f16.
- * The tile is sized so that two workgroups fit on a CU (<= 80 KB of LDS for
- * (K - 1) * dilation <= 32): one stages its input while the other
- * multiplies.
+ * Workgroups are persistent (about two per CU) and walk the tiles; each
+ * loads the next tile's input into registers right after staging the
+ * current one, so the load latency overlaps the current tile's MFMAs,
+ * weight staging and stores. The tile is sized so that two workgroups fit
+ * on a CU (<= 80 KB of LDS for (K - 1) * dilation <= 32).
  * The weights of one tap k ([128 co][128 ci], 34 KB) sit in LDS too, shared
  * by the two waves of each channel block; tap k+1's slice is loaded into
  * registers while tap k's MFMAs run.
@@ -60,32 +62,54 @@ NSR_DEV cv_coef cv_row_coef(const nsr_conv_args& a, int b, int ci) {
   return c;
 }
 
-/* Halo'd tile columns are staged 64 at a time (one per lane); at most
- * CV_JT x 64 columns: (K - 1) * dilation <= CV_JT * 64 - CV_TT. */
-#define CV_JT 2
 
-template <bool FUSED>
+template <bool FUSED, int NP>
 NSR_DEV void conv_body(const nsr_conv_args& a) {
   extern __shared__ uint16_t cv_lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wco = wave >> 1, wt = wave & 1; /* the wave's 64-channel and 32-column block */
-  const int t0 = blockIdx.x * CV_TT, co0 = blockIdx.y * CV_CO, b = blockIdx.z;
+  const int hl = lane >> 5, l32 = lane & 31;
   const int TL = CV_TT + (a.K - 1) * a.dilation; /* staged columns */
   uint16_t* yhi = cv_lds;
   uint16_t* ylo = cv_lds + TL * CV_S;
   uint16_t* wb = cv_lds + 2 * TL * CV_S; /* weight slice [CV_CO][CV_S] of one tap k */
-  const int hl = lane >> 5, l32 = lane & 31;
+  const int n_t = (a.T_out + CV_TT - 1) / CV_TT, n_co = (a.C_out + CV_CO - 1) / CV_CO;
+  const int n_tiles = n_t * n_co * a.B, n_ch = (a.C_in + CV_CI - 1) / CV_CI;
 
-  nsr_f32x16 acc[2];
-#pragma unroll
-  for (int m = 0; m < 2; ++m)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc[m][i] = 0.f;
+  /* tile -> (batch, first output channel, first column); columns fastest */
+  auto coords = [&](int tile, int& b, int& co0, int& t0) {
+    const int r = tile / n_t;
+    t0 = (tile - r * n_t) * CV_TT;
+    b = r / n_co;
+    co0 = (r - b * n_co) * CV_CO;
+  };
 
-  /* weight slice staging: thread owns 16-byte chunks id = tid + 256 i of the
-   * [128 co][16 chunks of 8 ci] slice */
-  nsr_uint4 wr[8];
-  auto load_w = [&](int k, int c0, int cc) {
+  /* x of one (tile, chunk), in registers: lane owns channel quad
+   * q = wave + 4 (lane / 8) (4 channels) at staged columns j = lane % 8 + 8 i,
+   * i < NP (8 NP >= TL). Indices are clamped into the row, so every load is
+   * unconditional; 8 lanes cover 32 consecutive bytes of a row per load. */
+  const int lq = wave + 4 * (lane >> 3), lj = lane & 7;
+  float xv[NP][4];
+  auto fetch = [&](int tile, int ch) {
+    int b, co0, t0;
+    coords(tile, b, co0, t0);
+    const int c0 = ch * CV_CI, nq = min(CV_CI, a.C_in - c0) >> 2;
+    if (lq >= nq) return;
+    /* this (batch, chunk)'s rows through one buffer descriptor: 32-bit offsets */
+    const nsr_rsrc xr = make_rsrc(a.x + ((int64_t)b * a.C_in + c0) * a.T_in, (uint32_t)(4 * (nq * 4) * a.T_in));
+    const uint32_t rowoff = (uint32_t)(4 * lq) * (uint32_t)a.T_in;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int tc = min(max(t0 - a.padding + lj + 8 * i, 0), a.T_in - 1);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        xv[i][r] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(xr, (rowoff + (uint32_t)(r * a.T_in) + (uint32_t)tc) * 4u, 0, 0));
+    }
+  };
+
+  nsr_uint4 wr[8]; /* one tap's weight slice, 16-byte chunks id = tid + 256 i of [128 co][16 x 8 ci] */
+  auto load_w = [&](int co0, int k, int c0, int cc) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int id = tid + 256 * i, co = id >> 4, c8 = id & 15;
@@ -102,139 +126,143 @@ NSR_DEV void conv_body(const nsr_conv_args& a) {
     }
   };
 
-  /* the staged columns of this lane: index clamped into the row (loads are
-   * unconditional), value masked to zero outside it */
-  int tcl[CV_JT];
-  bool tin[CV_JT], jin[CV_JT];
-#pragma unroll
-  for (int jt = 0; jt < CV_JT; ++jt) {
-    const int j = jt * 64 + lane, ti = t0 - a.padding + j;
-    jin[jt] = j < TL;
-    tin[jt] = ti >= 0 && ti < a.T_in;
-    tcl[jt] = min(max(ti, 0), a.T_in - 1);
-  }
-
-  for (int c0 = 0; c0 < a.C_in; c0 += CV_CI) {
-    const int cc = min(CV_CI, a.C_in - c0);
-    load_w(0, c0, cc);
-    __syncthreads(); /* the previous chunk's readers are done */
-
-    /* stage y[c0 .. c0+cc) x [t0 - padding, t0 - padding + TL) as f16 hi/lo,
-     * [t][ci]: wave w takes channel quads w, w + 4, ... (at most CV_CI / 16
-     * of them); lanes run along t; every load of the chunk is issued before
-     * the first value is used */
-    {
-      constexpr int QB = FUSED ? 2 : 4; /* quads per load batch (16 or 32 floats per lane in flight) */
-      const float* xb = a.x + ((int64_t)b * a.C_in + c0) * a.T_in;
-      const int nq = cc >> 2;
-      for (int q0 = wave; q0 < nq; q0 += 4 * QB) {
-        float v[QB][4][CV_JT];
-#pragma unroll
-        for (int i = 0; i < QB; ++i) {
-          const int q = q0 + 4 * i;
-          if (q < nq) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-#pragma unroll
-              for (int jt = 0; jt < CV_JT; ++jt) v[i][r][jt] = xb[(int64_t)(4 * q + r) * a.T_in + tcl[jt]];
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < QB; ++i) {
-          const int q = q0 + 4 * i;
-          if (q >= nq) break;
-          cv_coef cf[4];
-          if constexpr (FUSED) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) cf[r] = cv_row_coef(a, b, c0 + 4 * q + r);
-          }
-#pragma unroll
-          for (int jt = 0; jt < CV_JT; ++jt) {
-            if (!jin[jt]) continue;
-            const int j = jt * 64 + lane;
-            uint32_t hw[2], lw[2];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              float y = v[i][r][jt];
-              if constexpr (FUSED) y = snake_eval(__builtin_fmaf(y - cf[r].mean, cf[r].A, cf[r].bet), cf[r].sc);
-              y = tin[jt] ? y : 0.f;
-              const _Float16 hi = (_Float16)y;
-              const _Float16 lo = (_Float16)(y - (float)hi);
-              const uint32_t hb = h_bits(hi), lb = h_bits(lo);
-              if (r & 1) {
-                hw[r >> 1] |= hb << 16;
-                lw[r >> 1] |= lb << 16;
-              } else {
-                hw[r >> 1] = hb;
-                lw[r >> 1] = lb;
-              }
-            }
-            *(nsr_uint2*)(yhi + j * CV_S + 4 * q) = nsr_uint2{hw[0], hw[1]};
-            *(nsr_uint2*)(ylo + j * CV_S + 4 * q) = nsr_uint2{lw[0], lw[1]};
-          }
-        }
-      }
-    }
-    store_w();
-    __syncthreads();
-
-    for (int k = 0; k < a.K; ++k) {
-      if (k + 1 < a.K) load_w(k + 1, c0, cc); /* in flight during this tap's MFMAs */
-      const int yoff = (wt * 32 + l32 + k * a.dilation) * CV_S + 8 * hl;
-      const int a0 = (wco * 64 + l32) * CV_S + 8 * hl;
-      /* two reduction steps per iteration: all LDS reads first */
-      for (int g = 0; g < cc; g += 32) {
-        const bool two = g + 16 < cc;
-        nsr_h8 A[2][2], Bh[2], Bl[2];
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          const int gg = g + 16 * s2;
-          if (s2 == 1 && !two) break;
-#pragma unroll
-          for (int m = 0; m < 2; ++m) A[s2][m] = *(const nsr_h8*)(wb + a0 + m * 32 * CV_S + gg);
-          Bh[s2] = *(const nsr_h8*)(yhi + yoff + gg);
-          Bl[s2] = *(const nsr_h8*)(ylo + yoff + gg);
-        }
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          if (s2 == 1 && !two) break;
-#pragma unroll
-          for (int m = 0; m < 2; ++m) acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[s2][m], Bh[s2], acc[m], 0, 0, 0);
-#pragma unroll
-          for (int m = 0; m < 2; ++m) acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[s2][m], Bl[s2], acc[m], 0, 0, 0);
-        }
-      }
-      if (k + 1 < a.K) {
-        __syncthreads(); /* every wave is done with tap k's slice */
-        store_w();
-        __syncthreads();
-      }
-    }
-  }
-
-  /* epilogue: lane holds rows 8(i/4) + 4 hl + i%4 of column l32 of each 32 x 32 tile */
-  const int t = t0 + wt * 32 + l32;
-  if (t < a.T_out) {
+  if ((int)blockIdx.x >= n_tiles) return;
+  fetch(blockIdx.x, 0);
+  for (int tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+    int b, co0, t0;
+    coords(tile, b, co0, t0);
+    nsr_f32x16 acc[2];
 #pragma unroll
     for (int m = 0; m < 2; ++m)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int co = co0 + wco * 64 + m * 32 + 8 * (i >> 2) + 4 * hl + (i & 3);
-        if (co >= a.C_out) continue;
-        const int64_t o = ((int64_t)b * a.C_out + co) * a.T_out + t;
-        float v = acc[m][i];
-        if (a.bias) v += f16_bits_to_f32(a.bias[co]);
-        if (a.residual) v += a.residual[o];
-        a.out[o] = v;
+      for (int i = 0; i < 16; ++i) acc[m][i] = 0.f;
+    for (int ch = 0; ch < n_ch; ++ch) {
+      const int c0 = ch * CV_CI, cc = min(CV_CI, a.C_in - c0), nq = cc >> 2;
+      load_w(co0, 0, c0, cc);
+      __syncthreads(); /* the previous item's readers of y and the weight slice are done */
+
+      /* stage y = x (or snake(AdaIN(x))) as f16 hi/lo, [t][ci]; a lane's four
+       * rows are transformed one row at a time (one row's coefficients live) */
+      if (lq < nq) {
+        if constexpr (FUSED) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const cv_coef cf = cv_row_coef(a, b, c0 + 4 * lq + r);
+#pragma unroll
+            for (int i = 0; i < NP; ++i) xv[i][r] = snake_eval(__builtin_fmaf(xv[i][r] - cf.mean, cf.A, cf.bet), cf.sc);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+          const int j = lj + 8 * i;
+          if (j >= TL) continue;
+          const int ti = t0 - a.padding + j;
+          const bool in = ti >= 0 && ti < a.T_in;
+          uint32_t hw[2], lw[2];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float y = in ? xv[i][r] : 0.f;
+            const _Float16 hi = (_Float16)y;
+            const _Float16 lo = (_Float16)(y - (float)hi);
+            const uint32_t hb = h_bits(hi), lb = h_bits(lo);
+            if (r & 1) {
+              hw[r >> 1] |= hb << 16;
+              lw[r >> 1] |= lb << 16;
+            } else {
+              hw[r >> 1] = hb;
+              lw[r >> 1] = lb;
+            }
+          }
+          *(nsr_uint2*)(yhi + j * CV_S + 4 * lq) = nsr_uint2{hw[0], hw[1]};
+          *(nsr_uint2*)(ylo + j * CV_S + 4 * lq) = nsr_uint2{lw[0], lw[1]};
+        }
       }
+      /* next item's input: in flight during this item's MFMAs and stores */
+      {
+        int ntile = tile, nch = ch + 1;
+        if (nch == n_ch) {
+          nch = 0;
+          ntile += gridDim.x;
+        }
+        if (ntile < n_tiles) fetch(ntile, nch);
+      }
+      store_w();
+      __syncthreads();
+
+      for (int k = 0; k < a.K; ++k) {
+        if (k + 1 < a.K) load_w(co0, k + 1, c0, cc); /* in flight during this tap's MFMAs */
+        const int yoff = (wt * 32 + l32 + k * a.dilation) * CV_S + 8 * hl;
+        const int a0 = (wco * 64 + l32) * CV_S + 8 * hl;
+        for (int g = 0; g < cc; g += 16) {
+          nsr_h8 A[2];
+#pragma unroll
+          for (int m = 0; m < 2; ++m) A[m] = *(const nsr_h8*)(wb + a0 + m * 32 * CV_S + g);
+          const nsr_h8 Bh = *(const nsr_h8*)(yhi + yoff + g);
+          const nsr_h8 Bl = *(const nsr_h8*)(ylo + yoff + g);
+#pragma unroll
+          for (int m = 0; m < 2; ++m) acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[m], Bh, acc[m], 0, 0, 0);
+#pragma unroll
+          for (int m = 0; m < 2; ++m) acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[m], Bl, acc[m], 0, 0, 0);
+        }
+        if (k + 1 < a.K) {
+          __syncthreads(); /* every wave is done with tap k's slice */
+          store_w();
+          __syncthreads();
+        }
+      }
+    }
+
+    /* epilogue: the accumulators (lane: rows 8(i/4) + 4 hl + i%4 of column
+     * l32 of each 32 x 32 tile) go through LDS (the y area, free once every
+     * wave is past its MFMAs) so that each row segment is written with
+     * 16-byte stores, 16 lanes per 64-column row */
+    __syncthreads();
+    float* ot = (float*)cv_lds; /* [CV_CO][CV_TT + 1] */
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        ot[(wco * 64 + m * 32 + 8 * (i >> 2) + 4 * hl + (i & 3)) * (CV_TT + 1) + wt * 32 + l32] = acc[m][i];
+    __syncthreads();
+    const bool vec = (a.pad_ & 1) != 0; /* T_out % 4 == 0 and 16-byte aligned out / residual */
+#pragma unroll
+    for (int it = 0; it < CV_CO / 16; ++it) {
+      const int row = it * 16 + (tid >> 4), c4 = (tid & 15) * 4;
+      const int co = co0 + row, t = t0 + c4;
+      if (co >= a.C_out || t >= a.T_out) continue;
+      const float bv = a.bias ? f16_bits_to_f32(a.bias[co]) : 0.f;
+      const int64_t o = ((int64_t)b * a.C_out + co) * a.T_out + t;
+      const float* src = ot + row * (CV_TT + 1) + c4;
+      if (vec && t + 3 < a.T_out) {
+        nsr_float4 v = {src[0] + bv, src[1] + bv, src[2] + bv, src[3] + bv};
+        if (a.residual) v += *(const nsr_float4*)(a.residual + o);
+        __builtin_nontemporal_store(v, (nsr_float4*)(a.out + o));
+      } else {
+        for (int e = 0; e < 4 && t + e < a.T_out; ++e) {
+          float v = src[e] + bv;
+          if (a.residual) v += a.residual[o + e];
+          a.out[o + e] = v;
+        }
+      }
+    }
   }
 }
 
-extern "C" __global__ void __launch_bounds__(256, 2) nsrk_conv1d_f16x2(const nsr_conv_args a) { conv_body<false>(a); }
+/* NP = ceil(TL / 8) staged columns per lane: TL <= 72, 96, 128 */
+/* OCC: workgroups per CU the register budget is sized for (NP 9: two, the
+ * LDS of short halos allows two; NP 12 / 16: one) */
+#define NSR_CONV(NP, OCC)                                                                                \
+  extern "C" __global__ void __launch_bounds__(256, OCC) nsrk_conv1d_f16x2_np##NP(const nsr_conv_args a) { \
+    conv_body<false, NP>(a);                                                                            \
+  }                                                                                                     \
+  extern "C" __global__ void __launch_bounds__(256, OCC)                                                \
+      nsrk_conv1d_adain_snake_f16x2_np##NP(const nsr_conv_args a) {                                     \
+    conv_body<true, NP>(a);                                                                             \
+  }
 
-extern "C" __global__ void __launch_bounds__(256, 2) nsrk_conv1d_adain_snake_f16x2(const nsr_conv_args a) {
-  conv_body<true>(a);
-}
+NSR_CONV(9, 2)
+NSR_CONV(12, 1)
+NSR_CONV(16, 1)
 
 /* [C_out][C_in][K] -> [C_out][K][C_in], one thread per weight. */
 extern "C" __global__ void __launch_bounds__(256) nsrk_conv1d_pack(const nsr_conv_pack_args a) {

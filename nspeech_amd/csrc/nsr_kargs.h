@@ -137,7 +137,8 @@ typedef struct nsr_conv_args {
   const void* alpha;
   int64_t gamma_bstride;
   int64_t beta_bstride;
-  int32_t B, C_in, C_out, T_in, T_out, K, padding, dilation, pdt, pad_;
+  int32_t B, C_in, C_out, T_in, T_out, K, padding, dilation, pdt;
+  int32_t pad_;            /* bit 0: 16-byte epilogue stores allowed */
 } nsr_conv_args;
 
 typedef struct nsr_conv_pack_args {

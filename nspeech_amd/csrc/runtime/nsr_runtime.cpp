@@ -67,6 +67,7 @@ struct DeviceModule {
   hipModule_t modules[kNumUnits] = {};
   std::unordered_map<std::string, hipFunction_t> fns;
   int max_lds = 0;
+  int n_cu = 0;
 };
 
 DeviceModule g_dev[kMaxDevices];
@@ -109,6 +110,9 @@ void load_module(DeviceModule& dm, int dev) {
   int lds = 0;
   hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   dm.max_lds = lds;
+  int ncu = 0;
+  hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+  dm.n_cu = ncu > 0 ? ncu : 256;
   dm.status = NSR_OK;
 }
 
@@ -239,7 +243,7 @@ int nsr_kernel_count(void) {
                                 "nsrk_adain_row_b512_v44_l14", "nsrk_adain_stats",
                                 "nsrk_adain_apply",          "nsrk_gelu_f32_v",
                                 "nsrk_gemv_q8_f16_f16",      "nsrk_gemv_q8t4_glu_f16_f16_b256",
-                                "nsrk_conv1d_f16x2",         "nsrk_conv1d_adain_snake_f16x2"};
+                                "nsrk_conv1d_f16x2_np9",     "nsrk_conv1d_adain_snake_f16x2_np9"};
   int n = 0;
   for (const char* p : probe) {
     hipFunction_t f;
@@ -582,7 +586,8 @@ nsr_status nsr_adain_snake_f32(const float* x, const void* gamma, const void* be
   }
   a.stats = stats;
   void* p1[] = {&a};
-  st = launch("nsrk_adain_stats", (unsigned)n_rows, 1, 1024, 0, stream, p1);
+  const bool rows16 = T % 4 == 0 && aligned(x, 16);
+  st = launch(rows16 ? "nsrk_adain_stats4" : "nsrk_adain_stats", (unsigned)n_rows, 1, 1024, 0, stream, p1);
   if (st == NSR_OK) {
     void* p2[] = {&a, &pdt};
     const int64_t gy = (T + 1023) / 1024;
@@ -892,7 +897,7 @@ nsr_status nsr_gemv_q8_t4_resadd_ln(const void* x, nsr_dtype x_dtype, const uint
 
 namespace {
 
-constexpr int kCvTT = 64, kCvCO = 128, kCvCI = 128, kCvS = kCvCI + 8, kCvJT = 2;
+constexpr int kCvTT = 64, kCvCO = 128, kCvCI = 128, kCvS = kCvCI + 8, kCvMaxTL = 128;
 
 nsr_status conv_validate(const float* x, const void* w, uintptr_t w_align, float* out, int64_t B, int64_t C_in,
                          int64_t C_out, int64_t T_in, int64_t K, int64_t padding, int64_t dilation, int64_t* T_out,
@@ -919,13 +924,21 @@ nsr_status conv_launch(bool fused, nsr_conv_args& a, nsr_stream_t stream, const 
   if (st != NSR_OK) return st;
   const int64_t TL = kCvTT + (int64_t)(a.K - 1) * a.dilation;
   const int64_t lds = (2 * TL + kCvCO) * kCvS * 2; /* y hi, y lo, one tap's weights */
-  if (TL > 64 * kCvJT || lds > dm->max_lds)
+  if (TL > kCvMaxTL || lds > dm->max_lds)
     return fail(NSR_ERR_UNSUPPORTED, "%s: (K - 1) * dilation = %lld needs %lld bytes of LDS, device allows %d", what,
                 (long long)((a.K - 1) * (int64_t)a.dilation), (long long)lds, dm->max_lds);
+  // 16-byte epilogue stores when every output (and residual) row starts 16-byte aligned
+  a.pad_ = (a.T_out % 4 == 0 && aligned(a.out, 16) && (!a.residual || aligned(a.residual, 16))) ? 1 : 0;
   void* params[] = {&a};
-  const unsigned gx = cdiv_u(a.T_out, kCvTT), gy = cdiv_u(a.C_out, kCvCO);
-  return launch3(fused ? "nsrk_conv1d_adain_snake_f16x2" : "nsrk_conv1d_f16x2", gx, gy, (unsigned)a.B, 256,
-                 (unsigned)lds, stream, params);
+  // persistent workgroups: as many as fit at once (two per CU when the LDS allows), each walking tiles
+  const int64_t tiles = (int64_t)cdiv_u(a.T_out, kCvTT) * cdiv_u(a.C_out, kCvCO) * a.B;
+  if (tiles > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "%s: too many tiles", what);
+  const int np = TL <= 72 ? 9 : TL <= 96 ? 12 : 16;  // register pairs per lane: 8 TL <= 64 np
+  // the np 9 kernels fit two workgroups per CU in registers; the others one
+  const int per_cu = (np == 9 && 2 * lds <= dm->max_lds) ? 2 : 1;
+  const int64_t groups = std::min<int64_t>(tiles, (int64_t)per_cu * dm->n_cu);
+  return launch(std::string(fused ? "nsrk_conv1d_adain_snake_f16x2_np" : "nsrk_conv1d_f16x2_np") + std::to_string(np),
+                (unsigned)groups, 1, 256, (unsigned)lds, stream, params);
 }
 
 }  // namespace
@@ -1034,7 +1047,8 @@ nsr_status nsr_adain_snake_conv1d_f32(const float* x, const void* gamma, const v
   s.eps = eps;
   s.inv_t = 1.0f / (float)T;
   void* p1[] = {&s};
-  st = launch("nsrk_adain_stats", (unsigned)(B * C_in), 1, 1024, 0, stream, p1);
+  const bool rows16 = T % 4 == 0 && aligned(x, 16);
+  st = launch(rows16 ? "nsrk_adain_stats4" : "nsrk_adain_stats", (unsigned)(B * C_in), 1, 1024, 0, stream, p1);
   if (st == NSR_OK) {
     nsr_conv_args a;
     std::memset(&a, 0, sizeof(a));
