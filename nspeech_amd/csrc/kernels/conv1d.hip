@@ -76,13 +76,26 @@ NSR_DEV void conv_body(const nsr_conv_args& a) {
   const int n_t = (a.T_out + CV_TT - 1) / CV_TT, n_co = (a.C_out + CV_CO - 1) / CV_CO;
   const int n_tiles = n_t * n_co * a.B, n_ch = (a.C_in + CV_CI - 1) / CV_CI;
 
-  /* tile -> (batch, first output channel, first column); columns fastest */
+  /* tile -> (batch, first output channel, first column); channel blocks
+   * fastest, then columns, so neighbouring tiles read the same or adjacent
+   * input columns */
   auto coords = [&](int tile, int& b, int& co0, int& t0) {
-    const int r = tile / n_t;
-    t0 = (tile - r * n_t) * CV_TT;
-    b = r / n_co;
-    co0 = (r - b * n_co) * CV_CO;
+    const int r = tile / n_co;
+    co0 = (tile - r * n_co) * CV_CO;
+    b = r / n_t;
+    t0 = (r - b * n_t) * CV_TT;
   };
+  /* The workgroups of one XCD (blockIdx % 8) walk one contiguous eighth of
+   * the tiles together, slot s = blockIdx / 8 taking its s-th, (s + S)-th,
+   * ... tile: the tiles in flight on an XCD are neighbours, so the halo
+   * columns one tile shares with the next are read from HBM once and hit
+   * that XCD's L2 the second time. (Grids that are not a multiple of 8
+   * workgroups walk the tiles in plain strided order.) */
+  const bool xcd = (gridDim.x & 7) == 0;
+  const int xid = xcd ? (int)(blockIdx.x & 7) : 0, S = xcd ? (int)(gridDim.x >> 3) : (int)gridDim.x;
+  const int slot = xcd ? (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+  const int t_lo = xcd ? (int)((int64_t)n_tiles * xid / 8) : 0;
+  const int t_hi = xcd ? (int)((int64_t)n_tiles * (xid + 1) / 8) : n_tiles;
 
   /* x of one (tile, chunk), in registers: lane owns channel quad
    * q = wave + 4 (lane / 8) (4 channels) at staged columns j = lane % 8 + 8 i,
@@ -96,7 +109,7 @@ NSR_DEV void conv_body(const nsr_conv_args& a) {
     const int c0 = ch * CV_CI, nq = min(CV_CI, a.C_in - c0) >> 2;
     if (lq >= nq) return;
     /* this (batch, chunk)'s rows through one buffer descriptor: 32-bit offsets */
-    const nsr_rsrc xr = make_rsrc(a.x + ((int64_t)b * a.C_in + c0) * a.T_in, (uint32_t)(4 * (nq * 4) * a.T_in));
+    const nsr_rsrc xr = make_rsrc_uniform(a.x + ((int64_t)b * a.C_in + c0) * a.T_in, (uint32_t)(4 * (nq * 4) * a.T_in));
     const uint32_t rowoff = (uint32_t)(4 * lq) * (uint32_t)a.T_in;
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
@@ -126,9 +139,9 @@ NSR_DEV void conv_body(const nsr_conv_args& a) {
     }
   };
 
-  if ((int)blockIdx.x >= n_tiles) return;
-  fetch(blockIdx.x, 0);
-  for (int tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+  if (t_lo + slot >= t_hi) return;
+  fetch(t_lo + slot, 0);
+  for (int tile = t_lo + slot; tile < t_hi; tile += S) {
     int b, co0, t0;
     coords(tile, b, co0, t0);
     nsr_f32x16 acc[2];
@@ -182,9 +195,9 @@ NSR_DEV void conv_body(const nsr_conv_args& a) {
         int ntile = tile, nch = ch + 1;
         if (nch == n_ch) {
           nch = 0;
-          ntile += gridDim.x;
+          ntile += S;
         }
-        if (ntile < n_tiles) fetch(ntile, nch);
+        if (ntile < t_hi) fetch(ntile, nch);
       }
       store_w();
       __syncthreads();
@@ -248,21 +261,238 @@ NSR_DEV void conv_body(const nsr_conv_args& a) {
   }
 }
 
+/*
+ * Resident-weight variant for C_in <= 128, C_out <= 128 and K <= 3 (the
+ * resblock's kernel-size-3 convs) with 16-byte aligned rows (T_out % 4 == 0):
+ * the whole packed weight tensor, [K][128 co][128 ci] f16 zero-padded, is
+ * loaded into LDS once per workgroup and stays there (<= 102 KB), so the tap
+ * loop issues no global loads and needs no barriers. One workgroup per CU
+ * (LDS), persistent over the tiles.
+ *
+ * Every tile issues the same global loads in the same order (the residual
+ * tile when RESID, then the next tile's input, with clamped indices instead
+ * of branches), so the compiler's in-order memory counter waits are exact:
+ * the epilogue waits for the residual alone and the staging for the input
+ * alone, never for loads issued after them. Bias and the per-row AdaIN +
+ * Snake coefficients are kept in registers (the coefficients reloaded only
+ * when the batch index changes). The MFMA loop loads step g + 1's operands
+ * from LDS before issuing step g's four MFMAs.
+ */
+template <bool FUSED, bool RESID, int NP>
+NSR_DEV void conv_rw_body(const nsr_conv_args& a) {
+  extern __shared__ uint16_t cv_lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wco = wave >> 1, wt = wave & 1;
+  const int hl = lane >> 5, l32 = lane & 31;
+  const int TL = CV_TT + (a.K - 1) * a.dilation;
+  uint16_t* wl = cv_lds; /* [K][CV_CO][CV_S] */
+  uint16_t* yhi = cv_lds + a.K * CV_CO * CV_S;
+  uint16_t* ylo = yhi + TL * CV_S;
+  const int n_t = (a.T_out + CV_TT - 1) / CV_TT;
+  const int n_tiles = n_t * a.B;
+  const int nq = a.C_in >> 2;
+
+  const bool xcd = (gridDim.x & 7) == 0;
+  const int xid = xcd ? (int)(blockIdx.x & 7) : 0, S = xcd ? (int)(gridDim.x >> 3) : (int)gridDim.x;
+  const int slot = xcd ? (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+  const int t_lo = xcd ? (int)((int64_t)n_tiles * xid / 8) : 0;
+  const int t_hi = xcd ? (int)((int64_t)n_tiles * (xid + 1) / 8) : n_tiles;
+  if (t_lo + slot >= t_hi) return;
+
+  /* weights, once: [C_out][K][C_in] -> [k][co][ci], zero outside the tensor */
+  for (int id = tid; id < a.K * CV_CO * 16; id += 256) {
+    const int c8 = id & 15, row = id >> 4;
+    const int k = row / CV_CO, co = row - k * CV_CO;
+    nsr_uint4 v = {0u, 0u, 0u, 0u};
+    if (co < a.C_out && 8 * c8 < a.C_in) v = *(const nsr_uint4*)(a.w + ((int64_t)co * a.K + k) * a.C_in + 8 * c8);
+    *(nsr_uint4*)(wl + row * CV_S + 8 * c8) = v;
+  }
+  /* bias of the epilogue rows it * 16 + tid / 16 */
+  float bias[CV_CO / 16];
+#pragma unroll
+  for (int it = 0; it < CV_CO / 16; ++it) {
+    const int co = it * 16 + (tid >> 4);
+    bias[it] = (a.bias && co < a.C_out) ? f16_bits_to_f32(a.bias[co]) : 0.f;
+  }
+
+  const int lq = wave + 4 * (lane >> 3), lj = lane & 7;
+  const bool live = lq < nq;
+  /* lanes past C_in read row C_in - 4.. (discarded) so every lane loads */
+  const uint32_t rowoff = (uint32_t)(4 * min(lq, nq - 1)) * (uint32_t)a.T_in;
+  float xv[NP][4];
+  auto fetch = [&](int tile) {
+    const int b = tile / n_t, t0 = (tile - b * n_t) * CV_TT;
+    const nsr_rsrc xr = make_rsrc_uniform(a.x + (int64_t)b * a.C_in * a.T_in, (uint32_t)(4 * a.C_in * a.T_in));
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int tc = min(max(t0 - a.padding + lj + 8 * i, 0), a.T_in - 1);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        xv[i][r] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(xr, (rowoff + (uint32_t)(r * a.T_in) + (uint32_t)tc) * 4u, 0, 0));
+    }
+  };
+
+  cv_coef cf[FUSED ? 4 : 1];
+  int coef_b = -1;
+  /* epilogue lane: rows it * 16 + tid / 16 (clamped for the residual load), columns c4 .. c4 + 3 */
+  const int c4 = (tid & 15) * 4;
+
+  fetch(t_lo + slot);
+  for (int tile = t_lo + slot; tile < t_hi; tile += S) {
+    const int b = tile / n_t, t0 = (tile - b * n_t) * CV_TT;
+    if constexpr (FUSED) {
+      if (b != coef_b) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) cf[r] = cv_row_coef(a, b, min(4 * lq + r, a.C_in - 1));
+        coef_b = b;
+      }
+    }
+    __syncthreads(); /* the previous tile's epilogue is done with the y area */
+
+    /* stage y (zero outside the row and for channels >= C_in), [t][ci] */
+    if constexpr (FUSED) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int i = 0; i < NP; ++i)
+          xv[i][r] = snake_eval(__builtin_fmaf(xv[i][r] - cf[r].mean, cf[r].A, cf[r].bet), cf[r].sc);
+    }
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int j = lj + 8 * i;
+      if (j >= TL) continue;
+      const int ti = t0 - a.padding + j;
+      const bool in = live && ti >= 0 && ti < a.T_in;
+      uint32_t hw[2], lw[2];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float y = in ? xv[i][r] : 0.f;
+        const _Float16 hi = (_Float16)y;
+        const _Float16 lo = (_Float16)(y - (float)hi);
+        const uint32_t hb = h_bits(hi), lb = h_bits(lo);
+        if (r & 1) {
+          hw[r >> 1] |= hb << 16;
+          lw[r >> 1] |= lb << 16;
+        } else {
+          hw[r >> 1] = hb;
+          lw[r >> 1] = lb;
+        }
+      }
+      *(nsr_uint2*)(yhi + j * CV_S + 4 * lq) = nsr_uint2{hw[0], hw[1]};
+      *(nsr_uint2*)(ylo + j * CV_S + 4 * lq) = nsr_uint2{lw[0], lw[1]};
+    }
+    /* this tile's residual, then the next tile's input (the last tile
+     * re-reads its own): both in flight during the MFMAs */
+    nsr_float4 rv[RESID ? CV_CO / 16 : 1];
+    if constexpr (RESID) {
+      const int tr = min(t0 + c4, a.T_out - 4);
+#pragma unroll
+      for (int it = 0; it < CV_CO / 16; ++it) {
+        const int co = min(it * 16 + (tid >> 4), a.C_out - 1);
+        rv[it] = *(const nsr_float4*)(a.residual + ((int64_t)b * a.C_out + co) * a.T_out + tr);
+      }
+    }
+    fetch(min(tile + S, t_hi - 1));
+    __syncthreads();
+
+    nsr_f32x16 acc[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[m][i] = 0.f;
+    {
+      /* operands of step s = (k, g) live in A[s & 1], B[s & 1]; step s + 1's
+       * are read before step s's MFMAs are issued */
+      const int wbase = (wco * 64 + l32) * CV_S + 8 * hl;
+      const int ybase = (wt * 32 + l32) * CV_S + 8 * hl;
+      nsr_h8 A[2][2], Bh[2], Bl[2];
+      auto ld = [&](int buf, int k, int g) {
+        const uint16_t* wk = wl + k * CV_CO * CV_S + wbase + g;
+        A[buf][0] = *(const nsr_h8*)wk;
+        A[buf][1] = *(const nsr_h8*)(wk + 32 * CV_S);
+        const int yo = ybase + k * a.dilation * CV_S + g;
+        Bh[buf] = *(const nsr_h8*)(yhi + yo);
+        Bl[buf] = *(const nsr_h8*)(ylo + yo);
+      };
+      ld(0, 0, 0);
+      for (int k = 0; k < a.K; ++k) {
+        const int kn = min(k + 1, a.K - 1); /* the last tap reloads its own first step (unused) */
+#pragma unroll
+        for (int g = 0; g < CV_CI; g += 16) {
+          const int cur = (g >> 4) & 1; /* CV_CI / 16 = 8 steps per tap: parity restarts each tap */
+          if (g + 16 < CV_CI) {
+            ld(cur ^ 1, k, g + 16);
+          } else {
+            ld(cur ^ 1, kn, 0);
+          }
+#pragma unroll
+          for (int m = 0; m < 2; ++m) acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[cur][m], Bh[cur], acc[m], 0, 0, 0);
+#pragma unroll
+          for (int m = 0; m < 2; ++m) acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[cur][m], Bl[cur], acc[m], 0, 0, 0);
+        }
+        /* keep the order written above: step g + 1's four LDS reads, then
+         * step g's four MFMAs (the scheduler would otherwise sink each read
+         * to its use and expose the LDS latency) */
+#pragma unroll
+        for (int g = 0; g < CV_CI; g += 16) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 4, 0); /* DS reads */
+          __builtin_amdgcn_sched_group_barrier(0x008, 4, 0); /* MFMA */
+        }
+      }
+    }
+
+    __syncthreads();
+    float* ot = (float*)yhi; /* [CV_CO][CV_TT + 1] */
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        ot[(wco * 64 + m * 32 + 8 * (i >> 2) + 4 * hl + (i & 3)) * (CV_TT + 1) + wt * 32 + l32] = acc[m][i];
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < CV_CO / 16; ++it) {
+      const int row = it * 16 + (tid >> 4), t = t0 + c4;
+      if (row >= a.C_out || t >= a.T_out) continue; /* T_out % 4 == 0: t < T_out covers t + 3 */
+      const float bv = bias[it];
+      const float* src = ot + row * (CV_TT + 1) + c4;
+      nsr_float4 v = {src[0] + bv, src[1] + bv, src[2] + bv, src[3] + bv};
+      if constexpr (RESID) v += rv[it];
+      __builtin_nontemporal_store(v, (nsr_float4*)(a.out + ((int64_t)b * a.C_out + row) * a.T_out + t));
+    }
+  }
+}
+
+#define NSR_CONV_RW1(NAME, FUSED, RESID, NP)                                                         \
+  extern "C" __global__ void __launch_bounds__(256, 1) NAME(const nsr_conv_args a) {                 \
+    conv_rw_body<FUSED, RESID, NP>(a);                                                              \
+  }
+#define NSR_CONV_RW(NP)                                                                              \
+  NSR_CONV_RW1(nsrk_conv1d_rw_f16x2_np##NP, false, false, NP)                                        \
+  NSR_CONV_RW1(nsrk_conv1d_rw_res_f16x2_np##NP, false, true, NP)                                     \
+  NSR_CONV_RW1(nsrk_conv1d_rw_adain_snake_f16x2_np##NP, true, false, NP)                             \
+  NSR_CONV_RW1(nsrk_conv1d_rw_adain_snake_res_f16x2_np##NP, true, true, NP)
+
+NSR_CONV_RW(9)
+NSR_CONV_RW(12)
+
 /* NP = ceil(TL / 8) staged columns per lane: TL <= 72, 96, 128 */
-/* OCC: workgroups per CU the register budget is sized for (NP 9: two, the
- * LDS of short halos allows two; NP 12 / 16: one) */
-#define NSR_CONV(NP, OCC)                                                                                \
+/* OCC, OCCF: workgroups per CU the register budget of the plain and the
+ * fused kernel is sized for (NP 9 plain: two, which the LDS of short halos
+ * allows; the others one: the fused NP 9 kernel needs more than 256
+ * registers per lane) */
+#define NSR_CONV(NP, OCC, OCCF)                                                                          \
   extern "C" __global__ void __launch_bounds__(256, OCC) nsrk_conv1d_f16x2_np##NP(const nsr_conv_args a) { \
     conv_body<false, NP>(a);                                                                            \
   }                                                                                                     \
-  extern "C" __global__ void __launch_bounds__(256, OCC)                                                \
+  extern "C" __global__ void __launch_bounds__(256, OCCF)                                               \
       nsrk_conv1d_adain_snake_f16x2_np##NP(const nsr_conv_args a) {                                     \
     conv_body<true, NP>(a);                                                                             \
   }
 
-NSR_CONV(9, 2)
-NSR_CONV(12, 1)
-NSR_CONV(16, 1)
+NSR_CONV(9, 2, 1)
+NSR_CONV(12, 1, 1)
+NSR_CONV(16, 1, 1)
 
 /* [C_out][C_in][K] -> [C_out][K][C_in], one thread per weight. */
 extern "C" __global__ void __launch_bounds__(256) nsrk_conv1d_pack(const nsr_conv_pack_args a) {

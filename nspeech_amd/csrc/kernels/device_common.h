@@ -314,6 +314,16 @@ NSR_DEV nsr_rsrc make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, (int)bytes, NSR_RSRC_WORD3);
 }
 
+/* make_rsrc for a base and size that are wave-uniform but that the
+ * compiler cannot prove so: readfirstlane keeps the descriptor in SGPRs
+ * instead of wrapping every load that uses it in a readfirstlane loop. */
+NSR_DEV nsr_rsrc make_rsrc_uniform(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  return make_rsrc((const void*)(((uint64_t)hi << 32) | lo), __builtin_amdgcn_readfirstlane(bytes));
+}
+
 /* 16-byte load at voff + soff (soff wave-uniform, kept in an SGPR). */
 NSR_DEV nsr_float4 buf_load4(nsr_rsrc r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(nsr_float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, NSR_AUX_NT));

@@ -934,8 +934,17 @@ nsr_status conv_launch(bool fused, nsr_conv_args& a, nsr_stream_t stream, const 
   const int64_t tiles = (int64_t)cdiv_u(a.T_out, kCvTT) * cdiv_u(a.C_out, kCvCO) * a.B;
   if (tiles > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "%s: too many tiles", what);
   const int np = TL <= 72 ? 9 : TL <= 96 ? 12 : 16;  // register pairs per lane: 8 TL <= 64 np
-  // the np 9 kernels fit two workgroups per CU in registers; the others one
-  const int per_cu = (np == 9 && 2 * lds <= dm->max_lds) ? 2 : 1;
+  // K <= 3 with one channel block each way: every weight resident in LDS, one workgroup per CU
+  const int64_t lds_rw = ((int64_t)a.K * kCvCO + 2 * TL) * kCvS * 2;
+  if (a.C_in <= kCvCI && a.C_out <= kCvCO && a.K <= 3 && np <= 12 && lds_rw <= dm->max_lds && (a.pad_ & 1) &&
+      a.T_in > 0) {
+    const int64_t groups = std::min<int64_t>(tiles, (int64_t)dm->n_cu);
+    return launch(std::string("nsrk_conv1d_rw") + (fused ? "_adain_snake" : "") + (a.residual ? "_res" : "") +
+                      "_f16x2_np" + std::to_string(np),
+                  (unsigned)groups, 1, 256, (unsigned)lds_rw, stream, params);
+  }
+  // the plain np 9 kernel fits two workgroups per CU in registers; the others one
+  const int per_cu = (!fused && np == 9 && 2 * lds <= dm->max_lds) ? 2 : 1;
   const int64_t groups = std::min<int64_t>(tiles, (int64_t)per_cu * dm->n_cu);
   return launch(std::string(fused ? "nsrk_conv1d_adain_snake_f16x2_np" : "nsrk_conv1d_f16x2_np") + std::to_string(np),
                 (unsigned)groups, 1, 256, (unsigned)lds, stream, params);

@@ -52,6 +52,10 @@ def test_conv1d_f32io_reference_self_test_shapes(dev, C, T, K, dil, pad):
     (1, 16, 16, 5, 3, 1, 1, True),       # shorter than one tile, residual
     (3, 144, 200, 257, 5, 2, 0, True),   # a 16-channel last chunk, valid padding (T_out < T_in)
     (1, 512, 128, 130, 1, 1, 0, False),  # 1x1 conv, four input chunks
+    # resident-weight kernel (C_in, C_out <= 128, K <= 3, T_out % 4 == 0):
+    (2, 64, 96, 1000, 3, 2, 2, True),    # residual, two batches
+    (1, 128, 128, 4096, 3, 5, 5, False), # 74 staged columns (the wider staging variant)
+    (1, 32, 32, 9, 2, 1, 0, True),       # K = 2, a single tile
 ])
 def test_conv1d_packed_edges(dev, B, C_in, C_out, T, K, dil, pad, res):
     say("conv1d packed", B, C_in, C_out, T, K, dil, pad, res)
@@ -73,15 +77,17 @@ def test_conv1d_packed_edges(dev, B, C_in, C_out, T, K, dil, pad, res):
     assert_close(out.cpu().numpy(), ref, RTOL_F32, "conv1d packed")
 
 
-@pytest.mark.parametrize("B,C,T,K,dil,pdt,per_batch", [
-    (1, 128, 4800, 3, 1, "f32", False),
-    (2, 128, 3000, 11, 5, "f16", True),
-    (1, 256, 1880, 7, 3, "f16", False),
+@pytest.mark.parametrize("B,C,T,K,dil,pdt,per_batch,with_res", [
+    (1, 128, 4800, 3, 1, "f32", False, True),
+    (2, 128, 3000, 11, 5, "f16", True, True),
+    (1, 256, 1880, 7, 3, "f16", False, True),
+    (3, 128, 2048, 3, 1, "f16", True, False),   # no residual; the batch index changes between tiles
+    (1, 128, 1024, 3, 5, "f32", False, True),   # 74 staged columns
 ])
-def test_adain_snake_conv1d_fused(dev, B, C, T, K, dil, pdt, per_batch):
-    """One ResBlock stage: conv1d(snake(AdaIN(x))) + bias + residual, fused,
+def test_adain_snake_conv1d_fused(dev, B, C, T, K, dil, pdt, per_batch, with_res):
+    """One ResBlock stage: conv1d(snake(AdaIN(x))) + bias (+ residual), fused,
     vs the oracle's adain_snake then conv1d_f32io (f64-pinned pieces)."""
-    say("adain_snake_conv1d", B, C, T, K, dil, pdt, per_batch)
+    say("adain_snake_conv1d", B, C, T, K, dil, pdt, per_batch, with_res)
     g = configs.rng(B + C + K)
     x = (g.standard_normal((B, C, T)) * 1.5 + 0.3).astype(np.float32)
     tdt = np.float32 if pdt == "f32" else np.float16
@@ -94,10 +100,13 @@ def test_adain_snake_conv1d_fused(dev, B, C, T, K, dil, pdt, per_batch):
     res = g.standard_normal((B, C, T)).astype(np.float32)
     wp = abi.conv1d_pack_f16(torch.from_numpy(w).cuda())
     dt = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
-    out = abi.adain_snake_conv1d(dt(x), dt(gam), dt(bet), dt(alp), wp, dt(b), dt(res), padding=pad, dilation=dil)
+    out = abi.adain_snake_conv1d(dt(x), dt(gam), dt(bet), dt(alp), wp, dt(b), dt(res) if with_res else None,
+                                 padding=pad, dilation=dil)
     torch.cuda.synchronize()
     y = R.adain_snake(x, gam.astype(np.float32), bet.astype(np.float32), alp.astype(np.float32))
-    ref = R.conv1d_f32io(y, w.view(np.uint16), b.view(np.uint16), 1, pad, dil, nthreads=16) + res
+    ref = R.conv1d_f32io(y, w.view(np.uint16), b.view(np.uint16), 1, pad, dil, nthreads=16)
+    if with_res:
+        ref = ref + res
     # the AdaIN+Snake bar carried through the conv: sum_k |w| * 1e-5 * max(|y|, 1)
     wabs = np.abs(w.astype(np.float32)).astype(np.float16)
     carried = R.conv1d_f32io(np.maximum(np.abs(y), 1.0).astype(np.float32), wabs.view(np.uint16), None, 1, pad, dil,
