@@ -45,6 +45,14 @@ NSR_DEV float conv_param(const void* p, int pdt, int64_t i) {
 
 NSR_DEV uint16_t h_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
 
+/* Value of lane (this lane ^ 1) / (this lane ^ 2) within its quad (DPP quad_perm). */
+NSR_DEV float quad_xor1(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+}
+NSR_DEV float quad_xor2(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+}
+
 /* AdaIN + Snake coefficients of input row (b, ci): y = snake((x - mean) A + beta). */
 struct cv_coef {
   float mean, A, bet;
@@ -249,7 +257,7 @@ NSR_DEV void conv_body(const nsr_conv_args& a) {
       if (vec && t + 3 < a.T_out) {
         nsr_float4 v = {src[0] + bv, src[1] + bv, src[2] + bv, src[3] + bv};
         if (a.residual) v += *(const nsr_float4*)(a.residual + o);
-        __builtin_nontemporal_store(v, (nsr_float4*)(a.out + o));
+        *(nsr_float4*)(a.out + o) = v;
       } else {
         for (int e = 0; e < 4 && t + e < a.T_out; ++e) {
           float v = src[e] + bv;
@@ -263,27 +271,36 @@ NSR_DEV void conv_body(const nsr_conv_args& a) {
 
 /*
  * Resident-weight variant for C_in <= 128, C_out <= 128 and K <= 3 (the
- * resblock's kernel-size-3 convs) with 16-byte aligned rows (T_out % 4 == 0):
- * the whole packed weight tensor, [K][128 co][128 ci] f16 zero-padded, is
- * loaded into LDS once per workgroup and stays there (<= 102 KB), so the tap
- * loop issues no global loads and needs no barriers. One workgroup per CU
- * (LDS), persistent over the tiles.
- *
- * Every tile issues the same global loads in the same order (the residual
- * tile when RESID, then the next tile's input, with clamped indices instead
- * of branches), so the compiler's in-order memory counter waits are exact:
- * the epilogue waits for the residual alone and the staging for the input
- * alone, never for loads issued after them. Bias and the per-row AdaIN +
- * Snake coefficients are kept in registers (the coefficients reloaded only
- * when the batch index changes). The MFMA loop loads step g + 1's operands
- * from LDS before issuing step g's four MFMAs.
+ * resblock's kernel-size-3 convs) with 16-byte aligned rows (T_in % 4 ==
+ * T_out % 4 == 0). The whole packed weight tensor, [K][128 co][128 ci] f16
+ * zero-padded, is loaded into LDS once per workgroup and stays there
+ * (<= 102 KB), next to one staged input tile. One 512-lane workgroup per
+ * CU, persistent over the tiles, in two roles that overlap:
+ *  - waves 0-3 (consumers) run the tile's MFMAs, 2 x 2 waves of 64 channels
+ *    x 32 columns; a 4 x 4 transpose across each lane quad (DPP) turns the
+ *    accumulators into four consecutive columns of one channel per lane, so
+ *    that they go, + bias (+ residual, loaded before the MFMAs), straight to
+ *    memory as 16-byte stores that fill whole 128-byte lines (cached stores:
+ *    measured faster here than streaming ones);
+ *  - waves 4-7 (producers) keep the input two tiles ahead: during tile n
+ *    they issue the 16-byte loads of tile n + 2, transform tile n + 1
+ *    (AdaIN + Snake when FUSED, then the f16 hi/lo split) into packed
+ *    registers while the consumers multiply, and write it to the LDS tile
+ *    once the consumers are done with tile n. A producer lane owns a 4
+ *    channel x 4 column block per step: 8 lanes cover 128 contiguous bytes
+ *    of a row, and the LDS writes of a wave fall on distinct bank pairs but
+ *    for a factor of two.
+ * Two barriers per tile. Each role's loads are unconditional (clamped
+ * indices, buffer range checks) and in a fixed order, so the compiler's
+ * in-order memory-counter waits are exact: a producer waits for tile n + 1
+ * with tile n + 2 still in flight, and a consumer waits for its residual
+ * alone.
  */
-template <bool FUSED, bool RESID, int NP>
+template <bool FUSED, bool RESID, int NU>
 NSR_DEV void conv_rw_body(const nsr_conv_args& a) {
   extern __shared__ uint16_t cv_lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wco = wave >> 1, wt = wave & 1;
-  const int hl = lane >> 5, l32 = lane & 31;
+  const bool producer = __builtin_amdgcn_readfirstlane(wave) >= 4; /* wave-uniform role */
   const int TL = CV_TT + (a.K - 1) * a.dilation;
   uint16_t* wl = cv_lds; /* [K][CV_CO][CV_S] */
   uint16_t* yhi = cv_lds + a.K * CV_CO * CV_S;
@@ -298,183 +315,254 @@ NSR_DEV void conv_rw_body(const nsr_conv_args& a) {
   const int t_lo = xcd ? (int)((int64_t)n_tiles * xid / 8) : 0;
   const int t_hi = xcd ? (int)((int64_t)n_tiles * (xid + 1) / 8) : n_tiles;
   if (t_lo + slot >= t_hi) return;
+  const int first = t_lo + slot, cnt = (t_hi - first + S - 1) / S; /* tiles of this workgroup */
+  auto tile_of = [&](int n) { return first + min(n, cnt - 1) * S; };
 
-  /* weights, once: [C_out][K][C_in] -> [k][co][ci], zero outside the tensor */
-  for (int id = tid; id < a.K * CV_CO * 16; id += 256) {
-    const int c8 = id & 15, row = id >> 4;
-    const int k = row / CV_CO, co = row - k * CV_CO;
-    nsr_uint4 v = {0u, 0u, 0u, 0u};
-    if (co < a.C_out && 8 * c8 < a.C_in) v = *(const nsr_uint4*)(a.w + ((int64_t)co * a.K + k) * a.C_in + 8 * c8);
-    *(nsr_uint4*)(wl + row * CV_S + 8 * c8) = v;
-  }
-  /* bias of the epilogue rows it * 16 + tid / 16 */
-  float bias[CV_CO / 16];
+  /* weights, once: [C_out][K][C_in] -> [k][co][ci], zero outside the
+   * tensor; all loads issued before the first LDS write (K <= 3: at most 12
+   * 16-byte chunks per lane) */
+  {
+    constexpr int NW = 3 * CV_CO * 16 / 512;
+    nsr_uint4 wv[NW];
 #pragma unroll
-  for (int it = 0; it < CV_CO / 16; ++it) {
-    const int co = it * 16 + (tid >> 4);
-    bias[it] = (a.bias && co < a.C_out) ? f16_bits_to_f32(a.bias[co]) : 0.f;
-  }
-
-  const int lq = wave + 4 * (lane >> 3), lj = lane & 7;
-  const bool live = lq < nq;
-  /* lanes past C_in read row C_in - 4.. (discarded) so every lane loads */
-  const uint32_t rowoff = (uint32_t)(4 * min(lq, nq - 1)) * (uint32_t)a.T_in;
-  float xv[NP][4];
-  auto fetch = [&](int tile) {
-    const int b = tile / n_t, t0 = (tile - b * n_t) * CV_TT;
-    const nsr_rsrc xr = make_rsrc_uniform(a.x + (int64_t)b * a.C_in * a.T_in, (uint32_t)(4 * a.C_in * a.T_in));
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      const int tc = min(max(t0 - a.padding + lj + 8 * i, 0), a.T_in - 1);
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        xv[i][r] = __builtin_bit_cast(
-            float, __builtin_amdgcn_raw_buffer_load_b32(xr, (rowoff + (uint32_t)(r * a.T_in) + (uint32_t)tc) * 4u, 0, 0));
+    for (int u = 0; u < NW; ++u) {
+      const int id = tid + 512 * u, c8 = id & 15, row = id >> 4;
+      const int k = row / CV_CO, co = row - k * CV_CO;
+      const bool ok = k < a.K && co < a.C_out && 8 * c8 < a.C_in;
+      const int64_t src = ok ? ((int64_t)co * a.K + k) * a.C_in + 8 * c8 : 0;
+      wv[u] = *(const nsr_uint4*)(a.w + src);
+      if (!ok) wv[u] = nsr_uint4{0u, 0u, 0u, 0u};
     }
-  };
-
-  cv_coef cf[FUSED ? 4 : 1];
-  int coef_b = -1;
-  /* epilogue lane: rows it * 16 + tid / 16 (clamped for the residual load), columns c4 .. c4 + 3 */
-  const int c4 = (tid & 15) * 4;
-
-  fetch(t_lo + slot);
-  for (int tile = t_lo + slot; tile < t_hi; tile += S) {
-    const int b = tile / n_t, t0 = (tile - b * n_t) * CV_TT;
-    if constexpr (FUSED) {
-      if (b != coef_b) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) cf[r] = cv_row_coef(a, b, min(4 * lq + r, a.C_in - 1));
-        coef_b = b;
+    for (int u = 0; u < NW; ++u) {
+      const int id = tid + 512 * u, row = id >> 4;
+      if (row < a.K * CV_CO) *(nsr_uint4*)(wl + row * CV_S + 8 * (id & 15)) = wv[u];
+    }
+  }
+
+  if (producer) {
+    /* lane: channel quad lq (channels 4 lq .. 4 lq + 3) x column quads
+     * jq = lane % 8 + 8 u, u < NU, of the window that starts at the
+     * 16-byte aligned column s0 = (t0 - padding) rounded down to 4 */
+    const int lq = 8 * (wave - 4) + (lane >> 3), jl = lane & 7;
+    const bool live = lq < nq;
+    const uint32_t rowoff = (uint32_t)(4 * min(lq, nq - 1)) * (uint32_t)a.T_in; /* lanes past C_in: discarded */
+    const int dsh = (-a.padding) & 3; /* (t0 - padding) - s0, the same for every tile (t0 % 64 == 0) */
+    nsr_float4 ra[NU][4], rb[NU][4];  /* [u][channel r]: 4 columns */
+    uint32_t pk[NU][4][4];            /* [u][column e]: hi channels 0-1, 2-3, lo channels 0-1, 2-3 */
+    cv_coef cf[FUSED ? 4 : 1];
+    int coef_b = -1;
+    auto fetch = [&](int n, nsr_float4 (&xv)[NU][4]) {
+      const int tile = tile_of(n);
+      const int b = tile / n_t, t0 = (tile - b * n_t) * CV_TT;
+      const int s0 = t0 - a.padding - dsh;
+      const nsr_rsrc xr = make_rsrc_uniform(a.x + (int64_t)b * a.C_in * a.T_in, (uint32_t)(4 * a.C_in * a.T_in));
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        /* a quad before column 0 wraps to a huge offset (range-checked to 0)
+         * or reads the previous row's tail; either way it is masked below */
+        const uint32_t col = (uint32_t)(s0 + 4 * (jl + 8 * u));
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          xv[u][r] = __builtin_bit_cast(nsr_float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        xr, (rowoff + (uint32_t)(r * a.T_in) + col) * 4u, 0, 0));
       }
-    }
-    __syncthreads(); /* the previous tile's epilogue is done with the y area */
-
-    /* stage y (zero outside the row and for channels >= C_in), [t][ci] */
-    if constexpr (FUSED) {
+    };
+    auto transform = [&](int n, nsr_float4 (&xv)[NU][4]) {
+      const int tile = tile_of(n);
+      const int b = tile / n_t, t0 = (tile - b * n_t) * CV_TT;
+      const int s0 = t0 - a.padding - dsh;
+      if constexpr (FUSED) {
+        if (b != coef_b) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int i = 0; i < NP; ++i)
-          xv[i][r] = snake_eval(__builtin_fmaf(xv[i][r] - cf[r].mean, cf[r].A, cf[r].bet), cf[r].sc);
-    }
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      const int j = lj + 8 * i;
-      if (j >= TL) continue;
-      const int ti = t0 - a.padding + j;
-      const bool in = live && ti >= 0 && ti < a.T_in;
-      uint32_t hw[2], lw[2];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float y = in ? xv[i][r] : 0.f;
-        const _Float16 hi = (_Float16)y;
-        const _Float16 lo = (_Float16)(y - (float)hi);
-        const uint32_t hb = h_bits(hi), lb = h_bits(lo);
-        if (r & 1) {
-          hw[r >> 1] |= hb << 16;
-          lw[r >> 1] |= lb << 16;
-        } else {
-          hw[r >> 1] = hb;
-          lw[r >> 1] = lb;
+          for (int r = 0; r < 4; ++r) cf[r] = cv_row_coef(a, b, min(4 * lq + r, a.C_in - 1));
+          coef_b = b;
         }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int u = 0; u < NU; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              xv[u][r][e] = snake_eval(__builtin_fmaf(xv[u][r][e] - cf[r].mean, cf[r].A, cf[r].bet), cf[r].sc);
       }
-      *(nsr_uint2*)(yhi + j * CV_S + 4 * lq) = nsr_uint2{hw[0], hw[1]};
-      *(nsr_uint2*)(ylo + j * CV_S + 4 * lq) = nsr_uint2{lw[0], lw[1]};
-    }
-    /* this tile's residual, then the next tile's input (the last tile
-     * re-reads its own): both in flight during the MFMAs */
-    nsr_float4 rv[RESID ? CV_CO / 16 : 1];
-    if constexpr (RESID) {
-      const int tr = min(t0 + c4, a.T_out - 4);
 #pragma unroll
-      for (int it = 0; it < CV_CO / 16; ++it) {
-        const int co = min(it * 16 + (tid >> 4), a.C_out - 1);
-        rv[it] = *(const nsr_float4*)(a.residual + ((int64_t)b * a.C_out + co) * a.T_out + tr);
-      }
-    }
-    fetch(min(tile + S, t_hi - 1));
-    __syncthreads();
-
-    nsr_f32x16 acc[2];
+      for (int u = 0; u < NU; ++u)
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
+        for (int e = 0; e < 4; ++e) {
+          const int ti = s0 + 4 * (jl + 8 * u) + e;
+          const bool in = live && ti >= 0 && ti < a.T_in;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[m][i] = 0.f;
-    {
-      /* operands of step s = (k, g) live in A[s & 1], B[s & 1]; step s + 1's
-       * are read before step s's MFMAs are issued */
-      const int wbase = (wco * 64 + l32) * CV_S + 8 * hl;
-      const int ybase = (wt * 32 + l32) * CV_S + 8 * hl;
-      nsr_h8 A[2][2], Bh[2], Bl[2];
-      auto ld = [&](int buf, int k, int g) {
-        const uint16_t* wk = wl + k * CV_CO * CV_S + wbase + g;
-        A[buf][0] = *(const nsr_h8*)wk;
-        A[buf][1] = *(const nsr_h8*)(wk + 32 * CV_S);
-        const int yo = ybase + k * a.dilation * CV_S + g;
-        Bh[buf] = *(const nsr_h8*)(yhi + yo);
-        Bl[buf] = *(const nsr_h8*)(ylo + yo);
-      };
-      ld(0, 0, 0);
-      for (int k = 0; k < a.K; ++k) {
-        const int kn = min(k + 1, a.K - 1); /* the last tap reloads its own first step (unused) */
-#pragma unroll
-        for (int g = 0; g < CV_CI; g += 16) {
-          const int cur = (g >> 4) & 1; /* CV_CI / 16 = 8 steps per tap: parity restarts each tap */
-          if (g + 16 < CV_CI) {
-            ld(cur ^ 1, k, g + 16);
-          } else {
-            ld(cur ^ 1, kn, 0);
+          for (int h = 0; h < 2; ++h) {
+            const float y0 = in ? xv[u][2 * h][e] : 0.f, y1 = in ? xv[u][2 * h + 1][e] : 0.f;
+            const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1;
+            const _Float16 l0 = (_Float16)(y0 - (float)h0), l1 = (_Float16)(y1 - (float)h1);
+            pk[u][e][h] = (uint32_t)h_bits(h0) | ((uint32_t)h_bits(h1) << 16);
+            pk[u][e][2 + h] = (uint32_t)h_bits(l0) | ((uint32_t)h_bits(l1) << 16);
           }
-#pragma unroll
-          for (int m = 0; m < 2; ++m) acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[cur][m], Bh[cur], acc[m], 0, 0, 0);
-#pragma unroll
-          for (int m = 0; m < 2; ++m) acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[cur][m], Bl[cur], acc[m], 0, 0, 0);
         }
-        /* keep the order written above: step g + 1's four LDS reads, then
-         * step g's four MFMAs (the scheduler would otherwise sink each read
-         * to its use and expose the LDS latency) */
+    };
+    auto write = [&]() {
 #pragma unroll
-        for (int g = 0; g < CV_CI; g += 16) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 4, 0); /* DS reads */
-          __builtin_amdgcn_sched_group_barrier(0x008, 4, 0); /* MFMA */
+      for (int u = 0; u < NU; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = 4 * (jl + 8 * u) + e - dsh; /* staged column */
+          if (j >= 0 && j < TL) {
+            *(nsr_uint2*)(yhi + j * CV_S + 4 * lq) = nsr_uint2{pk[u][e][0], pk[u][e][1]};
+            *(nsr_uint2*)(ylo + j * CV_S + 4 * lq) = nsr_uint2{pk[u][e][2], pk[u][e][3]};
+          }
+        }
+    };
+    /* phase n (tile n being multiplied): x(n + 2) -> `refill`, x(n + 1) in `ready` */
+    auto phase = [&](int n, nsr_float4 (&refill)[NU][4], nsr_float4 (&ready)[NU][4]) {
+      fetch(n + 2, refill);
+      transform(n + 1, ready);
+      __syncthreads(); /* consumers are done with tile n's input */
+      write();
+      __syncthreads(); /* tile n + 1's input is staged */
+    };
+    fetch(0, ra);
+    fetch(1, rb);
+    transform(0, ra);
+    write();
+    __syncthreads(); /* weights and tile 0 staged */
+    for (int n = 0; n < cnt; n += 2) {
+      phase(n, ra, rb);
+      phase(n + 1, rb, ra);
+    }
+  } else {
+    const int wco = wave >> 1, wt = wave & 1;
+    const int hl = lane >> 5, l32 = lane & 31, c4 = lane & 3;
+    /* accumulator element (m, i): channel wco*64 + m*32 + 8*(i/4) + 4*hl + i%4,
+     * column wt*32 + l32. After the quad transpose, group q = i/4 of lane
+     * (hl, l32) holds channel wco*64 + m*32 + 8*q + 4*hl + l32%4 at columns
+     * wt*32 + 4*(l32/4) .. + 3. */
+    float bias[2][4] = {};
+    if (a.bias) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int co = wco * 64 + m * 32 + 8 * q + 4 * hl + c4;
+          const float v = f16_bits_to_f32(a.bias[min(co, a.C_out - 1)]);
+          bias[m][q] = co < a.C_out ? v : 0.f;
+        }
+    }
+    const uint32_t obytes = (uint32_t)(4 * a.C_out * a.T_out);
+    const int wbase = (wco * 64 + l32) * CV_S + 8 * hl;
+    const int ybase = (wt * 32 + l32) * CV_S + 8 * hl;
+    __syncthreads(); /* weights and tile 0 staged */
+    const int cnt2 = (cnt + 1) & ~1; /* the producers' phase count */
+    for (int n = 0; n < cnt2; ++n) {
+      const int tile = tile_of(n);
+      const int b = tile / n_t, t0 = (tile - b * n_t) * CV_TT;
+      const int t = t0 + wt * 32 + 4 * (l32 >> 2); /* this lane's column quad after the transpose */
+      /* per-batch output (and residual) range: channels past C_out fall outside it */
+      nsr_float4 rv[RESID ? 2 : 1][RESID ? 4 : 1];
+      if constexpr (RESID) {
+        const nsr_rsrc rr = make_rsrc_uniform(a.residual + (int64_t)b * a.C_out * a.T_out, obytes);
+        const uint32_t tc = (uint32_t)min(t, a.T_out - 4);
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t co = (uint32_t)(wco * 64 + m * 32 + 8 * q + 4 * hl + c4);
+            rv[m][q] = __builtin_bit_cast(nsr_float4,
+                                          __builtin_amdgcn_raw_buffer_load_b128(rr, (co * (uint32_t)a.T_out + tc) * 4u, 0, 0));
+          }
+      }
+      nsr_f32x16 acc[2];
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[m][i] = 0.f;
+      {
+        /* operands of step s = (k, g) live in A[s & 1], B[s & 1]; step s + 1's
+         * are read before step s's MFMAs are issued */
+        nsr_h8 A[2][2], Bh[2], Bl[2];
+        auto ld = [&](int buf, int k, int g) {
+          const uint16_t* wk = wl + k * CV_CO * CV_S + wbase + g;
+          A[buf][0] = *(const nsr_h8*)wk;
+          A[buf][1] = *(const nsr_h8*)(wk + 32 * CV_S);
+          const int yo = ybase + k * a.dilation * CV_S + g;
+          Bh[buf] = *(const nsr_h8*)(yhi + yo);
+          Bl[buf] = *(const nsr_h8*)(ylo + yo);
+        };
+        ld(0, 0, 0);
+        for (int k = 0; k < a.K; ++k) {
+          const int kn = min(k + 1, a.K - 1); /* the last tap reloads its own first step (unused) */
+#pragma unroll
+          for (int g = 0; g < CV_CI; g += 16) {
+            const int cur = (g >> 4) & 1; /* CV_CI / 16 = 8 steps per tap: parity restarts each tap */
+            if (g + 16 < CV_CI) {
+              ld(cur ^ 1, k, g + 16);
+            } else {
+              ld(cur ^ 1, kn, 0);
+            }
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+              acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[cur][m], Bh[cur], acc[m], 0, 0, 0);
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+              acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[cur][m], Bl[cur], acc[m], 0, 0, 0);
+          }
+          /* keep the order written above: step g + 1's four LDS reads, then
+           * step g's four MFMAs (the scheduler would otherwise sink each read
+           * to its use and expose the LDS latency) */
+#pragma unroll
+          for (int g = 0; g < CV_CI; g += 16) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0); /* DS reads */
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0); /* MFMA */
+          }
         }
       }
-    }
-
-    __syncthreads();
-    float* ot = (float*)yhi; /* [CV_CO][CV_TT + 1] */
+      __syncthreads(); /* done with this tile's input */
+      if (n < cnt) {
+        const nsr_rsrc orr = make_rsrc_uniform(a.out + (int64_t)b * a.C_out * a.T_out, obytes);
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
+        for (int m = 0; m < 2; ++m)
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        ot[(wco * 64 + m * 32 + 8 * (i >> 2) + 4 * hl + (i & 3)) * (CV_TT + 1) + wt * 32 + l32] = acc[m][i];
-    __syncthreads();
+          for (int q = 0; q < 4; ++q) {
+            /* 4 x 4 transpose across the quad: slot r of lane c goes to slot c
+             * of lane r, in two exchanges (lane bit 0, then bit 1) */
+            float v[4] = {acc[m][4 * q], acc[m][4 * q + 1], acc[m][4 * q + 2], acc[m][4 * q + 3]};
+            float x1[4];
 #pragma unroll
-    for (int it = 0; it < CV_CO / 16; ++it) {
-      const int row = it * 16 + (tid >> 4), t = t0 + c4;
-      if (row >= a.C_out || t >= a.T_out) continue; /* T_out % 4 == 0: t < T_out covers t + 3 */
-      const float bv = bias[it];
-      const float* src = ot + row * (CV_TT + 1) + c4;
-      nsr_float4 v = {src[0] + bv, src[1] + bv, src[2] + bv, src[3] + bv};
-      if constexpr (RESID) v += rv[it];
-      __builtin_nontemporal_store(v, (nsr_float4*)(a.out + ((int64_t)b * a.C_out + row) * a.T_out + t));
+            for (int r = 0; r < 4; ++r) x1[r] = quad_xor1(v[r ^ 1]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = ((r ^ c4) & 1) ? x1[r] : v[r];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x1[r] = quad_xor2(v[r ^ 2]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = ((r ^ c4) & 2) ? x1[r] : v[r];
+            const uint32_t co = (uint32_t)(wco * 64 + m * 32 + 8 * q + 4 * hl + c4);
+            nsr_float4 o = {v[0] + bias[m][q], v[1] + bias[m][q], v[2] + bias[m][q], v[3] + bias[m][q]};
+            if constexpr (RESID) o += rv[m][q];
+            if (t < a.T_out) /* T_out % 4 == 0: t < T_out covers t + 3 */
+              __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(nsr_uint4, o), orr,
+                                                     (co * (uint32_t)a.T_out + (uint32_t)t) * 4u, 0, 0);
+          }
+      }
+      __syncthreads(); /* the next tile's input is staged */
     }
   }
 }
 
 #define NSR_CONV_RW1(NAME, FUSED, RESID, NP)                                                         \
-  extern "C" __global__ void __launch_bounds__(256, 1) NAME(const nsr_conv_args a) {                 \
+  extern "C" __global__ void __launch_bounds__(512, 1) NAME(const nsr_conv_args a) {                 \
     conv_rw_body<FUSED, RESID, NP>(a);                                                              \
   }
-#define NSR_CONV_RW(NP)                                                                              \
-  NSR_CONV_RW1(nsrk_conv1d_rw_f16x2_np##NP, false, false, NP)                                        \
-  NSR_CONV_RW1(nsrk_conv1d_rw_res_f16x2_np##NP, false, true, NP)                                     \
-  NSR_CONV_RW1(nsrk_conv1d_rw_adain_snake_f16x2_np##NP, true, false, NP)                             \
-  NSR_CONV_RW1(nsrk_conv1d_rw_adain_snake_res_f16x2_np##NP, true, true, NP)
+/* NU = column quads per producer lane / 8: staged window (TL + 3 alignment
+ * columns) of at most 96 (NU 3) or 128 (NU 4) columns */
+#define NSR_CONV_RW(NU)                                                                              \
+  NSR_CONV_RW1(nsrk_conv1d_rw_f16x2_nu##NU, false, false, NU)                                        \
+  NSR_CONV_RW1(nsrk_conv1d_rw_res_f16x2_nu##NU, false, true, NU)                                     \
+  NSR_CONV_RW1(nsrk_conv1d_rw_adain_snake_f16x2_nu##NU, true, false, NU)                             \
+  NSR_CONV_RW1(nsrk_conv1d_rw_adain_snake_res_f16x2_nu##NU, true, true, NU)
 
-NSR_CONV_RW(9)
-NSR_CONV_RW(12)
+NSR_CONV_RW(3)
+NSR_CONV_RW(4)
 
 /* NP = ceil(TL / 8) staged columns per lane: TL <= 72, 96, 128 */
 /* OCC, OCCF: workgroups per CU the register budget of the plain and the

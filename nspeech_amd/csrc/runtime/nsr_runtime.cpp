@@ -905,12 +905,14 @@ nsr_status conv_validate(const float* x, const void* w, uintptr_t w_align, float
   if (!x || !w || !out) return fail(NSR_ERR_BAD_ARG, "%s: null pointer", what);
   if (B < 0 || C_in <= 0 || C_out <= 0 || T_in < 0 || K <= 0 || padding < 0 || dilation <= 0 || B > 65535 ||
       C_out > 65535LL * kCvCO || C_in > (1 << 20) || K > 4096 || dilation > (1 << 20) || padding > (1 << 24) ||
-      T_in > 0x3fffffffLL)
+      T_in >= (1LL << 23))
     return fail(NSR_ERR_BAD_ARG, "%s: bad shape B=%lld C_in=%lld C_out=%lld T=%lld K=%lld pad=%lld dil=%lld", what,
                 (long long)B, (long long)C_in, (long long)C_out, (long long)T_in, (long long)K, (long long)padding,
                 (long long)dilation);
   if (C_in % 16 != 0) return fail(NSR_ERR_UNSUPPORTED, "%s: C_in=%lld must be a multiple of 16", what, (long long)C_in);
   *T_out = T_in + 2 * padding - dilation * (K - 1);
+  // rows of 128 channels are addressed with 32-bit byte offsets
+  if (*T_out >= (1LL << 23)) return fail(NSR_ERR_BAD_ARG, "%s: T_out=%lld too long", what, (long long)*T_out);
   if (*T_out <= 0 && T_in > 0)
     return fail(NSR_ERR_BAD_ARG, "%s: empty output (T_in + 2 padding < dilation (K - 1) + 1)", what);
   if (!aligned(x, 4) || !aligned(out, 4) || !aligned(w, w_align))
@@ -934,14 +936,16 @@ nsr_status conv_launch(bool fused, nsr_conv_args& a, nsr_stream_t stream, const 
   const int64_t tiles = (int64_t)cdiv_u(a.T_out, kCvTT) * cdiv_u(a.C_out, kCvCO) * a.B;
   if (tiles > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "%s: too many tiles", what);
   const int np = TL <= 72 ? 9 : TL <= 96 ? 12 : 16;  // register pairs per lane: 8 TL <= 64 np
-  // K <= 3 with one channel block each way: every weight resident in LDS, one workgroup per CU
+  // K <= 3 with one channel block each way and 16-byte aligned rows: every weight resident in LDS,
+  // one 512-lane workgroup per CU (producer and consumer waves)
   const int64_t lds_rw = ((int64_t)a.K * kCvCO + 2 * TL) * kCvS * 2;
-  if (a.C_in <= kCvCI && a.C_out <= kCvCO && a.K <= 3 && np <= 12 && lds_rw <= dm->max_lds && (a.pad_ & 1) &&
-      a.T_in > 0) {
+  const int64_t win = TL + ((-(int64_t)a.padding) & 3);  // staged window from a 16-byte aligned column
+  if (a.C_in <= kCvCI && a.C_out <= kCvCO && a.K <= 3 && win <= 128 && lds_rw <= dm->max_lds && (a.pad_ & 1) &&
+      a.T_in > 0 && a.T_in % 4 == 0 && aligned(a.x, 16)) {
     const int64_t groups = std::min<int64_t>(tiles, (int64_t)dm->n_cu);
     return launch(std::string("nsrk_conv1d_rw") + (fused ? "_adain_snake" : "") + (a.residual ? "_res" : "") +
-                      "_f16x2_np" + std::to_string(np),
-                  (unsigned)groups, 1, 256, (unsigned)lds_rw, stream, params);
+                      "_f16x2_nu" + (win <= 96 ? "3" : "4"),
+                  (unsigned)groups, 1, 512, (unsigned)lds_rw, stream, params);
   }
   // the plain np 9 kernel fits two workgroups per CU in registers; the others one
   const int per_cu = (!fused && np == 9 && 2 * lds <= dm->max_lds) ? 2 : 1;
