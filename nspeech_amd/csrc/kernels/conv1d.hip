@@ -564,6 +564,294 @@ NSR_DEV void conv_rw_body(const nsr_conv_args& a) {
 NSR_CONV_RW(3)
 NSR_CONV_RW(4)
 
+/*
+ * Streamed-weight producer/consumer variant: any K, C_in in chunks of 128,
+ * C_out in blocks of 128, 16-byte aligned rows (T_in % 4 == T_out % 4 == 0)
+ * and a staged window (TL + 3 alignment columns) of at most 128 columns.
+ * One 512-lane workgroup per CU, persistent over the items (tile, input
+ * chunk), tiles ordered channel block fastest:
+ *  - waves 0-3 (consumers) multiply tap k from one LDS weight slot while
+ *    tap k + 1's weights ([128 co][128 ci], 32 KB) travel through their
+ *    registers into the other slot: one barrier per tap (the last tap of an
+ *    item loads the next item's first). Each slice is read from L2 once per
+ *    CU (loading A fragments per wave instead doubles the L1 traffic, which
+ *    measured slower). After a tile's last
+ *    chunk they store it as the resident-weight kernel does (quad transpose,
+ *    16-byte stores, + bias, + residual loaded before the last chunk's MFMAs);
+ *  - waves 4-7 (producers) keep the input two items ahead as in the
+ *    resident-weight kernel and write the next item's staged tile once the
+ *    consumers are past its last tap.
+ * K + 1 barriers per item.
+ */
+template <bool FUSED, bool RESID, int NU>
+NSR_DEV void conv_pc_body(const nsr_conv_args& a) {
+  extern __shared__ uint16_t cv_lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool producer = __builtin_amdgcn_readfirstlane(wave) >= 4; /* wave-uniform role */
+  const int TL = CV_TT + (a.K - 1) * a.dilation;
+  uint16_t* yhi = cv_lds;
+  uint16_t* ylo = yhi + TL * CV_S;
+  uint16_t* wsl = ylo + TL * CV_S; /* two weight slots [CV_CO][CV_S] */
+  float* bias_l = (float*)(wsl + 2 * CV_CO * CV_S); /* [C_out] (0 without bias) */
+  const int n_t = (a.T_out + CV_TT - 1) / CV_TT, n_co = (a.C_out + CV_CO - 1) / CV_CO;
+  const int n_ch = (a.C_in + CV_CI - 1) / CV_CI;
+  const int n_tiles = n_t * n_co * a.B;
+
+  const bool xcd = (gridDim.x & 7) == 0;
+  const int xid = xcd ? (int)(blockIdx.x & 7) : 0, S = xcd ? (int)(gridDim.x >> 3) : (int)gridDim.x;
+  const int slot = xcd ? (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+  const int t_lo = xcd ? (int)((int64_t)n_tiles * xid / 8) : 0;
+  const int t_hi = xcd ? (int)((int64_t)n_tiles * (xid + 1) / 8) : n_tiles;
+  if (t_lo + slot >= t_hi) return;
+  const int first = t_lo + slot, cnt = (t_hi - first + S - 1) / S; /* tiles of this workgroup */
+  const int items = cnt * n_ch, items2 = (items + 1) & ~1;       /* phases: even, the last ones repeat */
+  /* item n -> tile (b, co0, t0) and input chunk c0 */
+  auto item_of = [&](int n, int& b, int& co0, int& t0, int& c0) {
+    const int nn = min(n, items - 1);
+    const int tn = nn / n_ch, ch = nn - tn * n_ch;
+    const int tile = first + tn * S;
+    const int r = tile / n_co;
+    co0 = (tile - r * n_co) * CV_CO;
+    b = r / n_t;
+    t0 = (r - b * n_t) * CV_TT;
+    c0 = ch * CV_CI;
+  };
+
+  if (producer) {
+    const int lq = 8 * (wave - 4) + (lane >> 3), jl = lane & 7;
+    const int dsh = (-a.padding) & 3;
+    nsr_float4 ra[NU][4], rb[NU][4];
+    uint32_t pk[NU][4][4];
+    cv_coef cf[FUSED ? 4 : 1];
+    int coef_key = -1;
+    auto fetch = [&](int n, nsr_float4 (&xv)[NU][4]) {
+      int b, co0, t0, c0;
+      item_of(n, b, co0, t0, c0);
+      const int nq = min(CV_CI, a.C_in - c0) >> 2;
+      const uint32_t rowoff = (uint32_t)(4 * min(lq, nq - 1)) * (uint32_t)a.T_in;
+      const int s0 = t0 - a.padding - dsh;
+      const nsr_rsrc xr = make_rsrc_uniform(a.x + ((int64_t)b * a.C_in + c0) * a.T_in, (uint32_t)(4 * nq * 4 * a.T_in));
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const uint32_t col = (uint32_t)(s0 + 4 * (jl + 8 * u));
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          xv[u][r] = __builtin_bit_cast(nsr_float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        xr, (rowoff + (uint32_t)(r * a.T_in) + col) * 4u, 0, 0));
+      }
+    };
+    auto transform = [&](int n, nsr_float4 (&xv)[NU][4]) {
+      int b, co0, t0, c0;
+      item_of(n, b, co0, t0, c0);
+      const int nq = min(CV_CI, a.C_in - c0) >> 2;
+      const bool live = lq < nq;
+      const int s0 = t0 - a.padding - dsh;
+      if constexpr (FUSED) {
+        const int key = b * n_ch + (c0 / CV_CI);
+        if (key != coef_key) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) cf[r] = cv_row_coef(a, b, c0 + min(4 * lq + r, 4 * nq - 1));
+          coef_key = key;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int u = 0; u < NU; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              xv[u][r][e] = snake_eval(__builtin_fmaf(xv[u][r][e] - cf[r].mean, cf[r].A, cf[r].bet), cf[r].sc);
+      }
+#pragma unroll
+      for (int u = 0; u < NU; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int ti = s0 + 4 * (jl + 8 * u) + e;
+          const bool in = live && ti >= 0 && ti < a.T_in;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float y0 = in ? xv[u][2 * h][e] : 0.f, y1 = in ? xv[u][2 * h + 1][e] : 0.f;
+            const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1;
+            const _Float16 l0 = (_Float16)(y0 - (float)h0), l1 = (_Float16)(y1 - (float)h1);
+            pk[u][e][h] = (uint32_t)h_bits(h0) | ((uint32_t)h_bits(h1) << 16);
+            pk[u][e][2 + h] = (uint32_t)h_bits(l0) | ((uint32_t)h_bits(l1) << 16);
+          }
+        }
+    };
+    auto write = [&]() {
+#pragma unroll
+      for (int u = 0; u < NU; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = 4 * (jl + 8 * u) + e - dsh;
+          if (j >= 0 && j < TL) {
+            *(nsr_uint2*)(yhi + j * CV_S + 4 * lq) = nsr_uint2{pk[u][e][0], pk[u][e][1]};
+            *(nsr_uint2*)(ylo + j * CV_S + 4 * lq) = nsr_uint2{pk[u][e][2], pk[u][e][3]};
+          }
+        }
+    };
+    auto phase = [&](int n, nsr_float4 (&refill)[NU][4], nsr_float4 (&ready)[NU][4]) {
+      fetch(n + 2, refill);
+      transform(n + 1, ready);
+      for (int k = 0; k < a.K; ++k) __syncthreads(); /* the consumers' taps of item n */
+      write();
+      __syncthreads(); /* item n + 1's input is staged */
+    };
+    fetch(0, ra);
+    fetch(1, rb);
+    transform(0, ra);
+    write();
+    __syncthreads(); /* item 0's input, tap 0's weights and the bias staged */
+    for (int n = 0; n < items2; n += 2) {
+      phase(n, ra, rb);
+      phase(n + 1, rb, ra);
+    }
+  } else {
+    const int wco = wave >> 1, wt = wave & 1;
+    const int hl = lane >> 5, l32 = lane & 31, c4 = lane & 3;
+    const uint32_t obytes = (uint32_t)(4 * a.C_out * a.T_out);
+    /* weight slice (item n, tap k) -> registers: 16-byte chunks id = tid + 256 i of [128 co][16 x 8 ci] */
+    nsr_uint4 wr[8];
+    auto load_w = [&](int n, int k) {
+      int b, co0, t0, c0;
+      item_of(n, b, co0, t0, c0);
+      const int cc = min(CV_CI, a.C_in - c0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int id = tid + 256 * i, co = id >> 4, c8 = id & 15;
+        const bool ok = co0 + co < a.C_out && 8 * c8 < cc;
+        const int64_t src = ok ? ((int64_t)(co0 + co) * a.K + k) * a.C_in + c0 + 8 * c8 : 0;
+        wr[i] = *(const nsr_uint4*)(a.w + src);
+        if (!ok) wr[i] = nsr_uint4{0u, 0u, 0u, 0u};
+      }
+    };
+    auto store_w = [&](int sl) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int id = tid + 256 * i;
+        *(nsr_uint4*)(wsl + sl * CV_CO * CV_S + (id >> 4) * CV_S + 8 * (id & 15)) = wr[i];
+      }
+    };
+    for (int c = tid; c < a.C_out; c += 256) bias_l[c] = a.bias ? f16_bits_to_f32(a.bias[c]) : 0.f;
+    load_w(0, 0);
+    store_w(0);
+    int ws = 0; /* slot of the tap about to be multiplied */
+    __syncthreads(); /* item 0's input, tap 0's weights and the bias staged */
+    const int wbase = (wco * 64 + l32) * CV_S + 8 * hl;
+    const int ybase = (wt * 32 + l32) * CV_S + 8 * hl;
+    nsr_f32x16 acc[2];
+    for (int n = 0; n < items2; ++n) {
+      int b, co0, t0, c0;
+      item_of(n, b, co0, t0, c0);
+      const bool last_chunk = c0 + CV_CI >= a.C_in;
+      const int t = t0 + wt * 32 + 4 * (l32 >> 2);
+      if (c0 == 0) {
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[m][i] = 0.f;
+      }
+      nsr_float4 rv[RESID ? 2 : 1][RESID ? 4 : 1];
+      for (int k = 0; k < a.K; ++k) {
+        if constexpr (RESID) {
+          /* at the tile's last tap, ahead of the weight load, so the epilogue waits for it alone */
+          if (k == a.K - 1 && last_chunk) {
+            const nsr_rsrc rr = make_rsrc_uniform(a.residual + (int64_t)b * a.C_out * a.T_out, obytes);
+            const uint32_t tc = (uint32_t)min(t, a.T_out - 4);
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const uint32_t co = (uint32_t)(co0 + wco * 64 + m * 32 + 8 * q + 4 * hl + c4);
+                rv[m][q] = __builtin_bit_cast(
+                    nsr_float4, __builtin_amdgcn_raw_buffer_load_b128(rr, (co * (uint32_t)a.T_out + tc) * 4u, 0, 0));
+              }
+          }
+        }
+        /* next tap's weights (or the next item's first) into registers during this tap's MFMAs */
+        if (k + 1 < a.K) {
+          load_w(n, k + 1);
+        } else {
+          load_w(n + 1, 0);
+        }
+        const uint16_t* wk0 = wsl + ws * CV_CO * CV_S + wbase;
+        const int yk = ybase + k * a.dilation * CV_S;
+        nsr_h8 A[2][2], Bh[2], Bl[2];
+        auto ld = [&](int buf, int g) {
+          A[buf][0] = *(const nsr_h8*)(wk0 + g);
+          A[buf][1] = *(const nsr_h8*)(wk0 + 32 * CV_S + g);
+          Bh[buf] = *(const nsr_h8*)(yhi + yk + g);
+          Bl[buf] = *(const nsr_h8*)(ylo + yk + g);
+        };
+        ld(0, 0);
+#pragma unroll
+        for (int g = 0; g < CV_CI; g += 16) {
+          const int cur = (g >> 4) & 1;
+          if (g + 16 < CV_CI) ld(cur ^ 1, g + 16);
+#pragma unroll
+          for (int m = 0; m < 2; ++m)
+            acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[cur][m], Bh[cur], acc[m], 0, 0, 0);
+#pragma unroll
+          for (int m = 0; m < 2; ++m)
+            acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[cur][m], Bl[cur], acc[m], 0, 0, 0);
+        }
+        /* order: steps 0 and 1's reads, step 0's MFMAs, then step g + 1's
+         * reads before step g's MFMAs (the scheduler would otherwise sink each
+         * read to its use and expose the LDS latency) */
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+#pragma unroll
+        for (int g = 16; g < CV_CI - 16; g += 16) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        store_w(ws ^ 1); /* that slot's last readers (the previous tap) were past the previous barrier */
+        ws ^= 1;
+        __syncthreads(); /* tap k done everywhere; the next tap's weights staged */
+      }
+      if (last_chunk && n < items) {
+        const nsr_rsrc orr = make_rsrc_uniform(a.out + (int64_t)b * a.C_out * a.T_out, obytes);
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float v[4] = {acc[m][4 * q], acc[m][4 * q + 1], acc[m][4 * q + 2], acc[m][4 * q + 3]};
+            float x1[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x1[r] = quad_xor1(v[r ^ 1]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = ((r ^ c4) & 1) ? x1[r] : v[r];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x1[r] = quad_xor2(v[r ^ 2]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = ((r ^ c4) & 2) ? x1[r] : v[r];
+            const int co = co0 + wco * 64 + m * 32 + 8 * q + 4 * hl + c4;
+            const float bv = bias_l[min(co, a.C_out - 1)];
+            nsr_float4 o = {v[0] + bv, v[1] + bv, v[2] + bv, v[3] + bv};
+            if constexpr (RESID) o += rv[m][q];
+            if (t < a.T_out)
+              __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(nsr_uint4, o), orr,
+                                                     ((uint32_t)co * (uint32_t)a.T_out + (uint32_t)t) * 4u, 0, 0);
+          }
+      }
+      __syncthreads(); /* the next item's input is staged */
+    }
+  }
+}
+
+#define NSR_CONV_PC1(NAME, FUSED, RESID, NU)                                                         \
+  extern "C" __global__ void __launch_bounds__(512, 1) NAME(const nsr_conv_args a) {                 \
+    conv_pc_body<FUSED, RESID, NU>(a);                                                              \
+  }
+#define NSR_CONV_PC(NU)                                                                              \
+  NSR_CONV_PC1(nsrk_conv1d_pc_f16x2_nu##NU, false, false, NU)                                        \
+  NSR_CONV_PC1(nsrk_conv1d_pc_res_f16x2_nu##NU, false, true, NU)                                     \
+  NSR_CONV_PC1(nsrk_conv1d_pc_adain_snake_f16x2_nu##NU, true, false, NU)                             \
+  NSR_CONV_PC1(nsrk_conv1d_pc_adain_snake_res_f16x2_nu##NU, true, true, NU)
+
+NSR_CONV_PC(3)
+NSR_CONV_PC(4)
+
 /* NP = ceil(TL / 8) staged columns per lane: TL <= 72, 96, 128 */
 /* OCC, OCCF: workgroups per CU the register budget of the plain and the
  * fused kernel is sized for (NP 9 plain: two, which the LDS of short halos

@@ -947,6 +947,15 @@ nsr_status conv_launch(bool fused, nsr_conv_args& a, nsr_stream_t stream, const 
                       "_f16x2_nu" + (win <= 96 ? "3" : "4"),
                   (unsigned)groups, 1, 512, (unsigned)lds_rw, stream, params);
   }
+  // any K, C_in in chunks and C_out in blocks of 128, 16-byte aligned rows: weights streamed one tap ahead
+  // through two LDS slots, one 512-lane workgroup per CU (producer and consumer waves)
+  const int64_t lds_pc = (2 * TL + 2 * kCvCO) * kCvS * 2 + 4 * (int64_t)a.C_out; /* + the bias as f32 */
+  if (win <= 128 && lds_pc <= dm->max_lds && (a.pad_ & 1) && a.T_in > 0 && a.T_in % 4 == 0 && aligned(a.x, 16)) {
+    const int64_t groups = std::min<int64_t>(tiles, (int64_t)dm->n_cu);
+    return launch(std::string("nsrk_conv1d_pc") + (fused ? "_adain_snake" : "") + (a.residual ? "_res" : "") +
+                      "_f16x2_nu" + (win <= 96 ? "3" : "4"),
+                  (unsigned)groups, 1, 512, (unsigned)lds_pc, stream, params);
+  }
   // the plain np 9 kernel fits two workgroups per CU in registers; the others one
   const int per_cu = (!fused && np == 9 && 2 * lds <= dm->max_lds) ? 2 : 1;
   const int64_t groups = std::min<int64_t>(tiles, (int64_t)per_cu * dm->n_cu);

@@ -56,6 +56,9 @@ def test_conv1d_f32io_reference_self_test_shapes(dev, C, T, K, dil, pad):
     (2, 64, 96, 1000, 3, 2, 2, True),    # residual, two batches
     (1, 128, 128, 4096, 3, 5, 5, False), # 74 staged columns (the wider staging variant)
     (1, 32, 32, 9, 2, 1, 0, True),       # K = 2, a single tile
+    # streamed-weight kernel (16-byte aligned rows, other shapes):
+    (2, 144, 200, 1000, 5, 2, 4, True),  # two input chunks (the last of 16 channels), two output blocks, residual
+    (1, 512, 128, 132, 1, 1, 0, False),  # 1x1 conv, four input chunks
 ])
 def test_conv1d_packed_edges(dev, B, C_in, C_out, T, K, dil, pad, res):
     say("conv1d packed", B, C_in, C_out, T, K, dil, pad, res)
