@@ -301,7 +301,8 @@ def build_workload(name):
         return Workload(name, f"ResBlock stage AdaIN+Snake -> conv1d K={K} dil={dil} f32 x[{B},{C},{TT}]"
                         + (" (unfused: two kernels + y round trip)" if name == "kconv3u" else " (fused)"),
                         alg, x0.numel() * 4, make_set, launch,
-                        "nsrk_conv1d_f16x2" if name == "kconv3u" else "nsrk_conv1d_adain_snake_f16x2", "f32",
+                        {"kconv3": "nsrk_conv1d_rw_adain_snake_f16x2_nu3", "kconv11": "nsrk_conv1d_pc_adain_snake_f16x2_nu4",
+                         "kconv3u": "nsrk_conv1d_rw_f16x2_nu3"}[name], "f32",
                         flops=flops)
 
     if name == "c4a":

@@ -255,8 +255,10 @@ nsr_status nsr_residual_add(const void* x, const void* res, void* out,
  * sides, dilation `dilation`: T_out = T_in + 2 padding - dilation (K - 1).
  * f32 accuracy on f16 matrix cores (each activation is split into two f16
  * halves; f32 accumulation). Requirements: C_in % 16 == 0; (K - 1) *
- * dilation within the LDS budget (about 200 columns of halo at C_in chunks
- * of 128); stride != 1 returns NSR_ERR_UNSUPPORTED. Packs the weights into
+ * dilation <= 64; T_in, T_out < 2^23; stride != 1 returns
+ * NSR_ERR_UNSUPPORTED. Rows that start 16-byte aligned (T_in % 4 == 0,
+ * T_out % 4 == 0, 16-byte aligned x / out / residual) take the faster
+ * producer/consumer kernels. Packs the weights into
  * stream-ordered scratch on every call; callers that convolve repeatedly
  * pack once with nsr_conv1d_pack_f16 and call nsr_conv1d_f16w_packed.
  * Replaces KokoroGpuBackend::conv1d_f32 (src/kokoro/gpu_backend.rs:165-167;
