@@ -46,8 +46,11 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workloads", default="c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,q8fc1,q8fc2,q8fc1r,q8fc2r,q8conv,kconv3,kconv11,kconv3u",
-                    help="comma list of c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,q8fc1,q8fc2,q8fc1r,q8fc2r,q8conv,kconv3,kconv11,kconv3u,copy")
+    ap.add_argument("--workloads",
+                    default="c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,attn,attnx,q8fc1,q8fc2,q8fc1r,q8fc2r,q8conv,kconv3,kconv11,"
+                            "kconv3u",
+                    help="comma list of c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,attn,attnx,q8fc1,q8fc2,q8fc1r,q8fc2r,q8conv,"
+                         "kconv3,kconv11,kconv3u,copy")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline (0 = skip)")
     ap.add_argument("--no-rotate", action="store_true", help="one buffer set (warm MALL) for all timings")
     return ap.parse_args()
@@ -193,6 +196,37 @@ def build_workload(name):
                         + (" (one launch)" if name == "dec" else " (two launches, as the reference)"), alg,
                         2 * Hk * Lc * Dh * 2, make_set, launch,
                         "nsrk_rope_cache_f16", "f16")
+
+    if name in ("attn", "attnx"):
+        # Moonshine decoder attention at M = 1, 10 heads x 64, f16: "attn" = self-attention over the full KV
+        # cache [10, 448, 64] (nsr_attention_decode_f16, split chosen by the library); "attnx" = cross-attention
+        # over 30 s of encoder K/V [1500, 10, 64] with the reference's 32 splits (nsr_attention_splitkv_f16).
+        g = configs.rng(1012)
+        H, Dh = 10, 64
+        kv_len = 448 if name == "attn" else 1500
+        mk = lambda *sh: torch.from_numpy(g.standard_normal(sh).astype(np.float16)).to(dev)  # noqa: E731
+        shape = (H, kv_len, Dh) if name == "attn" else (kv_len, H, Dh)
+        skh, sks = (kv_len * Dh, Dh) if name == "attn" else (Dh, H * Dh)
+        part = torch.empty(H * 32 * (Dh + 2), dtype=torch.float32, device=dev)
+
+        def make_set(_):
+            return {"q": mk(H, Dh), "k": mk(*shape), "v": mk(*shape), "o": torch.empty((H, Dh), dtype=torch.float16,
+                                                                                      device=dev)}
+
+        def launch(s):
+            if name == "attn":
+                abi.check(L.nsr_attention_decode_f16(s["q"].data_ptr(), s["k"].data_ptr(), s["v"].data_ptr(),
+                                                     s["o"].data_ptr(), kv_len, Dh, H, H, 0.125, skh, sks, stream()))
+            else:
+                abi.check(L.nsr_attention_splitkv_f16(s["q"].data_ptr(), s["k"].data_ptr(), s["v"].data_ptr(),
+                                                      s["o"].data_ptr(), part.data_ptr(), kv_len, Dh, H, H, 0.125,
+                                                      skh, sks, 32, stream()))
+
+        alg = 2 * (2 * H * Dh) + 2 * (2 * kv_len * H * Dh)
+        return Workload(name, f"decode attention f16, 10 heads x 64, kv_len {kv_len}"
+                        + (" (self-attention over the KV cache)" if name == "attn"
+                           else " (cross-attention over the encoder K/V, 32 splits)"),
+                        alg, alg, make_set, launch, "nsrk_attn_decode_partial", "f16")
 
     if name in ("q8fc1", "q8fc2", "q8fc1r", "q8fc2r"):
         # Moonshine decoder MLP at M = 1 (dim 640, intermediate 2560; f16 activations, Q8 weights):

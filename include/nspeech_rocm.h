@@ -248,6 +248,41 @@ nsr_status nsr_glu_silu(const void* fc1, void* out, nsr_dtype dtype, int64_t n,
 nsr_status nsr_residual_add(const void* x, const void* res, void* out,
                             nsr_dtype dtype, int64_t n, nsr_stream_t stream);
 
+/* ---- Decode attention (one query position per head) ----------------------- */
+
+/* out[h, :] f16 = softmax_j(sm_scale * q[h, :] . K[kvh, j, :]) . V[kvh, j, :]
+ * over j < kv_len, kvh = h * n_kv_heads / n_q_heads (grouped-query heads);
+ * q, out f16 [n_q_heads, head_dim]; K and V f16 with element (kvh, j, d) at
+ * kvh * stride_kv_head + j * stride_kv_seq + d (elements). Scores, softmax
+ * and the weighted sum in f32. Requirements: head_dim a multiple of 4 in
+ * [4, 128]; strides multiples of 4, stride_kv_seq >= head_dim; q, K, V
+ * 8-byte aligned; 1 <= n_kv_heads <= n_q_heads; kv_len >= 1.
+ *
+ * nsr_attention_splitkv_f16: the positions are cut into n_splits ranges of
+ * ceil(kv_len / n_splits); `partial` is caller scratch of at least
+ * n_q_heads * n_splits * (head_dim + 2) floats (the reference's partial
+ * buffer, 3 * 128 floats per (head, split), is large enough). Two launches.
+ * Replaces attention_decode_splitkv_partial / _reduce via
+ * enc_attention_splitkv (src/triton_kernels.rs:925-973; kernels/
+ * moonshine_kernels.py:1631-1716), the decoder's cross-attention over the
+ * encoder K/V [kv_len, heads, head_dim] (src/moonshine/gpu_decoder_metal.rs:
+ * 170-182). */
+nsr_status nsr_attention_splitkv_f16(const void* q, const void* k, const void* v, void* out, float* partial,
+                                     int64_t kv_len, int64_t head_dim, int64_t n_kv_heads, int64_t n_q_heads,
+                                     float sm_scale, int64_t stride_kv_head, int64_t stride_kv_seq, int64_t n_splits,
+                                     nsr_stream_t stream);
+
+/* The same attention in one launch and without scratch: one workgroup per
+ * query head, whose waves take every W-th chunk of 64 positions and merge
+ * in LDS. Replaces triton_attention_decode /
+ * enc_attention_decode (src/triton_kernels.rs:648-675, 900-923; kernels/
+ * moonshine_kernels.py:1525-1625), the decoder's self-attention over its KV
+ * cache [heads, max_kv_len, head_dim] (src/moonshine/gpu_decoder_metal.rs:
+ * 158-168). */
+nsr_status nsr_attention_decode_f16(const void* q, const void* k, const void* v, void* out, int64_t kv_len,
+                                    int64_t head_dim, int64_t n_kv_heads, int64_t n_q_heads, float sm_scale,
+                                    int64_t stride_kv_head, int64_t stride_kv_seq, nsr_stream_t stream);
+
 /* ---- Kokoro resblock conv1d (MFMA) ----------------------------------------- */
 
 /* out [B, C_out, T_out] f32 = conv1d(x [B, C_in, T_in] f32, w [C_out, C_in, K]

@@ -81,13 +81,16 @@ def lib() -> C.CDLL:
         L.nsr_gemv_q8_t4_bias_glu.argtypes = [_P, C.c_int, _P, _P, _P, _P, C.c_int, _I64, _I64, _P]
         L.nsr_gemv_q8_t4_resadd_ln.argtypes = [_P, C.c_int, _P, _P, _P, _P, _P, C.c_int, _P, C.c_int, _I64, _I64,
                                                C.c_float, _P]
+        L.nsr_attention_splitkv_f16.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, C.c_float, _I64, _I64,
+                                                _I64, _P]
+        L.nsr_attention_decode_f16.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, C.c_float, _I64, _I64, _P]
         for name in ("nsr_init", "nsr_layernorm", "nsr_residual_add_layernorm", "nsr_rope_table_f32",
                      "nsr_rope_qk_cache_append", "nsr_kv_cache_append",
                      "nsr_rotary_partial_interleaved_f32", "nsr_adain_snake_f32", "nsr_q8_0_embed_gather",
                      "nsr_activation", "nsr_glu_silu", "nsr_residual_add", "nsr_gemv_q8",
                      "nsr_gemv_q8_bias_glu", "nsr_gemv_q8_resadd_ln", "nsr_q8_pack_t4", "nsr_gemv_q8_t4", "nsr_q8_0_to_gemv_q8", "nsr_q8_0_to_t4",
                      "nsr_conv1d_f32io", "nsr_conv1d_pack_f16", "nsr_conv1d_f16w_packed",
-                     "nsr_adain_snake_conv1d_f32",
+                     "nsr_adain_snake_conv1d_f32", "nsr_attention_splitkv_f16", "nsr_attention_decode_f16",
                      "nsr_gemv_q8_t4_bias_glu", "nsr_gemv_q8_t4_resadd_ln"):
             getattr(L, name).restype = C.c_int
         _lib = L
@@ -415,4 +418,26 @@ def adain_snake_conv1d(x, gamma, beta, alpha, wp, bias=None, residual=None, *, p
     check(lib().nsr_adain_snake_conv1d_f32(_ptr(x), _ptr(gamma), _ptr(beta), _ptr(alpha), _dt(gamma), gs, bs,
                                            _ptr(wp), _ptr(bias), _ptr(residual), _ptr(out), B, C_in, C_out, T, K,
                                            padding, dilation, eps, _stream(stream)))
+    return out
+
+
+# ------------------------------------------------------ decode attention ---
+
+def attention_decode(q, k, v, kv_len, n_kv_heads, sm_scale, *, stride_kv_head, stride_kv_seq, n_splits=None,
+                     partial=None, out=None, stream=None):
+    """f16 q [n_q_heads, head_dim]; k, v f16 device tensors addressed as (head, pos, d) ->
+    head * stride_kv_head + pos * stride_kv_seq + d. n_splits None: the library picks the split
+    (nsr_attention_decode_f16); else nsr_attention_splitkv_f16 with `partial` (allocated if None)."""
+    n_q_heads, head_dim = q.shape
+    if out is None:
+        out = torch.empty((n_q_heads, head_dim), dtype=torch.float16, device=q.device)
+    if n_splits is None:
+        check(lib().nsr_attention_decode_f16(_ptr(q), _ptr(k), _ptr(v), _ptr(out), kv_len, head_dim, n_kv_heads,
+                                             n_q_heads, sm_scale, stride_kv_head, stride_kv_seq, _stream(stream)))
+    else:
+        if partial is None:
+            partial = torch.empty(n_q_heads * n_splits * (head_dim + 2), dtype=torch.float32, device=q.device)
+        check(lib().nsr_attention_splitkv_f16(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(partial), kv_len, head_dim,
+                                              n_kv_heads, n_q_heads, sm_scale, stride_kv_head, stride_kv_seq,
+                                              n_splits, _stream(stream)))
     return out

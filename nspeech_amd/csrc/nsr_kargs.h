@@ -125,6 +125,19 @@ typedef struct nsr_q8_0_conv_args {
   int32_t glu_n;           /* t4 GLU: output columns (N = 2 glu_n); 0 = plain */
 } nsr_q8_0_conv_args;
 
+typedef struct nsr_attn_args {
+  const uint16_t* q;       /* f16 [n_q_heads, head_dim] */
+  const uint16_t* k;       /* f16, element (head, pos, d) at head*stride_kv_head + pos*stride_kv_seq + d */
+  const uint16_t* v;       /* same layout as k */
+  float* partial;          /* f32 [n_q_heads * n_splits][head_dim + 2]: m, l, acc[head_dim] */
+  uint16_t* out;           /* f16 [n_q_heads, head_dim] */
+  int64_t stride_kv_head;  /* elements */
+  int64_t stride_kv_seq;   /* elements */
+  int32_t kv_len, n_q_heads, n_kv_heads, head_dim, n_splits, kv_per_split;
+  float sm_scale;
+  int32_t pad_;
+} nsr_attn_args;
+
 typedef struct nsr_conv_args {
   const float* x;          /* [B, C_in, T_in] */
   const uint16_t* w;       /* packed f16 [C_out][K][C_in] */

@@ -20,5 +20,6 @@ NSR_EMBED(adain_snake)
 NSR_EMBED(elementwise)
 NSR_EMBED(gemv_q8)
 NSR_EMBED(conv1d)
+NSR_EMBED(attention)
 
     .section .note.GNU-stack, "", @progbits

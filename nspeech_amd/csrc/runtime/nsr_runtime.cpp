@@ -31,6 +31,7 @@ extern "C" const unsigned char nsr_co_adain_snake[];
 extern "C" const unsigned char nsr_co_elementwise[];
 extern "C" const unsigned char nsr_co_gemv_q8[];
 extern "C" const unsigned char nsr_co_conv1d[];
+extern "C" const unsigned char nsr_co_attention[];
 
 namespace {
 
@@ -44,7 +45,8 @@ const Unit kUnits[] = {{"q8_0_gather", nsr_co_q8_0_gather},
                        {"adain_snake", nsr_co_adain_snake},
                        {"elementwise", nsr_co_elementwise},
                        {"gemv_q8", nsr_co_gemv_q8},
-                       {"conv1d", nsr_co_conv1d}};
+                       {"conv1d", nsr_co_conv1d},
+                       {"attention", nsr_co_attention}};
 constexpr int kNumUnits = sizeof(kUnits) / sizeof(kUnits[0]);
 
 constexpr int kMaxDevices = 64;
@@ -140,7 +142,7 @@ int unit_of(const std::string& name) {
   static const P map[] = {{"nsrk_q8_0_", 0}, {"nsrk_ln_", 1},    {"nsrk_resln_", 1}, {"nsrk_rope_", 2},
                           {"nsrk_adain_", 3}, {"nsrk_silu_", 4}, {"nsrk_gelu_", 4},  {"nsrk_glu_", 4},
                           {"nsrk_add_", 4},  {"nsrk_gemv_", 5},
-                          {"nsrk_conv1d_", 6}};
+                          {"nsrk_conv1d_", 6}, {"nsrk_attn_", 7}};
   for (const P& p : map)
     if (name.compare(0, std::strlen(p.prefix), p.prefix) == 0) return p.unit;
   return -1;
@@ -480,6 +482,103 @@ nsr_status nsr_kv_cache_append(const void* new_kv, void* cache, nsr_dtype dtype,
   if (!new_kv || !cache) return fail(NSR_ERR_BAD_ARG, "kv_cache_append: null pointer");
   return rope_cache_launch(nullptr, nullptr, new_kv, dtype, nullptr, 0, nullptr, cache, 0, n_kv_heads, head_dim, 0,
                            pos, max_kv_len, false, stream, "kv_cache_append");
+}
+
+// ------------------------------------------------------ decode attention --
+
+namespace {
+
+// compile-time head_dim / 4 variants of the attention kernels (0: any)
+int attn_variant(int64_t head_dim) {
+  const int hd4 = (int)(head_dim / 4);
+  return (hd4 == 9 || hd4 == 13 || hd4 == 16 || hd4 == 32) ? hd4 : 0;
+}
+
+int64_t attn_wave_lds_bytes(int64_t head_dim) { return 4 * (2 * 64 * (head_dim / 4 + 1) * 2 + 64 + 256); }
+
+void attn_fill(nsr_attn_args& a, const void* q, const void* k, const void* v, void* out, float* partial,
+               int64_t kv_len, int64_t head_dim, int64_t n_kv_heads, int64_t n_q_heads, float sm_scale,
+               int64_t stride_kv_head, int64_t stride_kv_seq, int64_t n_splits) {
+  std::memset(&a, 0, sizeof(a));
+  a.q = (const uint16_t*)q;
+  a.k = (const uint16_t*)k;
+  a.v = (const uint16_t*)v;
+  a.out = (uint16_t*)out;
+  a.partial = partial;
+  a.stride_kv_head = stride_kv_head;
+  a.stride_kv_seq = stride_kv_seq;
+  a.kv_len = (int32_t)kv_len;
+  a.n_q_heads = (int32_t)n_q_heads;
+  a.n_kv_heads = (int32_t)n_kv_heads;
+  a.head_dim = (int32_t)head_dim;
+  a.n_splits = (int32_t)n_splits;
+  a.kv_per_split = (int32_t)((kv_len + n_splits - 1) / n_splits);
+  a.sm_scale = sm_scale;
+}
+
+nsr_status attn_validate(const void* q, const void* k, const void* v, void* out, int64_t kv_len, int64_t head_dim,
+                         int64_t n_kv_heads, int64_t n_q_heads, float sm_scale, int64_t stride_kv_head,
+                         int64_t stride_kv_seq, const char* what) {
+  if (!q || !k || !v || !out) return fail(NSR_ERR_BAD_ARG, "%s: null pointer", what);
+  if (kv_len < 1 || kv_len > 0x7fffffffLL || n_q_heads < 1 || n_kv_heads < 1 || n_q_heads > 65535 ||
+      n_kv_heads > n_q_heads)
+    return fail(NSR_ERR_BAD_ARG, "%s: bad shape kv_len=%lld n_q_heads=%lld n_kv_heads=%lld", what,
+                (long long)kv_len, (long long)n_q_heads, (long long)n_kv_heads);
+  if (head_dim < 4 || head_dim > 128 || head_dim % 4 != 0)
+    return fail(NSR_ERR_UNSUPPORTED, "%s: head_dim=%lld must be a multiple of 4 in [4, 128]", what,
+                (long long)head_dim);
+  if (stride_kv_head < 0 || stride_kv_seq < head_dim || stride_kv_head % 4 != 0 || stride_kv_seq % 4 != 0)
+    return fail(NSR_ERR_BAD_ARG, "%s: strides must be multiples of 4 elements, stride_kv_seq >= head_dim", what);
+  if (!aligned(q, 8) || !aligned(k, 8) || !aligned(v, 8) || !aligned(out, 2))
+    return fail(NSR_ERR_BAD_ARG, "%s: q, k, v need 8-byte alignment", what);
+  if (!(sm_scale == sm_scale)) return fail(NSR_ERR_BAD_ARG, "%s: sm_scale is NaN", what);
+  return NSR_OK;
+}
+
+}  // namespace
+
+nsr_status nsr_attention_splitkv_f16(const void* q, const void* k, const void* v, void* out, float* partial,
+                                     int64_t kv_len, int64_t head_dim, int64_t n_kv_heads, int64_t n_q_heads,
+                                     float sm_scale, int64_t stride_kv_head, int64_t stride_kv_seq, int64_t n_splits,
+                                     nsr_stream_t stream) {
+  nsr_status st = attn_validate(q, k, v, out, kv_len, head_dim, n_kv_heads, n_q_heads, sm_scale, stride_kv_head,
+                                stride_kv_seq, "attention_splitkv");
+  if (st != NSR_OK) return st;
+  if (!partial) return fail(NSR_ERR_BAD_ARG, "attention_splitkv: null partial buffer");
+  if (n_splits < 1 || n_splits > 65535 || n_q_heads * n_splits > 0x7fffffffLL)
+    return fail(NSR_ERR_BAD_ARG, "attention_splitkv: n_splits=%lld out of range", (long long)n_splits);
+  DeviceModule* dm = nullptr;
+  st = current_module(&dm);
+  if (st != NSR_OK) return st;
+  nsr_attn_args a;
+  attn_fill(a, q, k, v, out, partial, kv_len, head_dim, n_kv_heads, n_q_heads, sm_scale, stride_kv_head,
+            stride_kv_seq, n_splits);
+  void* params[] = {&a};
+  st = launch("nsrk_attn_partial_d" + std::to_string(attn_variant(head_dim)), (unsigned)(n_q_heads * n_splits), 1,
+              64, (unsigned)attn_wave_lds_bytes(head_dim), stream, params);
+  if (st != NSR_OK) return st;
+  return launch("nsrk_attn_reduce", (unsigned)n_q_heads, 1, 128, 0, stream, params);
+}
+
+nsr_status nsr_attention_decode_f16(const void* q, const void* k, const void* v, void* out, int64_t kv_len,
+                                    int64_t head_dim, int64_t n_kv_heads, int64_t n_q_heads, float sm_scale,
+                                    int64_t stride_kv_head, int64_t stride_kv_seq, nsr_stream_t stream) {
+  nsr_status st = attn_validate(q, k, v, out, kv_len, head_dim, n_kv_heads, n_q_heads, sm_scale, stride_kv_head,
+                                stride_kv_seq, "attention_decode");
+  if (st != NSR_OK) return st;
+  DeviceModule* dm = nullptr;
+  st = current_module(&dm);
+  if (st != NSR_OK) return st;
+  // one workgroup per query head, its waves taking every W-th chunk of 64 positions
+  const int64_t per_wave = attn_wave_lds_bytes(head_dim);
+  const int64_t fit = (dm->max_lds - 1024) / per_wave; /* 1 KB for the static q and merge slots */
+  const int64_t W = std::max<int64_t>(1, std::min<int64_t>({8, fit, (kv_len + 63) / 64}));
+  nsr_attn_args a;
+  attn_fill(a, q, k, v, out, nullptr, kv_len, head_dim, n_kv_heads, n_q_heads, sm_scale, stride_kv_head,
+            stride_kv_seq, 1);
+  void* params[] = {&a};
+  return launch("nsrk_attn_head_d" + std::to_string(attn_variant(head_dim)), (unsigned)n_q_heads, 1,
+                (unsigned)(64 * W), (unsigned)(W * per_wave), stream, params);
 }
 
 // -------------------------------------------------------- AdaIN + Snake --

@@ -541,3 +541,38 @@ ORC_API void orc_conv1d_f32io(const float* x, const uint16_t* w, const uint16_t*
       }
     }
 }
+
+/* ------------------------------------------------ decode attention ------- */
+
+/* attention_decode_1d_masked (kernels/moonshine_kernels.py:1579-1625), one
+ * query head at a time, f16 q / K / V widened exactly to f32:
+ *   kv_head = q_head * n_kv_heads / n_q_heads;
+ *   for each position j in order: s = (sum_d q[d] k_j[d]) * sm_scale (the sum
+ *   over d in d order), m' = max(m, s), a = exp(m - m'), p = exp(s - m'),
+ *   l = l a + p, acc = acc a + p v_j, m = m'  (m starts at -1e30, l = acc = 0);
+ *   out = acc / l, here left in f32 (the kernel stores f16).
+ * K/V element (h, j, d) at h * stride_kv_head + j * stride_kv_seq + d. */
+ORC_API void orc_attention_decode_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v, float* out,
+                                      int64_t kv_len, int64_t head_dim, int64_t n_kv_heads, int64_t n_q_heads,
+                                      float sm_scale, int64_t stride_kv_head, int64_t stride_kv_seq) {
+  float* acc = (float*)malloc((size_t)head_dim * sizeof(float));
+  for (int64_t qh = 0; qh < n_q_heads; ++qh) {
+    const int64_t kvh = qh * n_kv_heads / n_q_heads;
+    float m = -1e30f, l = 0.0f;
+    for (int64_t d = 0; d < head_dim; ++d) acc[d] = 0.0f;
+    for (int64_t j = 0; j < kv_len; ++j) {
+      const uint16_t* kr = k + kvh * stride_kv_head + j * stride_kv_seq;
+      const uint16_t* vr = v + kvh * stride_kv_head + j * stride_kv_seq;
+      float s = 0.0f;
+      for (int64_t d = 0; d < head_dim; ++d) s += f16_to_f32(q[qh * head_dim + d]) * f16_to_f32(kr[d]);
+      s = s * sm_scale;
+      const float mn = s > m ? s : m;
+      const float a = expf(m - mn), p = expf(s - mn);
+      l = l * a + p;
+      for (int64_t d = 0; d < head_dim; ++d) acc[d] = acc[d] * a + p * f16_to_f32(vr[d]);
+      m = mn;
+    }
+    for (int64_t d = 0; d < head_dim; ++d) out[qh * head_dim + d] = acc[d] / l;
+  }
+  free(acc);
+}

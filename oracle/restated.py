@@ -53,6 +53,8 @@ def lib() -> C.CDLL:
         L.orc_rotary_f32.argtypes = [_f32p, _f32p, _I64, _I64, _I64, _I64, C.c_int, C.c_float, _I64, _f32p, C.c_int]
         L.orc_adain_snake_f32.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _I64, _I64, _I64, _I64, _I64,
                                           C.c_float, C.c_int]
+        L.orc_attention_decode_f16.argtypes = [_u16p, _u16p, _u16p, _f32p, _I64, _I64, _I64, _I64, C.c_float,
+                                               _I64, _I64]
         L.orc_conv1d_f32io.argtypes = [_f32p, _u16p, C.c_void_p, _f32p, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                                        _I64, _I64, C.c_int]
         _lib = L
@@ -339,4 +341,16 @@ def conv1d_f32io(x, w_bits, bias_bits=None, stride=1, padding=0, dilation=1, nth
     b = None if bias_bits is None else _c(bias_bits, np.uint16)
     lib().orc_conv1d_f32io(x.ravel(), w.ravel(), _ptr(b), out.ravel(), B, C_in, C_out, T_in, T_out, K, stride,
                            padding, dilation, nthreads)
+    return out
+
+
+def attention_decode(q_bits, k_bits, v_bits, kv_len, n_kv_heads, sm_scale, stride_kv_head, stride_kv_seq):
+    """attention_decode_1d_masked restated: q f16 bits [n_q_heads, head_dim]; k, v f16 bits (flat, addressed as
+    head * stride_kv_head + pos * stride_kv_seq + d) -> f32 [n_q_heads, head_dim] before the f16 store."""
+    q = _c(q_bits, np.uint16)
+    n_q_heads, head_dim = q.shape
+    out = np.empty((n_q_heads, head_dim), np.float32)
+    lib().orc_attention_decode_f16(q.ravel(), _c(k_bits, np.uint16).ravel(), _c(v_bits, np.uint16).ravel(),
+                                   out.ravel(), kv_len, head_dim, n_kv_heads, n_q_heads, sm_scale, stride_kv_head,
+                                   stride_kv_seq)
     return out

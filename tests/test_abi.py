@@ -114,6 +114,17 @@ def test_version_and_header_is_plain_c():
     lambda L: L.nsr_q8_0_to_t4(16, 48, 64, 1, 16, 16, NULL),
     lambda L: L.nsr_q8_0_to_gemv_q8(17, 64, 64, 16, 16, NULL),
     lambda L: L.nsr_q8_0_to_t4(16, 64, 48, 0, 16, 16, NULL),
+    # decode attention: head_dim not a multiple of 4, head_dim > 128, kv_len 0, more KV heads than query heads,
+    # misaligned K, stride_kv_seq < head_dim, no partial buffer, no splits, null q
+    lambda L: L.nsr_attention_splitkv_f16(16, 16, 16, 16, 16, 8, 6, 2, 4, C.c_float(0.125), 64, 8, 2, NULL),
+    lambda L: L.nsr_attention_splitkv_f16(16, 16, 16, 16, 16, 8, 132, 2, 4, C.c_float(0.125), 1056, 132, 2, NULL),
+    lambda L: L.nsr_attention_splitkv_f16(16, 16, 16, 16, 16, 0, 64, 2, 4, C.c_float(0.125), 512, 64, 2, NULL),
+    lambda L: L.nsr_attention_splitkv_f16(16, 16, 16, 16, 16, 8, 64, 8, 4, C.c_float(0.125), 512, 64, 2, NULL),
+    lambda L: L.nsr_attention_splitkv_f16(16, 18, 16, 16, 16, 8, 64, 2, 4, C.c_float(0.125), 512, 64, 2, NULL),
+    lambda L: L.nsr_attention_splitkv_f16(16, 16, 16, 16, 16, 8, 64, 2, 4, C.c_float(0.125), 512, 32, 2, NULL),
+    lambda L: L.nsr_attention_splitkv_f16(16, 16, 16, 16, NULL, 8, 64, 2, 4, C.c_float(0.125), 512, 64, 2, NULL),
+    lambda L: L.nsr_attention_splitkv_f16(16, 16, 16, 16, 16, 8, 64, 2, 4, C.c_float(0.125), 512, 64, 0, NULL),
+    lambda L: L.nsr_attention_decode_f16(NULL, 16, 16, 16, 8, 64, 2, 4, C.c_float(0.125), 512, 64, NULL),
 ])
 def test_invalid_arguments_are_rejected_before_any_launch(call):
     L = abi.lib()

@@ -520,3 +520,67 @@ def test_conv1d_f32io_identity_and_delta():
         if 0 <= t < 40:
             exp[0, :, t] = w[:, 1, k].astype(np.float32)
     assert_bitexact(out, exp, "delta response")
+
+
+# ------------------------------------------------------------ decode attention
+
+def _attn_f64(q, k, v, kv_len, n_kv_heads, sm_scale, skh, sks):
+    """softmax(sm_scale q.K^T) V per query head in float64 (numpy), K/V addressed as
+    head * skh + pos * sks + d in the flat f16 arrays."""
+    nq, hd = q.shape
+    kf = k.astype(np.float64).ravel()
+    vf = v.astype(np.float64).ravel()
+    out = np.empty((nq, hd))
+    for h in range(nq):
+        kvh = h * n_kv_heads // nq
+        idx = kvh * skh + np.arange(kv_len)[:, None] * sks + np.arange(hd)[None, :]
+        s = kf[idx] @ q[h].astype(np.float64) * sm_scale
+        w = np.exp(s - s.max())
+        out[h] = (w / w.sum()) @ vf[idx]
+    return out
+
+
+@pytest.mark.parametrize("nq,nkv,hd,kv_len,layout", [
+    (4, 2, 64, 100, "cache"), (8, 8, 52, 37, "encoder"), (10, 10, 64, 1, "cache"), (6, 3, 128, 300, "encoder")])
+def test_attention_oracle_matches_f64_softmax(nq, nkv, hd, kv_len, layout):
+    g = configs.rng(nq * 31 + kv_len)
+    q = g.standard_normal((nq, hd)).astype(np.float16)
+    if layout == "cache":  # [heads, max_kv_len, hd], max_kv_len > kv_len
+        mx = kv_len + 5
+        k = g.standard_normal((nkv, mx, hd)).astype(np.float16)
+        v = g.standard_normal((nkv, mx, hd)).astype(np.float16)
+        skh, sks = mx * hd, hd
+    else:                  # [kv_len, heads, hd]
+        k = g.standard_normal((kv_len, nkv, hd)).astype(np.float16)
+        v = g.standard_normal((kv_len, nkv, hd)).astype(np.float16)
+        skh, sks = hd, nkv * hd
+    scale = 1.0 / math.sqrt(hd)
+    got = R.attention_decode(q.view(np.uint16), k.view(np.uint16), v.view(np.uint16), kv_len, nkv, scale, skh, sks)
+    ref = _attn_f64(q, k, v, kv_len, nkv, scale, skh, sks)
+    assert np.max(np.abs(got - ref)) <= 2e-6 * max(1.0, float(np.max(np.abs(ref))))
+
+
+def test_attention_oracle_special_cases():
+    g = configs.rng(77)
+    hd, L = 64, 50
+    v = g.standard_normal((1, L, hd)).astype(np.float16)
+    # one position: the output is that V row exactly (p = 1, l = 1)
+    q = g.standard_normal((1, hd)).astype(np.float16)
+    k = g.standard_normal((1, L, hd)).astype(np.float16)
+    one = R.attention_decode(q.view(np.uint16), k.view(np.uint16), v.view(np.uint16), 1, 1, 0.125, L * hd, hd)
+    assert np.array_equal(one[0], v[0, 0].astype(np.float32))
+    # q = 0: every score is 0, the output is the mean of the V rows
+    z = np.zeros((1, hd), np.float16)
+    mean = R.attention_decode(z.view(np.uint16), k.view(np.uint16), v.view(np.uint16), L, 1, 0.125, L * hd, hd)
+    assert np.max(np.abs(mean[0] - v[0].astype(np.float64).mean(axis=0))) < 1e-6
+    # one key aligned with q and a large scale: that position's V row dominates
+    k2 = np.zeros((1, L, hd), np.float16)
+    k2[0, 17] = q[0]
+    dom = R.attention_decode(q.view(np.uint16), k2.view(np.uint16), v.view(np.uint16), L, 1, 50.0, L * hd, hd)
+    assert np.max(np.abs(dom[0] - v[0, 17].astype(np.float32))) < 1e-6
+    # a permutation of the positions leaves the output unchanged (up to f32 rounding)
+    perm = g.permutation(L)
+    a = R.attention_decode(q.view(np.uint16), k.view(np.uint16), v.view(np.uint16), L, 1, 0.125, L * hd, hd)
+    b = R.attention_decode(q.view(np.uint16), np.ascontiguousarray(k[:, perm]).view(np.uint16),
+                           np.ascontiguousarray(v[:, perm]).view(np.uint16), L, 1, 0.125, L * hd, hd)
+    assert np.max(np.abs(a - b)) < 1e-6
