@@ -323,6 +323,45 @@ void enc_residual_add(Encoder enc, const RocmKernels&, const GpuBuffer& x, const
             "enc_residual_add");
 }
 
+// ------------------------------------------------------------ decoder step --
+
+void enc_rope_qk_cache_fused(Encoder enc, const RocmKernels&, const GpuBuffer& q, const GpuBuffer& k,
+                             const GpuBuffer& rope_table, const GpuBuffer& cache_k, size_t pos, size_t max_kv_len,
+                             size_t n_q_heads, size_t n_kv_heads, size_t head_dim, size_t rotary_dim) {
+  nsr_check(nsr_rope_qk_cache_append(q.at(), k.at(), nullptr, NSR_F16, static_cast<const float*>(rope_table.at()),
+                                     (int64_t)max_kv_len, cache_k.at(), nullptr, (int64_t)n_q_heads,
+                                     (int64_t)n_kv_heads, (int64_t)head_dim, (int)rotary_dim, (int64_t)pos,
+                                     (int64_t)max_kv_len, enc),
+            "enc_rope_qk_cache_fused");
+}
+
+void enc_kv_cache_append(Encoder enc, const RocmKernels&, const GpuBuffer& new_kv, const GpuBuffer& cache,
+                         size_t n_kv_heads, size_t head_dim, size_t max_kv_len, size_t pos) {
+  nsr_check(nsr_kv_cache_append(new_kv.at(), cache.at(), NSR_F16, (int64_t)n_kv_heads, (int64_t)head_dim,
+                                (int64_t)max_kv_len, (int64_t)pos, enc),
+            "enc_kv_cache_append");
+}
+
+void enc_attention_decode(Encoder enc, const RocmKernels&, const GpuBuffer& q, const GpuBuffer& k, const GpuBuffer& v,
+                          const GpuBuffer& out, size_t kv_len, size_t head_dim, size_t n_kv_heads, size_t n_q_heads,
+                          float sm_scale, size_t stride_kv_head, size_t stride_kv_seq) {
+  nsr_check(nsr_attention_decode_f16(q.at(), k.at(), v.at(), out.at(), (int64_t)kv_len, (int64_t)head_dim,
+                                     (int64_t)n_kv_heads, (int64_t)n_q_heads, sm_scale, (int64_t)stride_kv_head,
+                                     (int64_t)stride_kv_seq, enc),
+            "enc_attention_decode");
+}
+
+void enc_attention_splitkv(Encoder enc, const RocmKernels&, const GpuBuffer& q, const GpuBuffer& k,
+                           const GpuBuffer& v, const GpuBuffer& out, const GpuBuffer& partial_buf, size_t kv_len,
+                           size_t head_dim, size_t n_kv_heads, size_t n_q_heads, float sm_scale,
+                           size_t stride_kv_head, size_t stride_kv_seq, size_t n_splits) {
+  nsr_check(nsr_attention_splitkv_f16(q.at(), k.at(), v.at(), out.at(), static_cast<float*>(partial_buf.at()),
+                                      (int64_t)kv_len, (int64_t)head_dim, (int64_t)n_kv_heads, (int64_t)n_q_heads,
+                                      sm_scale, (int64_t)stride_kv_head, (int64_t)stride_kv_seq, (int64_t)n_splits,
+                                      enc),
+            "enc_attention_splitkv");
+}
+
 // ---------------------------------------------------------------- Kokoro --
 
 void RocmKokoroBackend::adain_snake_f32(const GpuBuffer& x, const GpuBuffer& gamma, const GpuBuffer& beta,

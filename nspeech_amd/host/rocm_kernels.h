@@ -156,6 +156,32 @@ void enc_gelu(Encoder enc, const RocmKernels& kernels, const GpuBuffer& x, const
 void enc_residual_add(Encoder enc, const RocmKernels& kernels, const GpuBuffer& x, const GpuBuffer& residual,
                       const GpuBuffer& out, size_t n_elements);
 
+// Decoder step (src/triton_kernels.rs:900-1010). The reference bakes the head
+// count, head_dim and rotary dim into the compiled rope kernel
+// (kernels/kernel_configs.py:102-104); here they are arguments.
+// enc_rope_qk_cache_fused (:975-991): RoPE on q [n_q_heads, head_dim] and
+// k [n_kv_heads, head_dim] f16 in place at `pos` (table row `pos` of the
+// [max_kv_len, rotary_dim] f32 RoPE table), rotated k into cache_k
+// [n_kv_heads, max_kv_len, head_dim].
+void enc_rope_qk_cache_fused(Encoder enc, const RocmKernels& kernels, const GpuBuffer& q, const GpuBuffer& k,
+                             const GpuBuffer& rope_table, const GpuBuffer& cache_k, size_t pos, size_t max_kv_len,
+                             size_t n_q_heads, size_t n_kv_heads, size_t head_dim, size_t rotary_dim);
+// enc_kv_cache_append (:993-1010): new_kv [n_kv_heads, head_dim] f16 into row `pos` of the cache.
+void enc_kv_cache_append(Encoder enc, const RocmKernels& kernels, const GpuBuffer& new_kv, const GpuBuffer& cache,
+                         size_t n_kv_heads, size_t head_dim, size_t max_kv_len, size_t pos);
+// enc_attention_decode (:900-923): f16 q [n_q_heads, head_dim] against kv_len
+// cached positions (strides in elements) -> f16 out [n_q_heads, head_dim].
+void enc_attention_decode(Encoder enc, const RocmKernels& kernels, const GpuBuffer& q, const GpuBuffer& k,
+                          const GpuBuffer& v, const GpuBuffer& out, size_t kv_len, size_t head_dim,
+                          size_t n_kv_heads, size_t n_q_heads, float sm_scale, size_t stride_kv_head,
+                          size_t stride_kv_seq);
+// enc_attention_splitkv (:925-973): as above over n_splits ranges with the
+// caller's partial buffer (3 * 128 f32 per head and split is enough).
+void enc_attention_splitkv(Encoder enc, const RocmKernels& kernels, const GpuBuffer& q, const GpuBuffer& k,
+                           const GpuBuffer& v, const GpuBuffer& out, const GpuBuffer& partial_buf, size_t kv_len,
+                           size_t head_dim, size_t n_kv_heads, size_t n_q_heads, float sm_scale,
+                           size_t stride_kv_head, size_t stride_kv_seq, size_t n_splits);
+
 // ---- Kokoro backend (src/kokoro/gpu_backend.rs) ------------------------------
 
 // The AdaIN+Snake part of KokoroGpuBackend for the ROCm device: Buf = GpuBuffer.

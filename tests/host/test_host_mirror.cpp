@@ -302,6 +302,100 @@ void test_rotary(const RocmDevice& dev, const RocmKernels& k) {
   report("apply_rotary_pos_emb (RoPE table)", err, 1e-5);
 }
 
+// One decoder step after another, as the reference's decoder runs them
+// (src/moonshine/gpu_decoder_metal.rs:144-182): RoPE + K cache write, V cache
+// append, self-attention over positions 0..pos, then cross-attention over a
+// fixed "encoder" K/V with the reference's min(32, kv_len) splits. The
+// expected values: float64 rotation (f32 angles as RotaryEmbedding) rounded
+// to f16 like the stored q/k, float64 softmax attention.
+void test_decode_step(const RocmDevice& dev, const RocmKernels& k) {
+  const size_t Hq = 8, Hk = 2, Dh = 64, rot = 32, L = 40, steps = 12, Lx = 70;
+  const float scale = 0.125f;
+  RotaryEmbedding re(dev, k, rot, L, 10000.0f);
+  std::vector<uint16_t> ck(Hk * L * Dh, 0), cv(Hk * L * Dh, 0);  // host mirror of the caches (f16)
+  Tensor CK = Tensor::from_host(dev, ck.data(), {Hk, L, Dh}, DType::F16);
+  Tensor CV = Tensor::from_host(dev, cv.data(), {Hk, L, Dh}, DType::F16);
+  // encoder K/V [Lx, Hk, Dh]
+  std::vector<uint16_t> xk(Lx * Hk * Dh), xv(Lx * Hk * Dh);
+  for (size_t i = 0; i < xk.size(); ++i) {
+    xk[i] = f2h(std::sin(0.011f * (float)i));
+    xv[i] = f2h(std::cos(0.017f * (float)i));
+  }
+  Tensor XK = Tensor::from_host(dev, xk.data(), {Lx, Hk, Dh}, DType::F16);
+  Tensor XV = Tensor::from_host(dev, xv.data(), {Lx, Hk, Dh}, DType::F16);
+  Tensor partial = Tensor::empty(dev, {Hq * 32 * 384}, DType::F32);
+  auto attend = [&](const std::vector<uint16_t>& q, const uint16_t* kk, const uint16_t* vv, size_t n, size_t skh,
+                    size_t sks, std::vector<double>& out) {
+    for (size_t h = 0; h < Hq; ++h) {
+      const size_t kvh = h * Hk / Hq;
+      std::vector<double> s(n);
+      double m = -1e300;
+      for (size_t j = 0; j < n; ++j) {
+        double d = 0;
+        for (size_t e = 0; e < Dh; ++e) d += (double)h2f(q[h * Dh + e]) * h2f(kk[kvh * skh + j * sks + e]);
+        s[j] = d * scale;
+        m = std::max(m, s[j]);
+      }
+      double l = 0;
+      for (size_t j = 0; j < n; ++j) l += (s[j] = std::exp(s[j] - m));
+      for (size_t e = 0; e < Dh; ++e) {
+        double a = 0;
+        for (size_t j = 0; j < n; ++j) a += s[j] * h2f(vv[kvh * skh + j * sks + e]);
+        out[h * Dh + e] = a / l;
+      }
+    }
+  };
+  double err_self = 0, err_cross = 0;
+  for (size_t pos = 0; pos < steps; ++pos) {
+    std::vector<uint16_t> q(Hq * Dh), kn(Hk * Dh), vn(Hk * Dh);
+    for (size_t i = 0; i < q.size(); ++i) q[i] = f2h(std::sin(0.37f * (float)(i + 97 * pos)));
+    for (size_t i = 0; i < kn.size(); ++i) kn[i] = f2h(std::cos(0.23f * (float)(i + 53 * pos)));
+    for (size_t i = 0; i < vn.size(); ++i) vn[i] = f2h(std::sin(0.13f * (float)(i + 31 * pos)));
+    Tensor Q = Tensor::from_host(dev, q.data(), {Hq, Dh}, DType::F16);
+    Tensor K = Tensor::from_host(dev, kn.data(), {Hk, Dh}, DType::F16);
+    Tensor V = Tensor::from_host(dev, vn.data(), {Hk, Dh}, DType::F16);
+    Tensor O = Tensor::empty(dev, {Hq, Dh}, DType::F16);
+    Tensor OX = Tensor::empty(dev, {Hq, Dh}, DType::F16);
+    enc_rope_qk_cache_fused(dev.stream(), k, Q.buffer(), K.buffer(), re.table().buffer(), CK.buffer(), pos, L, Hq,
+                            Hk, Dh, rot);
+    enc_kv_cache_append(dev.stream(), k, V.buffer(), CV.buffer(), Hk, Dh, L, pos);
+    enc_attention_decode(dev.stream(), k, Q.buffer(), CK.buffer(), CV.buffer(), O.buffer(), pos + 1, Dh, Hk, Hq,
+                         scale, L * Dh, Dh);
+    const size_t splits = std::min<size_t>(32, Lx);
+    enc_attention_splitkv(dev.stream(), k, Q.buffer(), XK.buffer(), XV.buffer(), OX.buffer(), partial.buffer(), Lx,
+                          Dh, Hk, Hq, scale, Dh, Hk * Dh, splits);
+    dev.synchronize();
+    // host: rotate q, k (f32 angle, float64 products, f16 store), append to the caches
+    auto rope = [&](std::vector<uint16_t>& x, size_t H) {
+      for (size_t h = 0; h < H; ++h)
+        for (size_t p = 0; p < rot / 2; ++p) {
+          const float inv_freq = 1.0f / std::pow(10000.0f, (2.0f * (float)p) / (float)rot);
+          const double ang = (double)((float)pos * inv_freq);
+          const double x0 = h2f(x[h * Dh + 2 * p]), x1 = h2f(x[h * Dh + 2 * p + 1]);
+          x[h * Dh + 2 * p] = f2h((float)(x0 * std::cos(ang) - x1 * std::sin(ang)));
+          x[h * Dh + 2 * p + 1] = f2h((float)(x1 * std::cos(ang) + x0 * std::sin(ang)));
+        }
+    };
+    rope(q, Hq);
+    rope(kn, Hk);
+    for (size_t h = 0; h < Hk; ++h)
+      for (size_t e = 0; e < Dh; ++e) {
+        ck[(h * L + pos) * Dh + e] = kn[h * Dh + e];
+        cv[(h * L + pos) * Dh + e] = vn[h * Dh + e];
+      }
+    std::vector<double> ref(Hq * Dh), refx(Hq * Dh);
+    attend(q, ck.data(), cv.data(), pos + 1, L * Dh, Dh, ref);
+    attend(q, xk.data(), xv.data(), Lx, Dh, Hk * Dh, refx);
+    const std::vector<uint16_t> o = O.to_vec<uint16_t>(), ox = OX.to_vec<uint16_t>();
+    for (size_t i = 0; i < ref.size(); ++i) {
+      err_self = std::max(err_self, scaled(h2f(o[i]), ref[i]));
+      err_cross = std::max(err_cross, scaled(h2f(ox[i]), refx[i]));
+    }
+  }
+  report("decode step: rope+cache, self-attn", err_self, 2e-3);
+  report("decode step: cross-attn (splitkv)", err_cross, 2e-3);
+}
+
 void test_errors(const RocmDevice& dev, const RocmKernels& k) {
   float host[8] = {0};
   Tensor C = Tensor::cpu(host, {2, 4}, DType::F32);
@@ -335,6 +429,7 @@ int main() {
     test_residual_add_layernorm(dev, k);
     test_q8_embedding(dev, k);
     test_rotary(dev, k);
+    test_decode_step(dev, k);
     test_errors(dev, k);
   } catch (const Error& e) {
     std::printf("unexpected error: %s\n", e.what());
