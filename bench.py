@@ -48,9 +48,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workloads",
                     default="c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,attn,attnx,q8fc1,q8fc2,q8fc1r,q8fc2r,q8conv,kconv3,kconv11,"
-                            "kconv3u",
+                            "kconv3u,mrf,istft",
                     help="comma list of c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,attn,attnx,q8fc1,q8fc2,q8fc1r,q8fc2r,q8conv,"
-                         "kconv3,kconv11,kconv3u,copy")
+                         "kconv3,kconv11,kconv3u,mrf,istft,copy")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline (0 = skip)")
     ap.add_argument("--no-rotate", action="store_true", help="one buffer set (warm MALL) for all timings")
     return ap.parse_args()
@@ -299,6 +299,42 @@ def build_workload(name):
         alg = N * K // 32 * 34 + N * K + N * K // 32 * 2
         return Workload(name, f"GGUF Q8_0 weight [{N},{K}] -> t4 GLU tiles (load-time conversion)", alg, alg,
                         make_set, launch, "nsrk_gemv_q8_from_q8_0", "u8")
+
+    if name == "mrf":
+        # Kokoro multi-receptive-field average after the three resblocks of the last upsample stage, fused with the
+        # leaky ReLU(0.01) before conv_post: ((r0 + r1) + r2) * f32(1/3), f32 [8, 128, 115200] (the c4b shape).
+        B, C, TT = configs.c4b()["x"].shape
+        g = configs.rng(1013)
+        rs = [torch.from_numpy(g.standard_normal((B, C, TT), dtype=np.float32)).to(dev) for _ in range(3)]
+
+        def make_set(_):
+            return {"o": torch.empty_like(rs[0])}
+
+        def launch(s):
+            abi.check(L.nsr_resblock_average_f32(rs[0].data_ptr(), rs[1].data_ptr(), rs[2].data_ptr(),
+                                                 s["o"].data_ptr(), B * C * TT, 1, 0.01, stream()))
+
+        alg = 4 * 4 * B * C * TT
+        return Workload(name, f"Kokoro MRF average + leaky ReLU f32 3 x [{B},{C},{TT}]", alg, alg, make_set, launch,
+                        "nsrk_combine_f32_v", "f32")
+
+    if name == "istft":
+        # Kokoro iSTFT (n_fft 20, hop 5) of one utterance's conv_post output at the c4b frame count:
+        # x f32 [22, 115200] (log-magnitudes, raw phases) -> 575995 samples (24 s at 24 kHz).
+        n_frames, n_fft, hop = configs.c4b()["x"].shape[2], 20, 5
+        g = configs.rng(1014)
+        x0 = torch.from_numpy((g.standard_normal((2 * (n_fft // 2 + 1), n_frames)) * 0.7).astype(np.float32)).to(dev)
+        out_len = (n_frames - 1) * hop
+
+        def make_set(_):
+            return {"x": x0.clone(), "o": torch.empty(out_len, dtype=torch.float32, device=dev)}
+
+        def launch(s):
+            abi.check(L.nsr_istft_f32(s["x"].data_ptr(), s["o"].data_ptr(), n_frames, out_len, n_fft, hop, stream()))
+
+        alg = 4 * x0.numel() + 4 * out_len
+        return Workload(name, f"Kokoro iSTFT n_fft {n_fft} hop {hop}, x f32 [22,{n_frames}] -> [{out_len}]", alg, alg,
+                        make_set, launch, "nsrk_istft_f32_n20", "f32")
 
     if name in ("kconv3", "kconv11", "kconv3u"):
         # One Kokoro ResBlock stage at the final upsample shape (x [8, 128, 115200], as config c4b):

@@ -248,6 +248,42 @@ nsr_status nsr_glu_silu(const void* fc1, void* out, nsr_dtype dtype, int64_t n,
 nsr_status nsr_residual_add(const void* x, const void* res, void* out,
                             nsr_dtype dtype, int64_t n, nsr_stream_t stream);
 
+/* ---- Kokoro generator tail (f32) --------------------------------------------- */
+
+/* out = x * s. With s = 1/3 (the f32 nearest it): KokoroGpuBackend::
+ * scale_third_f32 (src/kokoro/gpu_backend.rs:193-195; kernels/
+ * kokoro_kernels.py:957-969); also the backend's `scale` (:39). */
+nsr_status nsr_scale_f32(const float* x, float* out, int64_t n, float s, nsr_stream_t stream);
+
+/* out = x > 0 ? x : x * slope. KokoroGpuBackend::leaky_relu_f32
+ * (src/kokoro/gpu_backend.rs:197-200; conv_post input, src/kokoro/
+ * decoder.rs:574-575). */
+nsr_status nsr_leaky_relu_f32(const float* x, float* out, int64_t n, float slope, nsr_stream_t stream);
+
+/* The generator's average of its three resblocks, in one pass:
+ *   out = ((r0 + r1) + r2) * f32(1/3), then, if leaky_relu != 0,
+ *   out = out > 0 ? out : out * slope
+ * with the rounding sequence of the reference GPU path's add_f32, add_f32,
+ * scale_third_f32 (and leaky_relu_f32 before conv_post) dispatches
+ * (src/kokoro/decoder.rs:540-546, 574-575). The residual add alone
+ * (KokoroGpuBackend::add_f32, :186-190) is nsr_residual_add with NSR_F32.
+ * No counterpart fuses these in the reference. */
+nsr_status nsr_resblock_average_f32(const float* r0, const float* r1, const float* r2, float* out, int64_t n,
+                                    int leaky_relu, float slope, nsr_stream_t stream);
+
+/* Inverse STFT of conv_post's output x [2 (n_fft / 2 + 1), n_frames] f32
+ * (log-magnitudes, then raw phases): magnitude exp(x), phase sin(x), one-
+ * sided iDFT, periodic Hann window, overlap-add, division by the window-
+ * square sum (0 where it is <= 1e-8), n_fft / 2 samples of centre padding
+ * removed: out [out_len], out_len <= (n_frames - 1) hop (the decoder asks
+ * for exactly that). n_fft 16, 20 or 32 (others: NSR_ERR_UNSUPPORTED), a
+ * multiple of hop (Kokoro: 20, 5).
+ * Replaces KokoroGpuBackend::istft_gpu (src/kokoro/gpu_backend.rs:220-225;
+ * Metal istft_fused, kernels/kokoro_kernels.py:1097-1183) and the CPU
+ * exp / sin / istft of src/kokoro/decoder.rs:606-612, 1546-1632. */
+nsr_status nsr_istft_f32(const float* x, float* out, int64_t n_frames, int64_t out_len, int n_fft, int hop,
+                         nsr_stream_t stream);
+
 /* ---- Decode attention (one query position per head) ----------------------- */
 
 /* out[h, :] f16 = softmax_j(sm_scale * q[h, :] . K[kvh, j, :]) . V[kvh, j, :]

@@ -84,6 +84,10 @@ def lib() -> C.CDLL:
         L.nsr_attention_splitkv_f16.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, C.c_float, _I64, _I64,
                                                 _I64, _P]
         L.nsr_attention_decode_f16.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, C.c_float, _I64, _I64, _P]
+        L.nsr_scale_f32.argtypes = [_P, _P, _I64, C.c_float, _P]
+        L.nsr_leaky_relu_f32.argtypes = [_P, _P, _I64, C.c_float, _P]
+        L.nsr_resblock_average_f32.argtypes = [_P, _P, _P, _P, _I64, C.c_int, C.c_float, _P]
+        L.nsr_istft_f32.argtypes = [_P, _P, _I64, _I64, C.c_int, C.c_int, _P]
         for name in ("nsr_init", "nsr_layernorm", "nsr_residual_add_layernorm", "nsr_rope_table_f32",
                      "nsr_rope_qk_cache_append", "nsr_kv_cache_append",
                      "nsr_rotary_partial_interleaved_f32", "nsr_adain_snake_f32", "nsr_q8_0_embed_gather",
@@ -91,6 +95,7 @@ def lib() -> C.CDLL:
                      "nsr_gemv_q8_bias_glu", "nsr_gemv_q8_resadd_ln", "nsr_q8_pack_t4", "nsr_gemv_q8_t4", "nsr_q8_0_to_gemv_q8", "nsr_q8_0_to_t4",
                      "nsr_conv1d_f32io", "nsr_conv1d_pack_f16", "nsr_conv1d_f16w_packed",
                      "nsr_adain_snake_conv1d_f32", "nsr_attention_splitkv_f16", "nsr_attention_decode_f16",
+                     "nsr_scale_f32", "nsr_leaky_relu_f32", "nsr_resblock_average_f32", "nsr_istft_f32",
                      "nsr_gemv_q8_t4_bias_glu", "nsr_gemv_q8_t4_resadd_ln"):
             getattr(L, name).restype = C.c_int
         _lib = L
@@ -440,4 +445,53 @@ def attention_decode(q, k, v, kv_len, n_kv_heads, sm_scale, *, stride_kv_head, s
         check(lib().nsr_attention_splitkv_f16(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(partial), kv_len, head_dim,
                                               n_kv_heads, n_q_heads, sm_scale, stride_kv_head, stride_kv_seq,
                                               n_splits, _stream(stream)))
+    return out
+
+
+# ------------------------------------------------- Kokoro generator tail ---
+
+def _same_f32(*ts):
+    n = ts[0].numel()
+    for t in ts:
+        if t.dtype != torch.float32:
+            raise ValueError("expected float32 tensors")
+        if t.numel() != n:
+            raise ValueError("element counts differ")
+    return n
+
+
+def scale_f32(x, s, *, out=None, stream=None):
+    out = torch.empty_like(x) if out is None else out
+    n = _same_f32(x, out)
+    check(lib().nsr_scale_f32(_ptr(x), _ptr(out), n, s, _stream(stream)))
+    return out
+
+
+def leaky_relu_f32(x, slope, *, out=None, stream=None):
+    out = torch.empty_like(x) if out is None else out
+    n = _same_f32(x, out)
+    check(lib().nsr_leaky_relu_f32(_ptr(x), _ptr(out), n, slope, _stream(stream)))
+    return out
+
+
+def resblock_average_f32(r0, r1, r2, *, leaky_slope=None, out=None, stream=None):
+    """((r0 + r1) + r2) * f32(1/3), then leaky ReLU when leaky_slope is given."""
+    out = torch.empty_like(r0) if out is None else out
+    n = _same_f32(r0, r1, r2, out)
+    check(lib().nsr_resblock_average_f32(_ptr(r0), _ptr(r1), _ptr(r2), _ptr(out), n,
+                                         0 if leaky_slope is None else 1,
+                                         0.0 if leaky_slope is None else leaky_slope, _stream(stream)))
+    return out
+
+
+def istft_f32(x, *, n_fft=20, hop=5, out_len=None, out=None, stream=None):
+    """x f32 [2 (n_fft/2 + 1), n_frames] (log-magnitude, raw phase) -> audio f32 [(n_frames - 1) hop]."""
+    if x.dim() != 2 or x.shape[0] != 2 * (n_fft // 2 + 1) or x.dtype != torch.float32:
+        raise ValueError("x must be f32 [2 * (n_fft // 2 + 1), n_frames]")
+    n_frames = x.shape[1]
+    out_len = (n_frames - 1) * hop if out_len is None else out_len
+    out = torch.empty(out_len, dtype=torch.float32, device=x.device) if out is None else out
+    if out.dtype != torch.float32 or out.numel() < out_len:
+        raise ValueError("out must be f32 with at least out_len elements")
+    check(lib().nsr_istft_f32(_ptr(x), _ptr(out), n_frames, out_len, n_fft, hop, _stream(stream)))
     return out

@@ -9,6 +9,13 @@
  *   glu_silu: out[i] = silu(fc1[n + i]) * fc1[i]  (glu_silu_fused,
  *     kernels/moonshine_kernels.py:846-862; DecoderMLP::forward decoder.rs:403-411)
  *   residual add: out = x + res  (FastAddOp, src/fast_ops.rs:16-36)
+ *   combine (f32): out = lrelu?(((a + b) + c) * scale), the Kokoro
+ *     generator's resblock average and conv_post input, as the reference GPU
+ *     path computes it in four dispatches: add_f32 (r0 + r1), add_f32 (+ r2),
+ *     scale_third_f32 (x * f32(1/3), kernels/kokoro_kernels.py:941-969) and
+ *     leaky_relu_f32 (x >= 0 ? x : x * slope) (src/kokoro/decoder.rs:540-577,
+ *     src/kokoro/gpu_backend.rs:186-200); one pass here, same rounding
+ *     sequence.
  *
  * One lane per 16-byte chunk (4 f32 or 8 f16/bf16 elements), flat grid,
  * arithmetic in f32 and one rounding to the storage dtype. The _s variants
@@ -112,3 +119,35 @@ NSR_DEV void add_scalar(const nsr_ew_args& a, int64_t first) {
 NSR_EW_SET(f32, DT_F32)
 NSR_EW_SET(f16, DT_F16)
 NSR_EW_SET(bf16, DT_BF16)
+
+/* ----------------------------------------------------------- combine -- */
+
+NSR_DEV float combine_one(const nsr_combine_args& a, float x, float y, float z) {
+  float v = x;
+  if (a.b) v = v + y;
+  if (a.c) v = v + z;
+  if (a.flags & 1) v = v * a.scale;
+  if (a.flags & 2) v = v > 0.f ? v : v * a.slope;
+  return v;
+}
+
+/* one lane per 4 elements (16-byte aligned pointers) */
+extern "C" __global__ void __launch_bounds__(256) nsrk_combine_f32_v(const nsr_combine_args a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.n / 4) return;
+  const nsr_float4 x = ldf4(a.a + 4 * i);
+  const nsr_float4 y = a.b ? ldf4(a.b + 4 * i) : x;
+  const nsr_float4 z = a.c ? ldf4(a.c + 4 * i) : x;
+  nsr_float4 o;
+  o.x = combine_one(a, x.x, y.x, z.x);
+  o.y = combine_one(a, x.y, y.y, z.y);
+  o.z = combine_one(a, x.z, y.z, z.z);
+  o.w = combine_one(a, x.w, y.w, z.w);
+  stf4(a.out + 4 * i, o);
+}
+
+extern "C" __global__ void __launch_bounds__(256) nsrk_combine_f32_s(const nsr_combine_args a, const int64_t first) {
+  const int64_t i = first + (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.n) return;
+  a.out[i] = combine_one(a, a.a[i], a.b ? a.b[i] : 0.f, a.c ? a.c[i] : 0.f);
+}

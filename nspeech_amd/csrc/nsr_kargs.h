@@ -160,6 +160,27 @@ typedef struct nsr_conv_pack_args {
   int64_t C_out, C_in, K;
 } nsr_conv_pack_args;
 
+/* out = lrelu?(((a + b) + c) * scale), b / c optional (NULL), f32 */
+typedef struct nsr_combine_args {
+  const float* a;
+  const float* b;          /* or NULL */
+  const float* c;          /* or NULL */
+  float* out;
+  int64_t n;
+  float scale;             /* applied when flags bit 0 */
+  float slope;             /* leaky ReLU slope, applied when flags bit 1 */
+  int32_t flags;
+  int32_t pad_;
+} nsr_combine_args;
+
+typedef struct nsr_istft_args {
+  const float* x;          /* [2 * bins, n_frames]: log-magnitudes, then raw phases (phase = sin(raw)) */
+  float* out;              /* [out_len], centre padding (n_fft / 2 each side) removed */
+  int64_t n_frames;
+  int64_t out_len;
+  int32_t n_fft, hop, frames_per_group, pad_;
+} nsr_istft_args;
+
 typedef struct nsr_ew_args {
   const void* a;
   const void* b;

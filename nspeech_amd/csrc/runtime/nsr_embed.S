@@ -21,5 +21,6 @@ NSR_EMBED(elementwise)
 NSR_EMBED(gemv_q8)
 NSR_EMBED(conv1d)
 NSR_EMBED(attention)
+NSR_EMBED(istft)
 
     .section .note.GNU-stack, "", @progbits

@@ -32,6 +32,7 @@ extern "C" const unsigned char nsr_co_elementwise[];
 extern "C" const unsigned char nsr_co_gemv_q8[];
 extern "C" const unsigned char nsr_co_conv1d[];
 extern "C" const unsigned char nsr_co_attention[];
+extern "C" const unsigned char nsr_co_istft[];
 
 namespace {
 
@@ -46,7 +47,8 @@ const Unit kUnits[] = {{"q8_0_gather", nsr_co_q8_0_gather},
                        {"elementwise", nsr_co_elementwise},
                        {"gemv_q8", nsr_co_gemv_q8},
                        {"conv1d", nsr_co_conv1d},
-                       {"attention", nsr_co_attention}};
+                       {"attention", nsr_co_attention},
+                       {"istft", nsr_co_istft}};
 constexpr int kNumUnits = sizeof(kUnits) / sizeof(kUnits[0]);
 
 constexpr int kMaxDevices = 64;
@@ -142,7 +144,7 @@ int unit_of(const std::string& name) {
   static const P map[] = {{"nsrk_q8_0_", 0}, {"nsrk_ln_", 1},    {"nsrk_resln_", 1}, {"nsrk_rope_", 2},
                           {"nsrk_adain_", 3}, {"nsrk_silu_", 4}, {"nsrk_gelu_", 4},  {"nsrk_glu_", 4},
                           {"nsrk_add_", 4},  {"nsrk_gemv_", 5},
-                          {"nsrk_conv1d_", 6}, {"nsrk_attn_", 7}};
+                          {"nsrk_conv1d_", 6}, {"nsrk_attn_", 7}, {"nsrk_combine_", 4}, {"nsrk_istft_", 8}};
   for (const P& p : map)
     if (name.compare(0, std::strlen(p.prefix), p.prefix) == 0) return p.unit;
   return -1;
@@ -763,6 +765,86 @@ static nsr_status ew_launch(const char* op, nsr_dtype dtype, nsr_ew_args& a, boo
                   p);
   }
   return NSR_OK;
+}
+
+// f32 combine: out = lrelu?(((a + b) + c) * scale)
+static nsr_status combine_launch(const float* a, const float* b, const float* c, float* out, int64_t n, bool scale,
+                                 float s, bool lrelu, float slope, nsr_stream_t stream, const char* what) {
+  if (!a || !out) return fail(NSR_ERR_BAD_ARG, "%s: null pointer", what);
+  if (n < 0) return fail(NSR_ERR_BAD_ARG, "%s: n < 0", what);
+  if (!aligned(a, 4) || !aligned(out, 4) || (b && !aligned(b, 4)) || (c && !aligned(c, 4)))
+    return fail(NSR_ERR_BAD_ARG, "%s: misaligned pointer", what);
+  if (n == 0) return NSR_OK;
+  nsr_combine_args g;
+  std::memset(&g, 0, sizeof(g));
+  g.a = a;
+  g.b = b;
+  g.c = c;
+  g.out = out;
+  g.n = n;
+  g.scale = s;
+  g.slope = slope;
+  g.flags = (scale ? 1 : 0) | (lrelu ? 2 : 0);
+  const bool vec = aligned(a, 16) && aligned(out, 16) && (!b || aligned(b, 16)) && (!c || aligned(c, 16));
+  int64_t first = 0;
+  if (vec && n / 4 > 0) {
+    if ((n / 4 + 255) / 256 > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "%s: too large", what);
+    void* p[] = {&g};
+    nsr_status st = launch("nsrk_combine_f32_v", cdiv_u(n / 4, 256), 1, 256, 0, stream, p);
+    if (st != NSR_OK) return st;
+    first = n / 4 * 4;
+  }
+  if (n > first) {
+    if ((n - first + 255) / 256 > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "%s: too large", what);
+    void* p[] = {&g, &first};
+    return launch("nsrk_combine_f32_s", cdiv_u(n - first, 256), 1, 256, 0, stream, p);
+  }
+  return NSR_OK;
+}
+
+nsr_status nsr_scale_f32(const float* x, float* out, int64_t n, float s, nsr_stream_t stream) {
+  return combine_launch(x, nullptr, nullptr, out, n, true, s, false, 0.f, stream, "scale_f32");
+}
+
+nsr_status nsr_leaky_relu_f32(const float* x, float* out, int64_t n, float slope, nsr_stream_t stream) {
+  return combine_launch(x, nullptr, nullptr, out, n, false, 1.f, true, slope, stream, "leaky_relu_f32");
+}
+
+nsr_status nsr_resblock_average_f32(const float* r0, const float* r1, const float* r2, float* out, int64_t n,
+                                    int leaky_relu, float slope, nsr_stream_t stream) {
+  if (!r1 || !r2) return fail(NSR_ERR_BAD_ARG, "resblock_average_f32: null pointer");
+  // the reference's elementwise_scale_third_f32 multiplies by the f32 nearest 1/3
+  return combine_launch(r0, r1, r2, out, n, true, (float)0.3333333333333333, leaky_relu != 0, slope, stream,
+                        "resblock_average_f32");
+}
+
+// ------------------------------------------------------------------ iSTFT --
+
+nsr_status nsr_istft_f32(const float* x, float* out, int64_t n_frames, int64_t out_len, int n_fft, int hop,
+                         nsr_stream_t stream) {
+  if (!x || !out) return fail(NSR_ERR_BAD_ARG, "istft: null pointer");
+  if (n_frames < 1 || n_frames > (1LL << 31) - 1 || hop < 1 || n_fft < 2 || n_fft % hop != 0)
+    return fail(NSR_ERR_BAD_ARG, "istft: need n_frames >= 1 and hop dividing n_fft");
+  if (n_fft != 16 && n_fft != 20 && n_fft != 32)
+    return fail(NSR_ERR_UNSUPPORTED, "istft: n_fft %d not built (16, 20, 32)", n_fft);
+  if (out_len < 0 || out_len > (n_frames - 1) * (int64_t)hop)
+    return fail(NSR_ERR_BAD_ARG, "istft: out_len must be in [0, (n_frames - 1) * hop]");
+  if (!aligned(x, 4) || !aligned(out, 4)) return fail(NSR_ERR_BAD_ARG, "istft: misaligned pointer");
+  if (out_len == 0) return NSR_OK;
+  nsr_istft_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.x = x;
+  a.out = out;
+  a.n_frames = n_frames;
+  a.out_len = out_len;
+  a.n_fft = n_fft;
+  a.hop = hop;
+  a.frames_per_group = 256;
+  const int64_t R = n_fft / hop, step = 256 - (R - 1);
+  const int64_t groups = n_frames <= 256 ? 1 : 1 + (n_frames - 256 + step - 1) / step;
+  void* params[] = {&a};
+  return launch("nsrk_istft_f32_n" + std::to_string(n_fft), (unsigned)groups, 1, 256,
+                (unsigned)(256 * n_fft * sizeof(float)), stream, params);
 }
 
 nsr_status nsr_activation(const void* x, void* y, nsr_dtype dtype, int64_t n, nsr_act act,

@@ -576,3 +576,77 @@ ORC_API void orc_attention_decode_f16(const uint16_t* q, const uint16_t* k, cons
   }
   free(acc);
 }
+
+/* Kokoro generator tail, element-wise part. The reference's GPU chain after
+ * the three resblocks of a stage (src/kokoro/decoder.rs:540-575; CPU
+ * restatement :604-606) is elementwise_add_f32 twice
+ * (kernels/kokoro_kernels.py:942-954), elementwise_scale_third_f32 (:958-969,
+ * x * 0.3333333333333333 rounded to f32) and, after the last stage,
+ * leaky_relu_f32 with slope 0.01 (the tl.where(x > 0, x, x * slope) form of
+ * :109-122 and :600-605). Per element, with b / c / scale / lrelu optional:
+ *   v = a; v = v + b; v = v + c; v = v * s; v = v > 0 ? v : v * slope. */
+ORC_API void orc_combine_f32(const float* a, const float* b, const float* c, float* out, int64_t n, int scale,
+                             float s, int lrelu, float slope) {
+  for (int64_t i = 0; i < n; ++i) {
+    float v = a[i];
+    if (b) v = v + b[i];
+    if (c) v = v + c[i];
+    if (scale) v = v * s;
+    if (lrelu) v = v > 0.0f ? v : v * slope;
+    out[i] = v;
+  }
+}
+
+/* Inverse STFT of conv_post's output, the reference's CPU istft
+ * (src/kokoro/decoder.rs:1545-1632) fed as at :610-612 (magnitude =
+ * exp(x[0 .. bins)), phase = sin(x[bins .. 2 bins))), batch 1:
+ *   x [2 bins][n_frames] (bins = n_fft / 2 + 1);
+ *   periodic Hann w[n] = 0.5 - 0.5 cos(2 pi n / n_fft) and the iDFT tables
+ *   cos / sin(2 pi k n / n_fft), all from f32 angles (:1556-1571);
+ *   frame[n] = (sum_k s_k (re_k cos_nk - im_k sin_nk)) / n_fft with
+ *   re = m cos(p), im = m sin(p), s_k = 1 for k = 0 and bins - 1, else 2
+ *   (:1585-1601); overlap-add of frame[n] * w[n] at f * hop + n, frames in
+ *   order (:1604-1610); window_sum of w[n]^2 in frame order (:1576-1583);
+ *   division where window_sum > 1e-8 (:1613-1618); trim n_fft / 2 at both
+ *   ends (:1621-1628). out has (n_frames - 1) * hop samples. */
+ORC_API void orc_istft_f32(const float* x, float* out, int64_t n_frames, int64_t n_fft, int64_t hop) {
+  const int64_t bins = n_fft / 2 + 1, full = (n_frames - 1) * hop + n_fft, trim = n_fft / 2;
+  const float PI = 3.14159265358979323846f;
+  float* win = (float*)malloc((size_t)n_fft * sizeof(float));
+  float* cb = (float*)malloc((size_t)(n_fft * bins) * sizeof(float));
+  float* sb = (float*)malloc((size_t)(n_fft * bins) * sizeof(float));
+  float* y = (float*)calloc((size_t)full, sizeof(float));
+  float* ws = (float*)calloc((size_t)full, sizeof(float));
+  float* fr = (float*)malloc((size_t)n_fft * sizeof(float));
+  for (int64_t n = 0; n < n_fft; ++n) win[n] = 0.5f - 0.5f * cosf(2.0f * PI * (float)n / (float)n_fft);
+  for (int64_t n = 0; n < n_fft; ++n)
+    for (int64_t k = 0; k < bins; ++k) {
+      const float ang = 2.0f * PI * (float)k * (float)n / (float)n_fft;
+      cb[n * bins + k] = cosf(ang);
+      sb[n * bins + k] = sinf(ang);
+    }
+  for (int64_t f = 0; f < n_frames; ++f)
+    for (int64_t n = 0; n < n_fft; ++n) ws[f * hop + n] += win[n] * win[n];
+  for (int64_t f = 0; f < n_frames; ++f) {
+    for (int64_t n = 0; n < n_fft; ++n) {
+      float v = 0.0f;
+      for (int64_t k = 0; k < bins; ++k) {
+        const float m = expf(x[k * n_frames + f]), p = sinf(x[(bins + k) * n_frames + f]);
+        const float re = m * cosf(p), im = m * sinf(p);
+        const float s = (k == 0 || k == bins - 1) ? 1.0f : 2.0f;
+        v += s * (re * cb[n * bins + k] - im * sb[n * bins + k]);
+      }
+      fr[n] = v / (float)n_fft;
+    }
+    for (int64_t n = 0; n < n_fft; ++n) y[f * hop + n] += fr[n] * win[n];
+  }
+  for (int64_t i = 0; i < full; ++i)
+    if (ws[i] > 1e-8f) y[i] /= ws[i];
+  for (int64_t i = 0; i < full - 2 * trim; ++i) out[i] = y[i + trim];
+  free(win);
+  free(cb);
+  free(sb);
+  free(y);
+  free(ws);
+  free(fr);
+}

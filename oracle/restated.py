@@ -55,6 +55,9 @@ def lib() -> C.CDLL:
                                           C.c_float, C.c_int]
         L.orc_attention_decode_f16.argtypes = [_u16p, _u16p, _u16p, _f32p, _I64, _I64, _I64, _I64, C.c_float,
                                                _I64, _I64]
+        L.orc_combine_f32.argtypes = [_f32p, C.c_void_p, C.c_void_p, _f32p, _I64, C.c_int, C.c_float, C.c_int,
+                                      C.c_float]
+        L.orc_istft_f32.argtypes = [_f32p, _f32p, _I64, _I64, _I64]
         L.orc_conv1d_f32io.argtypes = [_f32p, _u16p, C.c_void_p, _f32p, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                                        _I64, _I64, C.c_int]
         _lib = L
@@ -354,3 +357,33 @@ def attention_decode(q_bits, k_bits, v_bits, kv_len, n_kv_heads, sm_scale, strid
                                    out.ravel(), kv_len, head_dim, n_kv_heads, n_q_heads, sm_scale, stride_kv_head,
                                    stride_kv_seq)
     return out
+
+
+def combine(a, b=None, c=None, scale=None, lrelu_slope=None):
+    """((a + b) + c) * scale, then x > 0 ? x : x * slope (each step optional)."""
+    a = _c(a, np.float32).ravel()
+    b = None if b is None else _c(b, np.float32).ravel()
+    c = None if c is None else _c(c, np.float32).ravel()
+    out = np.empty_like(a)
+    lib().orc_combine_f32(a, _ptr(b), _ptr(c), out, a.size, int(scale is not None),
+                          0.0 if scale is None else float(scale), int(lrelu_slope is not None),
+                          0.0 if lrelu_slope is None else float(lrelu_slope))
+    return out
+
+
+def resblock_average(r0, r1, r2, lrelu_slope=None):
+    """The Kokoro MRF average ((r0 + r1) + r2) * f32(1/3) (+ leaky ReLU)."""
+    return combine(r0, r1, r2, np.float32(0.3333333333333333), lrelu_slope)
+
+
+def istft(x, n_fft: int, hop: int):
+    """x [2 * (n_fft // 2 + 1), n_frames] f32 (log-magnitudes, raw phases) ->
+    trimmed audio of (n_frames - 1) * hop samples."""
+    x = _c(x, np.float32)
+    bins = n_fft // 2 + 1
+    assert x.ndim == 2 and x.shape[0] == 2 * bins
+    n_frames = x.shape[1]
+    out = np.empty((n_frames - 1) * hop, np.float32)
+    lib().orc_istft_f32(x, out, n_frames, n_fft, hop)
+    return out
+

@@ -125,6 +125,16 @@ def test_version_and_header_is_plain_c():
     lambda L: L.nsr_attention_splitkv_f16(16, 16, 16, 16, NULL, 8, 64, 2, 4, C.c_float(0.125), 512, 64, 2, NULL),
     lambda L: L.nsr_attention_splitkv_f16(16, 16, 16, 16, 16, 8, 64, 2, 4, C.c_float(0.125), 512, 64, 0, NULL),
     lambda L: L.nsr_attention_decode_f16(NULL, 16, 16, 16, 8, 64, 2, 4, C.c_float(0.125), 512, 64, NULL),
+    # Kokoro tail: null input, negative n, misaligned pointer; iSTFT out_len past (n_frames - 1) * hop,
+    # hop not dividing n_fft, an n_fft with no kernel, no frames, null output
+    lambda L: L.nsr_resblock_average_f32(16, NULL, 16, 16, 8, 0, C.c_float(0.0), NULL),
+    lambda L: L.nsr_scale_f32(16, 16, -1, C.c_float(2.0), NULL),
+    lambda L: L.nsr_leaky_relu_f32(18, 16, 8, C.c_float(0.01), NULL),
+    lambda L: L.nsr_istft_f32(16, 16, 10, 46, 20, 5, NULL),
+    lambda L: L.nsr_istft_f32(16, 16, 10, 20, 20, 3, NULL),
+    lambda L: L.nsr_istft_f32(16, 16, 10, 20, 24, 4, NULL),
+    lambda L: L.nsr_istft_f32(16, 16, 0, 0, 20, 5, NULL),
+    lambda L: L.nsr_istft_f32(16, NULL, 10, 20, 20, 5, NULL),
 ])
 def test_invalid_arguments_are_rejected_before_any_launch(call):
     L = abi.lib()

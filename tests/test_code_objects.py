@@ -28,7 +28,7 @@ import pytest
 ROOT = Path(__file__).resolve().parent.parent
 LIB = ROOT / "nspeech_amd" / "lib"
 LLVM = Path("/opt/rocm/llvm/bin")
-UNITS = ["q8_0_gather", "layernorm", "rotary", "adain_snake", "elementwise", "gemv_q8", "conv1d", "attention"]
+UNITS = ["q8_0_gather", "layernorm", "rotary", "adain_snake", "elementwise", "gemv_q8", "conv1d", "attention", "istft"]
 
 
 def _co(unit):

@@ -584,3 +584,109 @@ def test_attention_oracle_special_cases():
     b = R.attention_decode(q.view(np.uint16), np.ascontiguousarray(k[:, perm]).view(np.uint16),
                            np.ascontiguousarray(v[:, perm]).view(np.uint16), L, 1, 0.125, L * hd, hd)
     assert np.max(np.abs(a - b)) < 1e-6
+
+
+# ------------------------------------------------------- Kokoro tail ---
+
+def _istft_f64(x, n_fft, hop):
+    """torch.istft(center=True, periodic Hann) semantics in float64 via numpy's
+    irfft: a different route (FFT, not the cos/sin basis sums)."""
+    x = x.astype(np.float64)
+    bins = n_fft // 2 + 1
+    n_frames = x.shape[1]
+    spec = np.exp(x[:bins]) * np.exp(1j * np.sin(x[bins:]))
+    # irfft drops the imaginary parts of the DC and Nyquist bins, as the
+    # basis sum does (sin(0) = sin(pi n) = 0)
+    frames = np.fft.irfft(spec.T, n=n_fft, axis=1)
+    w = 0.5 - 0.5 * np.cos(2 * np.pi * np.arange(n_fft) / n_fft)
+    full = (n_frames - 1) * hop + n_fft
+    y = np.zeros(full)
+    ws = np.zeros(full)
+    for f in range(n_frames):
+        y[f * hop:f * hop + n_fft] += frames[f] * w
+        ws[f * hop:f * hop + n_fft] += w * w
+    y = np.where(ws > 1e-8, y / np.where(ws > 1e-8, ws, 1.0), y)
+    return y[n_fft // 2: full - n_fft // 2]
+
+
+@pytest.mark.parametrize("n_fft,hop,n_frames", [(20, 5, 64), (20, 5, 2), (16, 4, 33), (32, 8, 17), (20, 10, 9)])
+def test_istft_oracle_matches_f64_irfft(n_fft, hop, n_frames):
+    g = configs.rng(n_fft * 100 + n_frames)
+    x = (g.standard_normal((2 * (n_fft // 2 + 1), n_frames)) * 0.7).astype(np.float32)
+    got = R.istft(x, n_fft, hop)
+    ref = _istft_f64(x, n_fft, hop)
+    assert got.shape == ref.shape == ((n_frames - 1) * hop,)
+    # f32 tables and sums over n_fft / 2 + 1 bins: a few f32 ulps of the peak
+    err = np.max(np.abs(got - ref)) / np.max(np.abs(ref))
+    assert err < 5e-6, err
+
+
+@pytest.mark.parametrize("N,hop,k0,A,x0", [(20, 5, 0, 1.5, 0.0), (20, 5, 4, 0.8, 0.0), (20, 5, 4, 0.8, 0.9),
+                                          (20, 5, 8, 2.0, -1.3), (16, 4, 8, 0.5, 0.0), (16, 4, 8, 0.5, 1.1),
+                                          (16, 4, 4, 1.0, 0.4)])
+def test_istft_oracle_closed_forms(N, hop, k0, A, x0):
+    """Interior samples (all N / hop = 4 frames overlap) of a periodic Hann
+    at 75% overlap: sum w = 2 and sum w^2 = 3/2. A bin-k0 spectrum of
+    magnitude A and phase phi with k0 hop / N an integer adds the same
+    sample in every frame, so it comes back as s (A / N)(4/3) cos(2 pi k0 p
+    / N + phi) (s = 2, or 1 for DC; the Nyquist bin keeps only A cos(phi))."""
+    F = 40
+    bins = N // 2 + 1
+    assert (k0 * hop) % N == 0
+    p = np.arange(N // 2, (F - 1) * hop + N // 2)  # untrimmed positions of the outputs
+    interior = (p >= N - hop) & (p < (F - 1) * hop + hop)
+    x = np.full((2 * bins, F), -200.0, np.float32)  # exp(-200) = 0 in f32
+    x[bins:] = 0.0
+    x[k0] = np.log(A)
+    x[bins + k0] = x0
+    phi = np.sin(np.float64(np.float32(x0)))
+    out = R.istft(x, N, hop).astype(np.float64)
+    if k0 == bins - 1:
+        want = A / N * (4.0 / 3.0) * np.cos(phi) * np.cos(np.pi * p)
+    else:
+        scale = 1.0 if k0 == 0 else 2.0
+        want = scale * A / N * (4.0 / 3.0) * np.cos(2 * np.pi * k0 * p / N + phi)
+    assert np.max(np.abs(out[interior] - want[interior])) < 2e-6 * A
+
+
+def test_istft_oracle_layout_and_trim():
+    """A single frame carrying energy shows where it lands: frame f's samples
+    occupy untrimmed positions [f hop, f hop + N), output index = position -
+    N / 2; every other output sample stays 0."""
+    N, hop, F = 20, 5, 12
+    bins = N // 2 + 1
+    x = np.full((2 * bins, F), -200.0, np.float32)
+    x[bins:] = 0.0
+    x[0, 6] = 0.0  # frame 6: DC bin of magnitude 1
+    out = R.istft(x, N, hop)
+    nz = np.nonzero(out)[0]
+    assert nz.min() == 6 * hop + 1 - N // 2 and nz.max() == 6 * hop + N - 1 - N // 2  # w[0] = 0
+    assert np.all(out[nz] > 0)
+
+
+def test_combine_oracle_special_cases():
+    g = configs.rng(91)
+    a, b, c = (g.standard_normal(4096).astype(np.float32) for _ in range(3))
+    third = np.float32(0.3333333333333333)
+    # association ((a + b) + c), then the f32 multiply by the rounded 1/3
+    ref = ((a.astype(np.float64) + b + c) / 3.0)
+    got = R.resblock_average(a, b, c)
+    assert np.max(np.abs(got - ref)) <= 4e-7 * np.max(np.abs(ref)) * 4
+    # the product by f32(1/3) is not the division by 3: some inputs differ by an ulp
+    ints = np.arange(1, 4096, dtype=np.float32) * np.float32(1.1)
+    z = np.zeros_like(ints)
+    mul = R.resblock_average(ints, z, z)
+    assert np.array_equal(mul, ints * third)
+    assert np.any(mul != ints / np.float32(3.0))
+    # the sum is associated left to right: big + (-big) + small keeps small
+    big = np.full(4, 3e7, np.float32)
+    small = np.full(4, 1.0, np.float32)
+    assert np.all(R.combine(big, -big, small) == 1.0)
+    assert np.all(R.combine(small, big, -big) == 0.0)
+    # leaky ReLU: positives untouched, negatives times slope, zeros stay zero
+    v = np.array([2.0, -2.0, 0.0, -0.0, 1e-30, -1e30], np.float32)
+    lr = R.combine(v, lrelu_slope=0.01)
+    assert np.array_equal(lr, np.array([2.0, np.float32(-2.0) * np.float32(0.01), 0.0, 0.0, 1e-30,
+                                        np.float32(-1e30) * np.float32(0.01)], np.float32))
+    # scale alone
+    assert np.array_equal(R.combine(a, scale=0.25), a * np.float32(0.25))
