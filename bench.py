@@ -47,10 +47,10 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workloads",
-                    default="c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,attn,attnx,q8fc1,q8fc2,q8fc1r,q8fc2r,q8conv,kconv3,kconv11,"
-                            "kconv3u,mrf,istft",
-                    help="comma list of c0,c1,c1t,c2,c3,c4a,c4b,dec,dec2,attn,attnx,q8fc1,q8fc2,q8fc1r,q8fc2r,q8conv,"
-                         "kconv3,kconv11,kconv3u,mrf,istft,copy")
+                    default="c0,c1,c1t,c2,c3,c4a,c4b,c2u,c2h,dec,dec2,attn,attnx,q8fc1,q8fc2,q8fc1r,q8fc2r,q8conv,kconv3,"
+                            "kconv11,kconv3u,mrf,istft",
+                    help="comma list of c0,c1,c1t,c2,c3,c4a,c4b,c2u,c2h,dec,dec2,attn,attnx,q8fc1,q8fc2,q8fc1r,q8fc2r,"
+                         "q8conv,kconv3,kconv11,kconv3u,mrf,istft,copy")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline (0 = skip)")
     ap.add_argument("--no-rotate", action="store_true", help="one buffer set (warm MALL) for all timings")
     return ap.parse_args()
@@ -149,6 +149,47 @@ def build_workload(name):
         kern = "nsrk_adain_row_b256_v5_l0" if name == "c2" else "nsrk_adain_row_b512_v44_l14"
         return Workload(name, f"AdaIN1d+Snake f32 x[{B},{C},{TT}]", configs.algorithmic_bytes(name),
                         2 * x0.numel() * 4, make_set, launch, kern, "f32")
+
+    if name == "c2u":
+        # c2 with an odd row length, as Kokoro's frame counts usually are: x f32 [1, 512, 4801] (rows not 16-byte
+        # aligned, the unaligned resident kernel).
+        c = configs.c2()
+        g_ = configs.rng(1015)
+        B, C, TT = 1, c["x"].shape[1], c["x"].shape[2] + 1
+        x0 = T(g_.standard_normal((B, C, TT), dtype=np.float32))
+        g, b, a = T(c["gamma"]), T(c["beta"]), T(c["alpha"])
+        gs = C if c["gamma"].ndim == 2 else 0
+
+        def make_set(_):
+            return {"x": x0.clone(), "o": torch.empty_like(x0)}
+
+        def launch(s):
+            abi.check(L.nsr_adain_snake_f32(s["x"].data_ptr(), g.data_ptr(), b.data_ptr(), a.data_ptr(), 0, gs, gs,
+                                            s["o"].data_ptr(), B, C, TT, 1e-5, stream()))
+
+        alg = 4 * 2 * B * C * TT + 4 * 3 * C
+        return Workload(name, f"AdaIN1d+Snake f32 x[{B},{C},{TT}] (unaligned rows)", alg, alg, make_set, launch,
+                        "nsrk_adain_res_b256_nv5_u", "f32")
+
+    if name == "c2h":
+        # The c2 shape through the f16-activation entry point (the reference's KokoroGpuBackend::adain_snake,
+        # whose Triton kernels take rows up to 8192): x, out f16 [1, 512, 4800], f16 style parameters.
+        c = configs.c2()
+        x0 = T(c["x"].astype(np.float16))
+        g, b, a = (T(c[n].astype(np.float16)) for n in ("gamma", "beta", "alpha"))
+        B, C, TT = c["x"].shape
+        gs = C if c["gamma"].ndim == 2 else 0
+
+        def make_set(_):
+            return {"x": x0.clone(), "o": torch.empty_like(x0)}
+
+        def launch(s):
+            abi.check(L.nsr_adain_snake_f16(s["x"].data_ptr(), g.data_ptr(), b.data_ptr(), a.data_ptr(), 1, gs, gs,
+                                            s["o"].data_ptr(), B, C, TT, 1e-5, stream()))
+
+        alg = 2 * 2 * B * C * TT + 2 * 3 * C
+        return Workload(name, f"AdaIN1d+Snake f16 activations x[{B},{C},{TT}]", alg, alg, make_set, launch,
+                        "nsrk_adain_f16_b256_nv3", "f16")
 
     if name == "c3":
         c = configs.c3()

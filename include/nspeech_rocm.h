@@ -206,6 +206,20 @@ nsr_status nsr_adain_snake_f32(const float* x, const void* gamma, const void* be
                                float* out, int64_t B, int64_t C, int64_t T,
                                float eps, nsr_stream_t stream);
 
+/* The same with f16 activations: x and out [B, C, T] f16 (f32 arithmetic,
+ * out rounded to nearest even). Any row start: x and out 2-byte aligned with
+ * the same offset within 16 bytes (two fresh allocations qualify); T up to
+ * 131072. Replaces KokoroGpuBackend::adain_snake (src/kokoro/gpu_backend.rs:
+ * 55-57; Metal impl src/kokoro/gpu_decoder.rs:563-588 over the Triton
+ * adain_snake_fused / adain_snake_looped, kernels/kokoro_kernels.py:222-331),
+ * which the decoder's resblocks call when the backend keeps f16
+ * intermediates (src/kokoro/decoder.rs:1009, 1035). */
+nsr_status nsr_adain_snake_f16(const void* x, const void* gamma, const void* beta,
+                               const void* alpha, nsr_dtype param_dtype,
+                               int64_t gamma_bstride, int64_t beta_bstride,
+                               void* out, int64_t B, int64_t C, int64_t T,
+                               float eps, nsr_stream_t stream);
+
 /* ---- GGUF Q8_0 embedding gather-dequant ----------------------------------- */
 
 /* blocks: the GGUF Q8_0 table, vocab rows of d/32 blocks of 34 bytes

@@ -61,6 +61,8 @@ def lib() -> C.CDLL:
         L.nsr_kv_cache_append.argtypes = [_P, _P, C.c_int, _I64, _I64, _I64, _I64, _P]
         L.nsr_adain_snake_f32.argtypes = [_P, _P, _P, _P, C.c_int, _I64, _I64, _P, _I64, _I64, _I64, C.c_float,
                                           _P]
+        L.nsr_adain_snake_f16.argtypes = [_P, _P, _P, _P, C.c_int, _I64, _I64, _P, _I64, _I64, _I64, C.c_float,
+                                          _P]
         L.nsr_q8_0_embed_gather.argtypes = [_P, _I64, _I64, _P, C.c_int, _I64, _P, C.c_int, _P, _P]
         L.nsr_activation.argtypes = [_P, _P, C.c_int, _I64, C.c_int, _P]
         L.nsr_glu_silu.argtypes = [_P, _P, C.c_int, _I64, _P]
@@ -90,7 +92,8 @@ def lib() -> C.CDLL:
         L.nsr_istft_f32.argtypes = [_P, _P, _I64, _I64, C.c_int, C.c_int, _P]
         for name in ("nsr_init", "nsr_layernorm", "nsr_residual_add_layernorm", "nsr_rope_table_f32",
                      "nsr_rope_qk_cache_append", "nsr_kv_cache_append",
-                     "nsr_rotary_partial_interleaved_f32", "nsr_adain_snake_f32", "nsr_q8_0_embed_gather",
+                     "nsr_rotary_partial_interleaved_f32", "nsr_adain_snake_f32", "nsr_adain_snake_f16",
+                     "nsr_q8_0_embed_gather",
                      "nsr_activation", "nsr_glu_silu", "nsr_residual_add", "nsr_gemv_q8",
                      "nsr_gemv_q8_bias_glu", "nsr_gemv_q8_resadd_ln", "nsr_q8_pack_t4", "nsr_gemv_q8_t4", "nsr_q8_0_to_gemv_q8", "nsr_q8_0_to_t4",
                      "nsr_conv1d_f32io", "nsr_conv1d_pack_f16", "nsr_conv1d_f16w_packed",
@@ -219,14 +222,17 @@ def kv_cache_append(new_kv, cache, pos, *, stream=None):
 
 
 def adain_snake(x, gamma, beta, alpha, *, eps=1e-5, out=None, stream=None):
-    """x [B,C,T] f32; gamma/beta [C] or [B,C]; alpha [C]; params f32 or f16."""
+    """x [B,C,T] f32 or f16 (out the same dtype); gamma/beta [C] or [B,C]; alpha [C]; params f32 or f16."""
     B, Cc, T = x.shape
     if out is None:
         out = torch.empty_like(x)
+    if out.dtype != x.dtype or x.dtype not in (torch.float32, torch.float16):
+        raise ValueError("x and out must both be float32 or both float16")
     gs = Cc if gamma.dim() == 2 else 0
     bs = Cc if beta.dim() == 2 else 0
-    check(lib().nsr_adain_snake_f32(_ptr(x), _ptr(gamma), _ptr(beta), _ptr(alpha), _dt(gamma), gs, bs, _ptr(out),
-                                    B, Cc, T, eps, _stream(stream)))
+    fn = lib().nsr_adain_snake_f32 if x.dtype == torch.float32 else lib().nsr_adain_snake_f16
+    check(fn(_ptr(x), _ptr(gamma), _ptr(beta), _ptr(alpha), _dt(gamma), gs, bs, _ptr(out), B, Cc, T, eps,
+             _stream(stream)))
     return out
 
 

@@ -32,8 +32,37 @@
  */
 #include "device_common.h"
 
-NSR_DEV float adain_param(const void* p, int pdt, int64_t i) {
-  return pdt == DT_F32 ? ((const float*)p)[i] : f16_bits_to_f32(((const uint16_t*)p)[i]);
+/* The three per-row parameters: loaded raw at the top of a kernel (in flight
+ * together, before the row's loads) and converted where they are first
+ * needed, so the wait for them falls after the row's loads were issued. The
+ * loads are branch-free (a dtype branch would make the compiler wait at the
+ * join): each reads the aligned dword holding the value (an f16 value and
+ * its dword share a page) and the half is selected afterwards. */
+struct adain_raw {
+  uint32_t g, b, l;
+};
+
+NSR_DEV uint32_t adain_raw_load(const void* p, int64_t i, int sz) {
+  const uint64_t addr = (uint64_t)p + (uint64_t)(i * sz);
+  typedef const __attribute__((address_space(1))) uint32_t gword; /* global, not flat */
+  const uint32_t w = *(gword*)(addr & ~(uint64_t)3);
+  return sz == 4 ? w : (w >> ((uint32_t)(addr & 2) * 8u)) & 0xffffu;
+}
+
+template <typename A>
+NSR_DEV adain_raw adain_params_load(const A& a, int pdt, int64_t bi, int64_t ci) {
+  const int sz = pdt == DT_F32 ? 4 : 2;
+  adain_raw r;
+  r.g = adain_raw_load(a.gamma, bi * a.gamma_bstride + ci, sz);
+  r.b = adain_raw_load(a.beta, bi * a.beta_bstride + ci, sz);
+  r.l = adain_raw_load(a.alpha, ci, sz);
+  return r;
+}
+
+NSR_DEV void adain_params_cvt(const adain_raw& r, int pdt, float& gam, float& bet, float& alp) {
+  gam = pdt == DT_F32 ? __uint_as_float(r.g) : f16_bits_to_f32(r.g);
+  bet = pdt == DT_F32 ? __uint_as_float(r.b) : f16_bits_to_f32(r.b);
+  alp = pdt == DT_F32 ? __uint_as_float(r.l) : f16_bits_to_f32(r.l);
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -79,9 +108,7 @@ NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
   /* per-row parameters first: their loads are then the oldest outstanding */
   const int64_t bi = row / a.C;
   const int64_t ci = row - bi * a.C;
-  const float gam = adain_param(a.gamma, pdt, bi * a.gamma_bstride + ci);
-  const float bet = adain_param(a.beta, pdt, bi * a.beta_bstride + ci);
-  const float alp = adain_param(a.alpha, pdt, ci);
+  const adain_raw pr = adain_params_load(a, pdt, bi, ci);
 
   const nsr_rsrc xr = make_rsrc(a.x + row * T, rbytes);
   nsr_float4 v[NV];
@@ -124,6 +151,8 @@ NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
   const float c = s1 * a.inv_t; /* mean - K */
   const float var = fmaxf(__builtin_fmaf(-c, c, s2 * a.inv_t), 0.0f);
   const float rstd = 1.0f / sqrtf(var + a.eps);
+  float gam, bet, alp;
+  adain_params_cvt(pr, pdt, gam, bet, alp);
   const float A = (gam + 1.0f) * rstd;
   const float Bc = __builtin_fmaf(-c, A, bet); /* (d - c) A + beta = d A + Bc */
   const snake_consts sc = make_snake_consts(alp);
@@ -180,39 +209,10 @@ NSR_ADAIN_ROW(512, 44, 18)
 
 /* ------------------------------------------------ unaligned resident rows -- */
 
-/* Element-wise access to a partial chunk (row edge): element idx of chunk
- * space belongs to the row iff lo <= idx < hi. */
-NSR_DEV nsr_float4 load_chunk_masked(const float* xb, int j, int lo, int64_t hi) {
-  nsr_float4 r = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int64_t idx = 4 * (int64_t)j + e;
-    if (idx >= lo && idx < hi) r[e] = xb[idx];
-  }
-  return r;
-}
-
-NSR_DEV nsr_float4 mask_chunk(nsr_float4 d, int j, int lo, int64_t hi) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int64_t idx = 4 * (int64_t)j + e;
-    if (idx < lo || idx >= hi) d[e] = 0.f;
-  }
-  return d;
-}
-
-NSR_DEV void store_chunk_masked(float* ob, int j, int lo, int64_t hi, nsr_float4 o) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int64_t idx = 4 * (int64_t)j + e;
-    if (idx >= lo && idx < hi) ob[idx] = o[e];
-  }
-}
-
 /* Rows whose start is not 16-byte aligned (misaligned views, T % 4 != 0).
  * Chunks lie on the float4 grid of the tensor: the row's first and last chunk
- * are partial and held by lane 0 (element access, e0/e1), the interior chunks
- * 1..nch-2 are full and spread as j = 1 + tid + BLOCK*k. Loads of the chunk
+ * are partial and taken one element per lane by the last 8 lanes, the
+ * interior chunks 1..nch-2 are full and spread as j = 1 + tid + BLOCK*k. Loads of the chunk
  * array are branch-free (index clamped in bounds, out-of-row slots zeroed by
  * a select), which keeps the array in VGPRs. Two-pass statistics over the
  * registers (mean, then centred sums with the corrected two-pass term). */
@@ -226,9 +226,7 @@ NSR_DEV void adain_resident_u(const nsr_adain_args& a, int pdt) {
   const int64_t bi = row / a.C;
   const int64_t ci = row - bi * a.C;
 
-  const float gam = adain_param(a.gamma, pdt, bi * a.gamma_bstride + ci);
-  const float bet = adain_param(a.beta, pdt, bi * a.beta_bstride + ci);
-  const float alp = adain_param(a.alpha, pdt, ci);
+  const adain_raw pr = adain_params_load(a, pdt, bi, ci);
 
   const int64_t s = row * T;
   const int64_t a0 = s & ~(int64_t)3;
@@ -254,13 +252,15 @@ NSR_DEV void adain_resident_u(const nsr_adain_args& a, int pdt) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) v[k] = zero4;
   }
-  nsr_float4 e0 = zero4, e1 = zero4;
-  if (tid == 0) {
-    e0 = load_chunk_masked(xb, 0, lo, hi);
-    if (jlast > 0) e1 = load_chunk_masked(xb, jlast, lo, hi);
-  }
+  /* the two edge chunks, one element per lane on the last 8 lanes of the
+   * workgroup: lane q = tid - (BLOCK - 8) takes element q & 3 of chunk 0
+   * (q < 4) or chunk nch - 1 (q >= 4) when it belongs to the row */
+  const int q = tid - (BLOCK - 8);
+  const int64_t eidx = q >= 4 ? 4 * (int64_t)jlast + (q & 3) : (int64_t)(q & 3);
+  const bool eok = q >= 0 && eidx >= lo && eidx < hi && (q < 4 || jlast > 0);
+  const float xe = eok ? xb[eidx] : 0.f;
 
-  float sum = sum4(e0) + sum4(e1);
+  float sum = xe;
 #pragma unroll
   for (int k = 0; k < NV; ++k) sum += sum4(v[k]);
   const float mean = block_sum<NW>(sum, red) * a.inv_t;
@@ -274,16 +274,17 @@ NSR_DEV void adain_resident_u(const nsr_adain_args& a, int pdt) {
     sq = sumsq4(v[k], sq);
     sd += sum4(v[k]);
   }
-  if (tid == 0) {
-    e0 = mask_chunk(e0 - mean, 0, lo, hi);
-    e1 = jlast > 0 ? mask_chunk(e1 - mean, jlast, lo, hi) : zero4;
+  if (eok) {
+    const float d = xe - mean;
+    sq = __builtin_fmaf(d, d, sq);
+    sd += d;
   }
-  sq = sumsq4(e0, sumsq4(e1, sq));
-  sd += sum4(e0) + sum4(e1);
   block_sum2<NW>(sq, sd, red);
   const float c = sd * a.inv_t;
   const float var = fmaxf(__builtin_fmaf(-c, sd, sq) * a.inv_t, 0.0f);
   const float rstd = 1.0f / sqrtf(var + a.eps);
+  float gam, bet, alp;
+  adain_params_cvt(pr, pdt, gam, bet, alp);
   const float A = (gam + 1.0f) * rstd;
   const float Bc = __builtin_fmaf(-c, A, bet);
   const snake_consts sc = make_snake_consts(alp);
@@ -294,10 +295,7 @@ NSR_DEV void adain_resident_u(const nsr_adain_args& a, int pdt) {
     const nsr_float4 o = adain_snake4(v[k], A, Bc, sc);
     if (j <= jmax) stf4(ob + 4 * (int64_t)j, o);
   }
-  if (tid == 0) {
-    store_chunk_masked(ob, 0, lo, hi, adain_snake4(e0, A, Bc, sc));
-    if (jlast > 0) store_chunk_masked(ob, jlast, lo, hi, adain_snake4(e1, A, Bc, sc));
-  }
+  if (eok) ob[eidx] = snake_eval(__builtin_fmaf(xe - mean, A, Bc), sc);
 }
 
 #define NSR_ADAIN_RES_U(BLOCK, NV)                                                      \
@@ -317,6 +315,152 @@ NSR_ADAIN_RES_U(512, 12)
 NSR_ADAIN_RES_U(512, 16)
 NSR_ADAIN_RES_U(512, 24)
 NSR_ADAIN_RES_U(512, 32)
+
+/* ------------------------------------------------------------- f16 rows -- */
+
+/* x, out [B, C, T] f16, the reference's f16-activation form
+ * (KokoroGpuBackend::adain_snake, src/kokoro/gpu_backend.rs:55-57; Triton
+ * adain_snake_fused / adain_snake_looped, kernels/kokoro_kernels.py:222-331:
+ * f16 loaded to f32, f32 statistics and snake, result rounded to f16).
+ * The row stays in VGPRs as raw 16-byte chunks (8 halves in 4 VGPRs) on the
+ * 16-byte grid of the address space, so any row start works: the row's first
+ * and last chunk may be partial and are taken one element per lane by the
+ * last 16 lanes, the interior chunks 1..nch-2 are spread as
+ * j = 1 + tid + BLOCK k with clamped, branch-free loads. out must share x's offset within 16 bytes (checked by
+ * the host). Two-pass statistics over the registers, as the f32 kernels. */
+/* pointers rebuilt from integer addresses are generic (flat accesses, which
+ * count against both memory counters); these keep them global */
+typedef __attribute__((address_space(1))) uint16_t nsr_gh;
+NSR_DEV nsr_uint4 ld16g(const nsr_gh* p) {
+  return __builtin_nontemporal_load((const __attribute__((address_space(1))) nsr_uint4*)p);
+}
+NSR_DEV void st16g(nsr_gh* p, nsr_uint4 v) {
+  __builtin_nontemporal_store(v, (__attribute__((address_space(1))) nsr_uint4*)p);
+}
+
+template <int BLOCK, int NV>
+NSR_DEV void adain_row_f16(const nsr_adain_h_args& a, int pdt) {
+  constexpr int NW = BLOCK / 64;
+  __shared__ float red[2 * NW];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  if (row >= a.n_rows) return; /* whole workgroup: the grid is one per row */
+  const int64_t T = a.T;
+  const int64_t bi = row / a.C;
+  const int64_t ci = row - bi * a.C;
+
+  const adain_raw pr = adain_params_load(a, pdt, bi, ci);
+
+  const uint64_t xa = (uint64_t)(a.x + row * T);
+  const uint64_t oa = (uint64_t)(a.out + row * T);
+  const int lo = (int)((xa & 15) >> 1); /* first row element in chunk space */
+  const int64_t hi = (int64_t)lo + T;   /* one past the last */
+  const int nch = (int)((hi + 7) >> 3);
+  const int jlast = nch - 1;
+  const int jmax = nch - 2;
+  const int jbase = 1 + tid;
+  const nsr_gh* xb = (const nsr_gh*)(xa & ~(uint64_t)15);
+  nsr_gh* ob = (nsr_gh*)(oa & ~(uint64_t)15);
+  const nsr_uint4 zero = {0u, 0u, 0u, 0u};
+
+  nsr_uint4 v[NV];
+  if (jmax >= 1) { /* at least one interior chunk (uniform) */
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int j = jbase + BLOCK * k;
+      const nsr_uint4 t = ld16g(xb + 8 * (int64_t)min(j, jmax));
+      v[k] = j <= jmax ? t : zero;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) v[k] = zero;
+  }
+  /* the two edge chunks, one element per lane on the last 16 lanes of the
+   * workgroup: lane q = tid - (BLOCK - 16) takes element q & 7 of chunk 0
+   * (q < 8) or chunk nch - 1 (q >= 8) when it belongs to the row */
+  const int q = tid - (BLOCK - 16);
+  const int64_t eidx = q >= 8 ? 8 * (int64_t)jlast + (q & 7) : (int64_t)(q & 7);
+  const bool eok = q >= 0 && eidx >= lo && eidx < hi && (q < 8 || jlast > 0);
+  const float xe = eok ? f16_bits_to_f32(xb[eidx]) : 0.f;
+
+  float sum = xe;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    float f[8];
+    unpack16<DT_F16>(v[k], f);
+    sum += ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
+  }
+  const float mean = block_sum<NW>(sum, red) * a.inv_t;
+
+  /* the chunks stay raw (4 VGPRs each) between passes: an empty asm that
+   * "modifies" them stops the compiler keeping their unpacked floats (8) live */
+#pragma unroll
+  for (int k = 0; k < NV; ++k) asm volatile("" : "+v"(v[k]));
+  /* centred sums; slots outside the interior hold zeros and are weighted out */
+  float sq = 0.f, sd = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int j = jbase + BLOCK * k;
+    float f[8], q = 0.f, t = 0.f;
+    unpack16<DT_F16>(v[k], f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float d = f[e] - mean;
+      q = __builtin_fmaf(d, d, q);
+      t += d;
+    }
+    sq += j <= jmax ? q : 0.f;
+    sd += j <= jmax ? t : 0.f;
+  }
+  if (eok) {
+    const float d = xe - mean;
+    sq = __builtin_fmaf(d, d, sq);
+    sd += d;
+  }
+  block_sum2<NW>(sq, sd, red);
+  const float c = sd * a.inv_t;
+  const float var = fmaxf(__builtin_fmaf(-c, sd, sq) * a.inv_t, 0.0f);
+  const float rstd = 1.0f / sqrtf(var + a.eps);
+  float gam, bet, alp;
+  adain_params_cvt(pr, pdt, gam, bet, alp);
+  const float A = (gam + 1.0f) * rstd;
+  const float Bc = __builtin_fmaf(-c, A, bet); /* (x - mean - c) A + beta */
+  const snake_consts sc = make_snake_consts(alp);
+
+#pragma unroll
+  for (int k = 0; k < NV; ++k) asm volatile("" : "+v"(v[k]));
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int j = jbase + BLOCK * k;
+    float f[8], o[8];
+    unpack16<DT_F16>(v[k], f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = snake_eval(__builtin_fmaf(f[e] - mean, A, Bc), sc);
+    if (j <= jmax) st16g(ob + 8 * (int64_t)j, pack16<DT_F16>(o));
+  }
+  if (eok) ob[eidx] = (uint16_t)f32_to_f16_bits(snake_eval(__builtin_fmaf(xe - mean, A, Bc), sc));
+}
+
+#define NSR_ADAIN_F16(BLOCK, NV)                                                        \
+  extern "C" __global__ void __launch_bounds__(BLOCK)                                  \
+      nsrk_adain_f16_b##BLOCK##_nv##NV(const nsr_adain_h_args a, const int pdt) {      \
+    adain_row_f16<BLOCK, NV>(a, pdt);                                                  \
+  }
+
+NSR_ADAIN_F16(256, 1)
+NSR_ADAIN_F16(256, 2)
+NSR_ADAIN_F16(256, 3)
+NSR_ADAIN_F16(256, 4)
+NSR_ADAIN_F16(256, 6)
+NSR_ADAIN_F16(256, 8)
+NSR_ADAIN_F16(512, 6)
+NSR_ADAIN_F16(512, 8)
+NSR_ADAIN_F16(512, 12)
+NSR_ADAIN_F16(512, 16)
+NSR_ADAIN_F16(512, 20)
+NSR_ADAIN_F16(512, 24)
+NSR_ADAIN_F16(512, 28)
+NSR_ADAIN_F16(512, 32)
 
 /* ------------------------------------------------------------ split path -- */
 
@@ -399,9 +543,9 @@ extern "C" __global__ void __launch_bounds__(256) nsrk_adain_apply(const nsr_ada
   const int64_t ci = row - bi * a.C;
   const float mean = a.stats[2 * row];
   const float rstd = a.stats[2 * row + 1];
-  const float gam = adain_param(a.gamma, pdt, bi * a.gamma_bstride + ci);
-  const float bet = adain_param(a.beta, pdt, bi * a.beta_bstride + ci);
-  const float alp = adain_param(a.alpha, pdt, ci);
+  const adain_raw pr = adain_params_load(a, pdt, bi, ci);
+  float gam, bet, alp;
+  adain_params_cvt(pr, pdt, gam, bet, alp);
   const float A = (gam + 1.0f) * rstd;
   const snake_consts sc = make_snake_consts(alp);
   const float* xr = a.x + row * T;

@@ -90,6 +90,22 @@ typedef struct nsr_adain_args {
   float inv_t;             /* 1 / T */
 } nsr_adain_args;
 
+typedef struct nsr_adain_h_args {
+  const uint16_t* x;       /* [B, C, T] f16 */
+  const void* gamma;       /* [B?, C] */
+  const void* beta;        /* [B?, C] */
+  const void* alpha;       /* [C] */
+  uint16_t* out;           /* [B, C, T] f16 */
+  int64_t n_rows;          /* B * C */
+  int64_t T;
+  int64_t gamma_bstride;
+  int64_t beta_bstride;
+  int32_t C;
+  float eps;
+  float inv_t;             /* 1 / T */
+  int32_t pad_;
+} nsr_adain_h_args;
+
 typedef struct nsr_gemv_args {
   const void* x;           /* [K], f16 or f32 */
   const uint32_t* qs;      /* weights: repacked Q8 [K, NW/4] words, or t4 tiles */

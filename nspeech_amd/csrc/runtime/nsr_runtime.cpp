@@ -702,6 +702,65 @@ nsr_status nsr_adain_snake_f32(const float* x, const void* gamma, const void* be
   return st;
 }
 
+nsr_status nsr_adain_snake_f16(const void* x, const void* gamma, const void* beta, const void* alpha,
+                               nsr_dtype param_dtype, int64_t gamma_bstride, int64_t beta_bstride, void* out,
+                               int64_t B, int64_t C, int64_t T, float eps, nsr_stream_t stream) {
+  if (!x || !gamma || !beta || !alpha || !out) return fail(NSR_ERR_BAD_ARG, "adain_snake_f16: null pointer");
+  if (param_dtype != NSR_F32 && param_dtype != NSR_F16)
+    return fail(NSR_ERR_BAD_ARG, "adain_snake_f16: params must be F32 or F16");
+  if (B < 0 || C <= 0 || T <= 0 || C > 0x7fffffffLL)
+    return fail(NSR_ERR_BAD_ARG, "adain_snake_f16: bad shape B=%lld C=%lld T=%lld", (long long)B, (long long)C,
+                (long long)T);
+  if (gamma_bstride < 0 || beta_bstride < 0) return fail(NSR_ERR_BAD_ARG, "adain_snake_f16: negative stride");
+  if (!(eps >= 0.0f)) return fail(NSR_ERR_BAD_ARG, "adain_snake_f16: eps must be >= 0");
+  if (!aligned(x, 2) || !aligned(out, 2)) return fail(NSR_ERR_BAD_ARG, "adain_snake_f16: misaligned pointer");
+  if ((((uintptr_t)x ^ (uintptr_t)out) & 15) != 0)
+    return fail(NSR_ERR_BAD_ARG, "adain_snake_f16: out must have the same offset within 16 bytes as x");
+  const int64_t n_rows = B * C;
+  if (n_rows == 0) return NSR_OK;
+  if (n_rows > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "adain_snake_f16: too many rows");
+  if (T > 131072) return fail(NSR_ERR_UNSUPPORTED, "adain_snake_f16: rows longer than 131072 elements");
+  // interior 16-byte chunks of a row, at the worst offset (7 elements into its first chunk)
+  const int64_t need = (T + 14) / 8 - 2;
+  unsigned block = 0;
+  int nv = 0;
+  static const int small[] = {1, 2, 3, 4, 6, 8};
+  for (int o : small)
+    if (256LL * o >= need) {
+      block = 256;
+      nv = o;
+      break;
+    }
+  if (!block) {
+    static const int large[] = {6, 8, 12, 16, 20, 24, 28, 32};
+    for (int o : large)
+      if (512LL * o >= need) {
+        block = 512;
+        nv = o;
+        break;
+      }
+  }
+  if (!block) return fail(NSR_ERR_UNSUPPORTED, "adain_snake_f16: rows longer than 131072 elements");
+  nsr_adain_h_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.x = (const uint16_t*)x;
+  a.gamma = gamma;
+  a.beta = beta;
+  a.alpha = alpha;
+  a.out = (uint16_t*)out;
+  a.n_rows = n_rows;
+  a.T = T;
+  a.gamma_bstride = gamma_bstride;
+  a.beta_bstride = beta_bstride;
+  a.C = (int32_t)C;
+  a.eps = eps;
+  a.inv_t = 1.0f / (float)T;
+  int pdt = param_dtype == NSR_F32 ? 0 : 1;
+  void* params[] = {&a, &pdt};
+  return launch("nsrk_adain_f16_b" + std::to_string(block) + "_nv" + std::to_string(nv), (unsigned)n_rows, 1, block,
+                0, stream, params);
+}
+
 // --------------------------------------------------------------- Q8_0 --
 
 nsr_status nsr_q8_0_embed_gather(const void* blocks, int64_t vocab, int64_t d, const void* ids,

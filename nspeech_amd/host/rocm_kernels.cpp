@@ -373,9 +373,12 @@ void RocmKokoroBackend::adain_snake_f32(const GpuBuffer& x, const GpuBuffer& gam
             "adain_snake_f32");
 }
 
-void RocmKokoroBackend::adain_snake(const GpuBuffer&, const GpuBuffer&, const GpuBuffer&, const GpuBuffer&,
-                                    const GpuBuffer&, size_t, size_t) const {
-  throw Error("adain_snake (f16 activations) not supported on the ROCm backend; use adain_snake_f32");
+void RocmKokoroBackend::adain_snake(const GpuBuffer& x, const GpuBuffer& gamma, const GpuBuffer& beta,
+                                    const GpuBuffer& alpha, const GpuBuffer& out, size_t channels,
+                                    size_t seq_len) const {
+  nsr_check(nsr_adain_snake_f16(x.at(), gamma.at(), beta.at(), alpha.at(), NSR_F16, 0, 0, out.at(), 1,
+                                (int64_t)channels, (int64_t)seq_len, 1e-5f, device_.stream()),
+            "adain_snake");
 }
 
 // ------------------------------------------------------------- embedding --

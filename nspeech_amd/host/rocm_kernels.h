@@ -192,8 +192,8 @@ class RocmKokoroBackend {
   // [channels] f16 (the precomputed style parameters, decoder.rs:966-981).
   void adain_snake_f32(const GpuBuffer& x, const GpuBuffer& gamma, const GpuBuffer& beta, const GpuBuffer& alpha,
                        const GpuBuffer& out, size_t channels, size_t seq_len) const;
-  // The f16-activation variant (gpu_backend.rs:55-57) is not built for this
-  // device: it throws, as the trait's unsupported methods return Err.
+  // The f16-activation variant (gpu_backend.rs:55-57): x, out [channels,
+  // seq_len] f16, parameters f16; seq_len up to 131072.
   void adain_snake(const GpuBuffer& x, const GpuBuffer& gamma, const GpuBuffer& beta, const GpuBuffer& alpha,
                    const GpuBuffer& out, size_t channels, size_t seq_len) const;
 

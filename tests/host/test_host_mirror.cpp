@@ -409,9 +409,48 @@ void test_errors(const RocmDevice& dev, const RocmKernels& k) {
   expect_throw("short tensor is rejected", [&] { triton_layernorm_std_f32in(dev, k, Xf, D, D, 4, 4); },
                "need 16");
   RocmKokoroBackend be(dev, k);
-  expect_throw("adain_snake f16 unsupported",
-               [&] { be.adain_snake(X.buffer(), X.buffer(), X.buffer(), X.buffer(), X.buffer(), 2, 4); },
-               "not supported");
+  expect_throw("adain_snake f16 row past the limit is rejected",
+               [&] { be.adain_snake(X.buffer(), X.buffer(), X.buffer(), X.buffer(), X.buffer(), 1, 200000); },
+               "131072");
+}
+
+// The same self-test inputs through the f16-activation form: x rounded to
+// f16, the f64 expectation taken on the rounded input, f16 output (2e-3 of
+// max(|ref|, 1), an f16 ulp being at most 9.8e-4 of the value).
+void test_adain_snake_f16(const RocmDevice& dev, const RocmKernels& k, size_t C, size_t T, const char* name) {
+  std::vector<uint16_t> x(C * T);
+  for (size_t i = 0; i < x.size(); ++i) x[i] = f2h(std::sin(0.001f * (float)i) * 3.0f);
+  std::vector<uint16_t> g(C), b(C), a(C);
+  for (size_t c = 0; c < C; ++c) {
+    g[c] = f2h(std::sin(0.01f * (float)c) * 0.5f);
+    b[c] = f2h(std::cos(0.02f * (float)c) * 0.3f);
+    a[c] = f2h(1.0f + std::sin(0.005f * (float)c));
+  }
+  Tensor X = Tensor::from_host(dev, x.data(), {C, T}, DType::F16);
+  Tensor G = Tensor::from_host(dev, g.data(), {C}, DType::F16);
+  Tensor B = Tensor::from_host(dev, b.data(), {C}, DType::F16);
+  Tensor A = Tensor::from_host(dev, a.data(), {C}, DType::F16);
+  Tensor O = Tensor::empty(dev, {C, T}, DType::F16);
+  RocmKokoroBackend be(dev, k);
+  be.adain_snake(X.buffer(), G.buffer(), B.buffer(), A.buffer(), O.buffer(), C, T);
+  dev.synchronize();
+  std::vector<uint16_t> o = O.to_vec<uint16_t>();
+  double err = 0;
+  for (size_t c = 0; c < C; ++c) {
+    double mean = 0, var = 0;
+    for (size_t t = 0; t < T; ++t) mean += h2f(x[c * T + t]);
+    mean /= (double)T;
+    for (size_t t = 0; t < T; ++t) var += (h2f(x[c * T + t]) - mean) * (h2f(x[c * T + t]) - mean);
+    var /= (double)T;
+    const double al = h2f(a[c]);
+    const double inv_a = (double)(1.0f / (h2f(a[c]) + 1e-9f));
+    for (size_t t = 0; t < T; ++t) {
+      const double y = (h2f(x[c * T + t]) - mean) / std::sqrt(var + 1e-5) * (1.0 + h2f(g[c])) + h2f(b[c]);
+      const double s = std::sin(al * y);
+      err = std::max(err, scaled(h2f(o[c * T + t]), y + s * s * inv_a));
+    }
+  }
+  report(name, err, 2e-3);
 }
 
 }  // namespace
@@ -423,6 +462,8 @@ int main() {
     std::printf("kernels loaded: %d probed\n", k.kernel_count());
     test_adain_snake_f32(dev, k, 4, 100, "adain_snake_f32 C=4 T=100");
     test_adain_snake_f32(dev, k, 128, 11281, "adain_snake_f32 C=128 T=11281");
+    test_adain_snake_f16(dev, k, 4, 100, "adain_snake (f16) C=4 T=100");
+    test_adain_snake_f16(dev, k, 128, 11281, "adain_snake (f16) C=128 T=11281");
     test_layernorm_std_f32in(dev, k);
     test_layernorm_unit_offset_and_bare(dev, k);
     test_elementwise(dev, k);

@@ -70,6 +70,11 @@ def test_version_and_header_is_plain_c():
     lambda L: L.nsr_adain_snake_f32(16, 16, 16, 16, 0, 0, 0, 16, 1, 4, 0, C.c_float(1e-5), NULL),
     lambda L: L.nsr_adain_snake_f32(16, NULL, 16, 16, 0, 0, 0, 16, 1, 4, 100, C.c_float(1e-5), NULL),
     lambda L: L.nsr_adain_snake_f32(16, 16, 16, 16, 2, 0, 0, 16, 1, 4, 100, C.c_float(1e-5), NULL),
+    # f16 AdaIN+Snake: null gamma, odd address, out at another offset within 16 bytes than x, row too long
+    lambda L: L.nsr_adain_snake_f16(16, NULL, 16, 16, 0, 0, 0, 16, 1, 4, 100, C.c_float(1e-5), NULL),
+    lambda L: L.nsr_adain_snake_f16(17, 16, 16, 16, 0, 0, 0, 17, 1, 4, 100, C.c_float(1e-5), NULL),
+    lambda L: L.nsr_adain_snake_f16(16, 16, 16, 16, 0, 0, 0, 18, 1, 4, 100, C.c_float(1e-5), NULL),
+    lambda L: L.nsr_adain_snake_f16(16, 16, 16, 16, 0, 0, 0, 16, 1, 4, 131073, C.c_float(1e-5), NULL),
     lambda L: L.nsr_q8_0_embed_gather(16, 100, 48, 16, 0, 4, 16, 0, NULL, NULL),
     lambda L: L.nsr_q8_0_embed_gather(16, 100, 64, 16, 0, 4, 20, 0, NULL, NULL),
     lambda L: L.nsr_q8_0_embed_gather(17, 100, 64, 16, 0, 4, 16, 0, NULL, NULL),
