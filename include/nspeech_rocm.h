@@ -285,6 +285,16 @@ nsr_status nsr_leaky_relu_f32(const float* x, float* out, int64_t n, float slope
 nsr_status nsr_resblock_average_f32(const float* r0, const float* r1, const float* r2, float* out, int64_t n,
                                     int leaky_relu, float slope, nsr_stream_t stream);
 
+/* Snake alone: out = x + sin^2(alpha_c x) * (1 / (alpha_c + 1e-9)) for x
+ * [rows, seq_len] (n_elements = rows * seq_len), row r in channel
+ * r % channels; x/out F32 or F16 (f32 arithmetic), alpha [channels] F32 or
+ * F16. Replaces KokoroGpuBackend::snake (src/kokoro/gpu_backend.rs:51-52;
+ * Metal impl src/kokoro/gpu_decoder.rs:545-561 over snake_activation,
+ * kernels/kokoro_kernels.py:24-55) and snake_activation_tensor
+ * (src/kokoro/decoder.rs:1471-1476). */
+nsr_status nsr_snake(const void* x, nsr_dtype dtype, const void* alpha, nsr_dtype alpha_dtype, void* out,
+                     int64_t n_elements, int64_t channels, int64_t seq_len, nsr_stream_t stream);
+
 /* Inverse STFT of conv_post's output x [2 (n_fft / 2 + 1), n_frames] f32
  * (log-magnitudes, then raw phases): magnitude exp(x), phase sin(x), one-
  * sided iDFT, periodic Hann window, overlap-add, division by the window-

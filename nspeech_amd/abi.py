@@ -90,6 +90,7 @@ def lib() -> C.CDLL:
         L.nsr_leaky_relu_f32.argtypes = [_P, _P, _I64, C.c_float, _P]
         L.nsr_resblock_average_f32.argtypes = [_P, _P, _P, _P, _I64, C.c_int, C.c_float, _P]
         L.nsr_istft_f32.argtypes = [_P, _P, _I64, _I64, C.c_int, C.c_int, _P]
+        L.nsr_snake.argtypes = [_P, C.c_int, _P, C.c_int, _P, _I64, _I64, _I64, _P]
         for name in ("nsr_init", "nsr_layernorm", "nsr_residual_add_layernorm", "nsr_rope_table_f32",
                      "nsr_rope_qk_cache_append", "nsr_kv_cache_append",
                      "nsr_rotary_partial_interleaved_f32", "nsr_adain_snake_f32", "nsr_adain_snake_f16",
@@ -98,7 +99,7 @@ def lib() -> C.CDLL:
                      "nsr_gemv_q8_bias_glu", "nsr_gemv_q8_resadd_ln", "nsr_q8_pack_t4", "nsr_gemv_q8_t4", "nsr_q8_0_to_gemv_q8", "nsr_q8_0_to_t4",
                      "nsr_conv1d_f32io", "nsr_conv1d_pack_f16", "nsr_conv1d_f16w_packed",
                      "nsr_adain_snake_conv1d_f32", "nsr_attention_splitkv_f16", "nsr_attention_decode_f16",
-                     "nsr_scale_f32", "nsr_leaky_relu_f32", "nsr_resblock_average_f32", "nsr_istft_f32",
+                     "nsr_scale_f32", "nsr_leaky_relu_f32", "nsr_resblock_average_f32", "nsr_istft_f32", "nsr_snake",
                      "nsr_gemv_q8_t4_bias_glu", "nsr_gemv_q8_t4_resadd_ln"):
             getattr(L, name).restype = C.c_int
         _lib = L
@@ -464,6 +465,16 @@ def _same_f32(*ts):
         if t.numel() != n:
             raise ValueError("element counts differ")
     return n
+
+
+def snake(x, alpha, *, out=None, stream=None):
+    """x [..., C, T] f32 or f16 (out the same dtype), alpha [C] f32 or f16."""
+    out = torch.empty_like(x) if out is None else out
+    if out.dtype != x.dtype or out.numel() != x.numel():
+        raise ValueError("out must match x")
+    C, T = alpha.numel(), x.shape[-1]
+    check(lib().nsr_snake(_ptr(x), _dt(x), _ptr(alpha), _dt(alpha), _ptr(out), x.numel(), C, T, _stream(stream)))
+    return out
 
 
 def scale_f32(x, s, *, out=None, stream=None):

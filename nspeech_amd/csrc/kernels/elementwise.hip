@@ -17,6 +17,12 @@
  *     src/kokoro/gpu_backend.rs:186-200); one pass here, same rounding
  *     sequence.
  *
+ *   snake (f32 or f16): out = x + sin^2(alpha_c x) / (alpha_c + 1e-9), one alpha
+ *     per channel of x [rows, T] (KokoroGpuBackend::snake,
+ *     src/kokoro/gpu_backend.rs:51-52; snake_activation
+ *     kernels/kokoro_kernels.py:24-55; snake_activation_tensor
+ *     src/kokoro/decoder.rs:1471-1476).
+ *
  * One lane per 16-byte chunk (4 f32 or 8 f16/bf16 elements), flat grid,
  * arithmetic in f32 and one rounding to the storage dtype. The _s variants
  * take one element per lane for unaligned pointers and ragged tails.
@@ -151,3 +157,34 @@ extern "C" __global__ void __launch_bounds__(256) nsrk_combine_f32_s(const nsr_c
   if (i >= a.n) return;
   a.out[i] = combine_one(a, a.a[i], a.b ? a.b[i] : 0.f, a.c ? a.c[i] : 0.f);
 }
+
+/* ------------------------------------------------------------- snake -- */
+
+/* Workgroup = (row, 1024-element chunk of the row): the row's alpha and the
+ * snake polynomial are set up once per workgroup; lanes take elements
+ * t0 + 256 k (coalesced, any alignment). */
+template <int DT>
+NSR_DEV void snake_body(const nsr_snake_args& a) {
+  const int64_t blk = blockIdx.x;
+  const int64_t row = blk / a.chunks;
+  const int64_t ch = blk - row * a.chunks;
+  const int64_t c = row % a.C;
+  const float alp = a.pdt == DT_F32 ? ((const float*)a.alpha)[c] : f16_bits_to_f32(((const uint16_t*)a.alpha)[c]);
+  const snake_consts sc = make_snake_consts(alp);
+  const int64_t base = row * a.T;
+  const int64_t t0 = ch * 1024 + threadIdx.x;
+  float v[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t t = t0 + 256 * k;
+    v[k] = t < a.T ? load_scalar<DT>(a.x, base + t) : 0.f;
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t t = t0 + 256 * k;
+    if (t < a.T) store_scalar<DT>(a.out, base + t, snake_eval(v[k], sc));
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256) nsrk_snake_f32(const nsr_snake_args a) { snake_body<DT_F32>(a); }
+extern "C" __global__ void __launch_bounds__(256) nsrk_snake_f16(const nsr_snake_args a) { snake_body<DT_F16>(a); }

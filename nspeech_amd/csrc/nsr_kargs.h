@@ -189,6 +189,16 @@ typedef struct nsr_combine_args {
   int32_t pad_;
 } nsr_combine_args;
 
+typedef struct nsr_snake_args {
+  const void* x;           /* [rows, T], f32 or f16 */
+  const void* alpha;       /* [C], f32 or f16 (pdt) */
+  void* out;               /* like x */
+  int64_t T;
+  int64_t chunks;          /* 1024-element chunks per row */
+  int32_t C;               /* channel of a row = row % C */
+  int32_t pdt;
+} nsr_snake_args;
+
 typedef struct nsr_istft_args {
   const float* x;          /* [2 * bins, n_frames]: log-magnitudes, then raw phases (phase = sin(raw)) */
   float* out;              /* [out_len], centre padding (n_fft / 2 each side) removed */

@@ -144,7 +144,8 @@ int unit_of(const std::string& name) {
   static const P map[] = {{"nsrk_q8_0_", 0}, {"nsrk_ln_", 1},    {"nsrk_resln_", 1}, {"nsrk_rope_", 2},
                           {"nsrk_adain_", 3}, {"nsrk_silu_", 4}, {"nsrk_gelu_", 4},  {"nsrk_glu_", 4},
                           {"nsrk_add_", 4},  {"nsrk_gemv_", 5},
-                          {"nsrk_conv1d_", 6}, {"nsrk_attn_", 7}, {"nsrk_combine_", 4}, {"nsrk_istft_", 8}};
+                          {"nsrk_conv1d_", 6}, {"nsrk_attn_", 7}, {"nsrk_combine_", 4}, {"nsrk_istft_", 8},
+                          {"nsrk_snake_", 4}};
   for (const P& p : map)
     if (name.compare(0, std::strlen(p.prefix), p.prefix) == 0) return p.unit;
   return -1;
@@ -875,6 +876,32 @@ nsr_status nsr_resblock_average_f32(const float* r0, const float* r1, const floa
   // the reference's elementwise_scale_third_f32 multiplies by the f32 nearest 1/3
   return combine_launch(r0, r1, r2, out, n, true, (float)0.3333333333333333, leaky_relu != 0, slope, stream,
                         "resblock_average_f32");
+}
+
+nsr_status nsr_snake(const void* x, nsr_dtype dtype, const void* alpha, nsr_dtype alpha_dtype, void* out,
+                     int64_t n_elements, int64_t channels, int64_t seq_len, nsr_stream_t stream) {
+  if (!x || !alpha || !out) return fail(NSR_ERR_BAD_ARG, "snake: null pointer");
+  if (dtype != NSR_F32 && dtype != NSR_F16) return fail(NSR_ERR_BAD_ARG, "snake: x must be F32 or F16");
+  if (alpha_dtype != NSR_F32 && alpha_dtype != NSR_F16) return fail(NSR_ERR_BAD_ARG, "snake: alpha must be F32 or F16");
+  if (n_elements < 0 || channels <= 0 || channels > 0x7fffffffLL || seq_len <= 0 || n_elements % seq_len != 0)
+    return fail(NSR_ERR_BAD_ARG, "snake: need channels > 0, seq_len > 0 dividing n_elements");
+  const int esz = dtype == NSR_F32 ? 4 : 2;
+  if (!aligned(x, esz) || !aligned(out, esz) || !aligned(alpha, alpha_dtype == NSR_F32 ? 4 : 2))
+    return fail(NSR_ERR_BAD_ARG, "snake: misaligned pointer");
+  if (n_elements == 0) return NSR_OK;
+  nsr_snake_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.x = x;
+  a.alpha = alpha;
+  a.out = out;
+  a.T = seq_len;
+  a.chunks = (seq_len + 1023) / 1024;
+  a.C = (int32_t)channels;
+  a.pdt = alpha_dtype == NSR_F32 ? 0 : 1;
+  const int64_t blocks = n_elements / seq_len * a.chunks;
+  if (blocks > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "snake: too large");
+  void* params[] = {&a};
+  return launch(dtype == NSR_F32 ? "nsrk_snake_f32" : "nsrk_snake_f16", (unsigned)blocks, 1, 256, 0, stream, params);
 }
 
 // ------------------------------------------------------------------ iSTFT --

@@ -381,6 +381,13 @@ void RocmKokoroBackend::adain_snake(const GpuBuffer& x, const GpuBuffer& gamma, 
             "adain_snake");
 }
 
+void RocmKokoroBackend::snake(const GpuBuffer& x, const GpuBuffer& alpha, const GpuBuffer& out, size_t n_elements,
+                              size_t channels, size_t seq_len) const {
+  nsr_check(nsr_snake(x.at(), NSR_F16, alpha.at(), NSR_F16, out.at(), (int64_t)n_elements, (int64_t)channels,
+                      (int64_t)seq_len, device_.stream()),
+            "snake");
+}
+
 // ------------------------------------------------------------- embedding --
 
 QEmbedding::QEmbedding(const RocmDevice& device, const RocmKernels& kernels, Tensor table, size_t vocab,

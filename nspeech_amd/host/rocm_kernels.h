@@ -196,6 +196,10 @@ class RocmKokoroBackend {
   // seq_len] f16, parameters f16; seq_len up to 131072.
   void adain_snake(const GpuBuffer& x, const GpuBuffer& gamma, const GpuBuffer& beta, const GpuBuffer& alpha,
                    const GpuBuffer& out, size_t channels, size_t seq_len) const;
+  // snake (gpu_backend.rs:51-52): out = x + sin^2(alpha_c x) / (alpha_c + 1e-9), x/out f16 [channels,
+  // seq_len] (n_elements = channels * seq_len), alpha [channels] f16.
+  void snake(const GpuBuffer& x, const GpuBuffer& alpha, const GpuBuffer& out, size_t n_elements, size_t channels,
+             size_t seq_len) const;
 
  private:
   RocmDevice device_;

@@ -650,3 +650,18 @@ ORC_API void orc_istft_f32(const float* x, float* out, int64_t n_frames, int64_t
   free(ws);
   free(fr);
 }
+
+/* Snake alone, snake_activation_tensor (src/kokoro/decoder.rs:1471-1476):
+ * ax = x * alpha_c; out = x + sin(ax)^2 * (1 / (alpha_c + 1e-9)), f32 ops in
+ * that order; x [rows][T], row r in channel r % C. */
+ORC_API void orc_snake_f32(const float* x, const float* alpha, float* out, int64_t rows, int64_t C, int64_t T) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float a = alpha[r % C];
+    const float inv_a = 1.0f / (a + 1e-9f);
+    for (int64_t t = 0; t < T; ++t) {
+      const float v = x[r * T + t];
+      const float s = sinf(v * a);
+      out[r * T + t] = v + (s * s) * inv_a;
+    }
+  }
+}

@@ -58,6 +58,7 @@ def lib() -> C.CDLL:
         L.orc_combine_f32.argtypes = [_f32p, C.c_void_p, C.c_void_p, _f32p, _I64, C.c_int, C.c_float, C.c_int,
                                       C.c_float]
         L.orc_istft_f32.argtypes = [_f32p, _f32p, _I64, _I64, _I64]
+        L.orc_snake_f32.argtypes = [_f32p, _f32p, _f32p, _I64, _I64, _I64]
         L.orc_conv1d_f32io.argtypes = [_f32p, _u16p, C.c_void_p, _f32p, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                                        _I64, _I64, C.c_int]
         _lib = L
@@ -385,5 +386,15 @@ def istft(x, n_fft: int, hop: int):
     n_frames = x.shape[1]
     out = np.empty((n_frames - 1) * hop, np.float32)
     lib().orc_istft_f32(x, out, n_frames, n_fft, hop)
+    return out
+
+
+def snake(x, alpha):
+    """x [..., C, T] (rows in channel row % C), alpha [C] -> x + sin^2(alpha x) / (alpha + 1e-9)."""
+    x = _c(x, np.float32)
+    alpha = _c(alpha, np.float32).ravel()
+    T = x.shape[-1]
+    out = np.empty_like(x)
+    lib().orc_snake_f32(x, alpha, out, x.size // T, alpha.size, T)
     return out
 

@@ -453,6 +453,28 @@ void test_adain_snake_f16(const RocmDevice& dev, const RocmKernels& k, size_t C,
   report(name, err, 2e-3);
 }
 
+// snake alone (gpu_backend.rs:51-52) on the same inputs, f16 in and out.
+void test_snake_f16(const RocmDevice& dev, const RocmKernels& k, size_t C, size_t T) {
+  std::vector<uint16_t> x(C * T), a(C);
+  for (size_t i = 0; i < x.size(); ++i) x[i] = f2h(std::sin(0.001f * (float)i) * 3.0f);
+  for (size_t c = 0; c < C; ++c) a[c] = f2h(1.0f + std::sin(0.005f * (float)c));
+  Tensor X = Tensor::from_host(dev, x.data(), {C, T}, DType::F16);
+  Tensor A = Tensor::from_host(dev, a.data(), {C}, DType::F16);
+  Tensor O = Tensor::empty(dev, {C, T}, DType::F16);
+  RocmKokoroBackend be(dev, k);
+  be.snake(X.buffer(), A.buffer(), O.buffer(), C * T, C, T);
+  dev.synchronize();
+  std::vector<uint16_t> o = O.to_vec<uint16_t>();
+  double err = 0;
+  for (size_t c = 0; c < C; ++c)
+    for (size_t t = 0; t < T; ++t) {
+      const double v = h2f(x[c * T + t]), al = h2f(a[c]);
+      const double s = std::sin(al * v);
+      err = std::max(err, scaled(h2f(o[c * T + t]), v + s * s / (al + 1e-9)));
+    }
+  report("snake (f16) C=16 T=3001", err, 2e-3);
+}
+
 }  // namespace
 
 int main() {
@@ -464,6 +486,7 @@ int main() {
     test_adain_snake_f32(dev, k, 128, 11281, "adain_snake_f32 C=128 T=11281");
     test_adain_snake_f16(dev, k, 4, 100, "adain_snake (f16) C=4 T=100");
     test_adain_snake_f16(dev, k, 128, 11281, "adain_snake (f16) C=128 T=11281");
+    test_snake_f16(dev, k, 16, 3001);
     test_layernorm_std_f32in(dev, k);
     test_layernorm_unit_offset_and_bare(dev, k);
     test_elementwise(dev, k);

@@ -140,6 +140,11 @@ def test_version_and_header_is_plain_c():
     lambda L: L.nsr_istft_f32(16, 16, 10, 20, 24, 4, NULL),
     lambda L: L.nsr_istft_f32(16, 16, 0, 0, 20, 5, NULL),
     lambda L: L.nsr_istft_f32(16, NULL, 10, 20, 20, 5, NULL),
+    # snake: bf16 x, seq_len not dividing n_elements, zero channels, misaligned f32 x
+    lambda L: L.nsr_snake(16, 2, 16, 0, 16, 8, 1, 8, NULL),
+    lambda L: L.nsr_snake(16, 0, 16, 0, 16, 10, 1, 4, NULL),
+    lambda L: L.nsr_snake(16, 0, 16, 0, 16, 8, 0, 8, NULL),
+    lambda L: L.nsr_snake(18, 0, 16, 0, 16, 8, 1, 8, NULL),
 ])
 def test_invalid_arguments_are_rejected_before_any_launch(call):
     L = abi.lib()

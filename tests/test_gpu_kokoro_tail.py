@@ -19,7 +19,7 @@ import torch
 from nspeech_amd import abi, configs
 from oracle import restated as R
 
-from ._util import RTOL_F32, assert_bitexact, assert_close, say
+from ._util import RTOL_F16, RTOL_F32, assert_bitexact, assert_close, say
 from .test_oracle import _istft_f64
 
 pytestmark = pytest.mark.gpu
@@ -123,3 +123,40 @@ def test_istft_short_out_len_and_single_frame():
                                       torch.cuda.current_stream().cuda_stream))
     torch.cuda.synchronize()
     assert np.all(guard.cpu().numpy()[777:] == 7.0)
+
+
+@pytest.mark.parametrize("dt", ["f32", "f16"])
+@pytest.mark.parametrize("B,C,T", [(1, 1, 1), (1, 3, 5), (2, 4, 1023), (1, 5, 1025), (1, 2, 4800), (2, 3, 11281)])
+def test_snake(dt, B, C, T):
+    """nsr_snake vs the oracle's snake_activation_tensor restatement and the
+    float64 formula (f32 bar for f32, f16 bar for f16 storage)."""
+    say("snake", dt, B, C, T)
+    g = configs.rng(B * 100 + C * 10 + T)
+    x = (g.standard_normal((B, C, T)) * 3).astype(np.float32)
+    alpha = g.uniform(0.3, 1.6, C).astype(np.float32)
+    if C >= 3:
+        alpha[2] = 0.0  # the formula's limit: out = x
+    if dt == "f16":
+        x = x.astype(np.float16).astype(np.float32)
+    xd = torch.from_numpy(x).cuda().to(torch.float32 if dt == "f32" else torch.float16)
+    out = abi.snake(xd, torch.from_numpy(alpha).cuda()).float().cpu().numpy()
+    orc = R.snake(x, alpha)
+    a64 = alpha.astype(np.float64)[None, :, None]
+    f64 = x + np.sin(a64 * x) ** 2 / (a64 + 1e-9)
+    if dt == "f32":
+        assert_close(out, orc, RTOL_F32, "snake vs oracle")
+        assert_close(out, f64, RTOL_F32, "snake vs f64")
+    else:
+        assert_close(out, orc.astype(np.float16).astype(np.float32), RTOL_F16, "snake f16 vs oracle")
+        assert_close(out, f64, RTOL_F16, "snake f16 vs f64")
+    if C >= 3:
+        assert np.array_equal(out[:, 2], x[:, 2]), "alpha = 0 must leave x unchanged"
+
+
+def test_snake_f16_alpha_and_in_place():
+    g = configs.rng(77)
+    x = (g.standard_normal((4, 999)) * 2).astype(np.float32)
+    alpha = g.uniform(0.5, 1.5, 4).astype(np.float16)
+    xd = torch.from_numpy(x).cuda()
+    abi.snake(xd, torch.from_numpy(alpha).cuda(), out=xd)
+    assert_close(xd.cpu().numpy(), R.snake(x, alpha.astype(np.float32)), RTOL_F32, "snake in place, f16 alpha")

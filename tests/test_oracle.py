@@ -690,3 +690,25 @@ def test_combine_oracle_special_cases():
                                         np.float32(-1e30) * np.float32(0.01)], np.float32))
     # scale alone
     assert np.array_equal(R.combine(a, scale=0.25), a * np.float32(0.25))
+
+
+def test_snake_oracle():
+    """snake(x) = x + sin^2(alpha x) / (alpha + 1e-9) against float64, plus
+    what the formula fixes: alpha = 0 gives x exactly (sin(0) = 0), the
+    periodic part repeats with period pi / alpha, and the added term lies in
+    [0, 1 / (alpha + 1e-9)]; the channel of row r is r % C."""
+    g = configs.rng(95)
+    C, T = 3, 257
+    x = (g.standard_normal((2, C, T)) * 3).astype(np.float32)
+    alpha = np.array([0.7, 1.3, 0.0], np.float32)
+    got = R.snake(x, alpha)
+    a64 = alpha.astype(np.float64)[None, :, None]
+    ref = x + np.sin(a64 * x) ** 2 / (a64 + 1e-9)
+    assert np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1)) < 2e-6
+    assert np.array_equal(got[:, 2], x[:, 2])
+    extra = got[:, :2].astype(np.float64) - x[:, :2]
+    assert np.all(extra >= -1e-6) and np.all(extra <= 1 / alpha[:2, None] + 1e-5)
+    # period pi / alpha of the added term (channel 0), up to f32 rounding of x + period
+    xp = (x[:, 0] + np.float32(np.pi / 0.7)).astype(np.float32)
+    per = R.snake(xp[:, None, :], alpha[:1]).astype(np.float64)[:, 0] - xp
+    assert np.max(np.abs(per - extra[:, 0])) < 1e-4
