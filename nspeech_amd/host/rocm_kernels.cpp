@@ -335,6 +335,33 @@ void enc_rope_qk_cache_fused(Encoder enc, const RocmKernels&, const GpuBuffer& q
             "enc_rope_qk_cache_fused");
 }
 
+void triton_attention_decode(const RocmDevice& device, const RocmKernels& kernels, const Tensor& q, const Tensor& k,
+                             const Tensor& v, const Tensor& out, size_t kv_len, size_t head_dim, size_t n_kv_heads,
+                             size_t n_q_heads, float sm_scale, size_t stride_kv_head, size_t stride_kv_seq) {
+  require_device({&q, &k, &v, &out});
+  for (const Tensor* t : {&q, &k, &v, &out}) require_dtype(*t, DType::F16, "triton_attention_decode");
+  require_elems(q, n_q_heads * head_dim, "triton_attention_decode q");
+  require_elems(out, n_q_heads * head_dim, "triton_attention_decode out");
+  if (kv_len > 0 && n_kv_heads > 0) {
+    const size_t last = (n_kv_heads - 1) * stride_kv_head + (kv_len - 1) * stride_kv_seq + head_dim;
+    require_elems(k, last, "triton_attention_decode k");
+    require_elems(v, last, "triton_attention_decode v");
+  }
+  enc_attention_decode(device.stream(), kernels, q.buffer(), k.buffer(), v.buffer(), out.buffer(), kv_len, head_dim,
+                       n_kv_heads, n_q_heads, sm_scale, stride_kv_head, stride_kv_seq);
+}
+
+void triton_kv_cache_append(const RocmDevice& device, const RocmKernels& kernels, const Tensor& new_kv,
+                            const Tensor& cache, size_t n_kv_heads, size_t head_dim, size_t max_kv_len, size_t pos) {
+  require_device({&new_kv, &cache});
+  require_dtype(new_kv, DType::F16, "triton_kv_cache_append new_kv");
+  require_dtype(cache, DType::F16, "triton_kv_cache_append cache");
+  require_elems(new_kv, n_kv_heads * head_dim, "triton_kv_cache_append new_kv");
+  require_elems(cache, n_kv_heads * max_kv_len * head_dim, "triton_kv_cache_append cache");
+  enc_kv_cache_append(device.stream(), kernels, new_kv.buffer(), cache.buffer(), n_kv_heads, head_dim, max_kv_len,
+                      pos);
+}
+
 void enc_kv_cache_append(Encoder enc, const RocmKernels&, const GpuBuffer& new_kv, const GpuBuffer& cache,
                          size_t n_kv_heads, size_t head_dim, size_t max_kv_len, size_t pos) {
   nsr_check(nsr_kv_cache_append(new_kv.at(), cache.at(), NSR_F16, (int64_t)n_kv_heads, (int64_t)head_dim,

@@ -140,6 +140,14 @@ void triton_glu_silu(const RocmDevice& device, const RocmKernels& kernels, const
 void triton_residual_add_layernorm(const RocmDevice& device, const RocmKernels& kernels, const Tensor& f16_proj,
                                    const Tensor& f32_residual, const Tensor& f32_out, const Tensor& weight,
                                    const Tensor& f16_norm, size_t n_rows, size_t dim);
+// Decode attention over f16 tensors (:648-678): q [n_q_heads, head_dim], K/V
+// with the given element strides, out [n_q_heads, head_dim].
+void triton_attention_decode(const RocmDevice& device, const RocmKernels& kernels, const Tensor& q, const Tensor& k,
+                             const Tensor& v, const Tensor& out, size_t kv_len, size_t head_dim, size_t n_kv_heads,
+                             size_t n_q_heads, float sm_scale, size_t stride_kv_head, size_t stride_kv_seq);
+// new_kv [n_kv_heads, head_dim] f16 into row `pos` of cache [n_kv_heads, max_kv_len, head_dim] (:680-711).
+void triton_kv_cache_append(const RocmDevice& device, const RocmKernels& kernels, const Tensor& new_kv,
+                            const Tensor& cache, size_t n_kv_heads, size_t head_dim, size_t max_kv_len, size_t pos);
 
 // ---- Buffer-level API (src/triton_kernels.rs:862-1423) ----------------------
 

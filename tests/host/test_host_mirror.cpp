@@ -358,9 +358,14 @@ void test_decode_step(const RocmDevice& dev, const RocmKernels& k) {
     Tensor OX = Tensor::empty(dev, {Hq, Dh}, DType::F16);
     enc_rope_qk_cache_fused(dev.stream(), k, Q.buffer(), K.buffer(), re.table().buffer(), CK.buffer(), pos, L, Hq,
                             Hk, Dh, rot);
-    enc_kv_cache_append(dev.stream(), k, V.buffer(), CV.buffer(), Hk, Dh, L, pos);
-    enc_attention_decode(dev.stream(), k, Q.buffer(), CK.buffer(), CV.buffer(), O.buffer(), pos + 1, Dh, Hk, Hq,
-                         scale, L * Dh, Dh);
+    if (pos % 2 == 0) {  // buffer-level and tensor-level forms on alternate steps
+      enc_kv_cache_append(dev.stream(), k, V.buffer(), CV.buffer(), Hk, Dh, L, pos);
+      enc_attention_decode(dev.stream(), k, Q.buffer(), CK.buffer(), CV.buffer(), O.buffer(), pos + 1, Dh, Hk, Hq,
+                           scale, L * Dh, Dh);
+    } else {
+      triton_kv_cache_append(dev, k, V, CV, Hk, Dh, L, pos);
+      triton_attention_decode(dev, k, Q, CK, CV, O, pos + 1, Dh, Hk, Hq, scale, L * Dh, Dh);
+    }
     const size_t splits = std::min<size_t>(32, Lx);
     enc_attention_splitkv(dev.stream(), k, Q.buffer(), XK.buffer(), XV.buffer(), OX.buffer(), partial.buffer(), Lx,
                           Dh, Hk, Hq, scale, Dh, Hk * Dh, splits);
@@ -408,6 +413,10 @@ void test_errors(const RocmDevice& dev, const RocmKernels& k) {
   Tensor Xf = Tensor::empty(dev, {2, 4}, DType::F32);
   expect_throw("short tensor is rejected", [&] { triton_layernorm_std_f32in(dev, k, Xf, D, D, 4, 4); },
                "need 16");
+  Tensor Q = Tensor::empty(dev, {2, 64}, DType::F16);
+  Tensor Kc = Tensor::empty(dev, {2, 10, 64}, DType::F16);
+  expect_throw("attention over more positions than the cache holds is rejected",
+               [&] { triton_attention_decode(dev, k, Q, Kc, Kc, Q, 11, 64, 2, 2, 0.125f, 640, 64); }, "need");
   RocmKokoroBackend be(dev, k);
   expect_throw("adain_snake f16 row past the limit is rejected",
                [&] { be.adain_snake(X.buffer(), X.buffer(), X.buffer(), X.buffer(), X.buffer(), 1, 200000); },
