@@ -17,11 +17,11 @@
  *
  * Design (gfx950): the reference evaluates, for every output sample, the
  * spectrum of each frame that overlaps it (n_fft / hop frames x bins exp /
- * sin / cos each). Here one lane computes one frame: its bins' magnitude and
- * phase once, then the n_fft windowed samples, into LDS; then each output
- * sample sums its frames (in frame order) and divides by the window sum. A
- * workgroup owns a run of frames and the samples that only those frames
- * reach; neighbouring workgroups recompute n_fft / hop - 1 boundary frames.
+ * sin / cos each). Here each frame's spectrum is computed once, then its
+ * n_fft windowed samples, into LDS; then each output sample sums its frames
+ * (in frame order) and divides by the window sum. A workgroup owns a run of
+ * 64 frames and the samples that only those frames reach; neighbouring
+ * workgroups recompute n_fft / hop - 1 boundary frames.
  * The frame phase bounds the kernel (VALU, not HBM), so it is cut down:
  *  - cos / sin of the phase, whose argument sin(raw) lies in [-1, 1], are
  *    Taylor polynomials to degree 14 / 13 (truncation below 1.2e-11, i.e.
@@ -58,79 +58,135 @@ NSR_DEV void sincos_unit(float x, float& s, float& c) {
   c = fmaf(-x2, pc, 1.0f);                         /* 1 - x^2 (1/2! - ...) */
 }
 
-/* N = n_fft at compile time (the bins' spectra stay in registers) */
+/* sin(x): Cody-Waite reduction x = j pi/2 + r (pi/2 split in three f32
+ * parts, j = rint(2x/pi), exact products by FMA), then Taylor polynomials of
+ * sin and cos on |r| <= pi/4 (to r^9 and r^10; first dropped terms below
+ * 2e-9 and 1.2e-10) and the quadrant j mod 4. Accurate to a few f32 ulps for
+ * |x| <= 65536; larger arguments take the library sinf. */
+NSR_DEV float sin_cw(float x) {
+  const float j = __builtin_rintf(x * 0.636619772367581343f);
+  float r = fmaf(j, -1.57079637050628662109375f, x);
+  r = fmaf(j, 4.37113882867379289e-08f, r);
+  r = fmaf(j, 1.71512451e-15f, r);
+  const float r2 = r * r;
+  float ps = 1.0f / 362880.0f;
+  ps = fmaf(ps, r2, -1.0f / 5040.0f);
+  ps = fmaf(ps, r2, 1.0f / 120.0f);
+  ps = fmaf(ps, r2, -1.0f / 6.0f);
+  const float sn = fmaf(r * r2, ps, r);
+  float pc = -1.0f / 3628800.0f;
+  pc = fmaf(pc, r2, 1.0f / 40320.0f);
+  pc = fmaf(pc, r2, -1.0f / 720.0f);
+  pc = fmaf(pc, r2, 1.0f / 24.0f);
+  pc = fmaf(pc, r2, -0.5f);
+  const float cs = fmaf(r2, pc, 1.0f);
+  const int q = (int)j & 3;
+  float v = (q & 1) ? cs : sn;
+  v = (q & 2) ? -v : v;
+  return __builtin_fabsf(x) <= 65536.0f ? v : sinf(x);
+}
+
+/* N = n_fft at compile time. A workgroup of 256 lanes owns NSR_ISTFT_FG
+ * frames and works in three phases, each spread over all lanes so that
+ * every lane carries a few items (and many waves hide each other's latency):
+ *  A. spectrum: item (bin k, frame) -> re, im into LDS [k][frame];
+ *  B. iDFT: item (sample pair n / N - n, frame) -> windowed samples into LDS
+ *     [frame][n] (row stride N + 1: conflict-free column writes);
+ *  C. overlap-add: item (output sample) -> sum of its frames / window sum. */
+#define NSR_ISTFT_FG 64
 template <int N>
 NSR_DEV void istft_body(const nsr_istft_args& a) {
-  constexpr int bins = N / 2 + 1, H = N / 2;
-  __shared__ float cosb[(H + 1) * bins]; /* [n = 0 .. N / 2][k] */
-  __shared__ float sinb[(H + 1) * bins];
+  constexpr int bins = N / 2 + 1, H = N / 2, FG = NSR_ISTFT_FG, NS = N + 1;
+  constexpr int IA = (bins * FG + 255) / 256;    /* phase A items per lane */
+  constexpr int IB = ((H + 1) * FG + 255) / 256; /* phase B items per lane */
+  __shared__ float cosm[N], sinm[N]; /* cos / sin(2 pi m / N), m = 0 .. N - 1 */
   __shared__ float win[N];
-  extern __shared__ float frames[]; /* [frames_per_group][n_fft] windowed frame samples */
+  __shared__ float sre[bins * FG], sim[bins * FG]; /* [k][frame] */
+  __shared__ float frames[FG * NS];                /* [frame][n], windowed */
   const int tid = threadIdx.x;
   const int hop = a.hop, R = N / hop, trim = N / 2;
   const float PI = 3.14159265358979323846f;
-  for (int i = tid; i < (H + 1) * bins; i += 256) {
-    const int n = i / bins, k = i - n * bins;
-    const float ang = 2.0f * PI * (float)((k * n) % N) / (float)N;
-    cosb[i] = cosf(ang);
-    sinb[i] = sinf(ang);
-  }
-  /* periodic Hann, the reference's f32 formula (decoder.rs:1558-1560) */
-  for (int n = tid; n < N; n += 256) win[n] = 0.5f - 0.5f * cosf(2.0f * PI * (float)n / (float)N);
-  __syncthreads();
 
-  /* frames [F0, F0 + FG) computed here; the samples owned are the untrimmed
-   * positions all of whose frames lie in that range (the first and last
-   * groups also own the positions the edges of the signal leave) */
-  const int FG = a.frames_per_group, step = FG - (R - 1);
+  const int step = FG - (R - 1);
   const int64_t F0 = (int64_t)blockIdx.x * step;
   const int nloc = (int)min((int64_t)FG, a.n_frames - F0); /* frames of this group */
-  if (tid < nloc) {
-    const int64_t f = F0 + tid;
-    /* all 2 bins loads first, so that one memory latency covers them */
-    float lm[bins], rp[bins];
+
+  /* phase A loads first (one memory latency for all), then the tables */
+  /* 32-bit element offsets (the host keeps 2 bins n_frames below 2^31) */
+  const int nfr = (int)a.n_frames, f0 = (int)F0;
+  float lm[IA], rp[IA];
 #pragma unroll
-    for (int k = 0; k < bins; ++k) {
-      lm[k] = a.x[(int64_t)k * a.n_frames + f];
-      rp[k] = a.x[(int64_t)(bins + k) * a.n_frames + f];
-    }
-    float re[bins], im[bins];
+  for (int it = 0; it < IA; ++it) {
+    const int i = tid + 256 * it;
+    const int k = i / FG, fl = i % FG;
+    const bool ok = i < bins * FG && fl < nloc;
+    const int off = (ok ? k : 0) * nfr + f0 + (ok ? fl : 0);
+    lm[it] = a.x[off];
+    rp[it] = a.x[off + bins * nfr];
+  }
+  /* the iDFT basis cos / sin(2 pi k n / N) takes N values, at m = k n mod N;
+   * the periodic Hann window is the reference's f32 formula (decoder.rs:
+   * 1558-1560), 0.5 - 0.5 cos(2 pi n / N), from the same cosines */
+  if (tid < N) {
+    const float ang = 2.0f * PI * (float)tid / (float)N;
+    const float c = cosf(ang);
+    cosm[tid] = c;
+    sinm[tid] = sinf(ang);
+    win[tid] = 0.5f - 0.5f * c;
+  }
 #pragma unroll
-    for (int k = 0; k < bins; ++k) {
-      const float m = (k == 0 || k == bins - 1) ? expf(lm[k]) : 2.0f * expf(lm[k]);
+  for (int it = 0; it < IA; ++it) {
+    const int i = tid + 256 * it;
+    if (i < bins * FG) {
+      const int k = i / FG;
+      const float e = expf(lm[it]);
+      const float m = (k == 0 || k == bins - 1) ? e : 2.0f * e; /* one-sided: inner bins twice */
       float sn, cs;
-      sincos_unit(sinf(rp[k]), sn, cs);
-      re[k] = m * cs;
-      im[k] = m * sn;
+      sincos_unit(sin_cw(rp[it]), sn, cs);
+      sre[i] = m * cs;
+      sim[i] = m * sn;
     }
+  }
+  __syncthreads();
+
 #pragma unroll
-    for (int n = 0; n <= H; ++n) {
+  for (int it = 0; it < IB; ++it) {
+    const int i = tid + 256 * it;
+    const int n = __builtin_amdgcn_readfirstlane(i / FG), fl = i % FG; /* n: uniform over a wave (FG = 64) */
+    if (i < (H + 1) * FG && fl < nloc) {
       float c = 0.f, sm = 0.f;
 #pragma unroll
       for (int k = 0; k < bins; ++k) {
-        c = fmaf(re[k], cosb[n * bins + k], c);
-        sm = fmaf(im[k], sinb[n * bins + k], sm);
+        const int m = (k * n) % N; /* wave-uniform */
+        c = fmaf(sre[k * FG + fl], cosm[m], c);
+        sm = fmaf(sim[k * FG + fl], sinm[m], sm);
       }
-      frames[tid * N + n] = ((c - sm) / (float)N) * win[n];
-      if (n > 0 && n < H) frames[tid * N + (N - n)] = ((c + sm) / (float)N) * win[N - n];
+      frames[fl * NS + n] = ((c - sm) / (float)N) * win[n];
+      if (n > 0 && n < H) frames[fl * NS + (N - n)] = ((c + sm) / (float)N) * win[N - n];
     }
   }
   __syncthreads();
 
   /* owned untrimmed positions base + [q_lo, q_hi), base = F0 * hop (the first
-   * sample of frame F0); frame F0 + g covers q in [g hop, g hop + N) */
+   * sample of frame F0); frame F0 + g covers q in [g hop, g hop + N); the
+   * first and last groups also own the positions the signal's edges leave */
   const int64_t base = F0 * hop;
+  const float inv_hop = 1.0f / (float)hop;
   const int q_lo = blockIdx.x == 0 ? 0 : (R - 1) * hop;
   const int q_hi = F0 + FG >= a.n_frames ? (nloc - 1) * hop + N : FG * hop;
   for (int q = q_lo + tid; q < q_hi; q += 256) {
     const int64_t i = base + q - trim; /* output index */
     if (i < 0 || i >= a.out_len) continue;
-    const int g_first = q - N + 1 <= 0 ? 0 : (q - N + hop) / hop; /* ceil((q - N + 1) / hop) */
-    const int g_last = min(q / hop, nloc - 1);
+    /* q / hop by a float reciprocal, exact after one correction (q < 2^16) */
+    int qd = (int)((float)q * inv_hop);
+    qd += (qd + 1) * hop <= q ? 1 : 0;
+    qd -= qd * hop > q ? 1 : 0;
+    const int g_last = min(qd, nloc - 1);
+    const int g_first = max(0, qd - (R - 1)); /* frames qd - R + 1 .. qd cover q */
     float acc = 0.f, ws = 0.f;
     for (int g = g_first; g <= g_last; ++g) {
       const int n = q - g * hop;
-      acc += frames[g * N + n];
+      acc += frames[g * NS + n];
       ws += win[n] * win[n];
     }
     a.out[i] = ws > 1e-8f ? acc / ws : 0.f;

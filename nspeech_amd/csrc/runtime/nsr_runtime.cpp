@@ -909,8 +909,10 @@ nsr_status nsr_snake(const void* x, nsr_dtype dtype, const void* alpha, nsr_dtyp
 nsr_status nsr_istft_f32(const float* x, float* out, int64_t n_frames, int64_t out_len, int n_fft, int hop,
                          nsr_stream_t stream) {
   if (!x || !out) return fail(NSR_ERR_BAD_ARG, "istft: null pointer");
-  if (n_frames < 1 || n_frames > (1LL << 31) - 1 || hop < 1 || n_fft < 2 || n_fft % hop != 0)
+  if (n_frames < 1 || hop < 1 || n_fft < 2 || n_fft % hop != 0)
     return fail(NSR_ERR_BAD_ARG, "istft: need n_frames >= 1 and hop dividing n_fft");
+  if (n_frames * (n_fft + 2) >= (1LL << 31))  // x holds 2 (n_fft / 2 + 1) rows of n_frames
+    return fail(NSR_ERR_UNSUPPORTED, "istft: input larger than 2^31 elements");
   if (n_fft != 16 && n_fft != 20 && n_fft != 32)
     return fail(NSR_ERR_UNSUPPORTED, "istft: n_fft %d not built (16, 20, 32)", n_fft);
   if (out_len < 0 || out_len > (n_frames - 1) * (int64_t)hop)
@@ -925,12 +927,13 @@ nsr_status nsr_istft_f32(const float* x, float* out, int64_t n_frames, int64_t o
   a.out_len = out_len;
   a.n_fft = n_fft;
   a.hop = hop;
-  a.frames_per_group = 256;
-  const int64_t R = n_fft / hop, step = 256 - (R - 1);
-  const int64_t groups = n_frames <= 256 ? 1 : 1 + (n_frames - 256 + step - 1) / step;
+  // 64 frames per workgroup (the kernel's NSR_ISTFT_FG); neighbours overlap by n_fft / hop - 1 frames
+  const int64_t FG = 64, R = n_fft / hop, step = FG - (R - 1);
+  a.frames_per_group = (int32_t)FG;
+  const int64_t groups = n_frames <= FG ? 1 : 1 + (n_frames - FG + step - 1) / step;
+  if (groups > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "istft: too many frames");
   void* params[] = {&a};
-  return launch("nsrk_istft_f32_n" + std::to_string(n_fft), (unsigned)groups, 1, 256,
-                (unsigned)(256 * n_fft * sizeof(float)), stream, params);
+  return launch("nsrk_istft_f32_n" + std::to_string(n_fft), (unsigned)groups, 1, 256, 0, stream, params);
 }
 
 nsr_status nsr_activation(const void* x, void* y, nsr_dtype dtype, int64_t n, nsr_act act,
