@@ -13,7 +13,7 @@
  *     generator's resblock average and conv_post input, as the reference GPU
  *     path computes it in four dispatches: add_f32 (r0 + r1), add_f32 (+ r2),
  *     scale_third_f32 (x * f32(1/3), kernels/kokoro_kernels.py:941-969) and
- *     leaky_relu_f32 (x >= 0 ? x : x * slope) (src/kokoro/decoder.rs:540-577,
+ *     leaky_relu_f32 (x > 0 ? x : x * slope) (src/kokoro/decoder.rs:540-577,
  *     src/kokoro/gpu_backend.rs:186-200); one pass here, same rounding
  *     sequence.
  *
