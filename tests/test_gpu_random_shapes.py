@@ -117,3 +117,90 @@ def test_kokoro_tail_random(i):
     x = (g.standard_normal((22, n_frames)) * 0.7).astype(np.float32)
     got = abi.istft_f32(torch.from_numpy(x).cuda()).cpu().numpy()
     assert_close(got, R.istft(x, 20, 5), RTOL_F32, f"istft {n_frames}")
+
+
+def _conv_f64(x, w, b, pad, dil):
+    """Exact (float64) conv1d of the f32 input and f16 weights, plus bias."""
+    B, C_in, T = x.shape
+    C_out, _, K = w.shape
+    T_out = T + 2 * pad - dil * (K - 1)
+    xp = np.zeros((B, C_in, T + 2 * pad))
+    xp[:, :, pad:pad + T] = x
+    out = np.zeros((B, C_out, T_out)) + (0 if b is None else b.astype(np.float64)[None, :, None])
+    w64 = w.astype(np.float64)
+    for k in range(K):
+        seg = xp[:, :, k * dil:k * dil + T_out]
+        out += np.matmul(w64[:, :, k][None], seg)
+    return out
+
+
+def _conv_shape(g, square=False):
+    while True:
+        B = int(g.integers(1, 3))
+        C_in = 16 * int(g.integers(1, 17))
+        C_out = C_in if square else int(g.integers(1, 261))
+        K = int(g.choice([1, 2, 3, 5, 7, 11]))
+        dil = int(g.choice([d for d in (1, 2, 3, 5) if (K - 1) * d <= 64]))
+        T = int(g.integers(1, 2500))
+        pad = int(g.integers(0, (K - 1) * dil + 1))
+        T_out = T + 2 * pad - dil * (K - 1)
+        if T_out >= 1 and B * C_in * C_out * K * T_out <= 300_000_000:
+            return B, C_in, C_out, K, dil, T, pad, T_out
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_conv1d_random(i):
+    g = _cases(6)[i]
+    B, C_in, C_out, K, dil, T, pad, T_out = _conv_shape(g)
+    res = bool(g.integers(0, 2))
+    say("conv1d random", B, C_in, C_out, K, dil, T, pad, res)
+    x = g.standard_normal((B, C_in, T)).astype(np.float32)
+    w = (g.standard_normal((C_out, C_in, K)) * 0.1).astype(np.float16)
+    b = g.standard_normal(C_out).astype(np.float16)
+    r = g.standard_normal((B, C_out, T_out)).astype(np.float32) if res else None
+    wp = abi.conv1d_pack_f16(torch.from_numpy(w).cuda())
+    out = abi.conv1d_f16w_packed(torch.from_numpy(x).cuda(), wp, torch.from_numpy(b).cuda(),
+                                 torch.from_numpy(r).cuda() if res else None, padding=pad, dilation=dil)
+    ref = R.conv1d_f32io(x, w.view(np.uint16), b.view(np.uint16), 1, pad, dil, nthreads=16)
+    ex = _conv_f64(x, w, b, pad, dil)
+    if res:
+        ref = ref + r
+        ex = ex + r
+    # long random dot products (C_in K up to 2816 terms): the reference's sequential f32 sums drift from the
+    # exact result by up to ~1.5e-5 here; the GPU must be as close to exact as 1e-5 or twice that drift
+    drift = rel_err(ref, ex)
+    got = out.cpu().numpy()
+    e = assert_close(got, ex, max(RTOL_F32, 2 * drift), f"conv1d random vs f64 (oracle drift {drift:.1e})")
+    assert_close(got, ref, RTOL_F32 + 2 * drift, "conv1d random vs oracle")
+    print(f"[conv random] gpu vs f64 {e:.2e}, oracle vs f64 {drift:.2e}")
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_adain_snake_conv1d_random(i):
+    """The fused stage, with the AdaIN+Snake bar carried through the conv
+    (sum_k |w| 1e-5 max(|y|, 1)) on top of the conv's own bar."""
+    g = _cases(7)[i]
+    B, C, _, K, dil, T, pad, T_out = _conv_shape(g, square=True)
+    with_res = bool(g.integers(0, 2))
+    say("adain_snake_conv1d random", B, C, K, dil, T, pad, with_res)
+    x = (g.standard_normal((B, C, T)) * 1.5 + 0.3).astype(np.float32)
+    gam = (g.standard_normal((B, C)) * 0.1).astype(np.float32)
+    bet = (g.standard_normal((B, C)) * 0.1).astype(np.float32)
+    alp = g.uniform(0.5, 1.5, C).astype(np.float32)
+    w = (g.standard_normal((C, C, K)) * 0.05).astype(np.float16)
+    b = g.standard_normal(C).astype(np.float16)
+    res = g.standard_normal((B, C, T_out)).astype(np.float32)
+    wp = abi.conv1d_pack_f16(torch.from_numpy(w).cuda())
+    dt = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    out = abi.adain_snake_conv1d(dt(x), dt(gam), dt(bet), dt(alp), wp, dt(b), dt(res) if with_res else None,
+                                 padding=pad, dilation=dil)
+    y = R.adain_snake(x, gam, bet, alp)
+    ref = R.conv1d_f32io(y, w.view(np.uint16), b.view(np.uint16), 1, pad, dil, nthreads=16)
+    if with_res:
+        ref = ref + res
+    wabs = np.abs(w.astype(np.float32)).astype(np.float16)
+    carried = R.conv1d_f32io(np.maximum(np.abs(y), 1.0).astype(np.float32), wabs.view(np.uint16), None, 1, pad, dil,
+                             nthreads=16).astype(np.float64) * RTOL_F32 * 1.01
+    err = np.abs(out.cpu().numpy().astype(np.float64) - ref)
+    bound = carried + RTOL_F32 * np.maximum(np.abs(ref), 1.0)
+    assert np.all(err <= bound), f"max excess {float(np.max(err - bound)):.3e}"
