@@ -204,3 +204,49 @@ def test_adain_snake_conv1d_random(i):
     err = np.abs(out.cpu().numpy().astype(np.float64) - ref)
     bound = carried + RTOL_F32 * np.maximum(np.abs(ref), 1.0)
     assert np.all(err <= bound), f"max excess {float(np.max(err - bound)):.3e}"
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_gemv_q8_random(i):
+    """Repacked-Q8 GEMV (+ bias), both weight layouts, at random K (a multiple
+    of 32) and N (a multiple of 16), within the f32 accumulation bound."""
+    from .test_gpu_gemv import _TD, _bound, _check, _dev_w, _run, _weight, _x
+
+    g = _cases(8)[i]
+    K = 32 * int(g.integers(1, 130))
+    N = 16 * int(g.integers(1, 300))
+    xd, od = str(g.choice(["f16", "f32"])), str(g.choice(["f16", "f32"]))
+    layout = str(g.choice(["ref", "t4"]))
+    with_bias = bool(g.integers(0, 2))
+    say("gemv_q8 random", layout, K, N, xd, od, with_bias)
+    qs, sc, W = _weight(g, K, N)
+    x, xt = _x(g, K, xd)
+    bias = g.standard_normal(N).astype(np.float32) if with_bias else None
+    q_t, s_t = _dev_w(qs, sc)
+    out = _run(layout, "gemv_q8", xt, q_t, s_t, torch.from_numpy(bias).cuda() if with_bias else None,
+               out_dtype=_TD[od])
+    ref = R.gemv_q8(x, qs, sc.view(np.uint16), bias).astype(np.float64)
+    _check(out, ref, _bound(x, W), od, f"gemv_q8 random K={K} N={N}")
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_attention_decode_random(i):
+    """Decode attention at random head counts (grouped-query included), head
+    dims, positions and both K/V layouts, one-launch and split forms."""
+    from .test_gpu_attention import _check as attn_check
+    from .test_gpu_attention import _inputs as attn_inputs
+
+    g = _cases(9)[i]
+    nkv = int(g.integers(1, 9))
+    nq = nkv * int(g.choice([1, 2, 4]))
+    hd = int(g.choice([16, 32, 36, 52, 64, 80, 128]))
+    kv_len = int(g.integers(1, 3000))
+    layout = str(g.choice(["cache", "enc"]))
+    splits = None if g.integers(0, 2) else int(g.integers(1, 64))
+    say("attention random", nq, nkv, hd, kv_len, layout, splits)
+    q, k, v, skh, sks = attn_inputs(nq, nkv, hd, kv_len, layout, int(g.integers(0, 1 << 30)))
+    scale = float(1.0 / np.sqrt(hd))
+    T = lambda a: torch.from_numpy(a).cuda()  # noqa: E731
+    out = abi.attention_decode(T(q), T(k), T(v), kv_len, n_kv_heads=nkv, sm_scale=scale, stride_kv_head=skh,
+                               stride_kv_seq=sks, n_splits=splits)
+    attn_check(out, q, k, v, kv_len, nkv, scale, skh, sks, f"attention random {nq}/{nkv} hd={hd} L={kv_len}")
