@@ -250,3 +250,81 @@ def test_attention_decode_random(i):
     out = abi.attention_decode(T(q), T(k), T(v), kv_len, n_kv_heads=nkv, sm_scale=scale, stride_kv_head=skh,
                                stride_kv_seq=sks, n_splits=splits)
     attn_check(out, q, k, v, kv_len, nkv, scale, skh, sks, f"attention random {nq}/{nkv} hd={hd} L={kv_len}")
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_residual_add_layernorm_random(i):
+    """Residual add + LayerNorm (+ GELU / SiLU) in the dtype profiles the
+    reference uses (bf16 everywhere; f16 projection + f32 residual -> f32 h
+    and f16 norm; f32), at random widths and row counts: h bit-exact, the
+    norm at the bar of its dtype against the float64 form on that h."""
+    from oracle import closed_form as CF_
+
+    from ._util import RTOL_BF16
+
+    g = _cases(10)[i]
+    rows = int(g.integers(1, 2000))
+    cols = int(g.choice([int(g.integers(1, 128)), int(g.integers(128, 4097)), 640, 1024]))
+    prof = str(g.choice(["bf16", "f16f32", "f32"]))
+    act = str(g.choice(["none", "gelu", "silu"]))
+    say("resadd+ln random", rows, cols, prof, act)
+    x = g.standard_normal((rows, cols)).astype(np.float32)
+    r = g.standard_normal((rows, cols)).astype(np.float32)
+    w = (1 + 0.1 * g.standard_normal(cols)).astype(np.float32)
+    b = (0.1 * g.standard_normal(cols)).astype(np.float32)
+    if prof == "bf16":
+        xt, rt = torch.from_numpy(x).bfloat16().cuda(), torch.from_numpy(r).bfloat16().cuda()
+        h, y = abi.residual_add_layernorm(xt, rt, torch.from_numpy(w).cuda(), torch.from_numpy(b).cuda(), act=act)
+        h_ref = (xt.float() + rt.float()).bfloat16()
+        tol = RTOL_BF16
+    elif prof == "f16f32":
+        xt, rt = torch.from_numpy(x).half().cuda(), torch.from_numpy(r).cuda()
+        h, y = abi.residual_add_layernorm(xt, rt, torch.from_numpy(w).cuda(), torch.from_numpy(b).cuda(), act=act,
+                                          h_dtype=torch.float32, out_dtype=torch.float16)
+        h_ref = xt.float() + rt
+        tol = RTOL_F16
+    else:
+        xt, rt = torch.from_numpy(x).cuda(), torch.from_numpy(r).cuda()
+        h, y = abi.residual_add_layernorm(xt, rt, torch.from_numpy(w).cuda(), torch.from_numpy(b).cuda(), act=act)
+        h_ref = xt + rt
+        tol = RTOL_F32
+    assert torch.equal(h.cpu(), h_ref.cpu()), "h"
+    ref = CF_.layernorm(h_ref.float().cpu().numpy().astype(np.float64), w, b)
+    if act == "gelu":
+        ref = CF_.gelu_erf(ref)
+    elif act == "silu":
+        ref = ref / (1 + np.exp(-ref))
+    assert_close(y.float().cpu().numpy(), ref, tol, f"norm {prof} {act}")
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_rope_qk_cache_random(i):
+    """Decode-step RoPE + K/V cache append (f16), random heads, head dims,
+    rotary dims, cache lengths and positions: bit-exact with the oracle."""
+    from .test_gpu_decode import _bits, _f16
+
+    g = _cases(11)[i]
+    Hk = int(g.integers(1, 9))
+    Hq = Hk * int(g.choice([1, 2, 4]))
+    Dh = 2 * int(g.integers(1, 65))
+    rot = 2 * int(g.integers(0, Dh // 2 + 1))
+    L = int(g.integers(1, 600))
+    pos = int(g.integers(0, L))
+    with_v = bool(g.integers(0, 2))
+    say("rope_qk_cache random", Hq, Hk, Dh, rot, L, pos, with_v)
+    q = g.standard_normal((Hq, Dh)).astype(np.float16).view(np.uint16)
+    k = g.standard_normal((Hk, Dh)).astype(np.float16).view(np.uint16)
+    v = g.standard_normal((Hk, Dh)).astype(np.float16).view(np.uint16) if with_v else None
+    ck0 = g.standard_normal((Hk, L, Dh)).astype(np.float16).view(np.uint16)
+    cv0 = g.standard_normal((Hk, L, Dh)).astype(np.float16).view(np.uint16) if with_v else None
+    tab = R.rope_table(L, rot, 1e4) if rot else np.zeros((1, 2), np.float32)
+    qd, kd, ckd = _f16(q), _f16(k), _f16(ck0)
+    vd = _f16(v) if with_v else None
+    cvd = _f16(cv0) if with_v else None
+    abi.rope_qk_cache_append(qd, kd, vd, torch.from_numpy(tab).cuda(), ckd, cvd, pos, rot)
+    qr, kr, ckr, cvr = R.rope_qk_cache_f16(q, k, v, tab, pos, rot, ck0, cv0)
+    assert_bitexact(_bits(qd), qr, "q")
+    assert_bitexact(_bits(kd), kr, "k")
+    assert_bitexact(_bits(ckd), ckr, "cache_k")
+    if with_v:
+        assert_bitexact(_bits(cvd), cvr, "cache_v")
