@@ -48,9 +48,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workloads",
                     default="c0,c1,c1t,c2,c3,c4a,c4b,c2u,c2h,dec,dec2,attn,attnx,q8fc1,q8fc2,q8fc1r,q8fc2r,q8conv,kconv3,"
-                            "kconv11,kconv3u,mrf,istft",
+                            "kconv11,kconv3u,kchain3,kchain11,mrf,istft",
                     help="comma list of c0,c1,c1t,c2,c3,c4a,c4b,c2u,c2h,dec,dec2,attn,attnx,q8fc1,q8fc2,q8fc1r,q8fc2r,"
-                         "q8conv,kconv3,kconv11,kconv3u,mrf,istft,copy")
+                         "q8conv,kconv3,kconv11,kconv3u,kchain3,kchain11,mrf,istft,copy")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline (0 = skip)")
     ap.add_argument("--no-rotate", action="store_true", help="one buffer set (warm MALL) for all timings")
     return ap.parse_args()
@@ -415,6 +415,44 @@ def build_workload(name):
                         {"kconv3": "nsrk_conv1d_rw_adain_snake_f16x2_nu3", "kconv11": "nsrk_conv1d_pc_adain_snake_f16x2_nu4",
                          "kconv3u": "nsrk_conv1d_rw_f16x2_nu3"}[name], "f32",
                         flops=flops)
+
+    if name in ("kchain3", "kchain11"):
+        # The same ResBlock stage as kconv3 / kconv11 in the steady state of a chain: the input's row statistics
+        # come from the previous stage (computed once, outside the timed calls) and the stage emits its output's
+        # statistics for the next one (nsr_adain_snake_conv1d_chain_f32) instead of a separate statistics pass.
+        c = configs.c4b()
+        x0 = T(c["x"])
+        B, C, TT = c["x"].shape
+        g_, b_, a_ = T(c["gamma"]), T(c["beta"]), T(c["alpha"])
+        K, dil = (11, 5) if name == "kchain11" else (3, 1)
+        pad = (K - 1) * dil // 2
+        g = configs.rng(1009)
+        wp = abi.conv1d_pack_f16(torch.from_numpy((g.standard_normal((C, C, K)) * 0.05).astype(np.float16)).to(dev))
+        bias = torch.from_numpy(g.standard_normal(C).astype(np.float16)).to(dev)
+        gs = C if c["gamma"].ndim == 2 else 0
+        xs = torch.empty((B * C, 2), dtype=torch.float32, device=dev)
+        tmp = torch.empty_like(x0)
+        abi.check(L.nsr_conv1d_f16w_packed_stats(x0.data_ptr(), wp.data_ptr(), None, None, tmp.data_ptr(),
+                                                 xs.data_ptr(), B, C, C, TT, K, pad, dil, 1e-5, stream()))
+        # (statistics of some f32 [B, C, T] tensor; the timed calls use them for x, which only changes the values)
+        del tmp
+
+        def make_set(_):
+            return {"x": x0, "o": torch.empty_like(x0), "s": torch.empty((B * C, 2), dtype=torch.float32,
+                                                                          device=dev)}
+
+        def launch(s):
+            abi.check(L.nsr_adain_snake_conv1d_chain_f32(s["x"].data_ptr(), xs.data_ptr(), g_.data_ptr(),
+                                                         b_.data_ptr(), a_.data_ptr(), 0, gs, gs, wp.data_ptr(),
+                                                         bias.data_ptr(), None, s["o"].data_ptr(), s["s"].data_ptr(),
+                                                         B, C, C, TT, K, pad, dil, 1e-5, stream()))
+
+        alg = 2 * x0.numel() * 4
+        flops = 2 * C * C * K * TT * B
+        return Workload(name, f"ResBlock stage in a chain (statistics handed along) K={K} dil={dil} f32 x[{B},{C},{TT}]",
+                        alg, x0.numel() * 4, make_set, launch,
+                        "nsrk_conv1d_rw_adain_snake_f16x2_nu3_st" if K == 3 else "nsrk_conv1d_pc_adain_snake_f16x2_nu4_st",
+                        "f32", flops=flops)
 
     if name == "c4a":
         c = configs.c4a()

@@ -398,6 +398,34 @@ nsr_status nsr_adain_snake_conv1d_f32(const float* x, const void* gamma, const v
                                       int64_t C_out, int64_t T, int64_t K, int64_t padding,
                                       int64_t dilation, float eps, nsr_stream_t stream);
 
+/* The same ResBlock stage with the row statistics handed along the chain
+ * instead of re-read. x_stats ([B*C_in][2]: mean, 1 / sqrt(var + eps) of
+ * each x row) replaces the statistics pass over x when not NULL (the
+ * previous stage's out_stats); out_stats, when not NULL, receives the same
+ * pair for each row of out (after bias and residual), for the next stage's
+ * AdaIN. With 16-byte aligned rows the conv's epilogue produces them from
+ * registers (per 32-column block count, mean and M2, merged per row by
+ * Chan's pairwise formula) instead of a second read of out. No counterpart
+ * in the reference, whose ResBlock (src/kokoro/decoder.rs:1352-1380, GPU
+ * path :1087-1160) runs adain_snake_f32 and conv1d_f32 one after the other;
+ * the results match nsr_adain_snake_conv1d_f32 within the fp32 bar. */
+nsr_status nsr_adain_snake_conv1d_chain_f32(const float* x, const float* x_stats, const void* gamma,
+                                            const void* beta, const void* alpha, nsr_dtype param_dtype,
+                                            int64_t gamma_bstride, int64_t beta_bstride,
+                                            const void* w_packed, const void* bias,
+                                            const float* residual, float* out, float* out_stats,
+                                            int64_t B, int64_t C_in, int64_t C_out, int64_t T, int64_t K,
+                                            int64_t padding, int64_t dilation, float eps,
+                                            nsr_stream_t stream);
+
+/* nsr_conv1d_f16w_packed that also writes out_stats ([B*C_out][2]: mean,
+ * 1 / sqrt(var + eps) of each output row), for an AdaIN that follows. */
+nsr_status nsr_conv1d_f16w_packed_stats(const float* x, const void* w_packed, const void* bias,
+                                        const float* residual, float* out, float* out_stats, int64_t B,
+                                        int64_t C_in, int64_t C_out, int64_t T_in, int64_t K,
+                                        int64_t padding, int64_t dilation, float eps,
+                                        nsr_stream_t stream);
+
 /* ---- Repacked-Q8 GEMV (decoder projections at M = 1) ---------------------- */
 
 /* Weights W [K, NW] in the repacked Q8 layout of the reference's decoder

@@ -78,6 +78,10 @@ def lib() -> C.CDLL:
         L.nsr_conv1d_f16w_packed.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]
         L.nsr_adain_snake_conv1d_f32.argtypes = [_P, _P, _P, _P, C.c_int, _I64, _I64, _P, _P, _P, _P, _I64, _I64,
                                                  _I64, _I64, _I64, _I64, _I64, C.c_float, _P]
+        L.nsr_adain_snake_conv1d_chain_f32.argtypes = [_P, _P, _P, _P, _P, C.c_int, _I64, _I64, _P, _P, _P, _P, _P,
+                                                       _I64, _I64, _I64, _I64, _I64, _I64, _I64, C.c_float, _P]
+        L.nsr_conv1d_f16w_packed_stats.argtypes = [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                                                   C.c_float, _P]
         L.nsr_q8_0_to_t4.argtypes = [_P, _I64, _I64, C.c_int, _P, _P, _P]
         L.nsr_gemv_q8_t4.argtypes = [_P, C.c_int, _P, _P, _P, _P, C.c_int, _I64, _I64, _P]
         L.nsr_gemv_q8_t4_bias_glu.argtypes = [_P, C.c_int, _P, _P, _P, _P, C.c_int, _I64, _I64, _P]
@@ -100,6 +104,7 @@ def lib() -> C.CDLL:
                      "nsr_conv1d_f32io", "nsr_conv1d_pack_f16", "nsr_conv1d_f16w_packed",
                      "nsr_adain_snake_conv1d_f32", "nsr_attention_splitkv_f16", "nsr_attention_decode_f16",
                      "nsr_scale_f32", "nsr_leaky_relu_f32", "nsr_resblock_average_f32", "nsr_istft_f32", "nsr_snake",
+                     "nsr_adain_snake_conv1d_chain_f32", "nsr_conv1d_f16w_packed_stats",
                      "nsr_gemv_q8_t4_bias_glu", "nsr_gemv_q8_t4_resadd_ln"):
             getattr(L, name).restype = C.c_int
         _lib = L
@@ -415,6 +420,37 @@ def conv1d_f16w_packed(x, wp, bias=None, residual=None, *, padding=0, dilation=1
     check(lib().nsr_conv1d_f16w_packed(_ptr(x), _ptr(wp), _ptr(bias), _ptr(residual), _ptr(out), B, C_in, C_out, T,
                                        K, padding, dilation, _stream(stream)))
     return out
+
+
+def adain_snake_conv1d_chain(x, gamma, beta, alpha, wp, bias=None, residual=None, *, x_stats=None, want_stats=True,
+                             padding=0, dilation=1, eps=1e-5, out=None, stream=None):
+    """adain_snake_conv1d with the row statistics handed along: x_stats f32 [B*C_in, 2] (mean, rstd) or None
+    (computed here); returns (out, out_stats) with out_stats f32 [B*C_out, 2] (None if not want_stats)."""
+    B, C_in, T = x.shape
+    C_out, K, _ = wp.shape
+    if out is None:
+        out = torch.empty((B, C_out, _conv_tout(T, K, padding, dilation)), dtype=torch.float32, device=x.device)
+    st = torch.empty((B * C_out, 2), dtype=torch.float32, device=x.device) if want_stats else None
+    gs = C_in if gamma.dim() == 2 else 0
+    bs = C_in if beta.dim() == 2 else 0
+    check(lib().nsr_adain_snake_conv1d_chain_f32(_ptr(x), _ptr(x_stats), _ptr(gamma), _ptr(beta), _ptr(alpha),
+                                                 _dt(gamma), gs, bs, _ptr(wp), _ptr(bias), _ptr(residual), _ptr(out),
+                                                 _ptr(st), B, C_in, C_out, T, K, padding, dilation, eps,
+                                                 _stream(stream)))
+    return out, st
+
+
+def conv1d_f16w_packed_stats(x, wp, bias=None, residual=None, *, padding=0, dilation=1, eps=1e-5, out=None,
+                             stream=None):
+    """conv1d_f16w_packed that also returns the output rows' (mean, rstd) f32 [B*C_out, 2]."""
+    B, C_in, T = x.shape
+    C_out, K, _ = wp.shape
+    if out is None:
+        out = torch.empty((B, C_out, _conv_tout(T, K, padding, dilation)), dtype=torch.float32, device=x.device)
+    st = torch.empty((B * C_out, 2), dtype=torch.float32, device=x.device)
+    check(lib().nsr_conv1d_f16w_packed_stats(_ptr(x), _ptr(wp), _ptr(bias), _ptr(residual), _ptr(out), _ptr(st), B,
+                                             C_in, C_out, T, K, padding, dilation, eps, _stream(stream)))
+    return out, st
 
 
 def adain_snake_conv1d(x, gamma, beta, alpha, wp, bias=None, residual=None, *, padding=0, dilation=1, eps=1e-5,

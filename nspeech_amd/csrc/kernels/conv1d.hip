@@ -296,7 +296,38 @@ NSR_DEV void conv_body(const nsr_conv_args& a) {
  * with tile n + 2 still in flight, and a consumer waits for its residual
  * alone.
  */
-template <bool FUSED, bool RESID, int NU>
+/* Row statistics of the stored output for the next AdaIN (STATS kernels):
+ * after the quad transpose, lanes hl*32 + 4j + c4 (j = 0..7) hold columns
+ * t .. t + 3 of one output row, 32 columns of it per wave. For each such
+ * row block the wave writes (mean, M2) of its valid columns (their count
+ * follows from T_out), two passes over the registers with sums across the
+ * 8 lanes: DPP rotations by 4 and 8 within each 16-lane row, then a swizzle
+ * that exchanges the two rows of the 32-lane half (no LDS traffic for the
+ * first two steps). nsrk_conv_rowstats_merge combines a row's blocks. */
+NSR_DEV float sum_lanes8(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+
+NSR_DEV void emit_row_block(const nsr_float4& o, int t, int tb, int T_out, int l32, bool row_ok, float* dst) {
+  const int nv = max(0, min(4, T_out - t));
+  const float n = (float)max(0, min(32, T_out - tb)); /* valid columns of the block */
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) s += e < nv ? o[e] : 0.f;
+  const float mean = sum_lanes8(s) / fmaxf(n, 1.f);
+  float qv = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float d = o[e] - mean;
+    qv += e < nv ? d * d : 0.f;
+  }
+  const float m2 = sum_lanes8(qv);
+  if (row_ok && l32 < 4 && n > 0.f) *(nsr_float2*)dst = nsr_float2{mean, m2};
+}
+
+template <bool FUSED, bool RESID, int NU, bool STATS = false>
 NSR_DEV void conv_rw_body(const nsr_conv_args& a) {
   extern __shared__ uint16_t cv_lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -542,6 +573,12 @@ NSR_DEV void conv_rw_body(const nsr_conv_args& a) {
             if (t < a.T_out) /* T_out % 4 == 0: t < T_out covers t + 3 */
               __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(nsr_uint4, o), orr,
                                                      (co * (uint32_t)a.T_out + (uint32_t)t) * 4u, 0, 0);
+            if constexpr (STATS) {
+              const int nblk = (a.T_out + 31) >> 5;
+              const int64_t row = (int64_t)b * a.C_out + (int64_t)min((int)co, a.C_out - 1);
+              emit_row_block(o, t, t0 + wt * 32, a.T_out, l32, (int)co < a.C_out,
+                             a.row_part + 2 * (row * nblk + ((t0 + wt * 32) >> 5)));
+            }
           }
       }
       __syncthreads(); /* the next tile's input is staged */
@@ -552,6 +589,9 @@ NSR_DEV void conv_rw_body(const nsr_conv_args& a) {
 #define NSR_CONV_RW1(NAME, FUSED, RESID, NP)                                                         \
   extern "C" __global__ void __launch_bounds__(512, 1) NAME(const nsr_conv_args a) {                 \
     conv_rw_body<FUSED, RESID, NP>(a);                                                              \
+  }                                                                                                 \
+  extern "C" __global__ void __launch_bounds__(512, 1) NAME##_st(const nsr_conv_args a) {            \
+    conv_rw_body<FUSED, RESID, NP, true>(a);                                                        \
   }
 /* NU = column quads per producer lane / 8: staged window (TL + 3 alignment
  * columns) of at most 96 (NU 3) or 128 (NU 4) columns */
@@ -583,7 +623,7 @@ NSR_CONV_RW(4)
  *    consumers are past its last tap.
  * K + 1 barriers per item.
  */
-template <bool FUSED, bool RESID, int NU>
+template <bool FUSED, bool RESID, int NU, bool STATS = false>
 NSR_DEV void conv_pc_body(const nsr_conv_args& a) {
   extern __shared__ uint16_t cv_lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -832,6 +872,12 @@ NSR_DEV void conv_pc_body(const nsr_conv_args& a) {
             if (t < a.T_out)
               __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(nsr_uint4, o), orr,
                                                      ((uint32_t)co * (uint32_t)a.T_out + (uint32_t)t) * 4u, 0, 0);
+            if constexpr (STATS) {
+              const int nblk = (a.T_out + 31) >> 5;
+              const int64_t row = (int64_t)b * a.C_out + (int64_t)min(co, a.C_out - 1);
+              emit_row_block(o, t, t0 + wt * 32, a.T_out, l32, co < a.C_out,
+                             a.row_part + 2 * (row * nblk + ((t0 + wt * 32) >> 5)));
+            }
           }
       }
       __syncthreads(); /* the next item's input is staged */
@@ -842,6 +888,9 @@ NSR_DEV void conv_pc_body(const nsr_conv_args& a) {
 #define NSR_CONV_PC1(NAME, FUSED, RESID, NU)                                                         \
   extern "C" __global__ void __launch_bounds__(512, 1) NAME(const nsr_conv_args a) {                 \
     conv_pc_body<FUSED, RESID, NU>(a);                                                              \
+  }                                                                                                 \
+  extern "C" __global__ void __launch_bounds__(512, 1) NAME##_st(const nsr_conv_args a) {            \
+    conv_pc_body<FUSED, RESID, NU, true>(a);                                                        \
   }
 #define NSR_CONV_PC(NU)                                                                              \
   NSR_CONV_PC1(nsrk_conv1d_pc_f16x2_nu##NU, false, false, NU)                                        \
@@ -879,4 +928,63 @@ extern "C" __global__ void __launch_bounds__(256) nsrk_conv1d_pack(const nsr_con
   const int64_t r = i - co * a.C_in * a.K;
   const int64_t ci = r / a.K, k = r - ci * a.K;
   a.wp[(co * a.K + k) * a.C_in + ci] = a.w[i];
+}
+
+/* Merge a row's (mean, M2) blocks (Chan, Golub and LeVeque's pairwise
+ * update: n = na + nb, d = mb - ma, mean = ma + d nb / n,
+ * M2 = M2a + M2b + d^2 na nb / n; block i holds min(32, T_out - 32 i)
+ * columns) into the row's mean and 1 / sqrt(M2 / n + eps), the statistics
+ * the fused AdaIN+Snake conv reads. One workgroup per row; each lane merges
+ * blocks i = tid + 256 k in order (eight loads in flight at a time), then a
+ * fixed tree over the lanes: the result does not depend on timing. */
+NSR_DEV void chan_merge(float& n, float& mean, float& m2, float nb, float mb, float m2b) {
+  const float nn = n + nb;
+  if (nb > 0.f) {
+    const float d = mb - mean;
+    const float f = nb / nn;
+    mean = __builtin_fmaf(d, f, mean);
+    m2 = m2 + m2b + d * d * n * f;
+    n = nn;
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256) nsrk_conv_rowstats_merge(const nsr_rowstats_args a) {
+  __shared__ float sn[256], sm[256], sq[256];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const nsr_float2* pr = (const nsr_float2*)a.part + row * a.nblk;
+  float n = 0.f, mean = 0.f, m2 = 0.f;
+  for (int i0 = 0; i0 < a.nblk; i0 += 8 * 256) {
+    nsr_float2 p[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + tid + 256 * u;
+      p[u] = pr[min(i, a.nblk - 1)];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + tid + 256 * u;
+      const float nb = i < a.nblk ? (float)min(32, a.T_out - 32 * i) : 0.f;
+      chan_merge(n, mean, m2, nb, p[u].x, p[u].y);
+    }
+  }
+  sn[tid] = n;
+  sm[tid] = mean;
+  sq[tid] = m2;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (tid < w) {
+      float n0 = sn[tid], m0 = sm[tid], q0 = sq[tid];
+      chan_merge(n0, m0, q0, sn[tid + w], sm[tid + w], sq[tid + w]);
+      sn[tid] = n0;
+      sm[tid] = m0;
+      sq[tid] = q0;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    const float var = fmaxf(sq[0] / fmaxf(sn[0], 1.f), 0.f);
+    a.stats[2 * row] = sm[0];
+    a.stats[2 * row + 1] = 1.0f / sqrtf(var + a.eps);
+  }
 }

@@ -168,7 +168,17 @@ typedef struct nsr_conv_args {
   int64_t beta_bstride;
   int32_t B, C_in, C_out, T_in, T_out, K, padding, dilation, pdt;
   int32_t pad_;            /* bit 0: 16-byte epilogue stores allowed */
+  float* row_part;         /* STATS kernels: [B*C_out][ceil(T_out/32)][2] (mean, M2) of out */
 } nsr_conv_args;
+
+typedef struct nsr_rowstats_args {
+  const float* part;       /* [rows][nblk][2] (mean, M2) of 32-column blocks */
+  float* stats;            /* [rows][2] mean, 1 / sqrt(var + eps) */
+  int32_t nblk;
+  int32_t T_out;           /* block i holds min(32, T_out - 32 i) columns */
+  float eps;
+  int32_t pad_;
+} nsr_rowstats_args;
 
 typedef struct nsr_conv_pack_args {
   const uint16_t* w;       /* f16 [C_out][C_in][K] */

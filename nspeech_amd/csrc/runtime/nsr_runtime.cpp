@@ -144,7 +144,7 @@ int unit_of(const std::string& name) {
   static const P map[] = {{"nsrk_q8_0_", 0}, {"nsrk_ln_", 1},    {"nsrk_resln_", 1}, {"nsrk_rope_", 2},
                           {"nsrk_adain_", 3}, {"nsrk_silu_", 4}, {"nsrk_gelu_", 4},  {"nsrk_glu_", 4},
                           {"nsrk_add_", 4},  {"nsrk_gemv_", 5},
-                          {"nsrk_conv1d_", 6}, {"nsrk_attn_", 7}, {"nsrk_combine_", 4}, {"nsrk_istft_", 8},
+                          {"nsrk_conv1d_", 6}, {"nsrk_conv_rowstats", 6}, {"nsrk_attn_", 7}, {"nsrk_combine_", 4}, {"nsrk_istft_", 8},
                           {"nsrk_snake_", 4}};
   for (const P& p : map)
     if (name.compare(0, std::strlen(p.prefix), p.prefix) == 0) return p.unit;
@@ -1190,7 +1190,7 @@ nsr_status conv_validate(const float* x, const void* w, uintptr_t w_align, float
   return NSR_OK;
 }
 
-nsr_status conv_launch(bool fused, nsr_conv_args& a, nsr_stream_t stream, const char* what) {
+nsr_status conv_launch(bool fused, nsr_conv_args& a, nsr_stream_t stream, const char* what, bool* emitted = nullptr) {
   DeviceModule* dm = nullptr;
   nsr_status st = current_module(&dm);
   if (st != NSR_OK) return st;
@@ -1213,8 +1213,9 @@ nsr_status conv_launch(bool fused, nsr_conv_args& a, nsr_stream_t stream, const 
   if (a.C_in <= kCvCI && a.C_out <= kCvCO && a.K <= 3 && win <= 128 && lds_rw <= dm->max_lds && (a.pad_ & 1) &&
       a.T_in > 0 && a.T_in % 4 == 0 && aligned(a.x, 16)) {
     const int64_t groups = std::min<int64_t>(tiles, (int64_t)dm->n_cu);
+    if (emitted) *emitted = a.row_part != nullptr;
     return launch(std::string("nsrk_conv1d_rw") + (fused ? "_adain_snake" : "") + (a.residual ? "_res" : "") +
-                      "_f16x2_nu" + (win <= 96 ? "3" : "4"),
+                      "_f16x2_nu" + (win <= 96 ? "3" : "4") + (a.row_part ? "_st" : ""),
                   (unsigned)groups, 1, 512, (unsigned)lds_rw, stream, params);
   }
   // any K, C_in in chunks and C_out in blocks of 128, 16-byte aligned rows: weights streamed one tap ahead
@@ -1222,11 +1223,14 @@ nsr_status conv_launch(bool fused, nsr_conv_args& a, nsr_stream_t stream, const 
   const int64_t lds_pc = (2 * TL + 2 * kCvCO) * kCvS * 2 + 4 * (int64_t)a.C_out; /* + the bias as f32 */
   if (win <= 128 && lds_pc <= dm->max_lds && (a.pad_ & 1) && a.T_in > 0 && a.T_in % 4 == 0 && aligned(a.x, 16)) {
     const int64_t groups = std::min<int64_t>(tiles, (int64_t)dm->n_cu);
+    if (emitted) *emitted = a.row_part != nullptr;
     return launch(std::string("nsrk_conv1d_pc") + (fused ? "_adain_snake" : "") + (a.residual ? "_res" : "") +
-                      "_f16x2_nu" + (win <= 96 ? "3" : "4"),
+                      "_f16x2_nu" + (win <= 96 ? "3" : "4") + (a.row_part ? "_st" : ""),
                   (unsigned)groups, 1, 512, (unsigned)lds_pc, stream, params);
   }
-  // the plain np 9 kernel fits two workgroups per CU in registers; the others one
+  // the plain np 9 kernel fits two workgroups per CU in registers; the others one (no row statistics: the
+  // caller takes them from the output)
+  if (emitted) *emitted = false;
   const int per_cu = (!fused && np == 9 && 2 * lds <= dm->max_lds) ? 2 : 1;
   const int64_t groups = std::min<int64_t>(tiles, (int64_t)per_cu * dm->n_cu);
   return launch(std::string(fused ? "nsrk_conv1d_adain_snake_f16x2_np" : "nsrk_conv1d_f16x2_np") + std::to_string(np),
@@ -1251,6 +1255,52 @@ nsr_status nsr_conv1d_pack_f16(const void* w, int64_t C_out, int64_t C_in, int64
   a.K = K;
   void* params[] = {&a};
   return launch("nsrk_conv1d_pack", cdiv_u(C_out * C_in * K, 256), 1, 256, 0, stream, params);
+}
+
+// Launch a conv and leave the per-(b, co) statistics of its output in row_stats ([B*C_out][2]: mean,
+// 1 / sqrt(var + eps)): the aligned-row kernels emit per-32-column (mean, M2) blocks from their
+// epilogue into stream-ordered scratch and a merge kernel combines them; the fallback kernel's output is
+// re-read by the row statistics kernel instead.
+static nsr_status conv_launch_stats(bool fused, nsr_conv_args& a, float eps, float* row_stats, nsr_stream_t stream,
+                                    const char* what) {
+  const int64_t rows = (int64_t)a.B * a.C_out, nblk = ((int64_t)a.T_out + 31) / 32;
+  if (rows > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "%s: too many rows", what);
+  float* part = nullptr;
+  hipError_t e = hipMallocAsync((void**)&part, (size_t)(rows * nblk) * 2 * sizeof(float), (hipStream_t)stream);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(NSR_ERR_HIP, "%s: hipMallocAsync: %s", what, hipGetErrorString(e));
+  }
+  a.row_part = part;
+  bool emitted = false;
+  nsr_status st = conv_launch(fused, a, stream, what, &emitted);
+  if (st == NSR_OK && emitted) {
+    nsr_rowstats_args m;
+    std::memset(&m, 0, sizeof(m));
+    m.part = part;
+    m.stats = row_stats;
+    m.nblk = (int32_t)nblk;
+    m.T_out = a.T_out;
+    m.eps = eps;
+    void* pm[] = {&m};
+    st = launch("nsrk_conv_rowstats_merge", (unsigned)rows, 1, 256, 0, stream, pm);
+  } else if (st == NSR_OK) {
+    nsr_adain_args s;
+    std::memset(&s, 0, sizeof(s));
+    s.x = a.out;
+    s.stats = row_stats;
+    s.n_rows = rows;
+    s.T = a.T_out;
+    s.C = a.C_out;
+    s.eps = eps;
+    s.inv_t = 1.0f / (float)a.T_out;
+    void* ps[] = {&s};
+    const bool rows16 = a.T_out % 4 == 0 && aligned(a.out, 16);
+    st = launch(rows16 ? "nsrk_adain_stats4" : "nsrk_adain_stats", (unsigned)rows, 1, 1024, 0, stream, ps);
+  }
+  a.row_part = nullptr;
+  hipFreeAsync(part, (hipStream_t)stream);
+  return st;
 }
 
 nsr_status nsr_conv1d_f16w_packed(const float* x, const void* w_packed, const void* bias, const float* residual,
@@ -1305,16 +1355,18 @@ nsr_status nsr_conv1d_f32io(const float* x, const void* w, const void* bias, flo
   return st;
 }
 
-nsr_status nsr_adain_snake_conv1d_f32(const float* x, const void* gamma, const void* beta, const void* alpha,
-                                      nsr_dtype param_dtype, int64_t gamma_bstride, int64_t beta_bstride,
-                                      const void* w_packed, const void* bias, const float* residual, float* out,
-                                      int64_t B, int64_t C_in, int64_t C_out, int64_t T, int64_t K, int64_t padding,
-                                      int64_t dilation, float eps, nsr_stream_t stream) {
-  const char* what = "adain_snake_conv1d";
+static nsr_status adain_conv_impl(const float* x, const float* x_stats, const void* gamma, const void* beta,
+                                  const void* alpha, nsr_dtype param_dtype, int64_t gamma_bstride,
+                                  int64_t beta_bstride, const void* w_packed, const void* bias, const float* residual,
+                                  float* out, float* out_stats, int64_t B, int64_t C_in, int64_t C_out, int64_t T,
+                                  int64_t K, int64_t padding, int64_t dilation, float eps, nsr_stream_t stream,
+                                  const char* what) {
   if (!gamma || !beta || !alpha) return fail(NSR_ERR_BAD_ARG, "%s: null parameter pointer", what);
   if (param_dtype != NSR_F32 && param_dtype != NSR_F16) return fail(NSR_ERR_BAD_ARG, "%s: params must be F32 or F16", what);
   if (gamma_bstride < 0 || beta_bstride < 0) return fail(NSR_ERR_BAD_ARG, "%s: negative batch stride", what);
   if (!(eps >= 0.0f)) return fail(NSR_ERR_BAD_ARG, "%s: eps must be >= 0", what);
+  if ((x_stats && !aligned(x_stats, 8)) || (out_stats && !aligned(out_stats, 8)))
+    return fail(NSR_ERR_BAD_ARG, "%s: row statistics need 8-byte alignment", what);
   int64_t T_out = 0;
   nsr_status st = conv_validate(x, w_packed, 16, out, B, C_in, C_out, T, K, padding, dilation, &T_out, what);
   if (st != NSR_OK) return st;
@@ -1322,25 +1374,27 @@ nsr_status nsr_adain_snake_conv1d_f32(const float* x, const void* gamma, const v
     return fail(NSR_ERR_BAD_ARG, "%s: misaligned bias or residual", what);
   if (B == 0 || T_out <= 0) return NSR_OK;
   if (T == 0) return fail(NSR_ERR_BAD_ARG, "%s: T == 0 (an empty row has no statistics)", what);
-  // per-(b, ci) mean and 1/sqrt(var + eps) of x in stream-ordered scratch
+  // per-(b, ci) mean and 1/sqrt(var + eps) of x: the caller's, or computed into stream-ordered scratch
   float* stats = nullptr;
-  hipError_t e = hipMallocAsync((void**)&stats, (size_t)(B * C_in) * 2 * sizeof(float), (hipStream_t)stream);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(NSR_ERR_HIP, "%s: hipMallocAsync: %s", what, hipGetErrorString(e));
+  if (!x_stats) {
+    hipError_t e = hipMallocAsync((void**)&stats, (size_t)(B * C_in) * 2 * sizeof(float), (hipStream_t)stream);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(NSR_ERR_HIP, "%s: hipMallocAsync: %s", what, hipGetErrorString(e));
+    }
+    nsr_adain_args s;
+    std::memset(&s, 0, sizeof(s));
+    s.x = x;
+    s.stats = stats;
+    s.n_rows = B * C_in;
+    s.T = T;
+    s.C = (int32_t)C_in;
+    s.eps = eps;
+    s.inv_t = 1.0f / (float)T;
+    void* p1[] = {&s};
+    const bool rows16 = T % 4 == 0 && aligned(x, 16);
+    st = launch(rows16 ? "nsrk_adain_stats4" : "nsrk_adain_stats", (unsigned)(B * C_in), 1, 1024, 0, stream, p1);
   }
-  nsr_adain_args s;
-  std::memset(&s, 0, sizeof(s));
-  s.x = x;
-  s.stats = stats;
-  s.n_rows = B * C_in;
-  s.T = T;
-  s.C = (int32_t)C_in;
-  s.eps = eps;
-  s.inv_t = 1.0f / (float)T;
-  void* p1[] = {&s};
-  const bool rows16 = T % 4 == 0 && aligned(x, 16);
-  st = launch(rows16 ? "nsrk_adain_stats4" : "nsrk_adain_stats", (unsigned)(B * C_in), 1, 1024, 0, stream, p1);
   if (st == NSR_OK) {
     nsr_conv_args a;
     std::memset(&a, 0, sizeof(a));
@@ -1349,7 +1403,7 @@ nsr_status nsr_adain_snake_conv1d_f32(const float* x, const void* gamma, const v
     a.bias = (const uint16_t*)bias;
     a.residual = residual;
     a.out = out;
-    a.stats = stats;
+    a.stats = x_stats ? x_stats : stats;
     a.gamma = gamma;
     a.beta = beta;
     a.alpha = alpha;
@@ -1364,10 +1418,63 @@ nsr_status nsr_adain_snake_conv1d_f32(const float* x, const void* gamma, const v
     a.padding = (int32_t)padding;
     a.dilation = (int32_t)dilation;
     a.pdt = param_dtype == NSR_F32 ? 0 : 1;
-    st = conv_launch(true, a, stream, what);
+    st = out_stats ? conv_launch_stats(true, a, eps, out_stats, stream, what) : conv_launch(true, a, stream, what);
   }
-  (void)hipFreeAsync(stats, (hipStream_t)stream);
+  if (stats) (void)hipFreeAsync(stats, (hipStream_t)stream);
   return st;
+}
+
+nsr_status nsr_adain_snake_conv1d_f32(const float* x, const void* gamma, const void* beta, const void* alpha,
+                                      nsr_dtype param_dtype, int64_t gamma_bstride, int64_t beta_bstride,
+                                      const void* w_packed, const void* bias, const float* residual, float* out,
+                                      int64_t B, int64_t C_in, int64_t C_out, int64_t T, int64_t K, int64_t padding,
+                                      int64_t dilation, float eps, nsr_stream_t stream) {
+  return adain_conv_impl(x, nullptr, gamma, beta, alpha, param_dtype, gamma_bstride, beta_bstride, w_packed, bias,
+                         residual, out, nullptr, B, C_in, C_out, T, K, padding, dilation, eps, stream,
+                         "adain_snake_conv1d");
+}
+
+nsr_status nsr_adain_snake_conv1d_chain_f32(const float* x, const float* x_stats, const void* gamma,
+                                            const void* beta, const void* alpha, nsr_dtype param_dtype,
+                                            int64_t gamma_bstride, int64_t beta_bstride, const void* w_packed,
+                                            const void* bias, const float* residual, float* out, float* out_stats,
+                                            int64_t B, int64_t C_in, int64_t C_out, int64_t T, int64_t K,
+                                            int64_t padding, int64_t dilation, float eps, nsr_stream_t stream) {
+  return adain_conv_impl(x, x_stats, gamma, beta, alpha, param_dtype, gamma_bstride, beta_bstride, w_packed, bias,
+                         residual, out, out_stats, B, C_in, C_out, T, K, padding, dilation, eps, stream,
+                         "adain_snake_conv1d_chain");
+}
+
+nsr_status nsr_conv1d_f16w_packed_stats(const float* x, const void* w_packed, const void* bias,
+                                        const float* residual, float* out, float* out_stats, int64_t B, int64_t C_in,
+                                        int64_t C_out, int64_t T_in, int64_t K, int64_t padding, int64_t dilation,
+                                        float eps, nsr_stream_t stream) {
+  const char* what = "conv1d_f16w_packed_stats";
+  int64_t T_out = 0;
+  nsr_status st = conv_validate(x, w_packed, 16, out, B, C_in, C_out, T_in, K, padding, dilation, &T_out, what);
+  if (st != NSR_OK) return st;
+  if (!out_stats || !aligned(out_stats, 8)) return fail(NSR_ERR_BAD_ARG, "%s: null or misaligned out_stats", what);
+  if ((bias && !aligned(bias, 2)) || (residual && !aligned(residual, 4)))
+    return fail(NSR_ERR_BAD_ARG, "%s: misaligned bias or residual", what);
+  if (!(eps >= 0.0f)) return fail(NSR_ERR_BAD_ARG, "%s: eps must be >= 0", what);
+  if (B == 0 || T_out <= 0) return NSR_OK;
+  if (T_in == 0) return fail(NSR_ERR_BAD_ARG, "%s: T_in == 0", what);
+  nsr_conv_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.x = x;
+  a.w = (const uint16_t*)w_packed;
+  a.bias = (const uint16_t*)bias;
+  a.residual = residual;
+  a.out = out;
+  a.B = (int32_t)B;
+  a.C_in = (int32_t)C_in;
+  a.C_out = (int32_t)C_out;
+  a.T_in = (int32_t)T_in;
+  a.T_out = (int32_t)T_out;
+  a.K = (int32_t)K;
+  a.padding = (int32_t)padding;
+  a.dilation = (int32_t)dilation;
+  return conv_launch_stats(false, a, eps, out_stats, stream, what);
 }
 
 }  // extern "C"
