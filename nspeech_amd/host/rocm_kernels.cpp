@@ -415,6 +415,39 @@ void RocmKokoroBackend::snake(const GpuBuffer& x, const GpuBuffer& alpha, const 
             "snake");
 }
 
+void RocmKokoroBackend::conv1d_f32(const GpuBuffer& x, const GpuBuffer& w, const GpuBuffer& bias,
+                                   const GpuBuffer& out, size_t c_in, size_t c_out, size_t t_in, size_t t_out,
+                                   size_t k, size_t stride, size_t padding, size_t dilation) const {
+  if ((int64_t)t_out != (int64_t)t_in + 2 * (int64_t)padding - (int64_t)dilation * ((int64_t)k - 1))
+    throw Error("conv1d_f32: t_out does not match t_in, k, padding and dilation");
+  nsr_check(nsr_conv1d_f32io(static_cast<const float*>(x.at()), w.at(), bias.at(), static_cast<float*>(out.at()), 1,
+                             (int64_t)c_in, (int64_t)c_out, (int64_t)t_in, (int64_t)k, (int64_t)stride,
+                             (int64_t)padding, (int64_t)dilation, device_.stream()),
+            "conv1d_f32");
+}
+
+void RocmKokoroBackend::add_f32(const GpuBuffer& a, const GpuBuffer& b, const GpuBuffer& out, size_t n) const {
+  nsr_check(nsr_residual_add(a.at(), b.at(), out.at(), NSR_F32, (int64_t)n, device_.stream()), "add_f32");
+}
+
+void RocmKokoroBackend::scale_third_f32(const GpuBuffer& x, const GpuBuffer& out, size_t n) const {
+  nsr_check(nsr_scale_f32(static_cast<const float*>(x.at()), static_cast<float*>(out.at()), (int64_t)n,
+                          (float)0.3333333333333333, device_.stream()),
+            "scale_third_f32");
+}
+
+void RocmKokoroBackend::leaky_relu_f32(const GpuBuffer& x, const GpuBuffer& out, size_t n, float slope) const {
+  nsr_check(nsr_leaky_relu_f32(static_cast<const float*>(x.at()), static_cast<float*>(out.at()), (int64_t)n, slope,
+                               device_.stream()),
+            "leaky_relu_f32");
+}
+
+void RocmKokoroBackend::istft_gpu(const GpuBuffer& x, const GpuBuffer& out, size_t n_frames, size_t out_len) const {
+  nsr_check(nsr_istft_f32(static_cast<const float*>(x.at()), static_cast<float*>(out.at()), (int64_t)n_frames,
+                          (int64_t)out_len, 20, 5, device_.stream()),
+            "istft_gpu");
+}
+
 // ------------------------------------------------------------- embedding --
 
 QEmbedding::QEmbedding(const RocmDevice& device, const RocmKernels& kernels, Tensor table, size_t vocab,

@@ -208,6 +208,19 @@ class RocmKokoroBackend {
   // seq_len] (n_elements = channels * seq_len), alpha [channels] f16.
   void snake(const GpuBuffer& x, const GpuBuffer& alpha, const GpuBuffer& out, size_t n_elements, size_t channels,
              size_t seq_len) const;
+  // The f32-intermediate path (gpu_backend.rs:134-225): this backend has it.
+  bool has_f32_intermediates() const { return true; }
+  // conv1d_f32 (:165-177): x f32 [c_in, t_in], w f16 [c_out, c_in, k], bias f16 [c_out] -> f32 [c_out, t_out];
+  // stride 1 (the decoder's only stride), t_out must be what padding and dilation give.
+  void conv1d_f32(const GpuBuffer& x, const GpuBuffer& w, const GpuBuffer& bias, const GpuBuffer& out, size_t c_in,
+                  size_t c_out, size_t t_in, size_t t_out, size_t k, size_t stride, size_t padding,
+                  size_t dilation) const;
+  // add_f32 (:186-190), scale_third_f32 (:191-195), leaky_relu_f32 (:196-200): f32 elementwise over n.
+  void add_f32(const GpuBuffer& a, const GpuBuffer& b, const GpuBuffer& out, size_t n) const;
+  void scale_third_f32(const GpuBuffer& x, const GpuBuffer& out, size_t n) const;
+  void leaky_relu_f32(const GpuBuffer& x, const GpuBuffer& out, size_t n, float slope) const;
+  // istft_gpu (:220-225): conv_post output [22, n_frames] f32 -> audio [out_len] f32 (n_fft 20, hop 5).
+  void istft_gpu(const GpuBuffer& x, const GpuBuffer& out, size_t n_frames, size_t out_len) const;
 
  private:
   RocmDevice device_;

@@ -484,6 +484,96 @@ void test_snake_f16(const RocmDevice& dev, const RocmKernels& k, size_t C, size_
   report("snake (f16) C=16 T=3001", err, 2e-3);
 }
 
+// The generator tail through the backend methods, the reference's order
+// (decoder.rs:542-589): add_f32 twice, scale_third_f32, leaky_relu_f32 (bit-
+// exact against the same f32 operations on the host), conv1d_f32 into 22
+// channels (float64 host conv, 1e-5 of max(|ref|, 1)) and istft_gpu (float64
+// host overlap-add of the same formulas, 1e-5 of max(|ref|, 1)).
+void test_kokoro_tail(const RocmDevice& dev, const RocmKernels& k) {
+  const size_t C = 32, T = 301, n = C * T, CO = 22, K = 7;
+  std::vector<float> r0(n), r1(n), r2(n);
+  for (size_t i = 0; i < n; ++i) {
+    r0[i] = std::sin(0.013f * (float)i);
+    r1[i] = std::cos(0.007f * (float)i) * 0.5f;
+    r2[i] = std::sin(0.031f * (float)i + 1.0f) * 0.8f;
+  }
+  Tensor R0 = Tensor::from_host(dev, r0.data(), {C, T}, DType::F32);
+  Tensor R1 = Tensor::from_host(dev, r1.data(), {C, T}, DType::F32);
+  Tensor R2 = Tensor::from_host(dev, r2.data(), {C, T}, DType::F32);
+  Tensor S = Tensor::empty(dev, {C, T}, DType::F32), S2 = Tensor::empty(dev, {C, T}, DType::F32);
+  Tensor A = Tensor::empty(dev, {C, T}, DType::F32), L = Tensor::empty(dev, {C, T}, DType::F32);
+  RocmKokoroBackend be(dev, k);
+  be.add_f32(R0.buffer(), R1.buffer(), S.buffer(), n);
+  be.add_f32(S.buffer(), R2.buffer(), S2.buffer(), n);
+  be.scale_third_f32(S2.buffer(), A.buffer(), n);
+  be.leaky_relu_f32(A.buffer(), L.buffer(), n, 0.01f);
+  // conv_post: 32 -> 22 channels, K = 7, padding 3
+  std::vector<uint16_t> w(CO * C * K), b(CO);
+  for (size_t i = 0; i < w.size(); ++i) w[i] = f2h(0.05f * std::cos(0.37f * (float)i));
+  for (size_t i = 0; i < CO; ++i) b[i] = f2h(-0.5f + 0.01f * (float)i);
+  Tensor W = Tensor::from_host(dev, w.data(), {CO, C, K}, DType::F16);
+  Tensor Bi = Tensor::from_host(dev, b.data(), {CO}, DType::F16);
+  Tensor X = Tensor::empty(dev, {CO, T}, DType::F32);
+  be.conv1d_f32(L.buffer(), W.buffer(), Bi.buffer(), X.buffer(), C, CO, T, T, K, 1, 3, 1);
+  const size_t out_len = (T - 1) * 5;
+  Tensor AU = Tensor::empty(dev, {out_len}, DType::F32);
+  be.istft_gpu(X.buffer(), AU.buffer(), T, out_len);
+  dev.synchronize();
+  // host: the same f32 element-wise chain
+  std::vector<float> lr(n);
+  bool exact = true;
+  const std::vector<float> l_gpu = L.to_vec<float>();
+  for (size_t i = 0; i < n; ++i) {
+    float v = (r0[i] + r1[i]) + r2[i];
+    v = v * (float)0.3333333333333333;
+    v = v > 0.f ? v : v * 0.01f;
+    lr[i] = v;
+    if (std::memcmp(&v, &l_gpu[i], 4) != 0) exact = false;
+  }
+  report("tail: add, add, scale_third, leaky_relu bit-exact", exact ? 0.0 : 1.0, 0.0);
+  // host conv in float64 on the GPU's own leaky-ReLU output
+  std::vector<double> xr(CO * T, 0.0);
+  for (size_t o = 0; o < CO; ++o)
+    for (size_t t = 0; t < T; ++t) {
+      double acc = h2f(b[o]);
+      for (size_t c = 0; c < C; ++c)
+        for (size_t kk = 0; kk < K; ++kk) {
+          const long ti = (long)t + (long)kk - 3;
+          if (ti >= 0 && ti < (long)T) acc += (double)h2f(w[(o * C + c) * K + kk]) * l_gpu[c * T + (size_t)ti];
+        }
+      xr[o * T + t] = acc;
+    }
+  const std::vector<float> x_gpu = X.to_vec<float>();
+  double err = 0;
+  for (size_t i = 0; i < xr.size(); ++i) err = std::max(err, scaled(x_gpu[i], xr[i]));
+  report("tail: conv1d_f32 (conv_post)", err, 1e-5);
+  // host iSTFT in float64 on the GPU's conv output
+  const int N = 20, hop = 5, bins = 11;
+  const double PI = 3.14159265358979323846;
+  std::vector<double> y((T - 1) * hop + N, 0.0), ws(y.size(), 0.0);
+  for (size_t f = 0; f < T; ++f)
+    for (int nn = 0; nn < N; ++nn) {
+      double v = 0;
+      for (int kb = 0; kb < bins; ++kb) {
+        const double m = std::exp((double)x_gpu[kb * T + f]), p = std::sin((double)x_gpu[(bins + kb) * T + f]);
+        const double sc = (kb == 0 || kb == bins - 1) ? 1.0 : 2.0;
+        const double ang = 2 * PI * kb * nn / N;
+        v += sc * (m * std::cos(p) * std::cos(ang) - m * std::sin(p) * std::sin(ang));
+      }
+      const double wn = 0.5 - 0.5 * std::cos(2 * PI * nn / N);
+      y[f * hop + nn] += v / N * wn;
+      ws[f * hop + nn] += wn * wn;
+    }
+  const std::vector<float> au = AU.to_vec<float>();
+  double err2 = 0;
+  for (size_t i = 0; i < out_len; ++i) {
+    const size_t pp = i + N / 2;
+    const double ref = ws[pp] > 1e-8 ? y[pp] / ws[pp] : 0.0;
+    err2 = std::max(err2, scaled(au[i], ref));
+  }
+  report("tail: istft_gpu", err2, 1e-5);
+}
+
 }  // namespace
 
 int main() {
@@ -496,6 +586,7 @@ int main() {
     test_adain_snake_f16(dev, k, 4, 100, "adain_snake (f16) C=4 T=100");
     test_adain_snake_f16(dev, k, 128, 11281, "adain_snake (f16) C=128 T=11281");
     test_snake_f16(dev, k, 16, 3001);
+    test_kokoro_tail(dev, k);
     test_layernorm_std_f32in(dev, k);
     test_layernorm_unit_offset_and_bare(dev, k);
     test_elementwise(dev, k);
