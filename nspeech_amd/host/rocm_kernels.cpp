@@ -389,6 +389,32 @@ void enc_attention_splitkv(Encoder enc, const RocmKernels&, const GpuBuffer& q, 
             "enc_attention_splitkv");
 }
 
+void enc_gemv_q8(Encoder enc, const RocmKernels&, const GpuBuffer& x, const GpuBuffer& qs, const GpuBuffer& scales,
+                 const GpuBuffer* bias, const GpuBuffer& out, size_t k, size_t n) {
+  nsr_check(nsr_gemv_q8(x.at(), NSR_F16, static_cast<const uint32_t*>(qs.at()), static_cast<const uint16_t*>(scales.at()),
+                        bias ? static_cast<const float*>(bias->at()) : nullptr, out.at(), NSR_F16, (int64_t)k,
+                        (int64_t)n, enc),
+            "enc_gemv_q8");
+}
+
+void enc_gemv_q8_bias_glu(Encoder enc, const RocmKernels&, const GpuBuffer& x, const GpuBuffer& qs,
+                          const GpuBuffer& scales, const GpuBuffer& bias, const GpuBuffer& out, size_t k, size_t n) {
+  nsr_check(nsr_gemv_q8_bias_glu(x.at(), NSR_F16, static_cast<const uint32_t*>(qs.at()),
+                                 static_cast<const uint16_t*>(scales.at()), static_cast<const float*>(bias.at()),
+                                 out.at(), NSR_F16, (int64_t)k, (int64_t)n, enc),
+            "enc_gemv_q8_bias_glu");
+}
+
+void enc_gemv_q8_resadd_ln(Encoder enc, const RocmKernels&, const GpuBuffer& x, const GpuBuffer& qs,
+                           const GpuBuffer& scales, const GpuBuffer& residual, const GpuBuffer& out_f32,
+                           const GpuBuffer& ln_weight, const GpuBuffer& norm, size_t k, size_t dim, float eps) {
+  nsr_check(nsr_gemv_q8_resadd_ln(x.at(), NSR_F16, static_cast<const uint32_t*>(qs.at()),
+                                  static_cast<const uint16_t*>(scales.at()), static_cast<const float*>(residual.at()),
+                                  static_cast<float*>(out_f32.at()), ln_weight.at(), NSR_F16, norm.at(), NSR_F16,
+                                  (int64_t)k, (int64_t)dim, eps, enc),
+            "enc_gemv_q8_resadd_ln");
+}
+
 // ---------------------------------------------------------------- Kokoro --
 
 void RocmKokoroBackend::adain_snake_f32(const GpuBuffer& x, const GpuBuffer& gamma, const GpuBuffer& beta,

@@ -190,6 +190,20 @@ void enc_attention_splitkv(Encoder enc, const RocmKernels& kernels, const GpuBuf
                            size_t head_dim, size_t n_kv_heads, size_t n_q_heads, float sm_scale,
                            size_t stride_kv_head, size_t stride_kv_seq, size_t n_splits);
 
+// Decoder MLP GEMVs at M = 1 over the reference's repacked-Q8 layout (qs u32 [K, NW/4], scales f16 [K/32, NW]),
+// the kernels of kernels/moonshine_kernels.py:616-677, 1721-1819 (the reference's Triton source has them; its
+// Metal decoder does not dispatch them). x and the f16 outputs as the decoder holds them.
+// enc_gemv_q8: out [N] f16 = x [K] f16 @ W + bias (bias f32 [N] or an empty buffer).
+void enc_gemv_q8(Encoder enc, const RocmKernels& kernels, const GpuBuffer& x, const GpuBuffer& qs,
+                 const GpuBuffer& scales, const GpuBuffer* bias, const GpuBuffer& out, size_t k, size_t n);
+// enc_gemv_q8_bias_glu: out [N] f16 = silu(gate) * up over fc1's 2N columns (+ bias f32 [2N]).
+void enc_gemv_q8_bias_glu(Encoder enc, const RocmKernels& kernels, const GpuBuffer& x, const GpuBuffer& qs,
+                          const GpuBuffer& scales, const GpuBuffer& bias, const GpuBuffer& out, size_t k, size_t n);
+// enc_gemv_q8_resadd_ln: out_f32 [dim] = f16(x @ W) + residual f32; norm [dim] f16 = LN(out_f32) * weight f16.
+void enc_gemv_q8_resadd_ln(Encoder enc, const RocmKernels& kernels, const GpuBuffer& x, const GpuBuffer& qs,
+                           const GpuBuffer& scales, const GpuBuffer& residual, const GpuBuffer& out_f32,
+                           const GpuBuffer& ln_weight, const GpuBuffer& norm, size_t k, size_t dim, float eps);
+
 // ---- Kokoro backend (src/kokoro/gpu_backend.rs) ------------------------------
 
 // The AdaIN+Snake part of KokoroGpuBackend for the ROCm device: Buf = GpuBuffer.

@@ -574,6 +574,77 @@ void test_kokoro_tail(const RocmDevice& dev, const RocmKernels& k) {
   report("tail: istft_gpu", err2, 1e-5);
 }
 
+// The decoder MLP GEMVs through the buffer-level mirror: fc1 + bias + GLU and
+// fc2 + residual + LN at a small Moonshine-like shape, against float64 host
+// sums of the dequantised weights (f16 outputs: 2e-3 of max(|ref|, 1)).
+void test_gemv_q8(const RocmDevice& dev, const RocmKernels& k) {
+  const size_t K = 96, N = 64;  // fc1: K -> 2N (GLU to N); fc2: N -> K
+  std::vector<uint16_t> x(K), x2(N);
+  for (size_t i = 0; i < K; ++i) x[i] = f2h(std::sin(0.3f * (float)i));
+  std::vector<uint32_t> qs1(K * 2 * N / 4), qs2(N * K / 4);
+  std::vector<uint16_t> sc1(K / 32 * 2 * N), sc2(N / 32 * K), lnw(K);
+  uint32_t st = 12345u;
+  auto rnd = [&]() { st = st * 1664525u + 1013904223u; return st; };
+  for (auto& w : qs1) w = rnd();
+  for (auto& w : qs2) w = rnd();
+  for (size_t i = 0; i < sc1.size(); ++i) sc1[i] = f2h(0.002f * (1 + (float)(i % 7)));
+  for (size_t i = 0; i < sc2.size(); ++i) sc2[i] = f2h(0.002f * (1 + (float)(i % 5)));
+  for (size_t i = 0; i < K; ++i) lnw[i] = f2h(1.0f + 0.01f * (float)(i % 9));
+  std::vector<float> bias(2 * N), res(K);
+  for (size_t i = 0; i < 2 * N; ++i) bias[i] = 0.1f * std::cos((float)i);
+  for (size_t i = 0; i < K; ++i) res[i] = std::sin(0.11f * (float)i);
+  auto wq = [](const std::vector<uint32_t>& qs, const std::vector<uint16_t>& sc, size_t NW, size_t kk, size_t j) {
+    const int8_t q = (int8_t)((qs[kk * (NW / 4) + j / 4] >> (8 * (j % 4))) & 0xff);
+    return (double)q * h2f(sc[(kk / 32) * NW + j]);
+  };
+  Tensor X = Tensor::from_host(dev, x.data(), {K}, DType::F16);
+  Tensor Q1 = Tensor::from_host(dev, qs1.data(), {qs1.size()}, DType::U32);
+  Tensor S1 = Tensor::from_host(dev, sc1.data(), {sc1.size()}, DType::F16);
+  Tensor B1 = Tensor::from_host(dev, bias.data(), {2 * N}, DType::F32);
+  Tensor H = Tensor::empty(dev, {N}, DType::F16);
+  enc_gemv_q8_bias_glu(dev.stream(), k, X.buffer(), Q1.buffer(), S1.buffer(), B1.buffer(), H.buffer(), K, N);
+  dev.synchronize();
+  const std::vector<uint16_t> h = H.to_vec<uint16_t>();
+  double err = 0;
+  for (size_t j = 0; j < N; ++j) {
+    double up = bias[j], gate = bias[N + j];
+    for (size_t kk = 0; kk < K; ++kk) {
+      up += (double)h2f(x[kk]) * wq(qs1, sc1, 2 * N, kk, j);
+      gate += (double)h2f(x[kk]) * wq(qs1, sc1, 2 * N, kk, N + j);
+    }
+    err = std::max(err, scaled(h2f(h[j]), gate / (1 + std::exp(-gate)) * up));
+  }
+  report("enc_gemv_q8_bias_glu", err, 2e-3);
+  Tensor Q2 = Tensor::from_host(dev, qs2.data(), {qs2.size()}, DType::U32);
+  Tensor S2 = Tensor::from_host(dev, sc2.data(), {sc2.size()}, DType::F16);
+  Tensor RS = Tensor::from_host(dev, res.data(), {K}, DType::F32);
+  Tensor LW = Tensor::from_host(dev, lnw.data(), {K}, DType::F16);
+  Tensor OF = Tensor::empty(dev, {K}, DType::F32);
+  Tensor NM = Tensor::empty(dev, {K}, DType::F16);
+  enc_gemv_q8_resadd_ln(dev.stream(), k, H.buffer(), Q2.buffer(), S2.buffer(), RS.buffer(), OF.buffer(), LW.buffer(),
+                        NM.buffer(), N, K, 1e-5f);
+  dev.synchronize();
+  const std::vector<float> of = OF.to_vec<float>();
+  const std::vector<uint16_t> nm = NM.to_vec<uint16_t>();
+  std::vector<double> hv(K);
+  double err_h = 0, mean = 0, var = 0;
+  for (size_t j = 0; j < K; ++j) {
+    double acc = 0;
+    for (size_t kk = 0; kk < N; ++kk) acc += (double)h2f(h[kk]) * wq(qs2, sc2, K, kk, j);
+    hv[j] = (double)h2f(f2h((float)acc)) + res[j];
+    err_h = std::max(err_h, scaled(of[j], hv[j]));
+    mean += hv[j];
+  }
+  mean /= (double)K;
+  for (size_t j = 0; j < K; ++j) var += (hv[j] - mean) * (hv[j] - mean);
+  var /= (double)K;
+  double err_n = 0;
+  for (size_t j = 0; j < K; ++j)
+    err_n = std::max(err_n, scaled(h2f(nm[j]), (hv[j] - mean) / std::sqrt(var + 1e-5) * h2f(lnw[j])));
+  report("enc_gemv_q8_resadd_ln h", err_h, 2e-3);
+  report("enc_gemv_q8_resadd_ln norm", err_n, 2e-3);
+}
+
 }  // namespace
 
 int main() {
@@ -587,6 +658,7 @@ int main() {
     test_adain_snake_f16(dev, k, 128, 11281, "adain_snake (f16) C=128 T=11281");
     test_snake_f16(dev, k, 16, 3001);
     test_kokoro_tail(dev, k);
+    test_gemv_q8(dev, k);
     test_layernorm_std_f32in(dev, k);
     test_layernorm_unit_offset_and_bare(dev, k);
     test_elementwise(dev, k);
