@@ -310,21 +310,43 @@ NSR_DEV float sum_lanes8(float v) {
   return v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
 }
 
-NSR_DEV void emit_row_block(const nsr_float4& o, int t, int tb, int T_out, int l32, bool row_ok, float* dst) {
+/* All eight row blocks of a wave's tile at once (m = 0..1, q = 0..3: row
+ * co_lane + 32 m + 8 q), so the eight cross-lane sums are in flight together
+ * and the block's column count is divided out once. */
+NSR_DEV void emit_rows8(const nsr_float4 (&ov)[2][4], int t, int tb, int T_out, int l32, int co_lane, int C_out,
+                        int64_t row0, int nblk, int blk, float* part) {
   const int nv = max(0, min(4, T_out - t));
   const float n = (float)max(0, min(32, T_out - tb)); /* valid columns of the block */
-  float s = 0.f;
+  const float inv_n = 1.0f / fmaxf(n, 1.f);
+  float mean[8], m2[8];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) s += e < nv ? o[e] : 0.f;
-  const float mean = sum_lanes8(s) / fmaxf(n, 1.f);
-  float qv = 0.f;
+  for (int i = 0; i < 8; ++i) {
+    float s = 0.f;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float d = o[e] - mean;
-    qv += e < nv ? d * d : 0.f;
+    for (int e = 0; e < 4; ++e) s += e < nv ? ov[i >> 2][i & 3][e] : 0.f;
+    mean[i] = s;
   }
-  const float m2 = sum_lanes8(qv);
-  if (row_ok && l32 < 4 && n > 0.f) *(nsr_float2*)dst = nsr_float2{mean, m2};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) mean[i] = sum_lanes8(mean[i]) * inv_n;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float qv = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float d = ov[i >> 2][i & 3][e] - mean[i];
+      qv += e < nv ? d * d : 0.f;
+    }
+    m2[i] = qv;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m2[i] = sum_lanes8(m2[i]);
+  if (l32 < 4 && n > 0.f) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int co = co_lane + 32 * (i >> 2) + 8 * (i & 3);
+      if (co < C_out) *(nsr_float2*)(part + 2 * ((row0 + co) * nblk + blk)) = nsr_float2{mean[i], m2[i]};
+    }
+  }
 }
 
 template <bool FUSED, bool RESID, int NU, bool STATS = false>
@@ -551,6 +573,7 @@ NSR_DEV void conv_rw_body(const nsr_conv_args& a) {
       __syncthreads(); /* done with this tile's input */
       if (n < cnt) {
         const nsr_rsrc orr = make_rsrc_uniform(a.out + (int64_t)b * a.C_out * a.T_out, obytes);
+        nsr_float4 ov[STATS ? 2 : 1][STATS ? 4 : 1];
 #pragma unroll
         for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -573,13 +596,11 @@ NSR_DEV void conv_rw_body(const nsr_conv_args& a) {
             if (t < a.T_out) /* T_out % 4 == 0: t < T_out covers t + 3 */
               __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(nsr_uint4, o), orr,
                                                      (co * (uint32_t)a.T_out + (uint32_t)t) * 4u, 0, 0);
-            if constexpr (STATS) {
-              const int nblk = (a.T_out + 31) >> 5;
-              const int64_t row = (int64_t)b * a.C_out + (int64_t)min((int)co, a.C_out - 1);
-              emit_row_block(o, t, t0 + wt * 32, a.T_out, l32, (int)co < a.C_out,
-                             a.row_part + 2 * (row * nblk + ((t0 + wt * 32) >> 5)));
-            }
+            if constexpr (STATS) ov[m][q] = o;
           }
+        if constexpr (STATS)
+          emit_rows8(ov, t, t0 + wt * 32, a.T_out, l32, wco * 64 + 4 * hl + c4, a.C_out, (int64_t)b * a.C_out,
+                     (a.T_out + 31) >> 5, (t0 + wt * 32) >> 5, a.row_part);
       }
       __syncthreads(); /* the next tile's input is staged */
     }
@@ -851,6 +872,7 @@ NSR_DEV void conv_pc_body(const nsr_conv_args& a) {
       }
       if (last_chunk && n < items) {
         const nsr_rsrc orr = make_rsrc_uniform(a.out + (int64_t)b * a.C_out * a.T_out, obytes);
+        nsr_float4 ov[STATS ? 2 : 1][STATS ? 4 : 1];
 #pragma unroll
         for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -872,13 +894,11 @@ NSR_DEV void conv_pc_body(const nsr_conv_args& a) {
             if (t < a.T_out)
               __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(nsr_uint4, o), orr,
                                                      ((uint32_t)co * (uint32_t)a.T_out + (uint32_t)t) * 4u, 0, 0);
-            if constexpr (STATS) {
-              const int nblk = (a.T_out + 31) >> 5;
-              const int64_t row = (int64_t)b * a.C_out + (int64_t)min(co, a.C_out - 1);
-              emit_row_block(o, t, t0 + wt * 32, a.T_out, l32, co < a.C_out,
-                             a.row_part + 2 * (row * nblk + ((t0 + wt * 32) >> 5)));
-            }
+            if constexpr (STATS) ov[m][q] = o;
           }
+        if constexpr (STATS)
+          emit_rows8(ov, t, t0 + wt * 32, a.T_out, l32, co0 + wco * 64 + 4 * hl + c4, a.C_out, (int64_t)b * a.C_out,
+                     (a.T_out + 31) >> 5, (t0 + wt * 32) >> 5, a.row_part);
       }
       __syncthreads(); /* the next item's input is staged */
     }
