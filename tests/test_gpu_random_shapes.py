@@ -328,3 +328,37 @@ def test_rope_qk_cache_random(i):
     assert_bitexact(_bits(ckd), ckr, "cache_k")
     if with_v:
         assert_bitexact(_bits(cvd), cvr, "cache_v")
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_conv_chain_random(i):
+    """Chained ResBlock stages at random shapes (every conv kernel family,
+    including rows that are not 16-byte aligned): stage output bit-identical
+    to the unchained kernel, row statistics against float64 of that output,
+    and the second stage with handed-over statistics against the unchained
+    second stage."""
+    from .test_gpu_conv_chain import _check_stats
+
+    g = _cases(12)[i]
+    B, C, _, K, dil, T, _, _ = _conv_shape(g, square=True)
+    pad = (K - 1) * dil // 2
+    if T + 2 * pad - dil * (K - 1) < 1:
+        pad = (K - 1) * dil
+    say("conv chain random", B, C, T, K, dil, pad)
+    x = (g.standard_normal((B, C, T)) * 1.5 + 0.3).astype(np.float32)
+    p = lambda *sh: torch.from_numpy((g.standard_normal(sh) * 0.1).astype(np.float32)).cuda()  # noqa: E731
+    g1, b1, g2, b2 = p(B, C), p(B, C), p(B, C), p(B, C)
+    a1 = torch.from_numpy(g.uniform(0.5, 1.5, C).astype(np.float32)).cuda()
+    a2 = torch.from_numpy(g.uniform(0.5, 1.5, C).astype(np.float32)).cuda()
+    w1 = abi.conv1d_pack_f16(torch.from_numpy((g.standard_normal((C, C, K)) * 0.05).astype(np.float16)).cuda())
+    w2 = abi.conv1d_pack_f16(torch.from_numpy((g.standard_normal((C, C, K)) * 0.05).astype(np.float16)).cuda())
+    bb = torch.from_numpy(g.standard_normal(C).astype(np.float16)).cuda()
+    xt = torch.from_numpy(x).cuda()
+    h, s_h = abi.adain_snake_conv1d_chain(xt, g1, b1, a1, w1, bb, padding=pad, dilation=dil)
+    h_ref = abi.adain_snake_conv1d(xt, g1, b1, a1, w1, bb, padding=pad, dilation=dil)
+    assert_bitexact(h.cpu().numpy(), h_ref.cpu().numpy(), "stage 1 output")
+    _check_stats(h, s_h, 1e-5, "stage 1 statistics")
+    y, _ = abi.adain_snake_conv1d_chain(h, g2, b2, a2, w2, bb, x_stats=s_h, want_stats=False, padding=pad,
+                                        dilation=dil)
+    y_ref = abi.adain_snake_conv1d(h_ref, g2, b2, a2, w2, bb, padding=pad, dilation=dil)
+    assert_close(y.cpu().numpy(), y_ref.cpu().numpy(), RTOL_F32, "stage 2 with handed-over statistics")
