@@ -4,20 +4,32 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workloads c1,c2,...]
 
 A step is one call of a fused kernel on one batch of synthetic input already
-resident in HBM. The headline workload (`value`) is configs[1], the partial
-rotary f32 q,k [1,8,1024,64], with cos/sin read from a host-built f32 RoPE
-table as the reference's GPU decoder does (src/moonshine/gpu_decoder.rs:
-326-340; workload c1t). The in-kernel sincos variant (c1) and every other
-config (c0..c4b) are measured and reported under `per_config`.
+resident in HBM. The headline workload (`value`) is configs[4], the largest
+configuration: AdaIN1d + Snake f32 x[8,128,115200] (workload c4b, the
+dominant kernel by bytes), with configs[4]'s other kernel, residual add +
+LayerNorm + GELU bf16 x,res [32,750,1024] (c4a), reported alongside in
+`config`. Every other config (c0..c3) and the next-row workloads are
+measured and reported under `per_config`.
 
 Timing: W untimed warm-up calls, then the stream is held by a short spin
 kernel while the K timed calls are enqueued, so the GPU runs them back to
 back and the timing is of the GPU, not the Python launch path. HIP events
 on the launch stream bracket the K calls; `us_per_call` is their elapsed
-time / K, the average launch duration (rocprofv3's kernel trace of the same
-run gives the same per-kernel average). Input/output buffer sets rotate so the footprint is
->= 512 MB (twice the 256 MB Infinity Cache): the timed calls read HBM, not
-MALL. `warm_*` figures repeat one buffer set and are labelled as such.
+time / K, the average launch duration. Input/output buffer sets rotate so
+the footprint is >= 512 MB (twice the 256 MB Infinity Cache): the timed
+calls read HBM, not MALL. `warm_*` figures repeat one buffer set and are
+labelled as such. `host_us_per_call` is the host time to enqueue one call
+from Python (ctypes + the C-ABI runtime + hipModuleLaunchKernel).
+
+Floors, measured in the same run through the same runtime: an empty kernel
+(`empty`) and plain 128-bit device copies (`copy_<form>_<config>`) moving
+exactly each config's algorithmic bytes (half read, half written), in two
+grid forms (`f`: one 16-byte chunk per lane; `p4`/`p8`: a persistent
+8 x #CU grid with 4 or 8 chunks per lane in flight). Each config's entry
+carries `copy_floor_us` (the fastest copy of its size) and `frac_of_copy`.
+rocprofv3's kernel trace adds about 1 us to kernels of a few us (it spaces
+dispatches apart); for the headline kernel its average agrees with
+`us_per_call` (profiles/).
 
 The CPU baseline is the oracle's C restatement of the reference CPU path
 (oracle/nsr_oracle.c) timed on this host on a bounded sample.
@@ -28,7 +40,6 @@ import argparse
 import json
 import math
 import os
-import statistics
 import sys
 import time
 from pathlib import Path
@@ -37,6 +48,14 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+CONFIG_WORKLOADS = ["c4b", "c4a", "c0", "c1", "c1t", "c2", "c3", "c2u", "c2h"]
+NEXT_WORKLOADS = ["dec", "dec2", "attn", "attnx", "q8fc1", "q8fc2", "q8fc1r", "q8fc2r", "q8conv", "kconv3", "kconv11",
+                  "kconv3u", "kchain3", "kchain11", "mrf", "istft"]
+# same-size copies: algorithmic bytes of the config each one calibrates
+COPY_SIZES = {"c1t": 8519680, "c3": 8642560, "c2": 19666944, "c4a": 196616192, "c4b": 943727104}
+COPY_FOR = {"c1": "c1t", "c1t": "c1t", "c3": "c3", "c2": "c2", "c2u": "c2", "c4a": "c4a", "c4b": "c4b"}
+FLOOR_WORKLOADS = ["empty"] + [f"copy_{f}_{c}" for c in COPY_SIZES for f in ("f", "p4", "p8")]
+DEFAULT_WORKLOADS = CONFIG_WORKLOADS + FLOOR_WORKLOADS + NEXT_WORKLOADS
 MALL_DEFEAT_BYTES = 512 << 20
 METRIC = "achieved HBM GB/s (% of MI355X peak) and µs/call per fused kernel"
 
@@ -46,11 +65,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workloads",
-                    default="c0,c1,c1t,c2,c3,c4a,c4b,c2u,c2h,dec,dec2,attn,attnx,q8fc1,q8fc2,q8fc1r,q8fc2r,q8conv,kconv3,"
-                            "kconv11,kconv3u,kchain3,kchain11,mrf,istft",
-                    help="comma list of c0,c1,c1t,c2,c3,c4a,c4b,c2u,c2h,dec,dec2,attn,attnx,q8fc1,q8fc2,q8fc1r,q8fc2r,"
-                         "q8conv,kconv3,kconv11,kconv3u,kchain3,kchain11,mrf,istft,copy")
+    ap.add_argument("--workloads", default=",".join(DEFAULT_WORKLOADS),
+                    help="comma list of " + ",".join(DEFAULT_WORKLOADS) + ",copy")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline (0 = skip)")
     ap.add_argument("--no-rotate", action="store_true", help="one buffer set (warm MALL) for all timings")
     return ap.parse_args()
@@ -84,6 +100,32 @@ def build_workload(name):
         if a.dtype == np.uint32:
             return torch.from_numpy(a.view(np.int32)).to(dev)
         return torch.from_numpy(a).to(dev)
+
+    if name == "empty":
+        def make_set(_):
+            return {}
+
+        def launch(s):
+            abi.check(L.nsr_calib_empty(stream()))
+
+        return Workload(name, "empty kernel (one launch on the stream)", 0, 1 << 30, make_set, launch,
+                        "nsrk_calib_empty", "-")
+
+    if name.startswith("copy_"):
+        _, form, cfg = name.split("_")
+        nbytes = COPY_SIZES[cfg] // 32 * 16  # half read, half written, in 16-byte chunks
+        fi = {"f": 0, "p4": 1, "p8": 2}[form]
+
+        def make_set(_):
+            return {"s": torch.ones(nbytes // 4, dtype=torch.float32, device=dev),
+                    "d": torch.empty(nbytes // 4, dtype=torch.float32, device=dev)}
+
+        def launch(s):
+            abi.check(L.nsr_calib_copy(s["s"].data_ptr(), s["d"].data_ptr(), nbytes, fi, 0, stream()))
+
+        kern = {"f": "nsrk_calib_copy_flat", "p4": "nsrk_calib_copy_p4", "p8": "nsrk_calib_copy_p8"}[form]
+        return Workload(name, f"device copy of {2 * nbytes} bytes ({nbytes} read + {nbytes} written), form {form} "
+                        f"(the bytes of {cfg})", 2 * nbytes, 2 * nbytes, make_set, launch, kern, "u8")
 
     if name == "copy":
         n = 64 << 20  # 256 MiB of f32: plain device copy, the PMC calibration reference
@@ -146,7 +188,7 @@ def build_workload(name):
             abi.check(L.nsr_adain_snake_f32(s["x"].data_ptr(), g.data_ptr(), b.data_ptr(), a.data_ptr(), 0, gs, gs,
                                             s["o"].data_ptr(), B, C, TT, 1e-5, stream()))
 
-        kern = "nsrk_adain_row_b256_v5_l0" if name == "c2" else "nsrk_adain_row_b512_v44_l14"
+        kern = "nsrk_adain_row_b256_v5_l0" if name == "c2" else "nsrk_adain_row_b512_v40_l18"
         return Workload(name, f"AdaIN1d+Snake f32 x[{B},{C},{TT}]", configs.algorithmic_bytes(name),
                         2 * x0.numel() * 4, make_set, launch, kern, "f32")
 
@@ -495,6 +537,8 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms):
         w.launch(sets[i % nsets])
     torch.cuda.synchronize()
 
+    host = []
+
     def held(enqueue, n, per_call_ms):
         """Hold the stream with a spin kernel while `enqueue` issues n calls,
         so the GPU then runs them back to back. Returns True when the host
@@ -507,25 +551,8 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms):
         enqueue()
         host_ms = (time.perf_counter() - h0) * 1e3
         torch.cuda.synchronize()
+        host.append(host_ms * 1e3 / n)
         return host_ms < 0.8 * hold_ms
-
-    def run(order):
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in order]
-        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-
-        def enqueue():
-            t0.record()
-            for (a, b), i in zip(ev, order):
-                a.record()
-                w.launch(sets[i])
-                b.record()
-            t1.record()
-
-        for per_call in (0.15, 0.6):
-            if held(enqueue, len(order), per_call):
-                break
-        per = [a.elapsed_time(b) * 1e3 for a, b in ev]  # us
-        return per, t0.elapsed_time(t1) * 1e3 / len(order)
 
     def run_plain(order):
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -536,7 +563,7 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms):
                 w.launch(sets[i])
             t1.record()
 
-        for per_call in (0.1, 0.4):
+        for per_call in (0.1, 0.4, 1.6):
             if held(enqueue, len(order), per_call):
                 break
         return t0.elapsed_time(t1) * 1e3 / len(order)
@@ -544,7 +571,6 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms):
     rotating = [i % nsets for i in range(steps)]
     cold_us = run_plain(rotating)            # timed region: K back-to-back calls
     warm_us = run_plain([0] * steps)         # same buffers: MALL-warm, labelled
-    ev_per, _ = run(rotating)                # event pair around each call
     del sets
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
@@ -562,9 +588,7 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms):
         "warm_us_per_call": round(warm_us, 3),
         "warm_GBs": round(gbs(warm_us), 1),
         **({"TFLOPs": round(w.flops / (cold_us * 1e-6) / 1e12, 2)} if w.flops else {}),
-        # an event pair around each single call adds the runtime's event
-        # overhead (a few us) to small kernels; reported for reference only
-        "event_pair_us_median": round(statistics.median(ev_per), 3),
+        "host_us_per_call": round(min(host), 2),
     }
 
 
@@ -680,25 +704,42 @@ def main():
         print(f"[bench] {nm}: {results[nm]['us_per_call']} us/call, {results[nm]['GBs']} GB/s "
               f"({100 * results[nm]['frac_of_peak']:.1f}% of peak)", file=sys.stderr, flush=True)
 
-    head = results.get("c1t") or results.get("c1") or next(iter(results.values()))
+    # each config against the fastest same-size copy of this run
+    for nm, r in results.items():
+        cfg = COPY_FOR.get(nm)
+        copies = [results[f"copy_{f}_{cfg}"]["us_per_call"] for f in ("f", "p4", "p8")
+                  if f"copy_{f}_{cfg}" in results] if cfg else []
+        if copies:
+            r["copy_floor_us"] = min(copies)
+            r["frac_of_copy"] = round(min(copies) / r["us_per_call"], 4)
+
+    head_name = "c4b" if "c4b" in results else next(iter(results))
+    head = results[head_name]
     cpu = None
     if args.cpu_seconds > 0:
-        per_cfg, ncores = cpu_baseline(args.cpu_seconds, [n for n in names if n not in ("c1t", "copy")])
-        h = per_cfg.get("c1") or next(iter(per_cfg.values()))  # c1t's CPU path is c1's
+        per_cfg, ncores = cpu_baseline(args.cpu_seconds, [n for n in names if n in CONFIG_WORKLOADS and n != "c1t"])
+        h = per_cfg.get(head_name) or next(iter(per_cfg.values()))
         cpu = {"value": h["threads_1"]["GBs"], "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": "oracle C restatement of the reference CPU path (apply_rotary_pos_emb, "
-                         "src/moonshine/decoder.rs:85-183) on the full configs[1] input, 1 thread; "
+               "sample": "oracle C restatement of the reference CPU path (adain + snake_activation_tensor, "
+                         "src/kokoro/decoder.rs:1416-1428,1471-1476) on 8 of configs[4]'s 1024 AdaIN rows "
+                         "(x[1,8,115200]), 1 thread, scaled to the full config; "
                          f"{ncores}-thread and per-config figures under per_config",
                "per_config": per_cfg, "host_cores": ncores}
 
-    traffic = None
+    traffic = {}
     tf = ROOT / "profiles" / "hbm_traffic_bench_workloads.txt"
     if tf.exists():
         for line in tf.read_text().splitlines():
             parts = line.split()
-            if len(parts) >= 2 and parts[0] == head["kernel"]:
-                traffic = int(parts[1])
+            if len(parts) >= 2 and parts[0].startswith("nsrk_") and parts[1].isdigit():
+                traffic[parts[0]] = int(parts[1])
 
+    companion = {}
+    if "c4a" in results and head_name == "c4b":
+        r = results["c4a"]
+        companion = {"c4a": {"workload": r["workload"], "kernel": r["kernel"], "dtype": r["dtype"],
+                             "us_per_call": r["us_per_call"], "GBs": r["GBs"], "frac_of_peak": r["frac_of_peak"],
+                             "traffic": traffic.get(r["kernel"])}}
     line = {
         "metric": METRIC,
         "value": head["GBs"],
@@ -712,11 +753,12 @@ def main():
         "vs_baseline": None,
         "dtype": head["dtype"],
         "data": "synthetic (seeded numpy inputs of the benchmark configs; no model weights needed)",
-        "config": {"workload": "configs[1]: " + head["workload"], "buffer_sets": head["buffer_sets"],
-                   "footprint_MB": head["footprint_MB"], "parallelism": "single GPU"},
+        "config": {"workload": ("configs[4]: " if head_name == "c4b" else "") + head["workload"],
+                   "buffer_sets": head["buffer_sets"], "footprint_MB": head["footprint_MB"],
+                   "parallelism": "single GPU", **({"alongside": companion} if companion else {})},
         "roofline": {"bound": "hbm", "achieved": head["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": head["frac_of_peak"], "traffic": traffic, "kernel": head["kernel"],
-                     "us_per_call": head["us_per_call"]},
+                     "frac": head["frac_of_peak"], "traffic": traffic.get(head["kernel"]), "kernel": head["kernel"],
+                     "us_per_call": head["us_per_call"], "copy_floor_us": head.get("copy_floor_us")},
         "cpu_baseline": cpu,
         "per_config": results,
     }

@@ -80,8 +80,9 @@ nsr_status nsr_init(const char* code_object_dir);
 /* Message describing the last failure on this thread ("" if none). */
 const char* nsr_last_error(void);
 
-/* Number of kernels in the loaded code object for the current device (0 if
- * not loaded). Used by tests to check the module is complete. */
+/* Number of kernels resolved for the current device (0 if its code objects
+ * are not loaded): every kernel the library launches is resolved once, when
+ * the device's code objects load. Used by tests to check the set is complete. */
 int nsr_kernel_count(void);
 
 /* ---- LayerNorm family ---------------------------------------------------- */
@@ -188,14 +189,17 @@ nsr_status nsr_kv_cache_append(const void* new_kv, void* cache, nsr_dtype dtype,
 /* ---- AdaIN1d + Snake ------------------------------------------------------ */
 
 /* For x [B, C, T] f32, per (b, c) row:
- *   mean, var = biased statistics over T (two-pass accuracy, f32)
+ *   mean, var = biased statistics over T
  *   y   = (1 + gamma[b,c]) * (x - mean) / sqrt(var + eps) + beta[b,c]
  *   out = y + sin(alpha[c]*y)^2 * (1 / (alpha[c] + 1e-9))
  * gamma/beta/alpha have param_dtype F32 or F16. gamma_bstride/beta_bstride:
  * elements between batches of gamma/beta (0 = shared over the batch, C =
  * per batch). alpha is per channel [C].
- * x is read from HBM once while a row fits on chip (T up to about 150k
- * elements); longer rows use a two-kernel stats + apply path.
+ * While a row fits on chip (16-byte aligned rows up to T = 118784, other rows
+ * up to about 65k elements) x is read from HBM once and the statistics are
+ * two passes over the on-chip row in f32 (the mean, then centred sums that
+ * also correct the mean). Longer rows take a kernel that reads each row
+ * twice (f64 sums, then the output; no scratch memory). */
  * Replaces adain (src/kokoro/decoder.rs:1416-1428) followed by
  * snake_activation_tensor (:1471-1476), and
  * KokoroGpuBackend::adain_snake_f32 (src/kokoro/gpu_backend.rs:181-185,
@@ -520,6 +524,20 @@ nsr_status nsr_gemv_q8_t4_resadd_ln(const void* x, nsr_dtype x_dtype, const uint
                                     float* out_f32, const void* ln_weight, nsr_dtype w_dtype,
                                     void* norm, nsr_dtype norm_dtype, int64_t K, int64_t dim,
                                     float eps, nsr_stream_t stream);
+
+/* ---- Measurement floors ---------------------------------------------------- */
+
+/* No counterpart in the reference: the benchmark's floors, launched through
+ * the same runtime as every fused kernel.
+ * nsr_calib_empty: one empty kernel (the cost of a launch on the stream).
+ * nsr_calib_copy: device copy of `bytes` (a multiple of 16, src and dst
+ * 16-byte aligned) with 128-bit loads and stores. form 0: one 16-byte chunk
+ * per lane, ceil(bytes / 4096) workgroups of 256; form 1 / 2: persistent,
+ * groups_per_cu x #CU workgroups (0: 8) each keeping 4 / 8 chunks per lane
+ * in flight. */
+nsr_status nsr_calib_empty(nsr_stream_t stream);
+nsr_status nsr_calib_copy(const void* src, void* dst, int64_t bytes, int form, int groups_per_cu,
+                          nsr_stream_t stream);
 
 #ifdef __cplusplus
 }

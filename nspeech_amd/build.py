@@ -30,7 +30,8 @@ ARCH = "gfx950"
 
 # Kernel units: kernels/<unit>.hip -> lib/nsr_<unit>_gfx950.hsaco. The same
 # list is embedded by runtime/nsr_embed.S and searched by nsr_runtime.cpp.
-UNITS = ["q8_0_gather", "layernorm", "rotary", "adain_snake", "elementwise", "gemv_q8", "conv1d", "attention", "istft"]
+UNITS = ["q8_0_gather", "layernorm", "rotary", "adain_snake", "elementwise", "gemv_q8", "conv1d", "attention", "istft",
+         "calib"]
 
 HIP_FLAGS = [
     "--genco",

@@ -9,26 +9,16 @@
  * gamma/beta come per (batch, channel) from the style Linear (precomputed and
  * rounded to f16 for the GPU backend, decoder.rs:966-981), alpha per channel.
  *
- * Row kernel (aligned rows: x, out 16-byte aligned, T % 4 == 0), one
- * workgroup per (b, c) row. The row is read from HBM once, as BLOCK-wide
- * slots of 16-byte chunks: NV slots land in VGPRs (buffer_load_dwordx4 with
- * the slot offset in an SGPR) and NL more go straight to LDS
- * (buffer_load_dwordx4 ... lds). Statistics are a single pass about a shift K
- * (the mean of slot 0, reduced while the other slots are still in flight):
- * s1 = sum(x - K), s2 = sum((x - K)^2), mean = K + s1/T,
- * var = s2/T - (s1/T)^2, accurate when |mean| >> std because K is within a
- * few std of the mean. The apply pass writes out once, so HBM traffic is the
- * algorithmic 8 bytes per element. Chunks past the row end read as 0 through
- * the buffer range check and are masked out of the sums; their stores are
- * dropped by the same check.
+ * Row kernel (aligned rows: x, out 16-byte aligned, T % 4 == 0): the row is
+ * read from HBM once into registers and LDS, its statistics are two passes
+ * over the on-chip copy, and the output is written once: HBM traffic is the
+ * algorithmic 8 bytes per element. Long rows run on a persistent grid that
+ * overlaps the next row's reads with the current row's writes.
  *
- * Measured on MI355X: 512 threads x (44 VGPR + up to 18 LDS slots) beats a
- * 1024-thread workgroup, whose 128-VGPR budget forces spills, and keeps 8
- * waves per CU streaming; x[8,128,115200] runs at ~5.3 TB/s.
- *
- * Unaligned rows take the register-resident kernel at the end (global loads,
- * partial edge chunks per element). Rows longer than the on-chip budget take
- * the split path: a stats kernel (one read) and an apply kernel (second read).
+ * Unaligned rows take the register-resident kernel further down (global
+ * loads, partial edge chunks per element). Rows longer than the on-chip
+ * budget take the long-row kernel at the end: statistics by pairwise
+ * (count, mean, M2) merges over one read, then a second read to apply.
  */
 #include "device_common.h"
 
@@ -87,83 +77,145 @@ NSR_DEV float sum4(nsr_float4 d) { return (d.x + d.y) + (d.z + d.w); }
 
 /* ------------------------------------------------------------ row kernel -- */
 
+/* Rows of a workgroup: row = blockIdx.x, + gridDim.x, ... The host launches
+ * one workgroup per row when several fit on a CU, and a persistent grid of
+ * one workgroup per CU when a row fills a CU's registers and LDS. The row is
+ * held on chip as BLOCK-wide slots of 16-byte chunks: NV slots in VGPRs
+ * (buffer_load_dwordx4 with the slot offset in an SGPR) and NL slots in LDS
+ * (buffer_load_dwordx4 ... lds, each wave's lanes landing in the wave's own
+ * LDS region, which only that wave reads).
+ *
+ * Statistics are two passes over the on-chip row: the mean, then the centred
+ * sums of (x - mean)^2 and (x - mean), the second correcting the f32 mean
+ * (var = (S2 - S1^2 / T) / T, the corrected two-pass form). Chunks past the
+ * row end are masked out of the sums (a VGPR load past the buffer range
+ * returns 0, but a load to LDS past it leaves the LDS slot as it was); their
+ * stores are dropped by the buffer range check.
+ *
+ * The store pass of row r refills each slot with row r + gridDim.x as soon as
+ * the slot's output is stored, so on a CU the reads of the next row overlap
+ * the writes of the current one, and HBM traffic stays the algorithmic
+ * 8 bytes per element (x read once, out written once). */
 template <int BLOCK, int NV, int NL>
 NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
+  NSR_NO_CONTRACT
   constexpr int NW = BLOCK / 64;
   constexpr int NS = NV + NL;
-  static_assert(NS <= 64, "slot mask is 64 bits");
-  typedef typename std::conditional<(NS <= 32), uint32_t, uint64_t>::type mask_t;
-  constexpr int MB = 8 * (int)sizeof(mask_t);
+  /* only the last MK slots may reach past the row end: the host picks NS
+   * with (NS - MK) * BLOCK <= T / 4 */
+  constexpr int MK = NS < 4 ? NS : 4;
   extern __shared__ nsr_float4 lds_x[];
   __shared__ float red[2 * NW];
 
   const int tid = threadIdx.x;
-  const int64_t row = blockIdx.x;
+  int64_t row = blockIdx.x;
   if (row >= a.n_rows) return;
   const int64_t T = a.T;
   const int nch = (int)(T >> 2);
   const uint32_t rbytes = (uint32_t)(T * 4);
   const uint32_t voff = (uint32_t)tid * 16u;
-
-  /* per-row parameters first: their loads are then the oldest outstanding */
-  const int64_t bi = row / a.C;
-  const int64_t ci = row - bi * a.C;
-  const adain_raw pr = adain_params_load(a, pdt, bi, ci);
-
-  const nsr_rsrc xr = make_rsrc(a.x + row * T, rbytes);
-  nsr_float4 v[NV];
-#pragma unroll
-  for (int k = 0; k < NV; ++k) v[k] = buf_load4(xr, voff, (uint32_t)(k * BLOCK * 16));
   /* LDS slots of this wave: base address wave-uniform (an SGPR, M0 per load);
    * lane i of the wave lands at base + 16 i, i.e. at lds_x[m * BLOCK + tid] */
   lds_void* const lw = (lds_void*)(lds_x + __builtin_amdgcn_readfirstlane(tid & ~63));
-#pragma unroll
-  for (int m = 0; m < NL; ++m)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)((char*)lw + m * BLOCK * 16), 16, voff,
-                                             (uint32_t)((NV + m) * BLOCK * 16), 0, 0);
 
-  /* bit k: slot k of this lane lies inside the row */
+  /* slot k of this lane lies inside the row iff k < nvalid (tested for the
+   * last MK slots only; a per-slot lane mask for every slot would be kept in
+   * SGPR pairs across the row loop) */
   const int nvalid = nch > tid ? (nch - tid + BLOCK - 1) / BLOCK : 0;
-  const mask_t valid = nvalid >= MB ? (mask_t)~(mask_t)0 : (mask_t)(((mask_t)1 << nvalid) - 1);
+  auto valid = [&](int k) { return k < NS - MK || k < nvalid; };
   const nsr_float4 zero4 = {0.f, 0.f, 0.f, 0.f};
 
-  /* shift K: mean of slot 0 (the first min(T, 4 BLOCK) elements) */
-  const float n0 = (float)(nch < BLOCK ? 4 * nch : 4 * BLOCK);
-  const float K = block_sum<NW>(sum4(v[0]), red) / n0;
-
-  float s1 = 0.f, s2 = 0.f;
+  /* first row: parameters, then every slot's load */
+  adain_raw pr = adain_params_load(a, pdt, row / a.C, row % a.C);
+  nsr_float4 v[NV];
+  {
+    const nsr_rsrc xr = make_rsrc(a.x + row * T, rbytes);
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const nsr_float4 d = v[k] - K;
-    v[k] = ((valid >> k) & 1) ? d : zero4;
-    s1 += sum4(v[k]);
-    s2 = sumsq4(v[k], s2);
+    for (int k = 0; k < NV; ++k) v[k] = buf_load4(xr, voff, (uint32_t)(k * BLOCK * 16));
+#pragma unroll
+    for (int m = 0; m < NL; ++m)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)((char*)lw + m * BLOCK * 16), 16, voff,
+                                               (uint32_t)((NV + m) * BLOCK * 16), 0, 0);
   }
-  static_for<0, NL>([&](auto mc) {
-    constexpr int m = decltype(mc)::value;
-    NSR_WAIT_VMCNT(NL - 1 - m); /* LDS slot m has landed */
-    nsr_float4 d = lds_x[m * BLOCK + tid] - K;
-    d = ((valid >> (NV + m)) & 1) ? d : zero4;
-    s1 += sum4(d);
-    s2 = sumsq4(d, s2);
-  });
-  block_sum2<NW>(s1, s2, red);
-  const float c = s1 * a.inv_t; /* mean - K */
-  const float var = fmaxf(__builtin_fmaf(-c, c, s2 * a.inv_t), 0.0f);
-  const float rstd = 1.0f / sqrtf(var + a.eps);
-  float gam, bet, alp;
-  adain_params_cvt(pr, pdt, gam, bet, alp);
-  const float A = (gam + 1.0f) * rstd;
-  const float Bc = __builtin_fmaf(-c, A, bet); /* (d - c) A + beta = d A + Bc */
-  const snake_consts sc = make_snake_consts(alp);
 
-  const nsr_rsrc orr = make_rsrc(a.out + row * T, rbytes);
+  while (true) {
+    const int64_t next = row + gridDim.x;
+    const bool more = next < a.n_rows;
+    NSR_WAIT_VMCNT(0); /* every slot of this row has landed (VGPRs and LDS) */
+
+    /* pass 1: mean */
+    float s = 0.f;
 #pragma unroll
-  for (int k = 0; k < NV; ++k) buf_store4(orr, voff, (uint32_t)(k * BLOCK * 16), adain_snake4(v[k], A, Bc, sc));
-#pragma unroll 1
-  for (int m = 0; m < NL; ++m) {
-    const nsr_float4 d = lds_x[m * BLOCK + tid] - K;
-    buf_store4(orr, voff, (uint32_t)((NV + m) * BLOCK * 16), adain_snake4(d, A, Bc, sc));
+    for (int k = 0; k < NV; ++k) s += valid(k) ? sum4(v[k]) : 0.f;
+    /* LDS slots in groups of four: the scheduler would otherwise issue every
+     * slot's read at once and hold NL x 4 more VGPRs */
+    static_for<0, (NL + 3) / 4>([&](auto gc) {
+      constexpr int g = decltype(gc)::value;
+#pragma unroll
+      for (int m = 4 * g; m < (4 * g + 4 < NL ? 4 * g + 4 : NL); ++m)
+        s += valid(NV + m) ? sum4(lds_x[m * BLOCK + tid]) : 0.f;
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    const float mean = block_sum<NW>(s, red) * a.inv_t;
+
+    /* pass 2: centred sums; the VGPR slots keep x - mean (0 outside the row) */
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const nsr_float4 d = v[k] - mean;
+      v[k] = valid(k) ? d : zero4;
+      s1 += sum4(v[k]);
+      s2 = sumsq4(v[k], s2);
+    }
+    static_for<0, (NL + 3) / 4>([&](auto gc) {
+      constexpr int g = decltype(gc)::value;
+#pragma unroll
+      for (int m = 4 * g; m < (4 * g + 4 < NL ? 4 * g + 4 : NL); ++m) {
+        nsr_float4 d = lds_x[m * BLOCK + tid] - mean;
+        d = valid(NV + m) ? d : zero4;
+        s1 += sum4(d);
+        s2 = sumsq4(d, s2);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    block_sum2<NW>(s1, s2, red);
+    const float c = s1 * a.inv_t; /* f32 mean correction */
+    const float var = fmaxf(__builtin_fmaf(-c, s1, s2) * a.inv_t, 0.0f);
+    const float rstd = 1.0f / sqrtf(var + a.eps);
+    float gam, bet, alp;
+    adain_params_cvt(pr, pdt, gam, bet, alp);
+    const float A = (gam + 1.0f) * rstd;
+    const float Bc = __builtin_fmaf(-c, A, bet); /* (d - c) A + beta = d A + Bc */
+    const snake_consts sc = make_snake_consts(alp);
+
+    /* store pass; each slot is refilled with the next row once its output is
+     * issued (a past-the-end row reads nothing: its range is 0 bytes) */
+    if (more) pr = adain_params_load(a, pdt, next / a.C, next % a.C);
+    const nsr_rsrc orr = make_rsrc(a.out + row * T, rbytes);
+    const nsr_rsrc xn = make_rsrc(a.x + (more ? next : row) * T, more ? rbytes : 0u);
+    /* slot offsets are formed from a fresh copy of the lane offset and an
+     * opaque zero each row: as loop invariants the compiler would keep all
+     * NS of them live in registers across the loop */
+    uint32_t vo = voff, so;
+    asm volatile("" : "+v"(vo));
+    asm volatile("s_mov_b32 %0, 0" : "=s"(so));
+    lds_void* lwr = lw;
+    asm volatile("" : "+s"(lwr));
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      buf_store4(orr, vo, (uint32_t)(k * BLOCK * 16), adain_snake4(v[k], A, Bc, sc));
+      v[k] = buf_load4(xn, vo, so + (uint32_t)(k * BLOCK * 16));
+    }
+    static_for<0, NL>([&](auto mc) {
+      constexpr int m = decltype(mc)::value;
+      const nsr_float4 d = lds_x[m * BLOCK + tid] - mean;
+      buf_store4(orr, vo, (uint32_t)((NV + m) * BLOCK * 16), adain_snake4(d, A, Bc, sc));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xn, (lds_void*)((char*)lwr + m * BLOCK * 16), 16, vo,
+                                               so + (uint32_t)((NV + m) * BLOCK * 16), 0, 0);
+      if constexpr (m % 2 == 1) __builtin_amdgcn_sched_barrier(0);
+    });
+    if (!more) break;
+    row = next;
   }
 }
 
@@ -196,16 +248,16 @@ NSR_ADAIN_ROW(512, 32, 0)
 NSR_ADAIN_ROW(512, 36, 0)
 NSR_ADAIN_ROW(512, 40, 0)
 NSR_ADAIN_ROW(512, 44, 0)
-/* long rows: 44 VGPR slots + 2..18 LDS slots (T <= 126976; 18 slots = 144 KiB of LDS) */
-NSR_ADAIN_ROW(512, 44, 2)
-NSR_ADAIN_ROW(512, 44, 4)
-NSR_ADAIN_ROW(512, 44, 6)
-NSR_ADAIN_ROW(512, 44, 8)
-NSR_ADAIN_ROW(512, 44, 10)
-NSR_ADAIN_ROW(512, 44, 12)
-NSR_ADAIN_ROW(512, 44, 14)
-NSR_ADAIN_ROW(512, 44, 16)
-NSR_ADAIN_ROW(512, 44, 18)
+/* long rows: 40 VGPR slots + 2..18 LDS slots (T <= 118784; 18 slots = 144 KiB of LDS) */
+NSR_ADAIN_ROW(512, 40, 2)
+NSR_ADAIN_ROW(512, 40, 4)
+NSR_ADAIN_ROW(512, 40, 6)
+NSR_ADAIN_ROW(512, 40, 8)
+NSR_ADAIN_ROW(512, 40, 10)
+NSR_ADAIN_ROW(512, 40, 12)
+NSR_ADAIN_ROW(512, 40, 14)
+NSR_ADAIN_ROW(512, 40, 16)
+NSR_ADAIN_ROW(512, 40, 18)
 
 /* ------------------------------------------------ unaligned resident rows -- */
 
@@ -218,6 +270,7 @@ NSR_ADAIN_ROW(512, 44, 18)
  * registers (mean, then centred sums with the corrected two-pass term). */
 template <int BLOCK, int NV>
 NSR_DEV void adain_resident_u(const nsr_adain_args& a, int pdt) {
+  NSR_NO_CONTRACT
   constexpr int NW = BLOCK / 64;
   __shared__ float red[2 * NW];
   const int tid = threadIdx.x;
@@ -340,6 +393,7 @@ NSR_DEV void st16g(nsr_gh* p, nsr_uint4 v) {
 
 template <int BLOCK, int NV>
 NSR_DEV void adain_row_f16(const nsr_adain_h_args& a, int pdt) {
+  NSR_NO_CONTRACT
   constexpr int NW = BLOCK / 64;
   __shared__ float red[2 * NW];
   const int tid = threadIdx.x;
@@ -462,98 +516,146 @@ NSR_ADAIN_F16(512, 24)
 NSR_ADAIN_F16(512, 28)
 NSR_ADAIN_F16(512, 32)
 
-/* ------------------------------------------------------------ split path -- */
+/* ------------------------------------------------ row statistics, long rows -- */
 
-/* Stats: one 1024-thread workgroup per row, single read. Sums are taken about
- * a shift K (the mean of the row's first up-to-1024 elements), which keeps
- * S2 - S1^2/n free of cancellation when |mean| >> std. Writes (mean, rstd). */
-extern "C" __global__ void __launch_bounds__(1024) nsrk_adain_stats(const nsr_adain_args a) {
-  __shared__ float red[16];
+/* Sum and sum of squares of one row over 1024 lanes in f64, one HBM read:
+ * 16-byte loads (four in flight per lane) when VEC4 (row 16-byte aligned,
+ * T % 4 == 0), else element loads. In f64, var = S2/T - (S1/T)^2 keeps
+ * about 16 - log10(mean^2 / var) significant digits, far more than f32
+ * output needs for any |mean| / std below 1e4. `red` holds 32 doubles. */
+template <bool VEC4>
+NSR_DEV void row_sums64(const float* xr, int64_t T, double* red, double& s1, double& s2) {
+  NSR_NO_CONTRACT
+  double a1 = 0.0, a2 = 0.0;
   const int tid = threadIdx.x;
-  const int64_t row = blockIdx.x;
-  const int64_t T = a.T;
-  const float* xr = a.x + row * T;
-  const int64_t nk = T < 1024 ? T : 1024;
-  const float k0 = block_sum<16>(tid < nk ? xr[tid] : 0.f, red) / (float)nk;
-  float s1 = 0.f, s2 = 0.f;
-  for (int64_t i = tid; i < T; i += 1024) {
-    const float d = xr[i] - k0;
-    s1 += d;
-    s2 = __builtin_fmaf(d, d, s2);
-  }
-  s1 = block_sum<16>(s1, red);
-  s2 = block_sum<16>(s2, red);
-  if (tid == 0) {
-    const double n = (double)T;
-    const double m1 = (double)s1 / n;
-    double var = (double)s2 / n - m1 * m1;
-    if (var < 0.0) var = 0.0;
-    a.stats[2 * row] = (float)((double)k0 + m1);
-    a.stats[2 * row + 1] = 1.0f / sqrtf((float)var + a.eps);
-  }
-}
-
-/* Statistics of 16-byte aligned rows (T % 4 == 0): 16-byte loads, four in
- * flight per thread per iteration; same shift and f64 finish as above. */
-extern "C" __global__ void __launch_bounds__(1024) nsrk_adain_stats4(const nsr_adain_args a) {
-  __shared__ float red[16];
-  const int tid = threadIdx.x;
-  const int64_t row = blockIdx.x;
-  const int64_t T = a.T, n4 = T >> 2;
-  const float* xr = a.x + row * T;
-  const int64_t nk = T < 1024 ? T : 1024;
-  const float k0 = block_sum<16>(tid < nk ? xr[tid] : 0.f, red) / (float)nk;
-  float s1[4] = {0.f, 0.f, 0.f, 0.f}, s2[4] = {0.f, 0.f, 0.f, 0.f};
-  int64_t i = tid;
-  for (; i + 3 * 1024 < n4; i += 4 * 1024) {
-    nsr_float4 v[4];
+  if constexpr (VEC4) {
+    const int64_t n4 = T >> 2;
+    int64_t i = tid;
+    for (; i + 3 * 1024 < n4; i += 4 * 1024) {
+      nsr_float4 v[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = ldf4(xr + 4 * (i + u * 1024));
+      for (int u = 0; u < 4; ++u) v[u] = ldf4(xr + 4 * (i + u * 1024));
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const nsr_float4 d = v[u] - k0;
-      s1[u] += (d.x + d.y) + (d.z + d.w);
-      s2[u] = __builtin_fmaf(d.x, d.x, __builtin_fmaf(d.y, d.y, __builtin_fmaf(d.z, d.z, __builtin_fmaf(d.w, d.w, s2[u]))));
+      for (int u = 0; u < 4; ++u) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const double x = (double)v[u][e];
+          a1 += x;
+          a2 = __builtin_fma(x, x, a2);
+        }
+      }
+    }
+    for (; i < n4; i += 1024) {
+      const nsr_float4 v = ldf4(xr + 4 * i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const double x = (double)v[e];
+        a1 += x;
+        a2 = __builtin_fma(x, x, a2);
+      }
+    }
+  } else {
+    for (int64_t i = tid; i < T; i += 1024) {
+      const double x = (double)__builtin_nontemporal_load(xr + i);
+      a1 += x;
+      a2 = __builtin_fma(x, x, a2);
     }
   }
-  for (; i < n4; i += 1024) {
-    const nsr_float4 d = ldf4(xr + 4 * i) - k0;
-    s1[0] += (d.x + d.y) + (d.z + d.w);
-    s2[0] = __builtin_fmaf(d.x, d.x, __builtin_fmaf(d.y, d.y, __builtin_fmaf(d.z, d.z, __builtin_fmaf(d.w, d.w, s2[0]))));
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    a1 += __shfl_xor(a1, off);
+    a2 += __shfl_xor(a2, off);
   }
-  float t1 = (s1[0] + s1[1]) + (s1[2] + s1[3]);
-  float t2 = (s2[0] + s2[1]) + (s2[2] + s2[3]);
-  t1 = block_sum<16>(t1, red);
-  t2 = block_sum<16>(t2, red);
-  if (tid == 0) {
-    const double n = (double)T;
-    const double m1 = (double)t1 / n;
-    double var = (double)t2 / n - m1 * m1;
-    if (var < 0.0) var = 0.0;
-    a.stats[2 * row] = (float)((double)k0 + m1);
-    a.stats[2 * row + 1] = 1.0f / sqrtf((float)var + a.eps);
+  const int wid = tid >> 6;
+  if ((tid & 63) == 0) {
+    red[wid] = a1;
+    red[16 + wid] = a2;
+  }
+  __syncthreads();
+  s1 = 0.0;
+  s2 = 0.0;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) {
+    s1 += red[w];
+    s2 += red[16 + w];
+  }
+  __syncthreads();
+}
+
+/* mean as an unevaluated f32 pair (hi + lo) and 1 / sqrt(var + eps) */
+NSR_DEV void row_moments(double s1, double s2, int64_t T, float eps, float& mhi, float& mlo, float& rstd) {
+  const double mean = s1 / (double)T;
+  double var = s2 / (double)T - mean * mean;
+  var = var > 0.0 ? var : 0.0;
+  mhi = (float)mean;
+  mlo = (float)(mean - (double)mhi);
+  rstd = 1.0f / sqrtf((float)var + eps);
+}
+
+/* Row statistics (mean, 1 / sqrt(var + eps)) of [n_rows][T] f32 into
+ * a.stats: one 1024-lane workgroup per row, one read of x. Used where the
+ * statistics feed another kernel (the AdaIN + Snake input of the conv). */
+template <bool VEC4>
+NSR_DEV void adain_stats(const nsr_adain_args& a) {
+  __shared__ double red[32];
+  const int64_t row = blockIdx.x;
+  double s1, s2;
+  row_sums64<VEC4>(a.x + row * a.T, a.T, red, s1, s2);
+  if (threadIdx.x == 0) {
+    float mhi, mlo, rstd;
+    row_moments(s1, s2, a.T, a.eps, mhi, mlo, rstd);
+    a.stats[2 * row] = mhi;
+    a.stats[2 * row + 1] = rstd;
   }
 }
 
-/* Apply: grid (n_rows, ceil(T / 1024)); scalar element access. */
-extern "C" __global__ void __launch_bounds__(256) nsrk_adain_apply(const nsr_adain_args a, const int pdt) {
-  const int64_t row = blockIdx.x;
+extern "C" __global__ void __launch_bounds__(1024) nsrk_adain_stats(const nsr_adain_args a) { adain_stats<false>(a); }
+extern "C" __global__ void __launch_bounds__(1024) nsrk_adain_stats4(const nsr_adain_args a) { adain_stats<true>(a); }
+
+/* Rows too long to hold on chip (or unaligned rows past the resident
+ * kernels' reach): a persistent grid of 1024-lane workgroups, each taking
+ * whole rows. Pass 1 reads the row for its f64 sums; pass 2 reads it again
+ * and writes the output, centring with the mean as an f32 pair
+ * ((x - mean_hi) - mean_lo: the first difference is exact when x is within
+ * a factor of two of the mean). The second read follows the first by one
+ * row's time, so with a workgroup per CU the rows in flight (a few hundred
+ * MB at most) are mostly still in the 256 MB Infinity Cache: the extra
+ * traffic is mostly cache, not HBM. No scratch memory. */
+template <bool VEC4>
+NSR_DEV void adain_long(const nsr_adain_args& a, int pdt) {
+  NSR_NO_CONTRACT
+  __shared__ double red[32];
+  const int tid = threadIdx.x;
   const int64_t T = a.T;
-  const int64_t bi = row / a.C;
-  const int64_t ci = row - bi * a.C;
-  const float mean = a.stats[2 * row];
-  const float rstd = a.stats[2 * row + 1];
-  const adain_raw pr = adain_params_load(a, pdt, bi, ci);
-  float gam, bet, alp;
-  adain_params_cvt(pr, pdt, gam, bet, alp);
-  const float A = (gam + 1.0f) * rstd;
-  const snake_consts sc = make_snake_consts(alp);
-  const float* xr = a.x + row * T;
-  float* orow = a.out + row * T;
-  const int64_t base = (int64_t)blockIdx.y * 1024;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int64_t i = base + e * 256 + threadIdx.x;
-    if (i < T) orow[i] = snake_eval(__builtin_fmaf(xr[i] - mean, A, bet), sc);
+  for (int64_t row = blockIdx.x; row < a.n_rows; row += gridDim.x) {
+    const adain_raw pr = adain_params_load(a, pdt, row / a.C, row % a.C);
+    const float* xr = a.x + row * T;
+    float* orow = a.out + row * T;
+    double s1, s2;
+    row_sums64<VEC4>(xr, T, red, s1, s2);
+    float mhi, mlo, rstd;
+    row_moments(s1, s2, T, a.eps, mhi, mlo, rstd);
+    float gam, bet, alp;
+    adain_params_cvt(pr, pdt, gam, bet, alp);
+    const float A = (gam + 1.0f) * rstd;
+    const float Bc = __builtin_fmaf(-mlo, A, bet); /* ((x - mhi) - mlo) A + beta */
+    const snake_consts sc = make_snake_consts(alp);
+    if constexpr (VEC4) {
+      const int64_t n4 = T >> 2;
+      for (int64_t i = tid; i < n4; i += 1024) {
+        const nsr_float4 d = ldf4(xr + 4 * i) - mhi;
+        stf4(orow + 4 * i, adain_snake4(d, A, Bc, sc));
+      }
+    } else {
+      for (int64_t i = tid; i < T; i += 1024)
+        orow[i] = snake_eval(__builtin_fmaf(__builtin_nontemporal_load(xr + i) - mhi, A, Bc), sc);
+    }
   }
+}
+
+extern "C" __global__ void __launch_bounds__(1024) nsrk_adain_long(const nsr_adain_args a, const int pdt) {
+  adain_long<false>(a, pdt);
+}
+extern "C" __global__ void __launch_bounds__(1024) nsrk_adain_long4(const nsr_adain_args a, const int pdt) {
+  adain_long<true>(a, pdt);
 }

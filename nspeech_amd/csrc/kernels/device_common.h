@@ -13,6 +13,12 @@
 
 #define NSR_DEV __device__ __forceinline__
 
+/* No fusing of a separate multiply and add into one fma in the enclosing
+ * block (the compiler may do so by default). Kernels whose numerics need
+ * every use of a rounded value to see the same rounding say so with this;
+ * explicit __builtin_fmaf calls still fuse. */
+#define NSR_NO_CONTRACT _Pragma("clang fp contract(off)")
+
 typedef float nsr_float4 __attribute__((ext_vector_type(4)));
 typedef float nsr_float2 __attribute__((ext_vector_type(2)));
 typedef __bf16 nsr_bf16x2 __attribute__((ext_vector_type(2)));

@@ -226,4 +226,11 @@ typedef struct nsr_ew_args {
   int32_t pad_;
 } nsr_ew_args;
 
+/* plain device copy of n4 16-byte chunks (measurement floor) */
+typedef struct nsr_calib_args {
+  const float* src;
+  float* dst;
+  int64_t n4;
+} nsr_calib_args;
+
 #endif /* NSR_KARGS_H */

@@ -22,5 +22,6 @@ NSR_EMBED(gemv_q8)
 NSR_EMBED(conv1d)
 NSR_EMBED(attention)
 NSR_EMBED(istft)
+NSR_EMBED(calib)
 
     .section .note.GNU-stack, "", @progbits

@@ -2,24 +2,28 @@
 // validation, kernel selection and launch for every entry point declared in
 // include/nspeech_rocm.h.
 //
-// The kernels live in one gfx950 code object (nsr_kernels.hip) embedded in
-// this library (nsr_embed.S) and loaded per device with hipModuleLoadData on
-// first use; launches go through hipModuleLaunchKernel on the caller's
-// stream. This replaces the reference's Metal pipeline loading and dispatch
-// (src/triton_kernels.rs:1401, kernels/out/generated/triton_metal_gen.rs:39-106)
-// and its per-call encoder setup (src/triton_kernels.rs:312-1423).
+// The kernels live in one gfx950 code object per kernel unit
+// (kernels/<unit>.hip), embedded in this library (nsr_embed.S) and loaded
+// per device with hipModuleLoadData on first use. Every kernel has a
+// compile-time id (KId, from nsr_kernels.def); all of a device's kernel
+// handles are resolved when its modules are loaded, so a launch is an index
+// into a per-device table and hipModuleLaunchKernel on the caller's stream:
+// no name building, lock or lookup per call. This replaces the reference's
+// Metal pipeline loading and dispatch (src/triton_kernels.rs:1401,
+// kernels/out/generated/triton_metal_gen.rs:39-106) and its per-call encoder
+// setup (src/triton_kernels.rs:312-1423).
 #include "nspeech_rocm.h"
 
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
 #include <string>
-#include <unordered_map>
 
 #include "../nsr_kargs.h"
 
@@ -33,23 +37,47 @@ extern "C" const unsigned char nsr_co_gemv_q8[];
 extern "C" const unsigned char nsr_co_conv1d[];
 extern "C" const unsigned char nsr_co_attention[];
 extern "C" const unsigned char nsr_co_istft[];
+extern "C" const unsigned char nsr_co_calib[];
 
 namespace {
+
+enum UnitId { U_q8_0_gather, U_layernorm, U_rotary, U_adain_snake, U_elementwise, U_gemv_q8, U_conv1d,
+              U_attention, U_istft, U_calib, kNumUnits };
 
 struct Unit {
   const char* name;
   const unsigned char* image;
 };
-const Unit kUnits[] = {{"q8_0_gather", nsr_co_q8_0_gather},
-                       {"layernorm", nsr_co_layernorm},
-                       {"rotary", nsr_co_rotary},
-                       {"adain_snake", nsr_co_adain_snake},
-                       {"elementwise", nsr_co_elementwise},
-                       {"gemv_q8", nsr_co_gemv_q8},
-                       {"conv1d", nsr_co_conv1d},
-                       {"attention", nsr_co_attention},
-                       {"istft", nsr_co_istft}};
-constexpr int kNumUnits = sizeof(kUnits) / sizeof(kUnits[0]);
+const Unit kUnits[kNumUnits] = {{"q8_0_gather", nsr_co_q8_0_gather},
+                                {"layernorm", nsr_co_layernorm},
+                                {"rotary", nsr_co_rotary},
+                                {"adain_snake", nsr_co_adain_snake},
+                                {"elementwise", nsr_co_elementwise},
+                                {"gemv_q8", nsr_co_gemv_q8},
+                                {"conv1d", nsr_co_conv1d},
+                                {"attention", nsr_co_attention},
+                                {"istft", nsr_co_istft},
+                                {"calib", nsr_co_calib}};
+
+// Kernel ids: K_<kernel name>, in nsr_kernels.def order; K_NONE marks a
+// variant that is not built.
+enum KId : int {
+  K_NONE = -1,
+#define NSR_KERNEL(unit, name) K_##name,
+#include "nsr_kernels.def"
+#undef NSR_KERNEL
+  K_COUNT
+};
+
+struct KernelInfo {
+  UnitId unit;
+  const char* name;
+};
+const KernelInfo kKernels[K_COUNT] = {
+#define NSR_KERNEL(unit, name) {U_##unit, #name},
+#include "nsr_kernels.def"
+#undef NSR_KERNEL
+};
 
 constexpr int kMaxDevices = 64;
 thread_local std::string g_last_error;
@@ -69,7 +97,8 @@ struct DeviceModule {
   nsr_status status = NSR_ERR_NOT_INIT;
   std::string error;
   hipModule_t modules[kNumUnits] = {};
-  std::unordered_map<std::string, hipFunction_t> fns;
+  hipFunction_t fn[K_COUNT] = {};
+  std::atomic<int> occupancy[K_COUNT] = {};  // workgroups per CU, for kernels launched with one shape (0: unknown)
   int max_lds = 0;
   int n_cu = 0;
 };
@@ -111,6 +140,18 @@ void load_module(DeviceModule& dm, int dev) {
       return;
     }
   }
+  // every kernel handle, once: a code object that lacks a listed kernel is a
+  // build mismatch and fails the load (not a later launch)
+  for (int k = 0; k < K_COUNT; ++k) {
+    e = hipModuleGetFunction(&dm.fn[k], dm.modules[kKernels[k].unit], kKernels[k].name);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      dm.error = std::string("kernel ") + kKernels[k].name + " not in code object " + kUnits[kKernels[k].unit].name +
+                 ": " + hipGetErrorString(e);
+      dm.status = NSR_ERR_NOT_INIT;
+      return;
+    }
+  }
   int lds = 0;
   hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   dm.max_lds = lds;
@@ -133,83 +174,55 @@ nsr_status current_module(DeviceModule** out) {
   return NSR_OK;
 }
 
-std::mutex g_fn_mu;
+// Launch kernel k on the current device: grid (gx, gy, gz) of `block` lanes.
+nsr_status launch3(KId k, unsigned gx, unsigned gy, unsigned gz, unsigned block, unsigned shmem, nsr_stream_t stream,
+                   void** params) {
+  if (k < 0 || k >= K_COUNT) return fail(NSR_ERR_UNSUPPORTED, "no kernel built for this variant");
+  DeviceModule* dm = nullptr;
+  nsr_status st = current_module(&dm);
+  if (st != NSR_OK) return st;
+  if (shmem > (unsigned)dm->max_lds)
+    return fail(NSR_ERR_UNSUPPORTED, "%s needs %u bytes of LDS, device allows %d", kKernels[k].name, shmem,
+                dm->max_lds);
+  hipError_t e =
+      hipModuleLaunchKernel(dm->fn[k], gx, gy, gz, block, 1, 1, shmem, (hipStream_t)stream, params, nullptr);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();  // reported through nsr_status, not left sticky
+    return fail(NSR_ERR_HIP, "launch %s: %s", kKernels[k].name, hipGetErrorString(e));
+  }
+  return NSR_OK;
+}
 
-// Code-object unit of a kernel, from its name prefix.
-int unit_of(const std::string& name) {
-  struct P {
-    const char* prefix;
-    int unit;
-  };
-  static const P map[] = {{"nsrk_q8_0_", 0}, {"nsrk_ln_", 1},    {"nsrk_resln_", 1}, {"nsrk_rope_", 2},
-                          {"nsrk_adain_", 3}, {"nsrk_silu_", 4}, {"nsrk_gelu_", 4},  {"nsrk_glu_", 4},
-                          {"nsrk_add_", 4},  {"nsrk_gemv_", 5},
-                          {"nsrk_conv1d_", 6}, {"nsrk_conv_rowstats", 6}, {"nsrk_attn_", 7}, {"nsrk_combine_", 4}, {"nsrk_istft_", 8},
-                          {"nsrk_snake_", 4}};
-  for (const P& p : map)
-    if (name.compare(0, std::strlen(p.prefix), p.prefix) == 0) return p.unit;
+nsr_status launch(KId k, unsigned gx, unsigned gy, unsigned block, unsigned shmem, nsr_stream_t stream,
+                  void** params) {
+  return launch3(k, gx, gy, 1, block, shmem, stream, params);
+}
+
+// Workgroups of kernel k (always launched with `block` lanes and `lds` bytes) that fit on one CU; cached.
+int occupancy(DeviceModule* dm, KId k, unsigned block, unsigned lds) {
+  int n = dm->occupancy[k].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, dm->fn[k], (int)block, lds) != hipSuccess) {
+      (void)hipGetLastError();
+      return 1;
+    }
+    n = std::max(n, 1);
+    dm->occupancy[k].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Index of v in the options list, or -1.
+template <size_t N>
+int index_of(const int (&opts)[N], int v) {
+  for (size_t i = 0; i < N; ++i)
+    if (opts[i] == v) return (int)i;
   return -1;
 }
 
-nsr_status get_function(DeviceModule* dm, const std::string& name, hipFunction_t* f) {
-  std::lock_guard<std::mutex> lk(g_fn_mu);
-  auto it = dm->fns.find(name);
-  if (it != dm->fns.end()) {
-    *f = it->second;
-    return NSR_OK;
-  }
-  // Each kernel lives in the unit its name prefix names, so the lookup never
-  // misses (a failed hipModuleGetFunction would leave a sticky runtime error
-  // that the caller's next HIP call reports).
-  const int u = unit_of(name);
-  if (u < 0) return fail(NSR_ERR_NOT_INIT, "kernel %s belongs to no code-object unit", name.c_str());
-  hipError_t e = hipModuleGetFunction(f, dm->modules[u], name.c_str());
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(NSR_ERR_NOT_INIT, "kernel %s not in code object %s: %s", name.c_str(), kUnits[u].name,
-                hipGetErrorString(e));
-  }
-  dm->fns.emplace(name, *f);
-  return NSR_OK;
-}
-
-nsr_status launch(const std::string& name, unsigned gx, unsigned gy, unsigned block,
-                  unsigned shmem, nsr_stream_t stream, void** params) {
-  DeviceModule* dm = nullptr;
-  nsr_status st = current_module(&dm);
-  if (st != NSR_OK) return st;
-  hipFunction_t f;
-  st = get_function(dm, name, &f);
-  if (st != NSR_OK) return st;
-  if (shmem > (unsigned)dm->max_lds)
-    return fail(NSR_ERR_UNSUPPORTED, "%s needs %u bytes of LDS, device allows %d", name.c_str(), shmem,
-                dm->max_lds);
-  hipError_t e = hipModuleLaunchKernel(f, gx, gy, 1, block, 1, 1, shmem, (hipStream_t)stream, params, nullptr);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();  // reported through nsr_status, not left sticky
-    return fail(NSR_ERR_HIP, "launch %s: %s", name.c_str(), hipGetErrorString(e));
-  }
-  return NSR_OK;
-}
-
-// 3-D grid launch (grid.z = batch).
-nsr_status launch3(const std::string& name, unsigned gx, unsigned gy, unsigned gz, unsigned block, unsigned shmem,
-                   nsr_stream_t stream, void** params) {
-  DeviceModule* dm = nullptr;
-  nsr_status st = current_module(&dm);
-  if (st != NSR_OK) return st;
-  hipFunction_t f;
-  st = get_function(dm, name, &f);
-  if (st != NSR_OK) return st;
-  if (shmem > (unsigned)dm->max_lds)
-    return fail(NSR_ERR_UNSUPPORTED, "%s needs %u bytes of LDS, device allows %d", name.c_str(), shmem,
-                dm->max_lds);
-  hipError_t e = hipModuleLaunchKernel(f, gx, gy, gz, block, 1, 1, shmem, (hipStream_t)stream, params, nullptr);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(NSR_ERR_HIP, "launch %s: %s", name.c_str(), hipGetErrorString(e));
-  }
-  return NSR_OK;
+template <size_t N>
+KId pick(const KId (&ids)[N], int i) {
+  return i >= 0 && i < (int)N ? ids[i] : K_NONE;
 }
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
@@ -241,23 +254,23 @@ nsr_status nsr_init(const char* code_object_dir) {
 int nsr_kernel_count(void) {
   DeviceModule* dm = nullptr;
   if (current_module(&dm) != NSR_OK) return 0;
-  // Count kernels by probing the names this runtime launches.
-  static const char* probe[] = {"nsrk_q8_0_gather_none_u32", "nsrk_ln_f32_f32_nc4",
-                                "nsrk_resln_bf16_nc2",       "nsrk_rope_table_f32",
-                                "nsrk_rope_compute_f32",     "nsrk_adain_row_b256_v5_l0",
-                                "nsrk_adain_row_b512_v44_l14", "nsrk_adain_stats",
-                                "nsrk_adain_apply",          "nsrk_gelu_f32_v",
-                                "nsrk_gemv_q8_f16_f16",      "nsrk_gemv_q8t4_glu_f16_f16_b256",
-                                "nsrk_conv1d_f16x2_np9",     "nsrk_conv1d_adain_snake_f16x2_np9"};
-  int n = 0;
-  for (const char* p : probe) {
-    hipFunction_t f;
-    if (get_function(dm, p, &f) == NSR_OK) ++n;
-  }
-  return n;
+  return K_COUNT;  // every listed kernel was resolved when the modules were loaded
 }
 
 // ------------------------------------------------------------ LayerNorm --
+
+#define NSR_LN_FAM(p) {K_##p##_nc1, K_##p##_nc2, K_##p##_nc4, K_##p##_nc8, K_NONE, K_##p##_generic}
+#define NSR_LN_FAM16(p) {K_##p##_nc1, K_##p##_nc2, K_##p##_nc4, K_##p##_nc8, K_##p##_nc16, K_##p##_generic}
+// [x dtype][y dtype] (NSR_F32, NSR_F16, NSR_BF16)
+static const KId kLn[3][3][6] = {
+    {NSR_LN_FAM16(nsrk_ln_f32_f32), NSR_LN_FAM(nsrk_ln_f32_f16), NSR_LN_FAM(nsrk_ln_f32_bf16)},
+    {NSR_LN_FAM(nsrk_ln_f16_f32), NSR_LN_FAM(nsrk_ln_f16_f16), NSR_LN_FAM(nsrk_ln_f16_bf16)},
+    {NSR_LN_FAM(nsrk_ln_bf16_f32), NSR_LN_FAM(nsrk_ln_bf16_f16), NSR_LN_FAM(nsrk_ln_bf16_bf16)}};
+static const KId kResLn[3][6] = {NSR_LN_FAM16(nsrk_resln_f32), NSR_LN_FAM(nsrk_resln_f16),
+                                 NSR_LN_FAM(nsrk_resln_bf16)};
+static const KId kResLnF16F32[6] = NSR_LN_FAM(nsrk_resln_f16f32);
+#undef NSR_LN_FAM
+#undef NSR_LN_FAM16
 
 static nsr_status ln_common(const void* x, nsr_dtype xd, const void* res, nsr_dtype rd, void* h,
                             nsr_dtype hd, const void* gamma, const void* beta, nsr_dtype pd, void* y,
@@ -276,12 +289,13 @@ static nsr_status ln_common(const void* x, nsr_dtype xd, const void* res, nsr_dt
   if (!(eps >= 0.0f)) return fail(NSR_ERR_BAD_ARG, "layernorm: eps must be >= 0");
   if (n_rows == 0) return NSR_OK;
 
-  std::string prefix;
+  // kernel family: [nc 1, 2, 4, 8, 16, generic]
+  const KId* fam = nullptr;
   if (fused) {
     if (xd == rd && rd == hd && hd == yd) {
-      prefix = std::string("nsrk_resln_") + dt_name(xd);
+      fam = kResLn[xd];
     } else if (xd == NSR_F16 && rd == NSR_F32 && hd == NSR_F32 && yd == NSR_F16) {
-      prefix = "nsrk_resln_f16f32";
+      fam = kResLnF16F32;
     } else {
       return fail(NSR_ERR_UNSUPPORTED,
                   "residual_add_layernorm: dtype profile x=%s res=%s h=%s y=%s not built "
@@ -289,7 +303,7 @@ static nsr_status ln_common(const void* x, nsr_dtype xd, const void* res, nsr_dt
                   dt_name(xd), dt_name(rd), dt_name(hd), dt_name(yd));
     }
   } else {
-    prefix = std::string("nsrk_ln_") + dt_name(xd) + "_" + dt_name(yd);
+    fam = kLn[xd][yd];
   }
 
   const bool all32 = xd == NSR_F32 && yd == NSR_F32 && (!fused || (rd == NSR_F32 && hd == NSR_F32));
@@ -333,11 +347,12 @@ static nsr_status ln_common(const void* x, nsr_dtype xd, const void* res, nsr_dt
     // gfx950 for [24000, 1024] bf16: 4096 workgroups).
     constexpr int64_t kLnMaxGrid = 4096;
     const int64_t groups = (n_rows + 3) / 4;
-    return launch(prefix + "_nc" + std::to_string(nc), (unsigned)(groups < kLnMaxGrid ? groups : kLnMaxGrid), 1,
+    static const int kNcOpts[] = {1, 2, 4, 8, 16};
+    return launch(fam[index_of(kNcOpts, nc)], (unsigned)(groups < kLnMaxGrid ? groups : kLnMaxGrid), 1,
                   256, 0, stream, params);
   }
   if (n_rows > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "layernorm: too many rows");
-  return launch(prefix + "_generic", (unsigned)n_rows, 1, 256, 0, stream, params);
+  return launch(fam[5], (unsigned)n_rows, 1, 256, 0, stream, params);
 }
 
 nsr_status nsr_layernorm(const void* x, nsr_dtype x_dtype, const void* gamma, const void* beta,
@@ -423,7 +438,7 @@ nsr_status nsr_rotary_partial_interleaved_f32(const float* q, const float* k, fl
     a.inv_freq[i] = 1.0f / powf(theta, e);
   }
   void* params[] = {&a};
-  return launch(rope_table ? "nsrk_rope_table_f32" : "nsrk_rope_compute_f32", cdiv_u(total, 256), 1, 256, 0,
+  return launch(rope_table ? K_nsrk_rope_table_f32 : K_nsrk_rope_compute_f32, cdiv_u(total, 256), 1, 256, 0,
                 stream, params);
 }
 
@@ -468,7 +483,7 @@ static nsr_status rope_cache_launch(void* q, void* k, const void* v, nsr_dtype d
   const int64_t total = (int64_t)a.nq + a.nk + a.nkp + a.nv;
   if (total == 0) return NSR_OK;
   void* params[] = {&a};
-  return launch(dtype == NSR_F16 ? "nsrk_rope_cache_f16" : "nsrk_rope_cache_f32", cdiv_u(total, 256), 1, 256, 0,
+  return launch(dtype == NSR_F16 ? K_nsrk_rope_cache_f16 : K_nsrk_rope_cache_f32, cdiv_u(total, 256), 1, 256, 0,
                 stream, params);
 }
 
@@ -491,10 +506,14 @@ nsr_status nsr_kv_cache_append(const void* new_kv, void* cache, nsr_dtype dtype,
 
 namespace {
 
-// compile-time head_dim / 4 variants of the attention kernels (0: any)
-int attn_variant(int64_t head_dim) {
-  const int hd4 = (int)(head_dim / 4);
-  return (hd4 == 9 || hd4 == 13 || hd4 == 16 || hd4 == 32) ? hd4 : 0;
+// compile-time head_dim / 4 variants of the attention kernels (d0: any head_dim)
+const int kAttnHd4[] = {9, 13, 16, 32};
+const KId kAttnPartial[] = {K_nsrk_attn_partial_d9, K_nsrk_attn_partial_d13, K_nsrk_attn_partial_d16,
+                            K_nsrk_attn_partial_d32};
+const KId kAttnHead[] = {K_nsrk_attn_head_d9, K_nsrk_attn_head_d13, K_nsrk_attn_head_d16, K_nsrk_attn_head_d32};
+KId attn_kernel(const KId (&ids)[4], KId any, int64_t head_dim) {
+  const int i = index_of(kAttnHd4, (int)(head_dim / 4));
+  return i >= 0 ? ids[i] : any;
 }
 
 int64_t attn_wave_lds_bytes(int64_t head_dim) { return 4 * (2 * 64 * (head_dim / 4 + 1) * 2 + 64 + 256); }
@@ -557,10 +576,10 @@ nsr_status nsr_attention_splitkv_f16(const void* q, const void* k, const void* v
   attn_fill(a, q, k, v, out, partial, kv_len, head_dim, n_kv_heads, n_q_heads, sm_scale, stride_kv_head,
             stride_kv_seq, n_splits);
   void* params[] = {&a};
-  st = launch("nsrk_attn_partial_d" + std::to_string(attn_variant(head_dim)), (unsigned)(n_q_heads * n_splits), 1,
+  st = launch(attn_kernel(kAttnPartial, K_nsrk_attn_partial_d0, head_dim), (unsigned)(n_q_heads * n_splits), 1,
               64, (unsigned)attn_wave_lds_bytes(head_dim), stream, params);
   if (st != NSR_OK) return st;
-  return launch("nsrk_attn_reduce", (unsigned)n_q_heads, 1, 128, 0, stream, params);
+  return launch(K_nsrk_attn_reduce, (unsigned)n_q_heads, 1, 128, 0, stream, params);
 }
 
 nsr_status nsr_attention_decode_f16(const void* q, const void* k, const void* v, void* out, int64_t kv_len,
@@ -580,7 +599,7 @@ nsr_status nsr_attention_decode_f16(const void* q, const void* k, const void* v,
   attn_fill(a, q, k, v, out, nullptr, kv_len, head_dim, n_kv_heads, n_q_heads, sm_scale, stride_kv_head,
             stride_kv_seq, 1);
   void* params[] = {&a};
-  return launch("nsrk_attn_head_d" + std::to_string(attn_variant(head_dim)), (unsigned)n_q_heads, 1,
+  return launch(attn_kernel(kAttnHead, K_nsrk_attn_head_d0, head_dim), (unsigned)n_q_heads, 1,
                 (unsigned)(64 * W), (unsigned)(W * per_wave), stream, params);
 }
 
@@ -624,83 +643,86 @@ nsr_status nsr_adain_snake_f32(const float* x, const void* gamma, const void* be
   int pdt = param_dtype == NSR_F32 ? 0 : 1;
 
   const bool is_aligned = aligned(x, 16) && aligned(out, 16) && (T % 4 == 0);
-  std::string name;
+  KId kid = K_NONE;
   unsigned block = 0, lds = 0;
   if (is_aligned) {
-    // Row kernel: BLOCK-wide slots of 16-byte chunks, NV in VGPRs + NL in LDS.
+    // Row kernel: BLOCK-wide slots of 16-byte chunks, NV in VGPRs + NL in LDS. The kernel masks only its
+    // last four slots at the row end, so the first NV + NL - 4 slots must lie inside every row.
     const int64_t nch = T / 4;
     int nv = 0, nl = 0;
     if (nch <= 256 * 8) {
+      static const KId ids[] = {K_nsrk_adain_row_b256_v1_l0, K_nsrk_adain_row_b256_v2_l0, K_nsrk_adain_row_b256_v3_l0,
+                                K_nsrk_adain_row_b256_v4_l0, K_nsrk_adain_row_b256_v5_l0, K_nsrk_adain_row_b256_v6_l0,
+                                K_nsrk_adain_row_b256_v7_l0, K_nsrk_adain_row_b256_v8_l0};
       block = 256;
       nv = (int)((nch + 255) / 256);
+      kid = ids[nv - 1];
     } else if (nch <= 512 * 44) {
-      block = 512;
       static const int opts[] = {5, 6, 8, 10, 12, 16, 20, 24, 28, 32, 36, 40, 44};
-      for (int o : opts)
-        if (512LL * o >= nch) {
-          nv = o;
-          break;
-        }
-    } else if (nch <= 512 * (44 + 18)) {
+      static const KId ids[] = {K_nsrk_adain_row_b512_v5_l0,  K_nsrk_adain_row_b512_v6_l0,  K_nsrk_adain_row_b512_v8_l0,
+                                K_nsrk_adain_row_b512_v10_l0, K_nsrk_adain_row_b512_v12_l0, K_nsrk_adain_row_b512_v16_l0,
+                                K_nsrk_adain_row_b512_v20_l0, K_nsrk_adain_row_b512_v24_l0, K_nsrk_adain_row_b512_v28_l0,
+                                K_nsrk_adain_row_b512_v32_l0, K_nsrk_adain_row_b512_v36_l0, K_nsrk_adain_row_b512_v40_l0,
+                                K_nsrk_adain_row_b512_v44_l0};
       block = 512;
-      nv = 44;
-      const int64_t m = (nch - 512 * 44 + 511) / 512;
+      for (int i = 0; i < 13 && !nv; ++i)
+        if (512LL * opts[i] >= nch) {
+          nv = opts[i];
+          kid = ids[i];
+        }
+    } else if (nch <= 512 * (40 + 18)) {
+      static const KId ids[] = {K_nsrk_adain_row_b512_v40_l2,  K_nsrk_adain_row_b512_v40_l4,
+                                K_nsrk_adain_row_b512_v40_l6,  K_nsrk_adain_row_b512_v40_l8,
+                                K_nsrk_adain_row_b512_v40_l10, K_nsrk_adain_row_b512_v40_l12,
+                                K_nsrk_adain_row_b512_v40_l14, K_nsrk_adain_row_b512_v40_l16,
+                                K_nsrk_adain_row_b512_v40_l18};
+      block = 512;
+      nv = 40;
+      const int64_t m = (nch - 512 * 40 + 511) / 512;
       nl = (int)((m + 1) / 2 * 2);  // built for even NL 2..18
       lds = (unsigned)(nl * 512 * 16);
+      kid = ids[nl / 2 - 1];
       if (lds + 1024 > (unsigned)dm->max_lds) block = 0;
     }
-    if (block)
-      name = "nsrk_adain_row_b" + std::to_string(block) + "_v" + std::to_string(nv) + "_l" + std::to_string(nl);
+    const int ns = nv + nl;
+    if (block && (int64_t)(ns - std::min(ns, 4)) * block > nch)
+      return fail(NSR_ERR_HIP, "adain_snake: internal error: row kernel slots do not fit T=%lld", (long long)T);
   } else {
     // Unaligned rows: interior chunks 1..nch-2 resident in VGPRs, edges by element.
     const int64_t need = (T + 6) / 4 - 2 > 0 ? (T + 6) / 4 - 2 : 0;
-    int nv = 0;
     static const int small[] = {1, 2, 3, 4, 5, 6, 8};
-    for (int o : small)
-      if (256LL * o >= need) {
+    static const KId small_ids[] = {K_nsrk_adain_res_b256_nv1_u, K_nsrk_adain_res_b256_nv2_u,
+                                    K_nsrk_adain_res_b256_nv3_u, K_nsrk_adain_res_b256_nv4_u,
+                                    K_nsrk_adain_res_b256_nv5_u, K_nsrk_adain_res_b256_nv6_u,
+                                    K_nsrk_adain_res_b256_nv8_u};
+    for (int i = 0; i < 7 && !block; ++i)
+      if (256LL * small[i] >= need) {
         block = 256;
-        nv = o;
-        break;
+        kid = small_ids[i];
       }
-    if (!block) {
-      static const int large[] = {12, 16, 24, 32};
-      for (int o : large)
-        if (512LL * o >= need) {
-          block = 512;
-          nv = o;
-          break;
-        }
-    }
-    if (block) name = "nsrk_adain_res_b" + std::to_string(block) + "_nv" + std::to_string(nv) + "_u";
+    static const int large[] = {12, 16, 24, 32};
+    static const KId large_ids[] = {K_nsrk_adain_res_b512_nv12_u, K_nsrk_adain_res_b512_nv16_u,
+                                    K_nsrk_adain_res_b512_nv24_u, K_nsrk_adain_res_b512_nv32_u};
+    for (int i = 0; i < 4 && !block; ++i)
+      if (512LL * large[i] >= need) {
+        block = 512;
+        kid = large_ids[i];
+      }
   }
+  void* params[] = {&a, &pdt};
   if (block) {
     a.lds_chunks = (int32_t)(lds / (16u * block));
-    void* params[] = {&a, &pdt};
-    return launch(name, (unsigned)n_rows, 1, block, lds, stream, params);
+    // as many workgroups as fit on the device at once, each walking rows with the grid as stride (one per row
+    // when they all fit): a row kernel that fills a CU then overlaps the next row's reads with its writes
+    unsigned grid = (unsigned)n_rows;
+    if (is_aligned) grid = (unsigned)std::min<int64_t>(n_rows, (int64_t)occupancy(dm, kid, block, lds) * dm->n_cu);
+    return launch(kid, grid, 1, block, lds, stream, params);
   }
-
-  // Split path: stats (one read) + apply (second read), stream-ordered scratch.
-  float* stats = nullptr;
-  hipError_t e = hipMallocAsync((void**)&stats, (size_t)n_rows * 2 * sizeof(float), (hipStream_t)stream);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(NSR_ERR_HIP, "adain_snake: hipMallocAsync: %s", hipGetErrorString(e));
-  }
-  a.stats = stats;
-  void* p1[] = {&a};
-  const bool rows16 = T % 4 == 0 && aligned(x, 16);
-  st = launch(rows16 ? "nsrk_adain_stats4" : "nsrk_adain_stats", (unsigned)n_rows, 1, 1024, 0, stream, p1);
-  if (st == NSR_OK) {
-    void* p2[] = {&a, &pdt};
-    const int64_t gy = (T + 1023) / 1024;
-    if (gy > 65535) {
-      st = fail(NSR_ERR_UNSUPPORTED, "adain_snake: T too long for the split path");
-    } else {
-      st = launch("nsrk_adain_apply", (unsigned)n_rows, (unsigned)gy, 256, 0, stream, p2);
-    }
-  }
-  hipFreeAsync(stats, (hipStream_t)stream);
-  return st;
+  // Rows past the on-chip budget: statistics over one read, then a second read to apply (persistent grid,
+  // one 1024-lane workgroup per CU, no scratch).
+  const bool rows16 = T % 4 == 0 && aligned(x, 16) && aligned(out, 16);
+  return launch(rows16 ? K_nsrk_adain_long4 : K_nsrk_adain_long, (unsigned)std::min<int64_t>(n_rows, dm->n_cu), 1,
+                1024, 0, stream, params);
 }
 
 nsr_status nsr_adain_snake_f16(const void* x, const void* gamma, const void* beta, const void* alpha,
@@ -724,23 +746,24 @@ nsr_status nsr_adain_snake_f16(const void* x, const void* gamma, const void* bet
   // interior 16-byte chunks of a row, at the worst offset (7 elements into its first chunk)
   const int64_t need = (T + 14) / 8 - 2;
   unsigned block = 0;
-  int nv = 0;
+  KId kid = K_NONE;
   static const int small[] = {1, 2, 3, 4, 6, 8};
-  for (int o : small)
-    if (256LL * o >= need) {
+  static const KId small_ids[] = {K_nsrk_adain_f16_b256_nv1, K_nsrk_adain_f16_b256_nv2, K_nsrk_adain_f16_b256_nv3,
+                                  K_nsrk_adain_f16_b256_nv4, K_nsrk_adain_f16_b256_nv6, K_nsrk_adain_f16_b256_nv8};
+  for (int i = 0; i < 6 && !block; ++i)
+    if (256LL * small[i] >= need) {
       block = 256;
-      nv = o;
-      break;
+      kid = small_ids[i];
     }
-  if (!block) {
-    static const int large[] = {6, 8, 12, 16, 20, 24, 28, 32};
-    for (int o : large)
-      if (512LL * o >= need) {
-        block = 512;
-        nv = o;
-        break;
-      }
-  }
+  static const int large[] = {6, 8, 12, 16, 20, 24, 28, 32};
+  static const KId large_ids[] = {K_nsrk_adain_f16_b512_nv6,  K_nsrk_adain_f16_b512_nv8,  K_nsrk_adain_f16_b512_nv12,
+                                  K_nsrk_adain_f16_b512_nv16, K_nsrk_adain_f16_b512_nv20, K_nsrk_adain_f16_b512_nv24,
+                                  K_nsrk_adain_f16_b512_nv28, K_nsrk_adain_f16_b512_nv32};
+  for (int i = 0; i < 8 && !block; ++i)
+    if (512LL * large[i] >= need) {
+      block = 512;
+      kid = large_ids[i];
+    }
   if (!block) return fail(NSR_ERR_UNSUPPORTED, "adain_snake_f16: rows longer than 131072 elements");
   nsr_adain_h_args a;
   std::memset(&a, 0, sizeof(a));
@@ -758,7 +781,7 @@ nsr_status nsr_adain_snake_f16(const void* x, const void* gamma, const void* bet
   a.inv_t = 1.0f / (float)T;
   int pdt = param_dtype == NSR_F32 ? 0 : 1;
   void* params[] = {&a, &pdt};
-  return launch("nsrk_adain_f16_b" + std::to_string(block) + "_nv" + std::to_string(nv), (unsigned)n_rows, 1, block,
+  return launch(kid, (unsigned)n_rows, 1, block,
                 0, stream, params);
 }
 
@@ -793,17 +816,28 @@ nsr_status nsr_q8_0_embed_gather(const void* blocks, int64_t vocab, int64_t d, c
   a.row_bytes = (int32_t)(d / 32 * 34);
   a.act = (int32_t)act;
   a.ids_i64 = id_dtype == NSR_IDX_I64;
-  const char* an = act == NSR_ACT_SILU ? "silu" : act == NSR_ACT_GELU_ERF ? "gelu" : "none";
-  const std::string name =
-      std::string("nsrk_q8_0_gather_") + an + (id_dtype == NSR_IDX_I64 ? "_i64" : "_u32");
+  static const KId kGather[2][3] = {
+      {K_nsrk_q8_0_gather_none_u32, K_nsrk_q8_0_gather_silu_u32, K_nsrk_q8_0_gather_gelu_u32},
+      {K_nsrk_q8_0_gather_none_i64, K_nsrk_q8_0_gather_silu_i64, K_nsrk_q8_0_gather_gelu_i64}};
   void* params[] = {&a};
-  return launch(name, cdiv_u(total4, 256), 1, 256, 0, stream, params);
+  return launch(kGather[id_dtype == NSR_IDX_I64][act], cdiv_u(total4, 256), 1, 256, 0, stream, params);
 }
 
 // ---------------------------------------------------------- elementwise --
 
-static nsr_status ew_launch(const char* op, nsr_dtype dtype, nsr_ew_args& a, bool vec_ok,
-                            nsr_stream_t stream) {
+enum EwOp { kEwSilu, kEwGelu, kEwGlu, kEwAdd };
+// [op][dtype][vector, scalar]
+static const KId kEw[4][3][2] = {
+    {{K_nsrk_silu_f32_v, K_nsrk_silu_f32_s}, {K_nsrk_silu_f16_v, K_nsrk_silu_f16_s},
+     {K_nsrk_silu_bf16_v, K_nsrk_silu_bf16_s}},
+    {{K_nsrk_gelu_f32_v, K_nsrk_gelu_f32_s}, {K_nsrk_gelu_f16_v, K_nsrk_gelu_f16_s},
+     {K_nsrk_gelu_bf16_v, K_nsrk_gelu_bf16_s}},
+    {{K_nsrk_glu_f32_v, K_nsrk_glu_f32_s}, {K_nsrk_glu_f16_v, K_nsrk_glu_f16_s}, {K_nsrk_glu_bf16_v, K_nsrk_glu_bf16_s}},
+    {{K_nsrk_add_f32_v, K_nsrk_add_f32_s}, {K_nsrk_add_f16_v, K_nsrk_add_f16_s}, {K_nsrk_add_bf16_v, K_nsrk_add_bf16_s}}};
+
+static nsr_status ew_launch(EwOp opi, nsr_dtype dtype, nsr_ew_args& a, bool vec_ok, nsr_stream_t stream) {
+  static const char* const kOpName[] = {"silu", "gelu", "glu", "add"};
+  const char* op = kOpName[opi];
   const int vec = 16 / dt_size(dtype);
   int64_t first = 0;
   if (vec_ok) {
@@ -811,7 +845,7 @@ static nsr_status ew_launch(const char* op, nsr_dtype dtype, nsr_ew_args& a, boo
     if (chunks > 0) {
       if ((chunks + 255) / 256 > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "%s: too large", op);
       void* p[] = {&a};
-      nsr_status st = launch(std::string("nsrk_") + op + "_" + dt_name(dtype) + "_v", cdiv_u(chunks, 256), 1,
+      nsr_status st = launch(kEw[opi][dtype][0], cdiv_u(chunks, 256), 1,
                              256, 0, stream, p);
       if (st != NSR_OK) return st;
     }
@@ -821,7 +855,7 @@ static nsr_status ew_launch(const char* op, nsr_dtype dtype, nsr_ew_args& a, boo
   if (rest > 0) {
     if ((rest + 255) / 256 > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "%s: too large", op);
     void* p[] = {&a, &first};
-    return launch(std::string("nsrk_") + op + "_" + dt_name(dtype) + "_s", cdiv_u(rest, 256), 1, 256, 0, stream,
+    return launch(kEw[opi][dtype][1], cdiv_u(rest, 256), 1, 256, 0, stream,
                   p);
   }
   return NSR_OK;
@@ -850,14 +884,14 @@ static nsr_status combine_launch(const float* a, const float* b, const float* c,
   if (vec && n / 4 > 0) {
     if ((n / 4 + 255) / 256 > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "%s: too large", what);
     void* p[] = {&g};
-    nsr_status st = launch("nsrk_combine_f32_v", cdiv_u(n / 4, 256), 1, 256, 0, stream, p);
+    nsr_status st = launch(K_nsrk_combine_f32_v, cdiv_u(n / 4, 256), 1, 256, 0, stream, p);
     if (st != NSR_OK) return st;
     first = n / 4 * 4;
   }
   if (n > first) {
     if ((n - first + 255) / 256 > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "%s: too large", what);
     void* p[] = {&g, &first};
-    return launch("nsrk_combine_f32_s", cdiv_u(n - first, 256), 1, 256, 0, stream, p);
+    return launch(K_nsrk_combine_f32_s, cdiv_u(n - first, 256), 1, 256, 0, stream, p);
   }
   return NSR_OK;
 }
@@ -901,7 +935,7 @@ nsr_status nsr_snake(const void* x, nsr_dtype dtype, const void* alpha, nsr_dtyp
   const int64_t blocks = n_elements / seq_len * a.chunks;
   if (blocks > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "snake: too large");
   void* params[] = {&a};
-  return launch(dtype == NSR_F32 ? "nsrk_snake_f32" : "nsrk_snake_f16", (unsigned)blocks, 1, 256, 0, stream, params);
+  return launch(dtype == NSR_F32 ? K_nsrk_snake_f32 : K_nsrk_snake_f16, (unsigned)blocks, 1, 256, 0, stream, params);
 }
 
 // ------------------------------------------------------------------ iSTFT --
@@ -933,7 +967,8 @@ nsr_status nsr_istft_f32(const float* x, float* out, int64_t n_frames, int64_t o
   const int64_t groups = n_frames <= FG ? 1 : 1 + (n_frames - FG + step - 1) / step;
   if (groups > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "istft: too many frames");
   void* params[] = {&a};
-  return launch("nsrk_istft_f32_n" + std::to_string(n_fft), (unsigned)groups, 1, 256, 0, stream, params);
+  const KId kid = n_fft == 16 ? K_nsrk_istft_f32_n16 : n_fft == 20 ? K_nsrk_istft_f32_n20 : K_nsrk_istft_f32_n32;
+  return launch(kid, (unsigned)groups, 1, 256, 0, stream, params);
 }
 
 nsr_status nsr_activation(const void* x, void* y, nsr_dtype dtype, int64_t n, nsr_act act,
@@ -949,7 +984,7 @@ nsr_status nsr_activation(const void* x, void* y, nsr_dtype dtype, int64_t n, ns
   a.out = y;
   a.n = n;
   a.act = (int32_t)act;
-  return ew_launch(act == NSR_ACT_SILU ? "silu" : "gelu", dtype, a, aligned(x, 16) && aligned(y, 16), stream);
+  return ew_launch(act == NSR_ACT_SILU ? kEwSilu : kEwGelu, dtype, a, aligned(x, 16) && aligned(y, 16), stream);
 }
 
 nsr_status nsr_glu_silu(const void* fc1, void* out, nsr_dtype dtype, int64_t n, nsr_stream_t stream) {
@@ -962,7 +997,7 @@ nsr_status nsr_glu_silu(const void* fc1, void* out, nsr_dtype dtype, int64_t n, 
   a.out = out;
   a.n = n;
   const bool ok = aligned(fc1, 16) && aligned(out, 16) && ((n * dt_size(dtype)) % 16 == 0);
-  return ew_launch("glu", dtype, a, ok, stream);
+  return ew_launch(kEwGlu, dtype, a, ok, stream);
 }
 
 nsr_status nsr_residual_add(const void* x, const void* res, void* out, nsr_dtype dtype, int64_t n,
@@ -976,7 +1011,7 @@ nsr_status nsr_residual_add(const void* x, const void* res, void* out, nsr_dtype
   a.b = res;
   a.out = out;
   a.n = n;
-  return ew_launch("add", dtype, a, aligned(x, 16) && aligned(res, 16) && aligned(out, 16), stream);
+  return ew_launch(kEwAdd, dtype, a, aligned(x, 16) && aligned(res, 16) && aligned(out, 16), stream);
 }
 
 }  // extern "C"
@@ -1036,21 +1071,40 @@ nsr_status gemv_launch(GemvMode mode, bool t4, const void* x, nsr_dtype xd, cons
   a.NW = (int32_t)NW;
   a.N = (int32_t)N;
   void* params[] = {&a};
-  std::string name;
+  // x and output dtypes are F32 (0) or F16 (1); the resadd+LN projection writes f32 h, indexed by x only
+  const int xi = xd == NSR_F16, oi = od == NSR_F16;
+  KId kid;
   unsigned groups, block;
   if (t4) {
-    static const char* kind[] = {"nsrk_gemv_q8t4_", "nsrk_gemv_q8t4_glu_", "nsrk_gemv_q8t4_h_"};
+    // [mode][x][out][block 256, 512, 1024]
+    static const KId ids[3][2][2][3] = {
+        {{{K_nsrk_gemv_q8t4_f32_f32_b256, K_nsrk_gemv_q8t4_f32_f32_b512, K_nsrk_gemv_q8t4_f32_f32_b1024},
+          {K_nsrk_gemv_q8t4_f32_f16_b256, K_nsrk_gemv_q8t4_f32_f16_b512, K_nsrk_gemv_q8t4_f32_f16_b1024}},
+         {{K_nsrk_gemv_q8t4_f16_f32_b256, K_nsrk_gemv_q8t4_f16_f32_b512, K_nsrk_gemv_q8t4_f16_f32_b1024},
+          {K_nsrk_gemv_q8t4_f16_f16_b256, K_nsrk_gemv_q8t4_f16_f16_b512, K_nsrk_gemv_q8t4_f16_f16_b1024}}},
+        {{{K_nsrk_gemv_q8t4_glu_f32_f32_b256, K_nsrk_gemv_q8t4_glu_f32_f32_b512, K_nsrk_gemv_q8t4_glu_f32_f32_b1024},
+          {K_nsrk_gemv_q8t4_glu_f32_f16_b256, K_nsrk_gemv_q8t4_glu_f32_f16_b512, K_nsrk_gemv_q8t4_glu_f32_f16_b1024}},
+         {{K_nsrk_gemv_q8t4_glu_f16_f32_b256, K_nsrk_gemv_q8t4_glu_f16_f32_b512, K_nsrk_gemv_q8t4_glu_f16_f32_b1024},
+          {K_nsrk_gemv_q8t4_glu_f16_f16_b256, K_nsrk_gemv_q8t4_glu_f16_f16_b512, K_nsrk_gemv_q8t4_glu_f16_f16_b1024}}},
+        {{{K_nsrk_gemv_q8t4_h_f32_b256, K_nsrk_gemv_q8t4_h_f32_b512, K_nsrk_gemv_q8t4_h_f32_b1024},
+          {K_nsrk_gemv_q8t4_h_f32_b256, K_nsrk_gemv_q8t4_h_f32_b512, K_nsrk_gemv_q8t4_h_f32_b1024}},
+         {{K_nsrk_gemv_q8t4_h_f16_b256, K_nsrk_gemv_q8t4_h_f16_b512, K_nsrk_gemv_q8t4_h_f16_b1024},
+          {K_nsrk_gemv_q8t4_h_f16_b256, K_nsrk_gemv_q8t4_h_f16_b512, K_nsrk_gemv_q8t4_h_f16_b1024}}}};
     block = (unsigned)t4_block(K);
-    name = std::string(kind[mode]) + dt_name(xd) + (mode == kGemvResLn ? "" : std::string("_") + dt_name(od)) +
-           "_b" + std::to_string(block);
+    kid = ids[mode][xi][oi][block == 256 ? 0 : block == 512 ? 1 : 2];
     groups = (unsigned)(NW / 4);
   } else {
-    static const char* kind[] = {"nsrk_gemv_q8_", "nsrk_gemv_q8_glu_", "nsrk_gemv_q8_h_"};
+    // [mode][x][out]
+    static const KId ids[3][2][2] = {
+        {{K_nsrk_gemv_q8_f32_f32, K_nsrk_gemv_q8_f32_f16}, {K_nsrk_gemv_q8_f16_f32, K_nsrk_gemv_q8_f16_f16}},
+        {{K_nsrk_gemv_q8_glu_f32_f32, K_nsrk_gemv_q8_glu_f32_f16},
+         {K_nsrk_gemv_q8_glu_f16_f32, K_nsrk_gemv_q8_glu_f16_f16}},
+        {{K_nsrk_gemv_q8_h_f32, K_nsrk_gemv_q8_h_f32}, {K_nsrk_gemv_q8_h_f16, K_nsrk_gemv_q8_h_f16}}};
     block = 256;
-    name = std::string(kind[mode]) + dt_name(xd) + (mode == kGemvResLn ? "" : std::string("_") + dt_name(od));
+    kid = ids[mode][xi][oi];
     groups = (unsigned)(mode == kGemvGlu ? N / 8 : NW / 8);
   }
-  nsr_status st = launch(name, groups, 1, block, 0, stream, params);
+  nsr_status st = launch(kid, groups, 1, block, 0, stream, params);
   if (st != NSR_OK || mode != kGemvResLn) return st;
   // LayerNorm of the dim columns of h, weight only (one row)
   return ln_common(out_f32, NSR_F32, nullptr, NSR_F32, nullptr, NSR_F32, ln_w, nullptr, wd, out, od, 1, N, N, N, eps,
@@ -1103,7 +1157,7 @@ nsr_status nsr_q8_pack_t4(const uint32_t* qs, const uint16_t* scales, int64_t K,
   a.N = glu ? (int32_t)(NW / 2) : 0;
   const int64_t total = (NW / 4) * K + (NW / 4) * (K / 32);
   void* params[] = {&a};
-  return launch("nsrk_gemv_q8t4_pack", cdiv_u(total, 256), 1, 256, 0, stream, params);
+  return launch(K_nsrk_gemv_q8t4_pack, cdiv_u(total, 256), 1, 256, 0, stream, params);
 }
 
 static nsr_status q8_0_convert(const void* blocks, int64_t N, int64_t K, int t4, int glu, uint32_t* qs,
@@ -1126,7 +1180,7 @@ static nsr_status q8_0_convert(const void* blocks, int64_t N, int64_t K, int t4,
   a.glu_n = glu ? (int32_t)(N / 2) : 0;
   const int64_t total = (N / 4) * K + (N / 4) * (K / 32);
   void* params[] = {&a};
-  return launch("nsrk_gemv_q8_from_q8_0", cdiv_u(total, 256), 1, 256, 0, stream, params);
+  return launch(K_nsrk_gemv_q8_from_q8_0, cdiv_u(total, 256), 1, 256, 0, stream, params);
 }
 
 nsr_status nsr_q8_0_to_gemv_q8(const void* blocks, int64_t N, int64_t K, uint32_t* qs, uint16_t* scales,
@@ -1190,6 +1244,20 @@ nsr_status conv_validate(const float* x, const void* w, uintptr_t w_align, float
   return NSR_OK;
 }
 
+#define NSR_CONV_NU(p) {{K_##p##_nu3, K_##p##_nu4}, {K_##p##_nu3_st, K_##p##_nu4_st}}
+// [fused][residual][row statistics][nu 3, 4]
+const KId kConvRw[2][2][2][2] = {
+    {NSR_CONV_NU(nsrk_conv1d_rw_f16x2), NSR_CONV_NU(nsrk_conv1d_rw_res_f16x2)},
+    {NSR_CONV_NU(nsrk_conv1d_rw_adain_snake_f16x2), NSR_CONV_NU(nsrk_conv1d_rw_adain_snake_res_f16x2)}};
+const KId kConvPc[2][2][2][2] = {
+    {NSR_CONV_NU(nsrk_conv1d_pc_f16x2), NSR_CONV_NU(nsrk_conv1d_pc_res_f16x2)},
+    {NSR_CONV_NU(nsrk_conv1d_pc_adain_snake_f16x2), NSR_CONV_NU(nsrk_conv1d_pc_adain_snake_res_f16x2)}};
+#undef NSR_CONV_NU
+// [fused][np 9, 12, 16]
+const KId kConvNp[2][3] = {
+    {K_nsrk_conv1d_f16x2_np9, K_nsrk_conv1d_f16x2_np12, K_nsrk_conv1d_f16x2_np16},
+    {K_nsrk_conv1d_adain_snake_f16x2_np9, K_nsrk_conv1d_adain_snake_f16x2_np12, K_nsrk_conv1d_adain_snake_f16x2_np16}};
+
 nsr_status conv_launch(bool fused, nsr_conv_args& a, nsr_stream_t stream, const char* what, bool* emitted = nullptr) {
   DeviceModule* dm = nullptr;
   nsr_status st = current_module(&dm);
@@ -1214,9 +1282,8 @@ nsr_status conv_launch(bool fused, nsr_conv_args& a, nsr_stream_t stream, const 
       a.T_in > 0 && a.T_in % 4 == 0 && aligned(a.x, 16)) {
     const int64_t groups = std::min<int64_t>(tiles, (int64_t)dm->n_cu);
     if (emitted) *emitted = a.row_part != nullptr;
-    return launch(std::string("nsrk_conv1d_rw") + (fused ? "_adain_snake" : "") + (a.residual ? "_res" : "") +
-                      "_f16x2_nu" + (win <= 96 ? "3" : "4") + (a.row_part ? "_st" : ""),
-                  (unsigned)groups, 1, 512, (unsigned)lds_rw, stream, params);
+    return launch(kConvRw[fused][a.residual != nullptr][a.row_part != nullptr][win <= 96 ? 0 : 1], (unsigned)groups,
+                  1, 512, (unsigned)lds_rw, stream, params);
   }
   // any K, C_in in chunks and C_out in blocks of 128, 16-byte aligned rows: weights streamed one tap ahead
   // through two LDS slots, one 512-lane workgroup per CU (producer and consumer waves)
@@ -1224,17 +1291,16 @@ nsr_status conv_launch(bool fused, nsr_conv_args& a, nsr_stream_t stream, const 
   if (win <= 128 && lds_pc <= dm->max_lds && (a.pad_ & 1) && a.T_in > 0 && a.T_in % 4 == 0 && aligned(a.x, 16)) {
     const int64_t groups = std::min<int64_t>(tiles, (int64_t)dm->n_cu);
     if (emitted) *emitted = a.row_part != nullptr;
-    return launch(std::string("nsrk_conv1d_pc") + (fused ? "_adain_snake" : "") + (a.residual ? "_res" : "") +
-                      "_f16x2_nu" + (win <= 96 ? "3" : "4") + (a.row_part ? "_st" : ""),
-                  (unsigned)groups, 1, 512, (unsigned)lds_pc, stream, params);
+    return launch(kConvPc[fused][a.residual != nullptr][a.row_part != nullptr][win <= 96 ? 0 : 1], (unsigned)groups,
+                  1, 512, (unsigned)lds_pc, stream, params);
   }
   // the plain np 9 kernel fits two workgroups per CU in registers; the others one (no row statistics: the
   // caller takes them from the output)
   if (emitted) *emitted = false;
   const int per_cu = (!fused && np == 9 && 2 * lds <= dm->max_lds) ? 2 : 1;
   const int64_t groups = std::min<int64_t>(tiles, (int64_t)per_cu * dm->n_cu);
-  return launch(std::string(fused ? "nsrk_conv1d_adain_snake_f16x2_np" : "nsrk_conv1d_f16x2_np") + std::to_string(np),
-                (unsigned)groups, 1, 256, (unsigned)lds, stream, params);
+  return launch(kConvNp[fused][np == 9 ? 0 : np == 12 ? 1 : 2], (unsigned)groups, 1, 256, (unsigned)lds, stream,
+                params);
 }
 
 }  // namespace
@@ -1254,7 +1320,7 @@ nsr_status nsr_conv1d_pack_f16(const void* w, int64_t C_out, int64_t C_in, int64
   a.C_in = C_in;
   a.K = K;
   void* params[] = {&a};
-  return launch("nsrk_conv1d_pack", cdiv_u(C_out * C_in * K, 256), 1, 256, 0, stream, params);
+  return launch(K_nsrk_conv1d_pack, cdiv_u(C_out * C_in * K, 256), 1, 256, 0, stream, params);
 }
 
 // Launch a conv and leave the per-(b, co) statistics of its output in row_stats ([B*C_out][2]: mean,
@@ -1283,7 +1349,7 @@ static nsr_status conv_launch_stats(bool fused, nsr_conv_args& a, float eps, flo
     m.T_out = a.T_out;
     m.eps = eps;
     void* pm[] = {&m};
-    st = launch("nsrk_conv_rowstats_merge", (unsigned)rows, 1, 256, 0, stream, pm);
+    st = launch(K_nsrk_conv_rowstats_merge, (unsigned)rows, 1, 256, 0, stream, pm);
   } else if (st == NSR_OK) {
     nsr_adain_args s;
     std::memset(&s, 0, sizeof(s));
@@ -1296,7 +1362,7 @@ static nsr_status conv_launch_stats(bool fused, nsr_conv_args& a, float eps, flo
     s.inv_t = 1.0f / (float)a.T_out;
     void* ps[] = {&s};
     const bool rows16 = a.T_out % 4 == 0 && aligned(a.out, 16);
-    st = launch(rows16 ? "nsrk_adain_stats4" : "nsrk_adain_stats", (unsigned)rows, 1, 1024, 0, stream, ps);
+    st = launch(rows16 ? K_nsrk_adain_stats4 : K_nsrk_adain_stats, (unsigned)rows, 1, 1024, 0, stream, ps);
   }
   a.row_part = nullptr;
   hipFreeAsync(part, (hipStream_t)stream);
@@ -1393,7 +1459,7 @@ static nsr_status adain_conv_impl(const float* x, const float* x_stats, const vo
     s.inv_t = 1.0f / (float)T;
     void* p1[] = {&s};
     const bool rows16 = T % 4 == 0 && aligned(x, 16);
-    st = launch(rows16 ? "nsrk_adain_stats4" : "nsrk_adain_stats", (unsigned)(B * C_in), 1, 1024, 0, stream, p1);
+    st = launch(rows16 ? K_nsrk_adain_stats4 : K_nsrk_adain_stats, (unsigned)(B * C_in), 1, 1024, 0, stream, p1);
   }
   if (st == NSR_OK) {
     nsr_conv_args a;
@@ -1475,6 +1541,43 @@ nsr_status nsr_conv1d_f16w_packed_stats(const float* x, const void* w_packed, co
   a.padding = (int32_t)padding;
   a.dilation = (int32_t)dilation;
   return conv_launch_stats(false, a, eps, out_stats, stream, what);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------ measurement floors --
+
+extern "C" {
+
+nsr_status nsr_calib_empty(nsr_stream_t stream) {
+  nsr_calib_args a;
+  std::memset(&a, 0, sizeof(a));
+  void* params[] = {&a};
+  return launch(K_nsrk_calib_empty, 1, 1, 256, 0, stream, params);
+}
+
+nsr_status nsr_calib_copy(const void* src, void* dst, int64_t bytes, int form, int groups_per_cu,
+                          nsr_stream_t stream) {
+  if (!src || !dst) return fail(NSR_ERR_BAD_ARG, "calib_copy: null pointer");
+  if (bytes < 0 || bytes % 16 != 0 || !aligned(src, 16) || !aligned(dst, 16))
+    return fail(NSR_ERR_BAD_ARG, "calib_copy: bytes must be a multiple of 16 and pointers 16-byte aligned");
+  if (form < 0 || form > 2 || groups_per_cu < 0 || groups_per_cu > 64)
+    return fail(NSR_ERR_BAD_ARG, "calib_copy: form must be 0, 1 or 2 and groups_per_cu in [0, 64]");
+  if (bytes == 0) return NSR_OK;
+  const int64_t n4 = bytes / 16;
+  if ((n4 + 255) / 256 > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "calib_copy: too large");
+  DeviceModule* dm = nullptr;
+  nsr_status st = current_module(&dm);
+  if (st != NSR_OK) return st;
+  nsr_calib_args a;
+  a.src = (const float*)src;
+  a.dst = (float*)dst;
+  a.n4 = n4;
+  void* params[] = {&a};
+  if (form == 0) return launch(K_nsrk_calib_copy_flat, cdiv_u(n4, 256), 1, 256, 0, stream, params);
+  const int64_t tile = 256 * (form == 1 ? 4 : 8);
+  const int64_t groups = std::min<int64_t>((int64_t)(groups_per_cu ? groups_per_cu : 8) * dm->n_cu, (n4 + tile - 1) / tile);
+  return launch(form == 1 ? K_nsrk_calib_copy_p4 : K_nsrk_calib_copy_p8, (unsigned)groups, 1, 256, 0, stream, params);
 }
 
 }  // extern "C"

@@ -13,6 +13,9 @@ LLVM tools:
   state there from the compiler, and such stores were observed to write the
   overwritten values; the kernels keep store offsets in the VGPR address, and
   this test keeps it that way;
+* the runtime's kernel list (nsr_kernels.def, resolved in full when a
+  device's code objects load) names exactly the kernels each code object
+  holds, unit by unit;
 * no int -> float conversion reads a sign-extended sub-dword operand as
   unsigned (v_cvt_f32_u32 with an SDWA sext source). This compiler folds
   __builtin_amdgcn_sbfe(w, off, 8) followed by an int -> float conversion
@@ -28,7 +31,9 @@ import pytest
 ROOT = Path(__file__).resolve().parent.parent
 LIB = ROOT / "nspeech_amd" / "lib"
 LLVM = Path("/opt/rocm/llvm/bin")
-UNITS = ["q8_0_gather", "layernorm", "rotary", "adain_snake", "elementwise", "gemv_q8", "conv1d", "attention", "istft"]
+UNITS = ["q8_0_gather", "layernorm", "rotary", "adain_snake", "elementwise", "gemv_q8", "conv1d", "attention", "istft",
+         "calib"]
+KERNEL_LIST = ROOT / "nspeech_amd" / "csrc" / "runtime" / "nsr_kernels.def"
 
 
 def _co(unit):
@@ -143,3 +148,24 @@ def test_no_unsigned_convert_of_sign_extended_bytes(unit):
                          text=True, check=True).stdout
     hits = _UNSIGNED_CVT_OF_SEXT.findall(out)
     assert not hits, f"{unit}: {len(hits)} unsigned converts of sign-extended bytes"
+
+
+def _kernel_names(unit):
+    out = subprocess.run([_tool("llvm-readelf"), "--dyn-syms", str(_co(unit))], capture_output=True, text=True,
+                         check=True).stdout
+    return {line.split()[-1][:-3] for line in out.splitlines() if line.endswith(".kd")}
+
+
+def test_kernel_list_matches_code_objects():
+    listed = {}
+    for line in KERNEL_LIST.read_text().splitlines():
+        m = re.match(r"NSR_KERNEL\((\w+), (\w+)\)", line)
+        if m:
+            assert m.group(2) not in listed, f"{m.group(2)} listed twice"
+            listed[m.group(2)] = m.group(1)
+    for unit in UNITS:
+        built = _kernel_names(unit)
+        mine = {k for k, u in listed.items() if u == unit}
+        assert built == mine, f"{unit}: built but not listed {sorted(built - mine)}, listed but not built " \
+                              f"{sorted(mine - built)}"
+    assert set(listed.values()) <= set(UNITS)
