@@ -199,7 +199,7 @@ nsr_status nsr_kv_cache_append(const void* new_kv, void* cache, nsr_dtype dtype,
  * up to about 65k elements) x is read from HBM once and the statistics are
  * two passes over the on-chip row in f32 (the mean, then centred sums that
  * also correct the mean). Longer rows take a kernel that reads each row
- * twice (f64 sums, then the output; no scratch memory). */
+ * twice (f64 sums, then the output; no scratch memory).
  * Replaces adain (src/kokoro/decoder.rs:1416-1428) followed by
  * snake_activation_tensor (:1471-1476), and
  * KokoroGpuBackend::adain_snake_f32 (src/kokoro/gpu_backend.rs:181-185,

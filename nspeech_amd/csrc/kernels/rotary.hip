@@ -17,7 +17,12 @@
  * reference's own f32 values and the products are kept unfused
  * (fp contract off), giving the reference's rounding sequence exactly.
  * Without a table cos/sin are evaluated in-kernel (accurate sincosf) from
- * the same f32 angle.
+ * the same f32 angle. Measured on MI355X at config 1, each against the
+ * same box's copy of the same bytes: a 2-D grid (q / k in blockIdx.y, a
+ * lane's row and column from shifts, the first row's position from one
+ * scalar remainder per workgroup) reached 82% of the copy's rate (table
+ * path) against 86% for this flat grid with two 32-bit divisions per lane,
+ * so the flat grid is kept.
  */
 #include "device_common.h"
 
