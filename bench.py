@@ -231,7 +231,7 @@ def build_workload(name):
 
         alg = 2 * 2 * B * C * TT + 2 * 3 * C
         return Workload(name, f"AdaIN1d+Snake f16 activations x[{B},{C},{TT}]", alg, alg, make_set, launch,
-                        "nsrk_adain_f16_b256_nv3", "f16")
+                        "nsrk_adain_f16a_b256_nv3", "f16")
 
     if name == "c3":
         c = configs.c3()

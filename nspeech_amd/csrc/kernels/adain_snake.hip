@@ -516,6 +516,81 @@ NSR_ADAIN_F16(512, 24)
 NSR_ADAIN_F16(512, 28)
 NSR_ADAIN_F16(512, 32)
 
+/* f16 rows that start on 16 bytes with T % 8 == 0 (every row then does):
+ * one 256-lane workgroup per row, NV chunks of 8 halves per lane loaded with
+ * 16-byte buffer loads and unpacked to f32 once, then the same two passes and
+ * output as the f32 row kernel (only the last chunk of a lane can reach past
+ * the row; buffer loads there read 0 and stores are dropped). */
+template <int NV>
+NSR_DEV void adain_row_f16a(const nsr_adain_h_args& a, int pdt) {
+  NSR_NO_CONTRACT
+  constexpr int BLOCK = 256, NW = BLOCK / 64;
+  __shared__ float red[2 * NW];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  if (row >= a.n_rows) return;
+  const int64_t T = a.T;
+  const int nch = (int)(T >> 3);
+  const uint32_t rbytes = (uint32_t)(T * 2);
+  const uint32_t voff = (uint32_t)tid * 16u;
+  const adain_raw pr = adain_params_load(a, pdt, row / a.C, row % a.C);
+  const nsr_rsrc xr = make_rsrc(a.x + row * T, rbytes);
+  nsr_uint4 raw[NV];
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+    raw[k] = __builtin_amdgcn_raw_buffer_load_b128(xr, voff, (uint32_t)(k * BLOCK * 16), NSR_AUX_NT);
+  const int nvalid = nch > tid ? (nch - tid + BLOCK - 1) / BLOCK : 0;
+  float f[NV][8];
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    unpack16<DT_F16>(raw[k], f[k]);
+    const float t = ((f[k][0] + f[k][1]) + (f[k][2] + f[k][3])) + ((f[k][4] + f[k][5]) + (f[k][6] + f[k][7]));
+    s += k < nvalid ? t : 0.f;
+  }
+  const float mean = block_sum<NW>(s, red) * a.inv_t;
+  float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[k][e] = k < nvalid ? f[k][e] - mean : 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      s1 += f[k][e];
+      s2 = __builtin_fmaf(f[k][e], f[k][e], s2);
+    }
+  }
+  block_sum2<NW>(s1, s2, red);
+  const float c = s1 * a.inv_t;
+  const float var = fmaxf(__builtin_fmaf(-c, s1, s2) * a.inv_t, 0.0f);
+  const float rstd = 1.0f / sqrtf(var + a.eps);
+  float gam, bet, alp;
+  adain_params_cvt(pr, pdt, gam, bet, alp);
+  const float A = (gam + 1.0f) * rstd;
+  const float Bc = __builtin_fmaf(-c, A, bet);
+  const snake_consts sc = make_snake_consts(alp);
+  const nsr_rsrc orr = make_rsrc(a.out + row * T, rbytes);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = snake_eval(__builtin_fmaf(f[k][e], A, Bc), sc);
+    __builtin_amdgcn_raw_buffer_store_b128(pack16<DT_F16>(o), orr, voff + (uint32_t)(k * BLOCK * 16), 0, NSR_AUX_NT);
+  }
+}
+
+#define NSR_ADAIN_F16A(NV)                                                                 \
+  extern "C" __global__ void __launch_bounds__(256)                                       \
+      nsrk_adain_f16a_b256_nv##NV(const nsr_adain_h_args a, const int pdt) {              \
+    adain_row_f16a<NV>(a, pdt);                                                           \
+  }
+
+/* aligned f16 rows up to T = 8192 */
+NSR_ADAIN_F16A(1)
+NSR_ADAIN_F16A(2)
+NSR_ADAIN_F16A(3)
+NSR_ADAIN_F16A(4)
+
 /* ------------------------------------------------ row statistics, long rows -- */
 
 /* Sum and sum of squares of one row over 1024 lanes in f64, one HBM read:

@@ -743,6 +743,28 @@ nsr_status nsr_adain_snake_f16(const void* x, const void* gamma, const void* bet
   if (n_rows == 0) return NSR_OK;
   if (n_rows > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "adain_snake_f16: too many rows");
   if (T > 131072) return fail(NSR_ERR_UNSUPPORTED, "adain_snake_f16: rows longer than 131072 elements");
+  // rows starting on 16 bytes (T % 8 == 0, x and out 16-byte aligned) up to T = 8192: the aligned kernel
+  if (aligned(x, 16) && aligned(out, 16) && T % 8 == 0 && T <= 8 * 256 * 4) {
+    static const KId ids[] = {K_nsrk_adain_f16a_b256_nv1, K_nsrk_adain_f16a_b256_nv2, K_nsrk_adain_f16a_b256_nv3,
+                              K_nsrk_adain_f16a_b256_nv4};
+    nsr_adain_h_args a;
+    std::memset(&a, 0, sizeof(a));
+    a.x = (const uint16_t*)x;
+    a.gamma = gamma;
+    a.beta = beta;
+    a.alpha = alpha;
+    a.out = (uint16_t*)out;
+    a.n_rows = n_rows;
+    a.T = T;
+    a.gamma_bstride = gamma_bstride;
+    a.beta_bstride = beta_bstride;
+    a.C = (int32_t)C;
+    a.eps = eps;
+    a.inv_t = 1.0f / (float)T;
+    int pdt = param_dtype == NSR_F32 ? 0 : 1;
+    void* params[] = {&a, &pdt};
+    return launch(ids[(T / 8 + 255) / 256 - 1], (unsigned)n_rows, 1, 256, 0, stream, params);
+  }
   // interior 16-byte chunks of a row, at the worst offset (7 elements into its first chunk)
   const int64_t need = (T + 14) / 8 - 2;
   unsigned block = 0;
