@@ -336,6 +336,22 @@ nsr_status nsr_attention_splitkv_f16(const void* q, const void* k, const void* v
                                      float sm_scale, int64_t stride_kv_head, int64_t stride_kv_seq, int64_t n_splits,
                                      nsr_stream_t stream);
 
+/* nsr_attention_splitkv_f16 without the `partial` argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * The partials go to a fixed scratch array of NSR_NOALLOC_SCRATCH_BYTES
+ * (1 MiB) that the library holds on each GPU it runs on until the process
+ * ends; calls needing more than that, n_q_heads * n_splits * (head_dim + 2)
+ * > 262144 floats, fail with NSR_ERR_UNSUPPORTED. The call allocates
+ * nothing. Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, other host threads) race and must be
+ * serialised by the caller. Same results as nsr_attention_splitkv_f16. */
+#define NSR_NOALLOC_SCRATCH_BYTES (1024 * 1024)
+nsr_status nsr_attention_splitkv_f16_noalloc(const void* q, const void* k, const void* v, void* out,
+                                             int64_t kv_len, int64_t head_dim, int64_t n_kv_heads,
+                                             int64_t n_q_heads, float sm_scale, int64_t stride_kv_head,
+                                             int64_t stride_kv_seq, int64_t n_splits, nsr_stream_t stream);
+
 /* The same attention in one launch and without scratch: one workgroup per
  * query head, whose waves take every W-th chunk of 64 positions and merge
  * in LDS. Replaces triton_attention_decode /

@@ -95,6 +95,8 @@ def lib() -> C.CDLL:
         L.nsr_resblock_average_f32.argtypes = [_P, _P, _P, _P, _I64, C.c_int, C.c_float, _P]
         L.nsr_istft_f32.argtypes = [_P, _P, _I64, _I64, C.c_int, C.c_int, _P]
         L.nsr_snake.argtypes = [_P, C.c_int, _P, C.c_int, _P, _I64, _I64, _I64, _P]
+        L.nsr_attention_splitkv_f16_noalloc.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, C.c_float, _I64,
+                                                        _I64, _I64, _P]
         L.nsr_calib_empty.argtypes = [_P]
         L.nsr_calib_copy.argtypes = [_P, _P, _I64, C.c_int, C.c_int, _P]
         for name in ("nsr_init", "nsr_layernorm", "nsr_residual_add_layernorm", "nsr_rope_table_f32",
@@ -107,7 +109,8 @@ def lib() -> C.CDLL:
                      "nsr_adain_snake_conv1d_f32", "nsr_attention_splitkv_f16", "nsr_attention_decode_f16",
                      "nsr_scale_f32", "nsr_leaky_relu_f32", "nsr_resblock_average_f32", "nsr_istft_f32", "nsr_snake",
                      "nsr_adain_snake_conv1d_chain_f32", "nsr_conv1d_f16w_packed_stats",
-                     "nsr_gemv_q8_t4_bias_glu", "nsr_gemv_q8_t4_resadd_ln", "nsr_calib_empty", "nsr_calib_copy"):
+                     "nsr_gemv_q8_t4_bias_glu", "nsr_gemv_q8_t4_resadd_ln", "nsr_calib_empty", "nsr_calib_copy",
+                     "nsr_attention_splitkv_f16_noalloc"):
             getattr(L, name).restype = C.c_int
         _lib = L
     return _lib

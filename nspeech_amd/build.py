@@ -70,9 +70,21 @@ def build_code_objects() -> list[Path]:
         return list(ex.map(one, UNITS))
 
 
+def build_scratch_object() -> Path:
+    """runtime/nsr_scratch.hip (the fixed per-device scratch of the entry
+    points that allocate nothing) as a host object with its gfx950 device
+    code embedded, linked into libnspeech_rocm.so."""
+    out = LIB / "nsr_scratch.o"
+    _run([str(HIPCC), "-c", "-fPIC", "-O2", "-std=c++17", f"--offload-arch={ARCH}",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          str(CSRC / "runtime" / "nsr_scratch.hip"), "-o", str(out)])
+    return out
+
+
 def build_library() -> Path:
     out = LIB / "libnspeech_rocm.so"
     tmp = LIB / "libnspeech_rocm.so.tmp"
+    scratch = build_scratch_object()
     cmd = [
         "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math",
         "-Wall", "-Wextra", "-Wno-unused-parameter",
@@ -81,6 +93,7 @@ def build_library() -> Path:
         f"-DNSR_CO_DIR={LIB}",
         str(CSRC / "runtime" / "nsr_runtime.cpp"),
         str(CSRC / "runtime" / "nsr_embed.S"),
+        str(scratch),
         f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}",
         "-Wl,--no-undefined",
         "-o", str(tmp),

@@ -26,6 +26,7 @@
 #include <string>
 
 #include "../nsr_kargs.h"
+#include "nsr_scratch.h"
 
 // Embedded code objects, one per kernel unit (nsr_embed.S).
 extern "C" const unsigned char nsr_co_q8_0_gather[];
@@ -248,7 +249,14 @@ nsr_status nsr_init(const char* code_object_dir) {
     g_code_object_path = code_object_dir ? code_object_dir : "";
   }
   DeviceModule* dm = nullptr;
-  return current_module(&dm);
+  nsr_status st = current_module(&dm);
+  if (st != NSR_OK) return st;
+  // set up this device's fixed scratch for the entry points that allocate nothing; a failure here is
+  // reported by those entry points when they are called
+  int dev = 0;
+  float* scratch_ptr = nullptr;
+  if (hipGetDevice(&dev) == hipSuccess) (void)nsr_scratch_device_ptr(dev, &scratch_ptr);
+  return NSR_OK;
 }
 
 int nsr_kernel_count(void) {
@@ -559,18 +567,26 @@ nsr_status attn_validate(const void* q, const void* k, const void* v, void* out,
 
 }  // namespace
 
-nsr_status nsr_attention_splitkv_f16(const void* q, const void* k, const void* v, void* out, float* partial,
-                                     int64_t kv_len, int64_t head_dim, int64_t n_kv_heads, int64_t n_q_heads,
-                                     float sm_scale, int64_t stride_kv_head, int64_t stride_kv_seq, int64_t n_splits,
-                                     nsr_stream_t stream) {
+namespace {
+
+// Validation shared by the split-KV entry points (partial checked by the caller).
+nsr_status splitkv_validate(const void* q, const void* k, const void* v, void* out, int64_t kv_len, int64_t head_dim,
+                            int64_t n_kv_heads, int64_t n_q_heads, float sm_scale, int64_t stride_kv_head,
+                            int64_t stride_kv_seq, int64_t n_splits, const char* what) {
   nsr_status st = attn_validate(q, k, v, out, kv_len, head_dim, n_kv_heads, n_q_heads, sm_scale, stride_kv_head,
-                                stride_kv_seq, "attention_splitkv");
+                                stride_kv_seq, what);
   if (st != NSR_OK) return st;
-  if (!partial) return fail(NSR_ERR_BAD_ARG, "attention_splitkv: null partial buffer");
   if (n_splits < 1 || n_splits > 65535 || n_q_heads * n_splits > 0x7fffffffLL)
-    return fail(NSR_ERR_BAD_ARG, "attention_splitkv: n_splits=%lld out of range", (long long)n_splits);
+    return fail(NSR_ERR_BAD_ARG, "%s: n_splits=%lld out of range", what, (long long)n_splits);
+  return NSR_OK;
+}
+
+// The split-KV launches (partial kernel, then reduce) over a validated call.
+nsr_status splitkv_launch(const void* q, const void* k, const void* v, void* out, float* partial, int64_t kv_len,
+                          int64_t head_dim, int64_t n_kv_heads, int64_t n_q_heads, float sm_scale,
+                          int64_t stride_kv_head, int64_t stride_kv_seq, int64_t n_splits, nsr_stream_t stream) {
   DeviceModule* dm = nullptr;
-  st = current_module(&dm);
+  nsr_status st = current_module(&dm);
   if (st != NSR_OK) return st;
   nsr_attn_args a;
   attn_fill(a, q, k, v, out, partial, kv_len, head_dim, n_kv_heads, n_q_heads, sm_scale, stride_kv_head,
@@ -580,6 +596,50 @@ nsr_status nsr_attention_splitkv_f16(const void* q, const void* k, const void* v
               64, (unsigned)attn_wave_lds_bytes(head_dim), stream, params);
   if (st != NSR_OK) return st;
   return launch(K_nsrk_attn_reduce, (unsigned)n_q_heads, 1, 128, 0, stream, params);
+}
+
+}  // namespace
+
+nsr_status nsr_attention_splitkv_f16(const void* q, const void* k, const void* v, void* out, float* partial,
+                                     int64_t kv_len, int64_t head_dim, int64_t n_kv_heads, int64_t n_q_heads,
+                                     float sm_scale, int64_t stride_kv_head, int64_t stride_kv_seq, int64_t n_splits,
+                                     nsr_stream_t stream) {
+  nsr_status st = splitkv_validate(q, k, v, out, kv_len, head_dim, n_kv_heads, n_q_heads, sm_scale, stride_kv_head,
+                                   stride_kv_seq, n_splits, "attention_splitkv");
+  if (st != NSR_OK) return st;
+  if (!partial) return fail(NSR_ERR_BAD_ARG, "attention_splitkv: null partial buffer");
+  return splitkv_launch(q, k, v, out, partial, kv_len, head_dim, n_kv_heads, n_q_heads, sm_scale, stride_kv_head,
+                        stride_kv_seq, n_splits, stream);
+}
+
+nsr_status nsr_attention_splitkv_f16_noalloc(const void* q, const void* k, const void* v, void* out, int64_t kv_len,
+                                             int64_t head_dim, int64_t n_kv_heads, int64_t n_q_heads, float sm_scale,
+                                             int64_t stride_kv_head, int64_t stride_kv_seq, int64_t n_splits,
+                                             nsr_stream_t stream) {
+  const char* what = "attention_splitkv_noalloc";
+  nsr_status st = splitkv_validate(q, k, v, out, kv_len, head_dim, n_kv_heads, n_q_heads, sm_scale, stride_kv_head,
+                                   stride_kv_seq, n_splits, what);
+  if (st != NSR_OK) return st;
+  const int64_t need = n_q_heads * n_splits * (head_dim + 2);
+  if (need > NSR_NOALLOC_SCRATCH_FLOATS)
+    return fail(NSR_ERR_UNSUPPORTED,
+                "%s: n_q_heads * n_splits * (head_dim + 2) = %lld floats exceeds the fixed scratch of %d floats "
+                "(use nsr_attention_splitkv_f16 with a caller buffer, or fewer splits)",
+                what, (long long)need, NSR_NOALLOC_SCRATCH_FLOATS);
+  DeviceModule* dm = nullptr;
+  st = current_module(&dm);
+  if (st != NSR_OK) return st;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(NSR_ERR_HIP, "%s: hipGetDevice: %s", what, hipGetErrorString(e));
+  float* scratch_ptr = nullptr;
+  e = nsr_scratch_device_ptr(dev, &scratch_ptr);
+  if (e != hipSuccess || !scratch_ptr)
+    return fail(NSR_ERR_HIP, "%s: resolving the fixed scratch: %s", what, hipGetErrorString(e));
+  // every (head, split) slot the reduce reads is written by the partial kernel of the same call: nothing in the
+  // scratch needs clearing
+  return splitkv_launch(q, k, v, out, scratch_ptr, kv_len, head_dim, n_kv_heads, n_q_heads, sm_scale, stride_kv_head,
+                        stride_kv_seq, n_splits, stream);
 }
 
 nsr_status nsr_attention_decode_f16(const void* q, const void* k, const void* v, void* out, int64_t kv_len,
