@@ -434,6 +434,7 @@ def build_workload(name):
         bias = torch.from_numpy(g.standard_normal(C).astype(np.float16)).to(dev)
         gs = C if c["gamma"].ndim == 2 else 0
         y = torch.empty_like(x0) if name == "kconv3u" else None
+        ws = abi.conv_workspace(B, C, C, TT, K, pad, dil, abi.WS_IN_STATS, dev)
 
         def make_set(_):
             return {"x": x0, "o": torch.empty_like(x0)}
@@ -447,7 +448,8 @@ def build_workload(name):
             else:
                 abi.check(L.nsr_adain_snake_conv1d_f32(s["x"].data_ptr(), g_.data_ptr(), b_.data_ptr(), a_.data_ptr(),
                                                        0, gs, gs, wp.data_ptr(), bias.data_ptr(), None,
-                                                       s["o"].data_ptr(), B, C, C, TT, K, pad, dil, 1e-5, stream()))
+                                                       s["o"].data_ptr(), B, C, C, TT, K, pad, dil, 1e-5,
+                                                       ws.data_ptr(), ws.numel(), stream()))
 
         alg = 2 * x0.numel() * 4
         flops = 2 * C * C * K * TT * B
@@ -474,8 +476,10 @@ def build_workload(name):
         gs = C if c["gamma"].ndim == 2 else 0
         xs = torch.empty((B * C, 2), dtype=torch.float32, device=dev)
         tmp = torch.empty_like(x0)
+        ws = abi.conv_workspace(B, C, C, TT, K, pad, dil, abi.WS_OUT_STATS, dev)
         abi.check(L.nsr_conv1d_f16w_packed_stats(x0.data_ptr(), wp.data_ptr(), None, None, tmp.data_ptr(),
-                                                 xs.data_ptr(), B, C, C, TT, K, pad, dil, 1e-5, stream()))
+                                                 xs.data_ptr(), B, C, C, TT, K, pad, dil, 1e-5, ws.data_ptr(),
+                                                 ws.numel(), stream()))
         # (statistics of some f32 [B, C, T] tensor; the timed calls use them for x, which only changes the values)
         del tmp
 
@@ -487,7 +491,8 @@ def build_workload(name):
             abi.check(L.nsr_adain_snake_conv1d_chain_f32(s["x"].data_ptr(), xs.data_ptr(), g_.data_ptr(),
                                                          b_.data_ptr(), a_.data_ptr(), 0, gs, gs, wp.data_ptr(),
                                                          bias.data_ptr(), None, s["o"].data_ptr(), s["s"].data_ptr(),
-                                                         B, C, C, TT, K, pad, dil, 1e-5, stream()))
+                                                         B, C, C, TT, K, pad, dil, 1e-5, ws.data_ptr(), ws.numel(),
+                                                         stream()))
 
         alg = 2 * x0.numel() * 4
         flops = 2 * C * C * K * TT * B

@@ -373,8 +373,9 @@ nsr_status nsr_attention_decode_f16(const void* q, const void* k, const void* v,
  * dilation <= 64; T_in, T_out < 2^23; stride != 1 returns
  * NSR_ERR_UNSUPPORTED. Rows that start 16-byte aligned (T_in % 4 == 0,
  * T_out % 4 == 0, 16-byte aligned x / out / residual) take the faster
- * producer/consumer kernels. Packs the weights into
- * stream-ordered scratch on every call; callers that convolve repeatedly
+ * producer/consumer kernels. Packs the weights into the caller's workspace
+ * (NSR_WS_PACKED_WEIGHTS, see nsr_conv1d_workspace_bytes) on every call and
+ * allocates nothing; callers that convolve repeatedly with the same weights
  * pack once with nsr_conv1d_pack_f16 and call nsr_conv1d_f16w_packed.
  * Replaces KokoroGpuBackend::conv1d_f32 (src/kokoro/gpu_backend.rs:165-167;
  * Metal impl src/kokoro/gpu_decoder.rs:840, which runs conv1d_f32io,
@@ -383,7 +384,26 @@ nsr_status nsr_attention_decode_f16(const void* q, const void* k, const void* v,
  * (src/kokoro/decoder.rs:1366-1367, 1373-1374). */
 nsr_status nsr_conv1d_f32io(const float* x, const void* w, const void* bias, float* out, int64_t B,
                             int64_t C_in, int64_t C_out, int64_t T_in, int64_t K, int64_t stride,
-                            int64_t padding, int64_t dilation, nsr_stream_t stream);
+                            int64_t padding, int64_t dilation, void* workspace, int64_t workspace_bytes,
+                            nsr_stream_t stream);
+
+/* Device workspace of the conv entry points that need one: caller-owned,
+ * 256-byte aligned, held by one call until its launches have run on the
+ * stream. The library allocates nothing on these paths. Parts (OR them):
+ *   NSR_WS_PACKED_WEIGHTS  nsr_conv1d_f32io's packed weights,
+ *   NSR_WS_IN_STATS        the input's row statistics (nsr_adain_snake_conv1d_f32,
+ *                          and _chain when x_stats is NULL),
+ *   NSR_WS_OUT_STATS       per-32-column partials of the output's row
+ *                          statistics (_chain and nsr_conv1d_f16w_packed_stats
+ *                          when out_stats is not NULL).
+ * nsr_conv1d_workspace_bytes writes the bytes a call of that shape needs for
+ * the given parts (each part at a 256-byte aligned offset, in flag order).
+ * No counterpart in the reference (its Metal backend allocates per call). */
+#define NSR_WS_PACKED_WEIGHTS 1u
+#define NSR_WS_IN_STATS 2u
+#define NSR_WS_OUT_STATS 4u
+nsr_status nsr_conv1d_workspace_bytes(int64_t B, int64_t C_in, int64_t C_out, int64_t T_in, int64_t K,
+                                      int64_t padding, int64_t dilation, unsigned parts, int64_t* bytes);
 
 /* Weights [C_out, C_in, K] f16 -> the packed [C_out, K, C_in] f16 layout the
  * conv kernels read (16-byte aligned output, C_out*C_in*K halfs). No
@@ -406,8 +426,8 @@ nsr_status nsr_conv1d_f16w_packed(const float* x, const void* w_packed, const vo
  *   out = conv1d(y, w_packed) + bias (+ residual)
  * x [B, C_in, T] f32; gamma/beta/alpha as nsr_adain_snake_f32 (F32 or F16,
  * batch strides); y is never written to memory. Two launches (row
- * statistics, then the fused conv) and 8 bytes per row of stream-ordered
- * scratch. Replaces adain + snake_activation_tensor + conv1d + bias of
+ * statistics into the caller's workspace, NSR_WS_IN_STATS, then the fused
+ * conv); allocates nothing. Replaces adain + snake_activation_tensor + conv1d + bias of
  * ResBlock::forward (:1364-1376; Metal: adain_snake then conv1d_f32io,
  * src/kokoro/gpu_decoder.rs:886-950). */
 nsr_status nsr_adain_snake_conv1d_f32(const float* x, const void* gamma, const void* beta,
@@ -416,7 +436,8 @@ nsr_status nsr_adain_snake_conv1d_f32(const float* x, const void* gamma, const v
                                       const void* w_packed, const void* bias,
                                       const float* residual, float* out, int64_t B, int64_t C_in,
                                       int64_t C_out, int64_t T, int64_t K, int64_t padding,
-                                      int64_t dilation, float eps, nsr_stream_t stream);
+                                      int64_t dilation, float eps, void* workspace,
+                                      int64_t workspace_bytes, nsr_stream_t stream);
 
 /* The same ResBlock stage with the row statistics handed along the chain
  * instead of re-read. x_stats ([B*C_in][2]: mean, 1 / sqrt(var + eps) of
@@ -425,7 +446,9 @@ nsr_status nsr_adain_snake_conv1d_f32(const float* x, const void* gamma, const v
  * pair for each row of out (after bias and residual), for the next stage's
  * AdaIN. With 16-byte aligned rows the conv's epilogue produces them from
  * registers (per 32-column block count, mean and M2, merged per row by
- * Chan's pairwise formula) instead of a second read of out. No counterpart
+ * Chan's pairwise formula) instead of a second read of out. Workspace:
+ * NSR_WS_IN_STATS when x_stats is NULL, NSR_WS_OUT_STATS when out_stats is
+ * not NULL (0 bytes, workspace may be NULL, when neither). No counterpart
  * in the reference, whose ResBlock (src/kokoro/decoder.rs:1352-1380, GPU
  * path :1087-1160) runs adain_snake_f32 and conv1d_f32 one after the other;
  * the results match nsr_adain_snake_conv1d_f32 within the fp32 bar. */
@@ -435,16 +458,17 @@ nsr_status nsr_adain_snake_conv1d_chain_f32(const float* x, const float* x_stats
                                             const void* w_packed, const void* bias,
                                             const float* residual, float* out, float* out_stats,
                                             int64_t B, int64_t C_in, int64_t C_out, int64_t T, int64_t K,
-                                            int64_t padding, int64_t dilation, float eps,
-                                            nsr_stream_t stream);
+                                            int64_t padding, int64_t dilation, float eps, void* workspace,
+                                            int64_t workspace_bytes, nsr_stream_t stream);
 
 /* nsr_conv1d_f16w_packed that also writes out_stats ([B*C_out][2]: mean,
- * 1 / sqrt(var + eps) of each output row), for an AdaIN that follows. */
+ * 1 / sqrt(var + eps) of each output row), for an AdaIN that follows.
+ * Workspace: NSR_WS_OUT_STATS. */
 nsr_status nsr_conv1d_f16w_packed_stats(const float* x, const void* w_packed, const void* bias,
                                         const float* residual, float* out, float* out_stats, int64_t B,
                                         int64_t C_in, int64_t C_out, int64_t T_in, int64_t K,
-                                        int64_t padding, int64_t dilation, float eps,
-                                        nsr_stream_t stream);
+                                        int64_t padding, int64_t dilation, float eps, void* workspace,
+                                        int64_t workspace_bytes, nsr_stream_t stream);
 
 /* ---- Repacked-Q8 GEMV (decoder projections at M = 1) ---------------------- */
 

@@ -73,15 +73,18 @@ def lib() -> C.CDLL:
                                             C.c_float, _P]
         L.nsr_q8_pack_t4.argtypes = [_P, _P, _I64, _I64, C.c_int, _P, _P, _P]
         L.nsr_q8_0_to_gemv_q8.argtypes = [_P, _I64, _I64, _P, _P, _P]
-        L.nsr_conv1d_f32io.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]
+        L.nsr_conv1d_f32io.argtypes = [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P]
+        L.nsr_conv1d_workspace_bytes.argtypes = [_I64, _I64, _I64, _I64, _I64, _I64, _I64, C.c_uint,
+                                                 C.POINTER(C.c_int64)]
         L.nsr_conv1d_pack_f16.argtypes = [_P, _I64, _I64, _I64, _P, _P]
         L.nsr_conv1d_f16w_packed.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P]
         L.nsr_adain_snake_conv1d_f32.argtypes = [_P, _P, _P, _P, C.c_int, _I64, _I64, _P, _P, _P, _P, _I64, _I64,
-                                                 _I64, _I64, _I64, _I64, _I64, C.c_float, _P]
+                                                 _I64, _I64, _I64, _I64, _I64, C.c_float, _P, _I64, _P]
         L.nsr_adain_snake_conv1d_chain_f32.argtypes = [_P, _P, _P, _P, _P, C.c_int, _I64, _I64, _P, _P, _P, _P, _P,
-                                                       _I64, _I64, _I64, _I64, _I64, _I64, _I64, C.c_float, _P]
+                                                       _I64, _I64, _I64, _I64, _I64, _I64, _I64, C.c_float, _P, _I64,
+                                                       _P]
         L.nsr_conv1d_f16w_packed_stats.argtypes = [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
-                                                   C.c_float, _P]
+                                                   C.c_float, _P, _I64, _P]
         L.nsr_q8_0_to_t4.argtypes = [_P, _I64, _I64, C.c_int, _P, _P, _P]
         L.nsr_gemv_q8_t4.argtypes = [_P, C.c_int, _P, _P, _P, _P, C.c_int, _I64, _I64, _P]
         L.nsr_gemv_q8_t4_bias_glu.argtypes = [_P, C.c_int, _P, _P, _P, _P, C.c_int, _I64, _I64, _P]
@@ -110,7 +113,7 @@ def lib() -> C.CDLL:
                      "nsr_scale_f32", "nsr_leaky_relu_f32", "nsr_resblock_average_f32", "nsr_istft_f32", "nsr_snake",
                      "nsr_adain_snake_conv1d_chain_f32", "nsr_conv1d_f16w_packed_stats",
                      "nsr_gemv_q8_t4_bias_glu", "nsr_gemv_q8_t4_resadd_ln", "nsr_calib_empty", "nsr_calib_copy",
-                     "nsr_attention_splitkv_f16_noalloc"):
+                     "nsr_attention_splitkv_f16_noalloc", "nsr_conv1d_workspace_bytes"):
             getattr(L, name).restype = C.c_int
         _lib = L
     return _lib
@@ -398,14 +401,37 @@ def _conv_tout(T, K, padding, dilation):
     return T + 2 * padding - dilation * (K - 1)
 
 
-def conv1d_f32io(x, w, bias=None, *, padding=0, dilation=1, out=None, stream=None):
-    """x f32 [B, C_in, T]; w f16 [C_out, C_in, K]; bias f16 [C_out] or None."""
+WS_PACKED_WEIGHTS, WS_IN_STATS, WS_OUT_STATS = 1, 2, 4
+
+
+def conv1d_workspace_bytes(B, C_in, C_out, T, K, padding, dilation, parts) -> int:
+    """Bytes of device workspace a conv entry point of this shape needs for `parts` (WS_* flags ORed)."""
+    n = C.c_int64(0)
+    check(lib().nsr_conv1d_workspace_bytes(B, C_in, C_out, T, K, padding, dilation, parts, C.byref(n)))
+    return n.value
+
+
+def conv_workspace(B, C_in, C_out, T, K, padding, dilation, parts, device="cuda"):
+    """A device workspace (uint8 tensor, 256-byte aligned as torch allocates) for those parts, or None."""
+    n = conv1d_workspace_bytes(B, C_in, C_out, T, K, padding, dilation, parts)
+    return torch.empty(n, dtype=torch.uint8, device=device) if n else None
+
+
+def _ws(t):
+    return (_ptr(t), t.numel()) if t is not None else (None, 0)
+
+
+def conv1d_f32io(x, w, bias=None, *, padding=0, dilation=1, out=None, workspace=None, stream=None):
+    """x f32 [B, C_in, T]; w f16 [C_out, C_in, K]; bias f16 [C_out] or None. The packed weights go to
+    `workspace` (allocated here when not given)."""
     B, C_in, T = x.shape
     C_out, _, K = w.shape
     if out is None:
         out = torch.empty((B, C_out, _conv_tout(T, K, padding, dilation)), dtype=torch.float32, device=x.device)
+    if workspace is None:
+        workspace = conv_workspace(B, C_in, C_out, T, K, padding, dilation, WS_PACKED_WEIGHTS, x.device)
     check(lib().nsr_conv1d_f32io(_ptr(x), _ptr(w), _ptr(bias), _ptr(out), B, C_in, C_out, T, K, 1, padding,
-                                 dilation, _stream(stream)))
+                                 dilation, *_ws(workspace), _stream(stream)))
     return out
 
 
@@ -438,9 +464,11 @@ def adain_snake_conv1d_chain(x, gamma, beta, alpha, wp, bias=None, residual=None
     st = torch.empty((B * C_out, 2), dtype=torch.float32, device=x.device) if want_stats else None
     gs = C_in if gamma.dim() == 2 else 0
     bs = C_in if beta.dim() == 2 else 0
+    parts = (0 if x_stats is not None else WS_IN_STATS) | (WS_OUT_STATS if want_stats else 0)
+    ws = conv_workspace(B, C_in, C_out, T, K, padding, dilation, parts, x.device)
     check(lib().nsr_adain_snake_conv1d_chain_f32(_ptr(x), _ptr(x_stats), _ptr(gamma), _ptr(beta), _ptr(alpha),
                                                  _dt(gamma), gs, bs, _ptr(wp), _ptr(bias), _ptr(residual), _ptr(out),
-                                                 _ptr(st), B, C_in, C_out, T, K, padding, dilation, eps,
+                                                 _ptr(st), B, C_in, C_out, T, K, padding, dilation, eps, *_ws(ws),
                                                  _stream(stream)))
     return out, st
 
@@ -453,8 +481,9 @@ def conv1d_f16w_packed_stats(x, wp, bias=None, residual=None, *, padding=0, dila
     if out is None:
         out = torch.empty((B, C_out, _conv_tout(T, K, padding, dilation)), dtype=torch.float32, device=x.device)
     st = torch.empty((B * C_out, 2), dtype=torch.float32, device=x.device)
+    ws = conv_workspace(B, C_in, C_out, T, K, padding, dilation, WS_OUT_STATS, x.device)
     check(lib().nsr_conv1d_f16w_packed_stats(_ptr(x), _ptr(wp), _ptr(bias), _ptr(residual), _ptr(out), _ptr(st), B,
-                                             C_in, C_out, T, K, padding, dilation, eps, _stream(stream)))
+                                             C_in, C_out, T, K, padding, dilation, eps, *_ws(ws), _stream(stream)))
     return out, st
 
 
@@ -468,9 +497,10 @@ def adain_snake_conv1d(x, gamma, beta, alpha, wp, bias=None, residual=None, *, p
         out = torch.empty((B, C_out, _conv_tout(T, K, padding, dilation)), dtype=torch.float32, device=x.device)
     gs = C_in if gamma.dim() == 2 else 0
     bs = C_in if beta.dim() == 2 else 0
+    ws = conv_workspace(B, C_in, C_out, T, K, padding, dilation, WS_IN_STATS, x.device)
     check(lib().nsr_adain_snake_conv1d_f32(_ptr(x), _ptr(gamma), _ptr(beta), _ptr(alpha), _dt(gamma), gs, bs,
                                            _ptr(wp), _ptr(bias), _ptr(residual), _ptr(out), B, C_in, C_out, T, K,
-                                           padding, dilation, eps, _stream(stream)))
+                                           padding, dilation, eps, *_ws(ws), _stream(stream)))
     return out
 
 

@@ -1406,19 +1406,13 @@ nsr_status nsr_conv1d_pack_f16(const void* w, int64_t C_out, int64_t C_in, int64
 }
 
 // Launch a conv and leave the per-(b, co) statistics of its output in row_stats ([B*C_out][2]: mean,
-// 1 / sqrt(var + eps)): the aligned-row kernels emit per-32-column (mean, M2) blocks from their
-// epilogue into stream-ordered scratch and a merge kernel combines them; the fallback kernel's output is
-// re-read by the row statistics kernel instead.
-static nsr_status conv_launch_stats(bool fused, nsr_conv_args& a, float eps, float* row_stats, nsr_stream_t stream,
-                                    const char* what) {
+// 1 / sqrt(var + eps)): the aligned-row kernels emit per-32-column (mean, M2) blocks from their epilogue into
+// `part` (the caller's workspace, [B*C_out][ceil(T_out / 32)][2] f32) and a merge kernel combines them; the
+// fallback kernel's output is re-read by the row statistics kernel instead.
+static nsr_status conv_launch_stats(bool fused, nsr_conv_args& a, float eps, float* row_stats, float* part,
+                                    nsr_stream_t stream, const char* what) {
   const int64_t rows = (int64_t)a.B * a.C_out, nblk = ((int64_t)a.T_out + 31) / 32;
   if (rows > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "%s: too many rows", what);
-  float* part = nullptr;
-  hipError_t e = hipMallocAsync((void**)&part, (size_t)(rows * nblk) * 2 * sizeof(float), (hipStream_t)stream);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(NSR_ERR_HIP, "%s: hipMallocAsync: %s", what, hipGetErrorString(e));
-  }
   a.row_part = part;
   bool emitted = false;
   nsr_status st = conv_launch(fused, a, stream, what, &emitted);
@@ -1447,8 +1441,37 @@ static nsr_status conv_launch_stats(bool fused, nsr_conv_args& a, float eps, flo
     st = launch(rows16 ? K_nsrk_adain_stats4 : K_nsrk_adain_stats, (unsigned)rows, 1, 1024, 0, stream, ps);
   }
   a.row_part = nullptr;
-  hipFreeAsync(part, (hipStream_t)stream);
   return st;
+}
+
+// Workspace parts of the conv entry points, each at a 256-byte aligned offset in the order of the flags.
+static int64_t ws_round(int64_t b) { return (b + 255) / 256 * 256; }
+
+static void conv_ws_layout(int64_t B, int64_t C_in, int64_t C_out, int64_t T_out, int64_t K, unsigned parts,
+                           int64_t off[3], int64_t* total) {
+  int64_t o = 0;
+  const int64_t sz[3] = {ws_round(C_out * C_in * K * 2), ws_round(B * C_in * 2 * 4),
+                         ws_round(B * C_out * ((T_out + 31) / 32) * 2 * 4)};
+  for (int i = 0; i < 3; ++i) {
+    off[i] = -1;
+    if (parts & (1u << i)) {
+      off[i] = o;
+      o += sz[i];
+    }
+  }
+  *total = o;
+}
+
+// Check the caller's workspace and return the address of each requested part.
+static nsr_status conv_ws_parts(void* workspace, int64_t workspace_bytes, int64_t B, int64_t C_in, int64_t C_out,
+                                int64_t T_out, int64_t K, unsigned parts, char* ptr[3], const char* what) {
+  int64_t off[3], need = 0;
+  conv_ws_layout(B, C_in, C_out, std::max<int64_t>(T_out, 0), K, parts, off, &need);
+  if (need > 0 && (!workspace || !aligned(workspace, 256) || workspace_bytes < need))
+    return fail(NSR_ERR_BAD_ARG, "%s: needs a 256-byte aligned workspace of %lld bytes (nsr_conv1d_workspace_bytes)",
+                what, (long long)need);
+  for (int i = 0; i < 3; ++i) ptr[i] = off[i] >= 0 ? (char*)workspace + off[i] : nullptr;
+  return NSR_OK;
 }
 
 nsr_status nsr_conv1d_f16w_packed(const float* x, const void* w_packed, const void* bias, const float* residual,
@@ -1481,34 +1504,30 @@ nsr_status nsr_conv1d_f16w_packed(const float* x, const void* w_packed, const vo
 
 nsr_status nsr_conv1d_f32io(const float* x, const void* w, const void* bias, float* out, int64_t B, int64_t C_in,
                             int64_t C_out, int64_t T_in, int64_t K, int64_t stride, int64_t padding,
-                            int64_t dilation, nsr_stream_t stream) {
+                            int64_t dilation, void* workspace, int64_t workspace_bytes, nsr_stream_t stream) {
   if (stride != 1) return fail(NSR_ERR_UNSUPPORTED, "conv1d_f32io: stride %lld (only stride 1 is built)",
                                (long long)stride);
   int64_t T_out = 0;
   nsr_status st = conv_validate(x, w, 2, out, B, C_in, C_out, T_in, K, padding, dilation, &T_out, "conv1d_f32io");
   if (st != NSR_OK) return st;
   if (bias && !aligned(bias, 2)) return fail(NSR_ERR_BAD_ARG, "conv1d_f32io: misaligned bias");
+  char* part[3];
+  st = conv_ws_parts(workspace, workspace_bytes, B, C_in, C_out, T_out, K, NSR_WS_PACKED_WEIGHTS, part,
+                     "conv1d_f32io");
+  if (st != NSR_OK) return st;
   if (B == 0 || T_out <= 0) return NSR_OK;
-  // pack the weights into stream-ordered scratch, convolve, free
-  uint16_t* wp = nullptr;
-  const size_t bytes = (size_t)(C_out * C_in * K) * 2;
-  hipError_t e = hipMallocAsync((void**)&wp, bytes, (hipStream_t)stream);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    return fail(NSR_ERR_HIP, "conv1d_f32io: hipMallocAsync: %s", hipGetErrorString(e));
-  }
-  st = nsr_conv1d_pack_f16(w, C_out, C_in, K, wp, stream);
-  if (st == NSR_OK) st = nsr_conv1d_f16w_packed(x, wp, bias, nullptr, out, B, C_in, C_out, T_in, K, padding, dilation, stream);
-  (void)hipFreeAsync(wp, (hipStream_t)stream);
-  return st;
+  // pack the weights into the caller's workspace, then convolve
+  st = nsr_conv1d_pack_f16(w, C_out, C_in, K, part[0], stream);
+  if (st != NSR_OK) return st;
+  return nsr_conv1d_f16w_packed(x, part[0], bias, nullptr, out, B, C_in, C_out, T_in, K, padding, dilation, stream);
 }
 
 static nsr_status adain_conv_impl(const float* x, const float* x_stats, const void* gamma, const void* beta,
                                   const void* alpha, nsr_dtype param_dtype, int64_t gamma_bstride,
                                   int64_t beta_bstride, const void* w_packed, const void* bias, const float* residual,
                                   float* out, float* out_stats, int64_t B, int64_t C_in, int64_t C_out, int64_t T,
-                                  int64_t K, int64_t padding, int64_t dilation, float eps, nsr_stream_t stream,
-                                  const char* what) {
+                                  int64_t K, int64_t padding, int64_t dilation, float eps, void* workspace,
+                                  int64_t workspace_bytes, nsr_stream_t stream, const char* what) {
   if (!gamma || !beta || !alpha) return fail(NSR_ERR_BAD_ARG, "%s: null parameter pointer", what);
   if (param_dtype != NSR_F32 && param_dtype != NSR_F16) return fail(NSR_ERR_BAD_ARG, "%s: params must be F32 or F16", what);
   if (gamma_bstride < 0 || beta_bstride < 0) return fail(NSR_ERR_BAD_ARG, "%s: negative batch stride", what);
@@ -1520,16 +1539,16 @@ static nsr_status adain_conv_impl(const float* x, const float* x_stats, const vo
   if (st != NSR_OK) return st;
   if ((bias && !aligned(bias, 2)) || (residual && !aligned(residual, 4)))
     return fail(NSR_ERR_BAD_ARG, "%s: misaligned bias or residual", what);
+  const unsigned parts = (x_stats ? 0u : NSR_WS_IN_STATS) | (out_stats ? NSR_WS_OUT_STATS : 0u);
+  char* part[3];
+  st = conv_ws_parts(workspace, workspace_bytes, B, C_in, C_out, T_out, K, parts, part, what);
+  if (st != NSR_OK) return st;
   if (B == 0 || T_out <= 0) return NSR_OK;
   if (T == 0) return fail(NSR_ERR_BAD_ARG, "%s: T == 0 (an empty row has no statistics)", what);
-  // per-(b, ci) mean and 1/sqrt(var + eps) of x: the caller's, or computed into stream-ordered scratch
+  // per-(b, ci) mean and 1/sqrt(var + eps) of x: the caller's, or computed into the workspace
   float* stats = nullptr;
   if (!x_stats) {
-    hipError_t e = hipMallocAsync((void**)&stats, (size_t)(B * C_in) * 2 * sizeof(float), (hipStream_t)stream);
-    if (e != hipSuccess) {
-      (void)hipGetLastError();
-      return fail(NSR_ERR_HIP, "%s: hipMallocAsync: %s", what, hipGetErrorString(e));
-    }
+    stats = (float*)part[1];
     nsr_adain_args s;
     std::memset(&s, 0, sizeof(s));
     s.x = x;
@@ -1566,9 +1585,9 @@ static nsr_status adain_conv_impl(const float* x, const float* x_stats, const vo
     a.padding = (int32_t)padding;
     a.dilation = (int32_t)dilation;
     a.pdt = param_dtype == NSR_F32 ? 0 : 1;
-    st = out_stats ? conv_launch_stats(true, a, eps, out_stats, stream, what) : conv_launch(true, a, stream, what);
+    st = out_stats ? conv_launch_stats(true, a, eps, out_stats, (float*)part[2], stream, what)
+                   : conv_launch(true, a, stream, what);
   }
-  if (stats) (void)hipFreeAsync(stats, (hipStream_t)stream);
   return st;
 }
 
@@ -1576,10 +1595,11 @@ nsr_status nsr_adain_snake_conv1d_f32(const float* x, const void* gamma, const v
                                       nsr_dtype param_dtype, int64_t gamma_bstride, int64_t beta_bstride,
                                       const void* w_packed, const void* bias, const float* residual, float* out,
                                       int64_t B, int64_t C_in, int64_t C_out, int64_t T, int64_t K, int64_t padding,
-                                      int64_t dilation, float eps, nsr_stream_t stream) {
+                                      int64_t dilation, float eps, void* workspace, int64_t workspace_bytes,
+                                      nsr_stream_t stream) {
   return adain_conv_impl(x, nullptr, gamma, beta, alpha, param_dtype, gamma_bstride, beta_bstride, w_packed, bias,
-                         residual, out, nullptr, B, C_in, C_out, T, K, padding, dilation, eps, stream,
-                         "adain_snake_conv1d");
+                         residual, out, nullptr, B, C_in, C_out, T, K, padding, dilation, eps, workspace,
+                         workspace_bytes, stream, "adain_snake_conv1d");
 }
 
 nsr_status nsr_adain_snake_conv1d_chain_f32(const float* x, const float* x_stats, const void* gamma,
@@ -1587,16 +1607,17 @@ nsr_status nsr_adain_snake_conv1d_chain_f32(const float* x, const float* x_stats
                                             int64_t gamma_bstride, int64_t beta_bstride, const void* w_packed,
                                             const void* bias, const float* residual, float* out, float* out_stats,
                                             int64_t B, int64_t C_in, int64_t C_out, int64_t T, int64_t K,
-                                            int64_t padding, int64_t dilation, float eps, nsr_stream_t stream) {
+                                            int64_t padding, int64_t dilation, float eps, void* workspace,
+                                            int64_t workspace_bytes, nsr_stream_t stream) {
   return adain_conv_impl(x, x_stats, gamma, beta, alpha, param_dtype, gamma_bstride, beta_bstride, w_packed, bias,
-                         residual, out, out_stats, B, C_in, C_out, T, K, padding, dilation, eps, stream,
-                         "adain_snake_conv1d_chain");
+                         residual, out, out_stats, B, C_in, C_out, T, K, padding, dilation, eps, workspace,
+                         workspace_bytes, stream, "adain_snake_conv1d_chain");
 }
 
 nsr_status nsr_conv1d_f16w_packed_stats(const float* x, const void* w_packed, const void* bias,
                                         const float* residual, float* out, float* out_stats, int64_t B, int64_t C_in,
                                         int64_t C_out, int64_t T_in, int64_t K, int64_t padding, int64_t dilation,
-                                        float eps, nsr_stream_t stream) {
+                                        float eps, void* workspace, int64_t workspace_bytes, nsr_stream_t stream) {
   const char* what = "conv1d_f16w_packed_stats";
   int64_t T_out = 0;
   nsr_status st = conv_validate(x, w_packed, 16, out, B, C_in, C_out, T_in, K, padding, dilation, &T_out, what);
@@ -1605,6 +1626,9 @@ nsr_status nsr_conv1d_f16w_packed_stats(const float* x, const void* w_packed, co
   if ((bias && !aligned(bias, 2)) || (residual && !aligned(residual, 4)))
     return fail(NSR_ERR_BAD_ARG, "%s: misaligned bias or residual", what);
   if (!(eps >= 0.0f)) return fail(NSR_ERR_BAD_ARG, "%s: eps must be >= 0", what);
+  char* part[3];
+  st = conv_ws_parts(workspace, workspace_bytes, B, C_in, C_out, T_out, K, NSR_WS_OUT_STATS, part, what);
+  if (st != NSR_OK) return st;
   if (B == 0 || T_out <= 0) return NSR_OK;
   if (T_in == 0) return fail(NSR_ERR_BAD_ARG, "%s: T_in == 0", what);
   nsr_conv_args a;
@@ -1622,8 +1646,25 @@ nsr_status nsr_conv1d_f16w_packed_stats(const float* x, const void* w_packed, co
   a.K = (int32_t)K;
   a.padding = (int32_t)padding;
   a.dilation = (int32_t)dilation;
-  return conv_launch_stats(false, a, eps, out_stats, stream, what);
+  return conv_launch_stats(false, a, eps, out_stats, (float*)part[2], stream, what);
 }
+
+nsr_status nsr_conv1d_workspace_bytes(int64_t B, int64_t C_in, int64_t C_out, int64_t T_in, int64_t K,
+                                      int64_t padding, int64_t dilation, unsigned parts, int64_t* bytes) {
+  if (!bytes) return fail(NSR_ERR_BAD_ARG, "conv1d_workspace_bytes: null result pointer");
+  *bytes = 0;
+  if (parts & ~(unsigned)(NSR_WS_PACKED_WEIGHTS | NSR_WS_IN_STATS | NSR_WS_OUT_STATS))
+    return fail(NSR_ERR_BAD_ARG, "conv1d_workspace_bytes: unknown parts 0x%x", parts);
+  if (B < 0 || C_in <= 0 || C_out <= 0 || T_in < 0 || K <= 0 || padding < 0 || dilation <= 0 || B > 65535 ||
+      C_in > (1 << 20) || C_out > (1 << 24) || K > 4096 || T_in >= (1LL << 23) || padding > (1 << 24) ||
+      dilation > (1 << 20))
+    return fail(NSR_ERR_BAD_ARG, "conv1d_workspace_bytes: bad shape");
+  const int64_t T_out = std::max<int64_t>(0, T_in + 2 * padding - dilation * (K - 1));
+  int64_t off[3];
+  conv_ws_layout(B, C_in, C_out, T_out, K, parts, off, bytes);
+  return NSR_OK;
+}
+
 
 }  // extern "C"
 

@@ -446,10 +446,31 @@ void RocmKokoroBackend::conv1d_f32(const GpuBuffer& x, const GpuBuffer& w, const
                                    size_t k, size_t stride, size_t padding, size_t dilation) const {
   if ((int64_t)t_out != (int64_t)t_in + 2 * (int64_t)padding - (int64_t)dilation * ((int64_t)k - 1))
     throw Error("conv1d_f32: t_out does not match t_in, k, padding and dilation");
-  nsr_check(nsr_conv1d_f32io(static_cast<const float*>(x.at()), w.at(), bias.at(), static_cast<float*>(out.at()), 1,
-                             (int64_t)c_in, (int64_t)c_out, (int64_t)t_in, (int64_t)k, (int64_t)stride,
-                             (int64_t)padding, (int64_t)dilation, device_.stream()),
+  if (stride != 1) throw Error("conv1d_f32: only stride 1 is built");
+  const void* packed = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(conv_weights_->mu);
+    for (const PackedConvWeight& e : conv_weights_->entries)
+      if (e.w == w.at() && e.c_out == c_out && e.c_in == c_in && e.k == k) packed = e.packed.buffer().at();
+    if (!packed) {
+      // first call with this weight buffer: pack it once, in stream order before the conv below
+      Tensor t = Tensor::empty(device_, {c_out, k, c_in}, DType::F16);
+      nsr_check(nsr_conv1d_pack_f16(w.at(), (int64_t)c_out, (int64_t)c_in, (int64_t)k, t.buffer().at(),
+                                    device_.stream()),
+                "conv1d_f32");
+      packed = t.buffer().at();
+      conv_weights_->entries.push_back(PackedConvWeight{w.at(), c_out, c_in, k, t});
+    }
+  }
+  nsr_check(nsr_conv1d_f16w_packed(static_cast<const float*>(x.at()), packed, bias.at(), nullptr,
+                                   static_cast<float*>(out.at()), 1, (int64_t)c_in, (int64_t)c_out, (int64_t)t_in,
+                                   (int64_t)k, (int64_t)padding, (int64_t)dilation, device_.stream()),
             "conv1d_f32");
+}
+
+void RocmKokoroBackend::forget_conv_weights() const {
+  std::lock_guard<std::mutex> lk(conv_weights_->mu);
+  conv_weights_->entries.clear();
 }
 
 void RocmKokoroBackend::add_f32(const GpuBuffer& a, const GpuBuffer& b, const GpuBuffer& out, size_t n) const {

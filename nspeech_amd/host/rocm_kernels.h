@@ -23,6 +23,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <memory>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -209,7 +210,8 @@ void enc_gemv_q8_resadd_ln(Encoder enc, const RocmKernels& kernels, const GpuBuf
 // The AdaIN+Snake part of KokoroGpuBackend for the ROCm device: Buf = GpuBuffer.
 class RocmKokoroBackend {
  public:
-  RocmKokoroBackend(const RocmDevice& device, const RocmKernels& kernels) : device_(device), kernels_(kernels) {}
+  RocmKokoroBackend(const RocmDevice& device, const RocmKernels& kernels)
+      : device_(device), kernels_(kernels), conv_weights_(std::make_shared<ConvWeightCache>()) {}
   // out = snake(AdaIN(x)) over x [channels, seq_len] f32; gamma, beta, alpha
   // [channels] f16 (the precomputed style parameters, decoder.rs:966-981).
   void adain_snake_f32(const GpuBuffer& x, const GpuBuffer& gamma, const GpuBuffer& beta, const GpuBuffer& alpha,
@@ -225,10 +227,14 @@ class RocmKokoroBackend {
   // The f32-intermediate path (gpu_backend.rs:134-225): this backend has it.
   bool has_f32_intermediates() const { return true; }
   // conv1d_f32 (:165-177): x f32 [c_in, t_in], w f16 [c_out, c_in, k], bias f16 [c_out] -> f32 [c_out, t_out];
-  // stride 1 (the decoder's only stride), t_out must be what padding and dilation give.
+  // stride 1 (the decoder's only stride), t_out must be what padding and dilation give. The decoder passes the
+  // same weight buffers on every call: each is packed once (nsr_conv1d_pack_f16) on its first call and the
+  // packed copy reused, so later calls are one launch (nsr_conv1d_f16w_packed) and allocate nothing.
   void conv1d_f32(const GpuBuffer& x, const GpuBuffer& w, const GpuBuffer& bias, const GpuBuffer& out, size_t c_in,
                   size_t c_out, size_t t_in, size_t t_out, size_t k, size_t stride, size_t padding,
                   size_t dilation) const;
+  // Drop the packed weights conv1d_f32 keeps (for a caller that rewrites a weight buffer in place).
+  void forget_conv_weights() const;
   // add_f32 (:186-190), scale_third_f32 (:191-195), leaky_relu_f32 (:196-200): f32 elementwise over n.
   void add_f32(const GpuBuffer& a, const GpuBuffer& b, const GpuBuffer& out, size_t n) const;
   void scale_third_f32(const GpuBuffer& x, const GpuBuffer& out, size_t n) const;
@@ -237,8 +243,18 @@ class RocmKokoroBackend {
   void istft_gpu(const GpuBuffer& x, const GpuBuffer& out, size_t n_frames, size_t out_len) const;
 
  private:
+  struct PackedConvWeight {
+    const void* w;
+    size_t c_out, c_in, k;
+    Tensor packed;
+  };
+  struct ConvWeightCache {
+    std::mutex mu;
+    std::vector<PackedConvWeight> entries;
+  };
   RocmDevice device_;
   RocmKernels kernels_;
+  std::shared_ptr<ConvWeightCache> conv_weights_;
 };
 
 // ---- Embedding and rotary (model-side entry points the GPU also serves) ------

@@ -142,13 +142,22 @@ def test_version_and_header_is_plain_c():
     lambda L: L.nsr_istft_f32(16, NULL, 10, 20, 20, 5, NULL),
     # chained conv: null out_stats for the plain conv, misaligned statistics, C_in not a multiple of 16
     lambda L: L.nsr_conv1d_f16w_packed_stats(16, 16, NULL, NULL, 16, NULL, 1, 16, 16, 64, 3, 1, 1,
-                                             C.c_float(1e-5), NULL),
+                                             C.c_float(1e-5), 256, 1 << 20, NULL),
     lambda L: L.nsr_adain_snake_conv1d_chain_f32(16, 20, 16, 16, 16, 0, 0, 0, 16, NULL, NULL, 16, NULL, 1, 16, 16,
-                                                 64, 3, 1, 1, C.c_float(1e-5), NULL),
+                                                 64, 3, 1, 1, C.c_float(1e-5), 256, 1 << 20, NULL),
     lambda L: L.nsr_adain_snake_conv1d_chain_f32(16, NULL, 16, 16, 16, 0, 0, 0, 16, NULL, NULL, 16, 20, 1, 16, 16,
-                                                 64, 3, 1, 1, C.c_float(1e-5), NULL),
+                                                 64, 3, 1, 1, C.c_float(1e-5), 256, 1 << 20, NULL),
     lambda L: L.nsr_conv1d_f16w_packed_stats(16, 16, NULL, NULL, 16, 16, 1, 24, 16, 64, 3, 1, 1,
-                                             C.c_float(1e-5), NULL),
+                                             C.c_float(1e-5), 256, 1 << 20, NULL),
+    # conv workspaces: missing, too small, misaligned (256 bytes needed); unknown part flags
+    lambda L: L.nsr_conv1d_f16w_packed_stats(16, 16, NULL, NULL, 16, 16, 1, 16, 16, 64, 3, 1, 1,
+                                             C.c_float(1e-5), NULL, 0, NULL),
+    lambda L: L.nsr_conv1d_f16w_packed_stats(16, 16, NULL, NULL, 16, 16, 1, 16, 16, 64, 3, 1, 1,
+                                             C.c_float(1e-5), 256, 16, NULL),
+    lambda L: L.nsr_conv1d_f32io(16, 16, NULL, 16, 1, 16, 16, 64, 3, 1, 1, 1, 272, 1 << 20, NULL),
+    lambda L: L.nsr_adain_snake_conv1d_f32(16, 16, 16, 16, 0, 0, 0, 16, NULL, NULL, 16, 1, 16, 16, 64, 3, 1, 1,
+                                           C.c_float(1e-5), NULL, 0, NULL),
+    lambda L: L.nsr_conv1d_workspace_bytes(1, 16, 16, 64, 3, 1, 1, 8, C.byref(C.c_int64())),
     # snake: bf16 x, seq_len not dividing n_elements, zero channels, misaligned f32 x
     lambda L: L.nsr_snake(16, 2, 16, 0, 16, 8, 1, 8, NULL),
     lambda L: L.nsr_snake(16, 0, 16, 0, 16, 10, 1, 4, NULL),
