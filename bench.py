@@ -19,7 +19,10 @@ time / K, the average launch duration. Input/output buffer sets rotate so
 the footprint is >= 512 MB (twice the 256 MB Infinity Cache): the timed
 calls read HBM, not MALL. `warm_*` figures repeat one buffer set and are
 labelled as such. `host_us_per_call` is the host time to enqueue one call
-from Python (ctypes + the C-ABI runtime + hipModuleLaunchKernel).
+from Python (ctypes + the C-ABI runtime + hipModuleLaunchKernel);
+`host_enqueue` is the same measured in C++ (nspeech_amd/host/
+enqueue_bench.cpp) for the decode-step entry points, beside a bare
+hipModuleLaunchKernel of an empty kernel.
 
 Floors, measured in the same run through the same runtime: an empty kernel
 (`empty`) and plain 128-bit device copies (`copy_<form>_<config>`) moving
@@ -709,6 +712,21 @@ def main():
         print(f"[bench] {nm}: {results[nm]['us_per_call']} us/call, {results[nm]['GBs']} GB/s "
               f"({100 * results[nm]['frac_of_peak']:.1f}% of peak)", file=sys.stderr, flush=True)
 
+    # host time per call of the decode-step entry points, measured in C++ (no binding overhead)
+    host_enqueue = None
+    eb = ROOT / "nspeech_amd" / "lib" / "nsr_enqueue_bench"
+    if eb.exists():
+        import subprocess
+
+        r = subprocess.run([str(eb), str(eb.parent)], capture_output=True, text=True, timeout=120)
+        if r.returncode == 0 and r.stdout.strip():
+            host_enqueue = json.loads(r.stdout.strip().splitlines()[-1])
+            for nm in ("dec", "attn", "q8fc1"):
+                if nm in results:
+                    results[nm]["host_us_per_call_c"] = host_enqueue[nm]
+        else:
+            print(f"[bench] enqueue bench failed ({r.returncode}): {r.stderr[-300:]}", file=sys.stderr, flush=True)
+
     # each config against the fastest same-size copy of this run
     for nm, r in results.items():
         cfg = COPY_FOR.get(nm)
@@ -765,6 +783,7 @@ def main():
                      "frac": head["frac_of_peak"], "traffic": traffic.get(head["kernel"]), "kernel": head["kernel"],
                      "us_per_call": head["us_per_call"], "copy_floor_us": head.get("copy_floor_us")},
         "cpu_baseline": cpu,
+        "host_enqueue": host_enqueue,
         "per_config": results,
     }
     print(json.dumps(line), flush=True)

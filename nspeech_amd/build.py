@@ -9,6 +9,8 @@ tree):
                                             code objects embedded
   nspeech_amd/lib/libnspeech_rocm_host.so   C++ host side (nspeech_amd/host/
                                             rocm_kernels.h) over the C ABI
+  nspeech_amd/lib/nsr_enqueue_bench         host time per call of the decode-
+                                            step entry points (bench.py)
   tests/host/_build/test_host_mirror        C++ tests of the host side
   oracle/_build/libnsr_oracle.so            CPU oracle (test infrastructure)
 """
@@ -118,6 +120,18 @@ def build_host_library() -> Path:
     return out
 
 
+def build_enqueue_bench() -> Path:
+    """nspeech_amd/host/enqueue_bench.cpp -> lib/nsr_enqueue_bench: host time per call of the decode-step entry
+    points, run by bench.py."""
+    out = LIB / "nsr_enqueue_bench"
+    tmp = LIB / "nsr_enqueue_bench.tmp"
+    _run([*HOST_CXX, "-O2", f"-I{ROOT / 'include'}", f"-I{ROCM / 'include'}", str(PKG / "host" / "enqueue_bench.cpp"),
+          f"-L{LIB}", "-lnspeech_rocm", f"-L{ROCM / 'lib'}", "-lamdhip64", "-Wl,-rpath,$ORIGIN",
+          f"-Wl,-rpath,{ROCM / 'lib'}", "-o", str(tmp)])
+    os.replace(tmp, out)
+    return out
+
+
 def build_host_tests() -> Path:
     """tests/host/test_host_mirror.cpp -> tests/host/_build/test_host_mirror."""
     src = ROOT / "tests" / "host" / "test_host_mirror.cpp"
@@ -152,6 +166,7 @@ def build_all() -> None:
     build_code_objects()
     build_library()
     build_host_library()
+    build_enqueue_bench()
     build_host_tests()
     build_oracle()
 
