@@ -57,7 +57,7 @@ NEXT_WORKLOADS = ["dec", "dec2", "attn", "attnx", "q8fc1", "q8fc2", "q8fc1r", "q
 # same-size copies: algorithmic bytes of the config each one calibrates
 COPY_SIZES = {"c1t": 8519680, "c3": 8642560, "c2": 19666944, "c4a": 196616192, "c4b": 943727104}
 COPY_FOR = {"c1": "c1t", "c1t": "c1t", "c3": "c3", "c2": "c2", "c2u": "c2", "c4a": "c4a", "c4b": "c4b"}
-FLOOR_WORKLOADS = ["empty"] + [f"copy_{f}_{c}" for c in COPY_SIZES for f in ("f", "p4", "p8")]
+FLOOR_WORKLOADS = ["empty"] + [f"copy_{f}_{c}" for c in COPY_SIZES for f in ("f", "p4", "p8")] + ["copy_rows_c4b"]
 DEFAULT_WORKLOADS = CONFIG_WORKLOADS + FLOOR_WORKLOADS + NEXT_WORKLOADS
 MALL_DEFEAT_BYTES = 512 << 20
 METRIC = "achieved HBM GB/s (% of MI355X peak) and µs/call per fused kernel"
@@ -113,6 +113,21 @@ def build_workload(name):
 
         return Workload(name, "empty kernel (one launch on the stream)", 0, 1 << 30, make_set, launch,
                         "nsrk_calib_empty", "-")
+
+    if name == "copy_rows_c4b":
+        # c4b's bytes copied row by row (1024 rows of 115200 f32) with the AdaIN row kernel's access structure
+        rows, rb = 1024, 115200 * 4
+
+        def make_set(_):
+            return {"s": torch.ones(rows * rb // 4, dtype=torch.float32, device=dev),
+                    "d": torch.empty(rows * rb // 4, dtype=torch.float32, device=dev)}
+
+        def launch(s):
+            abi.check(L.nsr_calib_copy_rows(s["s"].data_ptr(), s["d"].data_ptr(), rows, rb, stream()))
+
+        return Workload(name, f"row-by-row device copy of {rows} rows of {rb} bytes (the AdaIN row kernel's access "
+                        "structure, one 512-lane workgroup per row)", 2 * rows * rb, 2 * rows * rb, make_set, launch,
+                        "nsrk_calib_copy_rows", "u8")
 
     if name.startswith("copy_"):
         _, form, cfg = name.split("_")
@@ -735,6 +750,9 @@ def main():
         if copies:
             r["copy_floor_us"] = min(copies)
             r["frac_of_copy"] = round(min(copies) / r["us_per_call"], 4)
+        if nm == "c4b" and "copy_rows_c4b" in results:
+            r["row_copy_floor_us"] = results["copy_rows_c4b"]["us_per_call"]
+            r["frac_of_row_copy"] = round(r["row_copy_floor_us"] / r["us_per_call"], 4)
 
     head_name = "c4b" if "c4b" in results else next(iter(results))
     head = results[head_name]
@@ -781,7 +799,8 @@ def main():
                    "parallelism": "single GPU", **({"alongside": companion} if companion else {})},
         "roofline": {"bound": "hbm", "achieved": head["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": head["frac_of_peak"], "traffic": traffic.get(head["kernel"]), "kernel": head["kernel"],
-                     "us_per_call": head["us_per_call"], "copy_floor_us": head.get("copy_floor_us")},
+                     "us_per_call": head["us_per_call"], "copy_floor_us": head.get("copy_floor_us"),
+                     "row_copy_floor_us": head.get("row_copy_floor_us")},
         "cpu_baseline": cpu,
         "host_enqueue": host_enqueue,
         "per_config": results,

@@ -578,6 +578,10 @@ nsr_status nsr_gemv_q8_t4_resadd_ln(const void* x, nsr_dtype x_dtype, const uint
 nsr_status nsr_calib_empty(nsr_stream_t stream);
 nsr_status nsr_calib_copy(const void* src, void* dst, int64_t bytes, int form, int groups_per_cu,
                           nsr_stream_t stream);
+/* nsr_calib_copy_rows: device copy of n_rows rows of row_bytes (a multiple of
+ * 16, 16-byte aligned) row by row, the AdaIN row kernel's access structure:
+ * one 512-lane workgroup per row, a persistent grid of one per CU. */
+nsr_status nsr_calib_copy_rows(const void* src, void* dst, int64_t n_rows, int64_t row_bytes, nsr_stream_t stream);
 
 #ifdef __cplusplus
 }

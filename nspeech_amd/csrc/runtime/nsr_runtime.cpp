@@ -1703,4 +1703,21 @@ nsr_status nsr_calib_copy(const void* src, void* dst, int64_t bytes, int form, i
   return launch(form == 1 ? K_nsrk_calib_copy_p4 : K_nsrk_calib_copy_p8, (unsigned)groups, 1, 256, 0, stream, params);
 }
 
+nsr_status nsr_calib_copy_rows(const void* src, void* dst, int64_t n_rows, int64_t row_bytes, nsr_stream_t stream) {
+  if (!src || !dst) return fail(NSR_ERR_BAD_ARG, "calib_copy_rows: null pointer");
+  if (n_rows < 0 || row_bytes <= 0 || row_bytes % 16 != 0 || row_bytes >= ((int64_t)1 << 31) ||
+      !aligned(src, 16) || !aligned(dst, 16))
+    return fail(NSR_ERR_BAD_ARG, "calib_copy_rows: rows of a positive multiple of 16 bytes, 16-byte aligned");
+  if (n_rows == 0) return NSR_OK;
+  DeviceModule* dm = nullptr;
+  nsr_status st = current_module(&dm);
+  if (st != NSR_OK) return st;
+  nsr_calib_args a;
+  a.src = (const float*)src;
+  a.dst = (float*)dst;
+  a.n4 = row_bytes / 16;
+  void* params[] = {&a, &n_rows};
+  return launch(K_nsrk_calib_copy_rows, (unsigned)std::min<int64_t>(n_rows, dm->n_cu), 1, 512, 0, stream, params);
+}
+
 }  // extern "C"
