@@ -30,9 +30,12 @@ exactly each config's algorithmic bytes (half read, half written), in two
 grid forms (`f`: one 16-byte chunk per lane; `p4`/`p8`: a persistent
 8 x #CU grid with 4 or 8 chunks per lane in flight). Each config's entry
 carries `copy_floor_us` (the fastest copy of its size) and `frac_of_copy`.
-rocprofv3's kernel trace adds about 1 us to kernels of a few us (it spaces
-dispatches apart); for the headline kernel its average agrees with
-`us_per_call` (profiles/).
+rocprofv3's kernel trace adds about 3 us to kernels of a few us (it spaces
+dispatches apart; the empty kernel shows 4.5 us there against 1.6 us back
+to back); for the headline kernel its average over the timed calls agrees
+with `us_per_call` to within 1% (profiles/bench_workloads_trace_and_traffic.md).
+`traffic` is HBM bytes per dispatch from rocprofv3's FETCH_SIZE / WRITE_SIZE
+counters, calibrated on the flat copy (profiles/hbm_traffic_bench_workloads.txt).
 
 The CPU baseline is the oracle's C restatement of the reference CPU path
 (oracle/nsr_oracle.c) timed on this host on a bounded sample.
@@ -327,7 +330,8 @@ def build_workload(name):
         return Workload(name, f"decode attention f16, 10 heads x 64, kv_len {kv_len}"
                         + (" (self-attention over the KV cache)" if name == "attn"
                            else " (cross-attention over the encoder K/V, 32 splits)"),
-                        alg, alg, make_set, launch, "nsrk_attn_decode_partial", "f16")
+                        alg, alg, make_set, launch,
+                        "nsrk_attn_head_d16" if name == "attn" else "nsrk_attn_partial_d16", "f16")
 
     if name in ("q8fc1", "q8fc2", "q8fc1r", "q8fc2r"):
         # Moonshine decoder MLP at M = 1 (dim 640, intermediate 2560; f16 activations, Q8 weights):
@@ -771,16 +775,19 @@ def main():
     tf = ROOT / "profiles" / "hbm_traffic_bench_workloads.txt"
     if tf.exists():
         for line in tf.read_text().splitlines():
-            parts = line.split()
-            if len(parts) >= 2 and parts[0].startswith("nsrk_") and parts[1].isdigit():
-                traffic[parts[0]] = int(parts[1])
+            parts = line.split()  # workload kernel bytes
+            if len(parts) == 3 and parts[2].isdigit() and parts[0] in results \
+                    and results[parts[0]]["kernel"] == parts[1]:
+                traffic[parts[0]] = int(parts[2])
+    for nm, r in results.items():
+        r["traffic"] = traffic.get(nm)
 
     companion = {}
     if "c4a" in results and head_name == "c4b":
         r = results["c4a"]
         companion = {"c4a": {"workload": r["workload"], "kernel": r["kernel"], "dtype": r["dtype"],
                              "us_per_call": r["us_per_call"], "GBs": r["GBs"], "frac_of_peak": r["frac_of_peak"],
-                             "traffic": traffic.get(r["kernel"])}}
+                             "traffic": traffic.get("c4a")}}
     line = {
         "metric": METRIC,
         "value": head["GBs"],
@@ -798,7 +805,7 @@ def main():
                    "buffer_sets": head["buffer_sets"], "footprint_MB": head["footprint_MB"],
                    "parallelism": "single GPU", **({"alongside": companion} if companion else {})},
         "roofline": {"bound": "hbm", "achieved": head["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": head["frac_of_peak"], "traffic": traffic.get(head["kernel"]), "kernel": head["kernel"],
+                     "frac": head["frac_of_peak"], "traffic": traffic.get(head_name), "kernel": head["kernel"],
                      "us_per_call": head["us_per_call"], "copy_floor_us": head.get("copy_floor_us"),
                      "row_copy_floor_us": head.get("row_copy_floor_us")},
         "cpu_baseline": cpu,
