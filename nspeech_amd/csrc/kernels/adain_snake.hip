@@ -17,8 +17,8 @@
  *
  * Unaligned rows take the register-resident kernel further down (global
  * loads, partial edge chunks per element). Rows longer than the on-chip
- * budget take the long-row kernel at the end: statistics by pairwise
- * (count, mean, M2) merges over one read, then a second read to apply.
+ * budget take the long-row kernel at the end: f64 sum and sum of squares
+ * over one read, then a second read to apply.
  */
 #include "device_common.h"
 

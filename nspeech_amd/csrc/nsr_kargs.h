@@ -79,7 +79,7 @@ typedef struct nsr_adain_args {
   const void* beta;        /* [B?, C] */
   const void* alpha;       /* [C] */
   float* out;              /* [B, C, T] */
-  float* stats;            /* [B*C][2] mean, rstd (split path only) */
+  float* stats;            /* [B*C][2] mean, rstd (nsrk_adain_stats* output only) */
   int64_t n_rows;          /* B * C */
   int64_t T;
   int64_t gamma_bstride;

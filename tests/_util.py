@@ -25,9 +25,20 @@ def rel_err(got, ref) -> float:
     return float(np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1.0)))
 
 
+def pure_rel_err(got, ref, floor=1e-3) -> float:
+    """max |got - ref| / |ref| over the elements with |ref| > floor (float64)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    big = np.abs(ref) > floor
+    if not big.any():
+        return 0.0
+    return float(np.max(np.abs(got[big] - ref[big]) / np.abs(ref[big])))
+
+
 def assert_close(got, ref, rtol, what=""):
     e = rel_err(got, ref)
-    assert e <= rtol, f"{what}: max scaled error {e:.3e} > {rtol:.1e}"
+    assert e <= rtol, (f"{what}: max error {e:.3e} scaled by max(|ref|, 1) > {rtol:.1e} "
+                       f"(relative over |ref| > 1e-3: {pure_rel_err(got, ref):.3e})")
     return e
 
 

@@ -178,7 +178,7 @@ def test_ill_conditioned_rows_and_special_alpha(dev, T):
     say("adain+snake ill-conditioned rows, alpha in {1, 0, -0.7, 1e-4}, T", T)
     got = _adain(x, gamma, beta, alpha)
     ref = CF.adain_snake(x, gamma, beta, alpha)
-    assert_close(got, ref, RTOL_F32, "vs f64 (two-pass and pairwise-merged statistics stay within 1e-5 here)")
+    assert_close(got, ref, RTOL_F32, "vs f64 (on-chip two-pass and f64 two-read statistics stay within 1e-5 here)")
 
 
 def test_misaligned_views(dev):
