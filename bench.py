@@ -55,8 +55,8 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 CONFIG_WORKLOADS = ["c4b", "c4a", "c0", "c1", "c1t", "c2", "c3", "c2u", "c2h"]
-NEXT_WORKLOADS = ["dec", "dec2", "attn", "attnx", "q8fc1", "q8fc2", "q8fc1r", "q8fc2r", "q8conv", "kconv3", "kconv11",
-                  "kconv3u", "kchain3", "kchain11", "mrf", "istft"]
+NEXT_WORKLOADS = ["dec", "dec2", "attn", "attnx", "q8fc1", "q8fc2", "q8fc1r", "q8fc2r", "q8conv", "kconv3", "kconv7",
+                  "kconv11", "kconv7f", "kconv11f", "kconv3u", "kchain3", "kchain11", "mrf", "istft"]
 # same-size copies: algorithmic bytes of the config each one calibrates
 COPY_SIZES = {"c1t": 8519680, "c3": 8642560, "c2": 19666944, "c4a": 196616192, "c4b": 943727104}
 COPY_FOR = {"c1": "c1t", "c1t": "c1t", "c3": "c3", "c2": "c2", "c2u": "c2", "c4a": "c4a", "c4b": "c4b"}
@@ -441,22 +441,27 @@ def build_workload(name):
         return Workload(name, f"Kokoro iSTFT n_fft {n_fft} hop {hop}, x f32 [22,{n_frames}] -> [{out_len}]", alg, alg,
                         make_set, launch, "nsrk_istft_f32_n20", "f32")
 
-    if name in ("kconv3", "kconv11", "kconv3u"):
+    if name in ("kconv3", "kconv7", "kconv11", "kconv3u", "kconv7f", "kconv11f"):
         # One Kokoro ResBlock stage at the final upsample shape (x [8, 128, 115200], as config c4b):
-        # conv1(snake(AdaIN(x))) + bias, K = 3 dilation 1 (kconv3) or K = 11 dilation 5 (kconv11), fused
-        # (row statistics + the fused conv); kconv3u = the same stage unfused (AdaIN+Snake kernel, then the conv).
+        # conv1(snake(AdaIN(x))) + bias at the Kokoro (K, dilation) pairs (3, 1), (7, 3), (11, 5), the workspace
+        # offering the records part: from K = 7 the library takes the record path (row statistics, the records
+        # pass with AdaIN + Snake, the MFMA kernel), below it the one-launch fused kernel (row statistics + the
+        # conv with AdaIN + Snake in its producer waves). kconv7f / kconv11f = the one-launch kernels at K = 7 /
+        # 11 (no records part); kconv3u = the K = 3 stage unfused (AdaIN+Snake kernel, then the one-launch conv).
         c = configs.c4b()
         x0 = T(c["x"])
         B, C, TT = c["x"].shape
         g_, b_, a_ = T(c["gamma"]), T(c["beta"]), T(c["alpha"])
-        K, dil = (11, 5) if name == "kconv11" else (3, 1)
+        K, dil = {"kconv3": (3, 1), "kconv3u": (3, 1), "kconv7": (7, 3), "kconv7f": (7, 3), "kconv11": (11, 5),
+                  "kconv11f": (11, 5)}[name]
         pad = (K - 1) * dil // 2
         g = configs.rng(1009)
         wp = abi.conv1d_pack_f16(torch.from_numpy((g.standard_normal((C, C, K)) * 0.05).astype(np.float16)).to(dev))
         bias = torch.from_numpy(g.standard_normal(C).astype(np.float16)).to(dev)
         gs = C if c["gamma"].ndim == 2 else 0
         y = torch.empty_like(x0) if name == "kconv3u" else None
-        ws = abi.conv_workspace(B, C, C, TT, K, pad, dil, abi.WS_IN_STATS, dev)
+        rec = name in ("kconv3", "kconv7", "kconv11")
+        ws = abi.conv_workspace(B, C, C, TT, K, pad, dil, abi.WS_IN_STATS | (abi.WS_RECORDS if rec else 0), dev)
 
         def make_set(_):
             return {"x": x0, "o": torch.empty_like(x0)}
@@ -476,9 +481,13 @@ def build_workload(name):
         alg = 2 * x0.numel() * 4
         flops = 2 * C * C * K * TT * B
         return Workload(name, f"ResBlock stage AdaIN+Snake -> conv1d K={K} dil={dil} f32 x[{B},{C},{TT}]"
-                        + (" (unfused: two kernels + y round trip)" if name == "kconv3u" else " (fused)"),
+                        + {"kconv3u": " (unfused: two kernels + y round trip)", "kconv3": " (one-launch fused conv)",
+                           "kconv7f": " (one-launch fused conv)", "kconv11f": " (one-launch fused conv)"}.get(
+                            name, " (record path: statistics, records pass, MFMA kernel)"),
                         alg, x0.numel() * 4, make_set, launch,
-                        {"kconv3": "nsrk_conv1d_rw_adain_snake_f16x2_nu3", "kconv11": "nsrk_conv1d_pc_adain_snake_f16x2_nu4",
+                        {"kconv3": "nsrk_conv1d_rw_adain_snake_f16x2_nu3", "kconv7": "nsrk_conv1d_pr_f16x2",
+                         "kconv11": "nsrk_conv1d_pr_f16x2", "kconv7f": "nsrk_conv1d_pc_adain_snake_f16x2_nu3",
+                         "kconv11f": "nsrk_conv1d_pc_adain_snake_f16x2_nu4",
                          "kconv3u": "nsrk_conv1d_rw_f16x2_nu3"}[name], "f32",
                         flops=flops)
 
@@ -498,7 +507,7 @@ def build_workload(name):
         gs = C if c["gamma"].ndim == 2 else 0
         xs = torch.empty((B * C, 2), dtype=torch.float32, device=dev)
         tmp = torch.empty_like(x0)
-        ws = abi.conv_workspace(B, C, C, TT, K, pad, dil, abi.WS_OUT_STATS, dev)
+        ws = abi.conv_workspace(B, C, C, TT, K, pad, dil, abi.WS_OUT_STATS | abi.WS_RECORDS, dev)
         abi.check(L.nsr_conv1d_f16w_packed_stats(x0.data_ptr(), wp.data_ptr(), None, None, tmp.data_ptr(),
                                                  xs.data_ptr(), B, C, C, TT, K, pad, dil, 1e-5, ws.data_ptr(),
                                                  ws.numel(), stream()))
@@ -518,9 +527,9 @@ def build_workload(name):
 
         alg = 2 * x0.numel() * 4
         flops = 2 * C * C * K * TT * B
-        return Workload(name, f"ResBlock stage in a chain (statistics handed along) K={K} dil={dil} f32 x[{B},{C},{TT}]",
-                        alg, x0.numel() * 4, make_set, launch,
-                        "nsrk_conv1d_rw_adain_snake_f16x2_nu3_st" if K == 3 else "nsrk_conv1d_pc_adain_snake_f16x2_nu4_st",
+        return Workload(name, f"ResBlock stage in a chain (statistics handed along) K={K} dil={dil} f32 x[{B},{C},{TT}]"
+                        + (" (record path)" if K >= 7 else " (one-launch fused conv)"), alg, x0.numel() * 4, make_set,
+                        launch, "nsrk_conv1d_pr_f16x2_st" if K >= 7 else "nsrk_conv1d_rw_adain_snake_f16x2_nu3_st",
                         "f32", flops=flops)
 
     if name == "c4a":

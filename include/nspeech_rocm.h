@@ -395,13 +395,29 @@ nsr_status nsr_conv1d_f32io(const float* x, const void* w, const void* bias, flo
  *                          and _chain when x_stats is NULL),
  *   NSR_WS_OUT_STATS       per-32-column partials of the output's row
  *                          statistics (_chain and nsr_conv1d_f16w_packed_stats
- *                          when out_stats is not NULL).
+ *                          when out_stats is not NULL),
+ *   NSR_WS_RECORDS         optional, for every entry point with a workspace:
+ *                          the conv input as f16 hi / lo records (B x
+ *                          ceil(C_in / 128) x (T_in + 2 padding) x 512 bytes,
+ *                          rounded up to 256) and the weights in MFMA
+ *                          fragment order (ceil(C_out / 128) x 4 x K x
+ *                          ceil(C_in / 128) x 8192 bytes). When the
+ *                          workspace also covers it (after the parts the call
+ *                          needs), rows with T_out % 4 == 0 and 16-byte
+ *                          aligned out / residual, and (K - 1) * dilation
+ *                          <= 56, take the two-launch record path: a
+ *                          bandwidth-bound pass writes the records (AdaIN +
+ *                          Snake included in the fused entry points) and the
+ *                          fragment weights, then an MFMA kernel with no
+ *                          per-element VALU work reads them. Same results as
+ *                          the one-launch kernels.
  * nsr_conv1d_workspace_bytes writes the bytes a call of that shape needs for
  * the given parts (each part at a 256-byte aligned offset, in flag order).
  * No counterpart in the reference (its Metal backend allocates per call). */
 #define NSR_WS_PACKED_WEIGHTS 1u
 #define NSR_WS_IN_STATS 2u
 #define NSR_WS_OUT_STATS 4u
+#define NSR_WS_RECORDS 8u
 nsr_status nsr_conv1d_workspace_bytes(int64_t B, int64_t C_in, int64_t C_out, int64_t T_in, int64_t K,
                                       int64_t padding, int64_t dilation, unsigned parts, int64_t* bytes);
 

@@ -402,7 +402,7 @@ def _conv_tout(T, K, padding, dilation):
     return T + 2 * padding - dilation * (K - 1)
 
 
-WS_PACKED_WEIGHTS, WS_IN_STATS, WS_OUT_STATS = 1, 2, 4
+WS_PACKED_WEIGHTS, WS_IN_STATS, WS_OUT_STATS, WS_RECORDS = 1, 2, 4, 8
 
 
 def conv1d_workspace_bytes(B, C_in, C_out, T, K, padding, dilation, parts) -> int:
@@ -422,15 +422,16 @@ def _ws(t):
     return (_ptr(t), t.numel()) if t is not None else (None, 0)
 
 
-def conv1d_f32io(x, w, bias=None, *, padding=0, dilation=1, out=None, workspace=None, stream=None):
-    """x f32 [B, C_in, T]; w f16 [C_out, C_in, K]; bias f16 [C_out] or None. The packed weights go to
-    `workspace` (allocated here when not given)."""
+def conv1d_f32io(x, w, bias=None, *, padding=0, dilation=1, out=None, workspace=None, records=True, stream=None):
+    """x f32 [B, C_in, T]; w f16 [C_out, C_in, K]; bias f16 [C_out] or None. The packed weights (and with
+    `records`, the input records of the two-launch path) go to `workspace` (allocated here when not given)."""
     B, C_in, T = x.shape
     C_out, _, K = w.shape
     if out is None:
         out = torch.empty((B, C_out, _conv_tout(T, K, padding, dilation)), dtype=torch.float32, device=x.device)
     if workspace is None:
-        workspace = conv_workspace(B, C_in, C_out, T, K, padding, dilation, WS_PACKED_WEIGHTS, x.device)
+        workspace = conv_workspace(B, C_in, C_out, T, K, padding, dilation,
+                                   WS_PACKED_WEIGHTS | (WS_RECORDS if records else 0), x.device)
     check(lib().nsr_conv1d_f32io(_ptr(x), _ptr(w), _ptr(bias), _ptr(out), B, C_in, C_out, T, K, 1, padding,
                                  dilation, *_ws(workspace), _stream(stream)))
     return out
@@ -455,9 +456,10 @@ def conv1d_f16w_packed(x, wp, bias=None, residual=None, *, padding=0, dilation=1
 
 
 def adain_snake_conv1d_chain(x, gamma, beta, alpha, wp, bias=None, residual=None, *, x_stats=None, want_stats=True,
-                             padding=0, dilation=1, eps=1e-5, out=None, stream=None):
+                             padding=0, dilation=1, eps=1e-5, out=None, records=True, stream=None):
     """adain_snake_conv1d with the row statistics handed along: x_stats f32 [B*C_in, 2] (mean, rstd) or None
-    (computed here); returns (out, out_stats) with out_stats f32 [B*C_out, 2] (None if not want_stats)."""
+    (computed here); returns (out, out_stats) with out_stats f32 [B*C_out, 2] (None if not want_stats).
+    `records`: give the workspace the records part (the two-launch path where the rows qualify)."""
     B, C_in, T = x.shape
     C_out, K, _ = wp.shape
     if out is None:
@@ -465,7 +467,8 @@ def adain_snake_conv1d_chain(x, gamma, beta, alpha, wp, bias=None, residual=None
     st = torch.empty((B * C_out, 2), dtype=torch.float32, device=x.device) if want_stats else None
     gs = C_in if gamma.dim() == 2 else 0
     bs = C_in if beta.dim() == 2 else 0
-    parts = (0 if x_stats is not None else WS_IN_STATS) | (WS_OUT_STATS if want_stats else 0)
+    parts = (0 if x_stats is not None else WS_IN_STATS) | (WS_OUT_STATS if want_stats else 0) | \
+        (WS_RECORDS if records else 0)
     ws = conv_workspace(B, C_in, C_out, T, K, padding, dilation, parts, x.device)
     check(lib().nsr_adain_snake_conv1d_chain_f32(_ptr(x), _ptr(x_stats), _ptr(gamma), _ptr(beta), _ptr(alpha),
                                                  _dt(gamma), gs, bs, _ptr(wp), _ptr(bias), _ptr(residual), _ptr(out),
@@ -475,21 +478,22 @@ def adain_snake_conv1d_chain(x, gamma, beta, alpha, wp, bias=None, residual=None
 
 
 def conv1d_f16w_packed_stats(x, wp, bias=None, residual=None, *, padding=0, dilation=1, eps=1e-5, out=None,
-                             stream=None):
+                             records=True, stream=None):
     """conv1d_f16w_packed that also returns the output rows' (mean, rstd) f32 [B*C_out, 2]."""
     B, C_in, T = x.shape
     C_out, K, _ = wp.shape
     if out is None:
         out = torch.empty((B, C_out, _conv_tout(T, K, padding, dilation)), dtype=torch.float32, device=x.device)
     st = torch.empty((B * C_out, 2), dtype=torch.float32, device=x.device)
-    ws = conv_workspace(B, C_in, C_out, T, K, padding, dilation, WS_OUT_STATS, x.device)
+    ws = conv_workspace(B, C_in, C_out, T, K, padding, dilation, WS_OUT_STATS | (WS_RECORDS if records else 0),
+                        x.device)
     check(lib().nsr_conv1d_f16w_packed_stats(_ptr(x), _ptr(wp), _ptr(bias), _ptr(residual), _ptr(out), _ptr(st), B,
                                              C_in, C_out, T, K, padding, dilation, eps, *_ws(ws), _stream(stream)))
     return out, st
 
 
 def adain_snake_conv1d(x, gamma, beta, alpha, wp, bias=None, residual=None, *, padding=0, dilation=1, eps=1e-5,
-                       out=None, stream=None):
+                       out=None, records=True, stream=None):
     """conv1d(snake(AdaIN(x))) + bias (+ residual); x f32 [B, C_in, T]; gamma/beta [C_in] or [B, C_in];
     alpha [C_in] (f32 or f16); wp packed f16 [C_out, K, C_in]."""
     B, C_in, T = x.shape
@@ -498,7 +502,8 @@ def adain_snake_conv1d(x, gamma, beta, alpha, wp, bias=None, residual=None, *, p
         out = torch.empty((B, C_out, _conv_tout(T, K, padding, dilation)), dtype=torch.float32, device=x.device)
     gs = C_in if gamma.dim() == 2 else 0
     bs = C_in if beta.dim() == 2 else 0
-    ws = conv_workspace(B, C_in, C_out, T, K, padding, dilation, WS_IN_STATS, x.device)
+    ws = conv_workspace(B, C_in, C_out, T, K, padding, dilation, WS_IN_STATS | (WS_RECORDS if records else 0),
+                        x.device)
     check(lib().nsr_adain_snake_conv1d_f32(_ptr(x), _ptr(gamma), _ptr(beta), _ptr(alpha), _dt(gamma), gs, bs,
                                            _ptr(wp), _ptr(bias), _ptr(residual), _ptr(out), B, C_in, C_out, T, K,
                                            padding, dilation, eps, *_ws(ws), _stream(stream)))

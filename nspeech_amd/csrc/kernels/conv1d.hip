@@ -31,6 +31,10 @@
  */
 #include "device_common.h"
 
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) nsr_uint4 lds_u4;
+typedef __attribute__((address_space(3))) nsr_float4 lds_f4;
+
 typedef _Float16 nsr_h8 __attribute__((ext_vector_type(8)));
 typedef float nsr_f32x16 __attribute__((ext_vector_type(16)));
 
@@ -51,6 +55,16 @@ NSR_DEV float quad_xor1(float v) {
 }
 NSR_DEV float quad_xor2(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+}
+/* Value of lane j of this lane's quad (DPP quad_perm [j, j, j, j]; j a constant after unrolling). */
+NSR_DEV float quad_bcast(float v, int j) {
+  const int x = __builtin_bit_cast(int, v);
+  switch (j) {
+    case 0: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x00, 0xF, 0xF, false));
+    case 1: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x55, 0xF, 0xF, false));
+    case 2: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0xAA, 0xF, 0xF, false));
+    default: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0xFF, 0xF, 0xF, false));
+  }
 }
 
 /* AdaIN + Snake coefficients of input row (b, ci): y = snake((x - mean) A + beta). */
@@ -920,6 +934,647 @@ NSR_DEV void conv_pc_body(const nsr_conv_args& a) {
 
 NSR_CONV_PC(3)
 NSR_CONV_PC(4)
+
+#define CV_TW 128           /* output columns per tile of the record kernel */
+
+/* --------------------------------------------- conv on pre-split input records -- */
+
+/* The MFMA kernel without per-element VALU work. On gfx950 a VALU
+ * instruction issued on a SIMD delays that SIMD's MFMAs by several cycles
+ * (measured: about 10 cycles of MFMA time per VALU instruction of another
+ * wave), so the elementwise work of the resblock input (AdaIN + Snake, the
+ * f16 hi / lo split, the transpose to [t][ci]) is done beforehand by
+ * nsrk_conv_presplit, a bandwidth-bound pass, into records: for input column
+ * tp - padding (tp = 0 .. T_out + (K - 1) dilation - 1) and each chunk of 128
+ * input channels, 512 bytes = 16 chunks of 8 hi halves then 16 of 8 lo
+ * halves (zeros outside the row and past C_in). The same pass writes the
+ * weights in MFMA fragment order: for each block of 32 output channels cb,
+ * tap k, channel chunk ch and step g, 1 KB = 64 lanes x 16 bytes, lane
+ * (l32, hl) holding w[32 cb + l32][k][128 ch + 16 g + 8 hl .. + 7].
+ *
+ * Tiles are 128 output channels x 128 columns; each workgroup takes a
+ * contiguous run of them (channel block fastest, then columns), so the next
+ * tile's window of TL = 128 + (K - 1) dilation records shares all or
+ * TL - 128 of its records with the current one. Records live in an LDS ring
+ * of 256 slots of 528 bytes (record tp in slot tp & 255; the 16-byte pad puts
+ * consecutive records in different bank groups, so 16 lanes reading one
+ * chunk of 16 consecutive records do not conflict):
+ *  - consumers (waves 0-3, 64 channels x 64 columns each as 2 x 2
+ *    accumulators) read B fragments from the ring and hold their A
+ *    fragments in registers, loaded one tap ahead straight from the fragment
+ *    weights (one 1 KB load per fragment, L2-resident);
+ *  - the record waves (4-7) load the next window's new records into
+ *    registers at the start of an item and write each into its slot as soon
+ *    as the record it replaces is dead: at once when the slot is free, after
+ *    tap K - 2 when it holds a record that only earlier taps read, after the
+ *    last tap otherwise (then one more barrier before the next item; never
+ *    for consecutive tiles of one row with an even (K - 1) dilation).
+ * Two barriers per item. LDS: 256 x 528 bytes. */
+#define CV_RB 512           /* bytes per record */
+#define CV_RS 528           /* bytes per record slot in LDS */
+#define CV_RING 256         /* record slots in LDS */
+#define CV_NRW 24           /* record rounds per transition: 24 x 8 records >= the largest window (192) */
+
+struct cv_item {
+  int b, co0, t0, ch;
+};
+
+/* The records of item n + 1 that item n's window lacks: [nb, ne) of (b, ch) of the next item. */
+struct cv_trans {
+  int nb, ne;
+};
+
+template <bool RESID, bool STATS = false>
+NSR_DEV void conv_pr_body(const nsr_conv_args& a, const uint8_t* xs, const uint8_t* wf) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t cv_ring[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); /* wave-uniform: role and tile math in SALU */
+  const int D = (a.K - 1) * a.dilation;
+  const int TLe = CV_TW + D + (D & 1);             /* window length, rounded to even */
+  const int Tp = a.T_out + D;                       /* records per (batch, channel chunk) */
+  const int n_t = (a.T_out + CV_TW - 1) / CV_TW, n_co = (a.C_out + CV_CO - 1) / CV_CO;
+  const int n_ch = (a.C_in + CV_CI - 1) / CV_CI;
+  const int n_tiles = n_t * n_co * a.B;
+
+  /* XCD-aware: XCD x (blocks x, x + 8, ...) takes an eighth of the tiles; each workgroup a contiguous run */
+  const int G = (int)gridDim.x;
+  const bool xcd = (G & 7) == 0;
+  const int nx = xcd ? 8 : 1, xid = xcd ? (int)(blockIdx.x & 7) : 0;
+  const int S = G / nx, slot = xcd ? (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+  const int x_lo = (int)((int64_t)n_tiles * xid / nx), x_hi = (int)((int64_t)n_tiles * (xid + 1) / nx);
+  const int first = x_lo + (int)((int64_t)(x_hi - x_lo) * slot / S);
+  const int last = x_lo + (int)((int64_t)(x_hi - x_lo) * (slot + 1) / S);
+  if (first >= last) return;
+  const int items = (last - first) * n_ch;
+  /* item n = tile first + n / n_ch, channel chunk n % n_ch; tiles run channel block fastest, then
+   * columns, then batch. The first item is decoded once, the others by stepping (no divisions). */
+  cv_item first_item;
+  {
+    const int r = first / n_co;
+    first_item.ch = 0;
+    first_item.co0 = (first - r * n_co) * CV_CO;
+    first_item.b = r / n_t;
+    first_item.t0 = (r - first_item.b * n_t) * CV_TW;
+  }
+  auto advance = [&](cv_item& it) {
+    if (++it.ch < n_ch) return;
+    it.ch = 0;
+    it.co0 += CV_CO;
+    if (it.co0 < n_co * CV_CO) return;
+    it.co0 = 0;
+    it.t0 += CV_TW;
+    if (it.t0 < n_t * CV_TW) return;
+    it.t0 = 0;
+    ++it.b;
+  };
+  /* the records of window nx that window cu lacks: [nb, ne) (cu == nullptr: none present) */
+  auto trans = [&](const cv_item* cu, const cv_item& nx_) {
+    cv_trans tr;
+    tr.nb = nx_.t0;
+    tr.ne = nx_.t0 + TLe;
+    if (cu && cu->b == nx_.b && cu->ch == nx_.ch && nx_.t0 >= cu->t0 && nx_.t0 < cu->t0 + TLe) tr.nb = cu->t0 + TLe;
+    return tr;
+  };
+  /* slot phase of a new record: 0 = its slot is free during item n, 1 = freed by tap K - 2, 2 = freed by
+   * the last tap (d = slot distance from the current window's start) */
+  auto phase_of = [&](int d) { return d >= TLe ? 0 : (d < D ? 1 : 2); };
+  /* Output staging: after item n's last tap its tile (row r = output channel co0 + r, 128 columns f32)
+   * goes to LDS while the ring holds window n + 1 (start nt0): rows r < FS in the ring slots outside
+   * that window, (nt0 + TLe + r) & 255, the other 128 - FS <= 56 rows after the ring. */
+  const int FS = (CV_RING - TLe) / 8 * 8;
+  auto stage_ring = [&](int nt0, int r) { return (uint32_t)((nt0 + TLe + r) & (CV_RING - 1)) * CV_RS; };
+  auto stage_tail = [&](int r) { return (uint32_t)(CV_RING * CV_RS + (r - FS) * 512); };
+
+  if (wave >= 4) {
+    /* record waves: pairs of records per wave and round (lanes 0-31 record q, 32-63 record q + 1) */
+    const int w4 = wave - 4;
+    const uint32_t vl = (uint32_t)((lane >> 5) * CV_RS + (lane & 31) * 16);
+    nsr_uint4 yr[CV_NRW];
+    /* Per-lane addresses are computed only before the first item and between an item's last two
+     * barriers, while the consumers run their epilogue: a VALU instruction issued while the consumer wave
+     * on the same SIMD streams MFMAs waits for a gap in that stream (and delays it), so what runs during
+     * the taps is memory and scalar instructions only. (The empty asm keeps the compiler from computing
+     * the addresses again where they are used.) */
+    auto pin = [](uint32_t& v) { asm volatile("" : "+v"(v)); };
+    auto pin_u4 = [](lds_u4*& p) { asm volatile("" : "+v"(p)); };
+    auto pin_f4 = [](lds_f4*& p) { asm volatile("" : "+v"(p)); };
+    uint32_t vlo = (uint32_t)lane * 16u;
+    pin(vlo);
+    lds_u4* waddr[CV_NRW]; /* ring address of round r's pair in the coming transition */
+    auto calc_waddr = [&](const cv_trans& tr) {
+#pragma unroll
+      for (int r = 0; r < CV_NRW; ++r) {
+        waddr[r] = (lds_u4*)(cv_ring + (uint32_t)((tr.nb + 2 * (4 * r + w4)) & (CV_RING - 1)) * CV_RS + vl);
+        pin_u4(waddr[r]);
+      }
+    };
+    /* The staged tile of an item to global memory: pairs of rows (lanes 0-31 row 2 j, 32-63 row 2 j + 1,
+     * 16 bytes per lane: 512 contiguous bytes per row). Wave w takes the pairs in the ring slots that it
+     * will itself overwrite with records of the transition after the next item (pair j sits in slot
+     * nt0 + TLe + 2 j, written by wave ((slot - nb2) / 2) & 3 of that transition), so no other wave
+     * overwrites a row before it is read. */
+    auto staged_jw = [&](int nt0, int nb2) { return (w4 - (((nt0 + TLe - nb2) & (CV_RING - 1)) >> 1)) & 3; };
+    lds_f4* saddr[16];
+    uint32_t svo = 0, sok = 0;
+    auto calc_saddr = [&](const cv_item& im, int nt0, int jw) {
+      const int quad = lane & 31, t = im.t0 + 4 * quad;
+      svo = (uint32_t)(lane >> 5) * (uint32_t)a.T_out * 4u + (uint32_t)t * 4u;
+      sok = t < a.T_out ? 1u : 0u;
+      pin(svo);
+      pin(sok);
+#pragma unroll
+      for (int p = 0; p < 16; ++p) {
+        const int r0 = 2 * (jw + 4 * p);
+        /* rows r0, r0 + 1: slot nt0 + TLe + r0 is even, so its neighbour does not wrap */
+        saddr[p] = (lds_f4*)(cv_ring + (r0 < FS ? stage_ring(nt0, r0) + (uint32_t)(lane >> 5) * CV_RS
+                                                : stage_tail(r0) + (uint32_t)(lane >> 5) * 512u) + 16u * (uint32_t)quad);
+        pin_f4(saddr[p]);
+      }
+    };
+    /* the staged rows of item m: read into registers before this wave's records overwrite their slots,
+     * stored after the records are written, one 16-byte store per lane every `gap` sleep units, spread
+     * over the taps so the consumers' A fragment loads do not queue behind a burst */
+    nsr_float4 sv[16];
+    auto read_staged = [&]() {
+#pragma unroll
+      for (int p = 0; p < 16; ++p) sv[p] = *saddr[p];
+    };
+    auto store_staged = [&](const cv_item& im, int jw, int gap) {
+      const uint32_t obytes = (uint32_t)(4 * a.C_out * a.T_out);
+      const nsr_rsrc orr = make_rsrc_uniform(a.out + (int64_t)im.b * a.C_out * a.T_out, obytes);
+      /* the residual (variants without statistics add it here), loaded 4 passes ahead */
+      const nsr_rsrc rr = make_rsrc_uniform(RESID ? a.residual + (int64_t)im.b * a.C_out * a.T_out : a.out, obytes);
+      nsr_float4 rq[RESID && !STATS ? 4 : 1];
+      auto load_rq = [&](int p) {
+        const int r0 = 2 * (jw + 4 * p);
+        rq[p & 3] = __builtin_bit_cast(nsr_float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       rr, svo, (uint32_t)(im.co0 + r0) * (uint32_t)a.T_out * 4u, 0));
+      };
+      if constexpr (RESID && !STATS) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) load_rq(p);
+      }
+#pragma unroll
+      for (int p = 0; p < 16; ++p) {
+        const int r0 = 2 * (jw + 4 * p);
+        nsr_float4 v = sv[p];
+        if constexpr (RESID && !STATS) {
+          v += rq[p & 3];
+          if (p + 4 < 16) load_rq(p + 4);
+        }
+        /* C_out is even on this path: both rows of a pair exist or neither */
+        if (sok && im.co0 + r0 < a.C_out)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(nsr_uint4, v), orr, svo,
+                                                 (uint32_t)(im.co0 + r0) * (uint32_t)a.T_out * 4u, 0);
+        for (int z = 0; z < gap; ++z) __builtin_amdgcn_s_sleep(1);
+      }
+    };
+    /* rolling items: ip = n - 1, ic = n, in = n + 1, in2 = n + 2 (valid below `items`); tc = the
+     * transition n -> n + 1 */
+    cv_item ip = first_item, ic = first_item, in = first_item, in2 = first_item;
+    advance(in2);
+    cv_trans tc = trans(nullptr, in);
+    calc_waddr(tc);
+    int jw_p = 0; /* staging pairs of item n - 1 */
+    /* sleep units (64 cycles) between staged stores: 16 stores over about (K - 2) / 2 taps */
+    const int gap = max(1, 3 * (a.K - 2) / 2);
+    for (int n = -1; n < items; ++n) {
+      const bool has_next = n + 1 < items;
+      if (has_next) {
+        const nsr_rsrc xr =
+            make_rsrc_uniform(xs + ((int64_t)in.b * n_ch + in.ch) * Tp * CV_RB, (uint32_t)(Tp * CV_RB));
+        /* 16 rounds always (128 new records for consecutive tiles; rounds past the new records re-read
+         * the last pair), 8 more for a window that shares nothing with the current one */
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int q = min(tc.nb + 2 * (4 * r + w4), tc.ne - 2);
+          yr[r] = __builtin_amdgcn_raw_buffer_load_b128(xr, vlo, (uint32_t)q * CV_RB, NSR_AUX_NT);
+        }
+        if (tc.ne - tc.nb > 128) {
+#pragma unroll
+          for (int r = 16; r < CV_NRW; ++r) {
+            const int q = min(tc.nb + 2 * (4 * r + w4), tc.ne - 2);
+            yr[r] = __builtin_amdgcn_raw_buffer_load_b128(xr, vlo, (uint32_t)q * CV_RB, NSR_AUX_NT);
+          }
+        }
+      }
+      const bool staged = n >= 1 && ip.ch == n_ch - 1;
+      if (staged) read_staged();
+      /* the rounds of each phase as bit masks, computed once per transition (scalar work here is shared
+       * with the consumers' waves: one test per round and phase below) */
+      uint32_t pm[3] = {0u, 0u, 0u};
+      if (has_next) {
+        const int dd = tc.nb + 2 * w4 - ic.t0;
+#pragma unroll
+        for (int r = 0; r < CV_NRW; ++r) {
+          if (tc.nb + 2 * (4 * r + w4) < tc.ne) {
+            const int d = (dd + 8 * r) & (CV_RING - 1); /* even; the pair's second record is d + 1 */
+            const int p = n < 0 ? 0 : max(phase_of(d), phase_of((d + 1) & (CV_RING - 1)));
+            pm[p] |= 1u << r;
+          }
+        }
+        NSR_WAIT_VMCNT(0);
+      }
+      auto write_phase = [&](int ph) {
+#pragma unroll
+        for (int r = 0; r < CV_NRW; ++r)
+          if ((pm[ph] >> r) & 1u) *waddr[r] = yr[r];
+      };
+      write_phase(0);
+      if (staged) store_staged(ip, jw_p, gap);
+      const bool has_next2 = n + 2 < items;
+      const cv_trans tn = has_next2 ? trans(&in, in2) : tc;
+      if (n < 0) {
+        if (has_next2) calc_waddr(tn);
+        __syncthreads(); /* item 0's window staged */
+      } else {
+        if (a.K > 1) __syncthreads(); /* taps 0 .. K - 2 of item n done */
+        write_phase(1);
+        __syncthreads(); /* item n done */
+        write_phase(2);
+        /* the consumers' epilogue: the next transition's and the staged tile's addresses */
+        if (has_next2) calc_waddr(tn);
+        if (ic.ch == n_ch - 1) {
+          const int nt0 = has_next ? in.t0 : ic.t0;
+          jw_p = staged_jw(nt0, has_next2 ? tn.nb : 0);
+          calc_saddr(ic, nt0, jw_p);
+        }
+        __syncthreads(); /* item n + 1's window and item n's output staged */
+      }
+      ip = ic;
+      ic = in;
+      in = in2;
+      advance(in2);
+      tc = tn;
+    }
+    if (ip.ch == n_ch - 1) {
+      read_staged();
+      store_staged(ip, jw_p, 0);
+    }
+  } else {
+    const int wco = wave >> 1, wt = wave & 1;
+    const int hl = lane >> 5, l32 = lane & 31, c4 = lane & 3;
+    const uint32_t obytes = (uint32_t)(4 * a.C_out * a.T_out);
+    const uint32_t kstride = (uint32_t)n_ch * 8192u, cbstride = (uint32_t)a.K * kstride;
+    const nsr_rsrc wr = make_rsrc_uniform(wf, (uint32_t)n_co * 4u * cbstride);
+    /* fragment weights of (item, tap) for this wave's 64 channels (m = 0: cb, m = 1: cb + 1) */
+    auto a_base = [&](const cv_item& it, int k) {
+      return (uint32_t)(it.co0 / 32 + 2 * wco) * cbstride + (uint32_t)k * kstride + (uint32_t)it.ch * 8192u;
+    };
+    nsr_h8 A[2][8];
+    {
+      const uint32_t ab = a_base(first_item, 0);
+#pragma unroll
+      for (int g = 0; g < 8; ++g)
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+          A[m][g] = __builtin_bit_cast(nsr_h8, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    wr, (uint32_t)lane * 16u, ab + m * cbstride + g * 1024u, 0));
+    }
+    nsr_f32x16 acc[2][2];
+    /* residual of column block tb (the statistics variants add it here; the others' record waves add it
+     * when they store the tile) */
+    nsr_float4 rv[RESID ? 2 : 1][RESID ? 2 : 1][RESID ? 4 : 1];
+    auto load_resid = [&](const cv_item& it, int tb) {
+      const nsr_rsrc rr = make_rsrc_uniform(a.residual + (int64_t)it.b * a.C_out * a.T_out, obytes);
+      const uint32_t tc = (uint32_t)min(it.t0 + wt * 64 + tb * 32 + 4 * (l32 >> 2), a.T_out - 4);
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t co = (uint32_t)(it.co0 + wco * 64 + m * 32 + 8 * q + 4 * hl + c4);
+          rv[tb][m][q] = __builtin_bit_cast(
+              nsr_float4, __builtin_amdgcn_raw_buffer_load_b128(rr, (co * (uint32_t)a.T_out + tc) * 4u, 0, 0));
+        }
+    };
+    uint32_t braw[2][4];
+    int bias_co0 = -1;
+    __syncthreads(); /* item 0's window staged */
+    NSR_WAIT_VMCNT(0); /* tap 0 of every item starts with its A fragments in place (see the epilogue) */
+    cv_item it = first_item, in = first_item;
+    advance(in);
+    for (int n = 0; n < items; ++n) {
+      const bool last_chunk = it.ch == n_ch - 1;
+      const bool has_next = n + 1 < items;
+      const cv_item nxt = has_next ? in : it;
+      if (it.ch == 0) {
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[m][tb][i] = 0.f;
+      }
+      if (last_chunk && it.co0 != bias_co0) {
+        /* the bias of this lane's 8 output channels, raw halves loaded when the channel block changes
+         * and converted in the epilogue (a conversion here would wait for every older memory operation) */
+        const uint16_t* bsrc = a.bias ? a.bias : (const uint16_t*)a.w; /* any readable halves when there is no bias */
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) braw[m][q] = bsrc[min(it.co0 + wco * 64 + m * 32 + 8 * q + 4 * hl + c4, a.C_out - 1)];
+        bias_co0 = it.co0;
+      }
+      const int j0 = it.t0 + 64 * wt + l32;
+      /* one tap; tap 0 is issued on its own (peeled) so its waits for the A fragments loaded before the
+       * previous item's epilogue count that epilogue's stores as younger operations, instead of sharing
+       * the loop's waits and so waiting for the stores too */
+      auto tap = [&](int k, auto reload) {
+        /* B fragment (tb, step g): record j0 + 32 tb + k dilation, hi chunk 2 g + hl, lo 256 bytes further */
+        const int j = j0 + k * a.dilation;
+        uint32_t va[2];
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) va[tb] = (uint32_t)((j + 32 * tb) & (CV_RING - 1)) * CV_RS + (uint32_t)hl * 16u;
+        /* the A fragments of the next tap (or of the next item's tap 0; the last item's own tap 0 after
+         * the last tap, a load never used) replace this tap's, step by step, unconditionally so the
+         * tap is one basic block the schedule below can order */
+        const uint32_t ab = k + 1 < a.K ? a_base(it, k + 1) : a_base(nxt, 0);
+        nsr_h8 Bh[2][2], Bl[2][2];
+        auto ld = [&](int buf, int g) {
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb) {
+            Bh[buf][tb] = *(const nsr_h8*)(cv_ring + va[tb] + 32 * g);
+            Bl[buf][tb] = *(const nsr_h8*)(cv_ring + va[tb] + 256 + 32 * g);
+          }
+        };
+        ld(0, 0);
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+          const int cur = g & 1;
+          if (g + 1 < 8) ld(cur ^ 1, g + 1);
+#pragma unroll
+          for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+              acc[m][tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[m][g], Bh[cur][tb], acc[m][tb], 0, 0, 0);
+#pragma unroll
+          for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+              acc[m][tb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[m][g], Bl[cur][tb], acc[m][tb], 0, 0, 0);
+          if constexpr (decltype(reload)::value) {
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+              A[m][g] = __builtin_bit_cast(nsr_h8, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        wr, (uint32_t)lane * 16u, ab + m * cbstride + g * 1024u, 0));
+          }
+        }
+        /* order: step 0's reads, then per step: the next step's reads, its 8 MFMAs, its 2 A reloads */
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int g = 0; g < 7; ++g) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+        if (k == a.K - 2) __syncthreads(); /* taps 0 .. K - 2 done: their records may be replaced */
+      };
+      /* with a residual and statistics the last tap does not reload: the epilogue's registers would not
+       * hold the next item's A fragments as well, which are loaded after it instead */
+      constexpr bool last_reload = !(RESID && STATS);
+      tap(0, std::true_type{});
+      for (int k = 1; k < a.K - 1; ++k) tap(k, std::true_type{});
+      if (a.K > 1) tap(a.K - 1, std::bool_constant<last_reload>{});
+      __syncthreads(); /* item n done */
+      /* the next tap's A fragments (loaded during the last tap) have arrived by now: waiting for them
+       * here keeps tap 0 of the next item free of waits */
+      NSR_WAIT_VMCNT(0);
+      if (last_chunk) {
+        float bv[2][4];
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) bv[m][q] = a.bias ? f16_bits_to_f32((uint16_t)braw[m][q]) : 0.f;
+        /* row r of the staged tile: in the ring (row groups of 8 lie wholly in the ring or after it) */
+        auto stage_row = [&](int R0, int r) { return R0 < FS ? stage_ring(nxt.t0, r) : stage_tail(r); };
+        if constexpr (!STATS) {
+          /* accumulator element i of lane (hl, l32) is channel 8 (i / 4) + 4 hl + i % 4 of its 32-channel
+           * block at column l32: dword writes, 32 consecutive columns per half-wave, no cross-lane moves;
+           * bv[m][q] holds channel 8 q + 4 hl + c4, so the bias of element i is in quad lane i % 4 */
+#pragma unroll
+          for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              const int R0 = 64 * wco + 32 * m + 8 * g4;
+#pragma unroll
+              for (int c = 0; c < 4; ++c) {
+                const int i = 4 * g4 + c;
+                const float bi = quad_bcast(bv[m][g4], c);
+                const uint32_t la = stage_row(R0, R0 + 4 * hl + c) + (uint32_t)(64 * wt + l32) * 4u;
+#pragma unroll
+                for (int tb = 0; tb < 2; ++tb) *(float*)(cv_ring + la + 128u * tb) = acc[m][tb][i] + bi;
+              }
+            }
+        } else {
+          /* row statistics: the quad transpose gives each lane 4 consecutive columns */
+          if constexpr (RESID) {
+            load_resid(it, 0);
+            load_resid(it, 1);
+          }
+#pragma unroll
+          for (int tb = 0; tb < 2; ++tb) {
+            const int tl = wt * 64 + tb * 32 + 4 * (l32 >> 2), t = it.t0 + tl;
+            nsr_float4 ov[2][4];
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                float v[4] = {acc[m][tb][4 * q], acc[m][tb][4 * q + 1], acc[m][tb][4 * q + 2], acc[m][tb][4 * q + 3]};
+                float x1[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) x1[r] = quad_xor1(v[r ^ 1]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[r] = ((r ^ c4) & 1) ? x1[r] : v[r];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) x1[r] = quad_xor2(v[r ^ 2]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[r] = ((r ^ c4) & 2) ? x1[r] : v[r];
+                const float bb = bv[m][q];
+                nsr_float4 o = {v[0] + bb, v[1] + bb, v[2] + bb, v[3] + bb};
+                if constexpr (RESID) o += rv[tb][m][q];
+                const int R0 = 64 * wco + 32 * m + 8 * q;
+                *(nsr_float4*)(cv_ring + stage_row(R0, R0 + 4 * hl + c4) + (uint32_t)tl * 4u) = o;
+                ov[m][q] = o;
+              }
+            emit_rows8(ov, t, it.t0 + wt * 64 + tb * 32, a.T_out, l32, it.co0 + wco * 64 + 4 * hl + c4, a.C_out,
+                       (int64_t)it.b * a.C_out, (a.T_out + 31) >> 5, (it.t0 + wt * 64 + tb * 32) >> 5, a.row_part);
+          }
+        }
+      }
+      if constexpr (!last_reload) {
+        const uint32_t ab = a_base(nxt, 0);
+#pragma unroll
+        for (int g = 0; g < 8; ++g)
+#pragma unroll
+          for (int m = 0; m < 2; ++m)
+            A[m][g] = __builtin_bit_cast(nsr_h8, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      wr, (uint32_t)lane * 16u, ab + m * cbstride + g * 1024u, 0));
+      }
+      if constexpr (!last_reload) {
+        const uint32_t ab = a_base(nxt, 0);
+#pragma unroll
+        for (int g = 0; g < 8; ++g)
+#pragma unroll
+          for (int m = 0; m < 2; ++m)
+            A[m][g] = __builtin_bit_cast(nsr_h8, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      wr, (uint32_t)lane * 16u, ab + m * cbstride + g * 1024u, 0));
+      }
+      __syncthreads(); /* item n + 1's window and item n's output staged */
+      it = in;
+      advance(in);
+    }
+    NSR_WAIT_VMCNT(0); /* the last tap's unused reloads */
+  }
+}
+
+#define NSR_CONV_PR1(NAME, RESID)                                                                    \
+  extern "C" __global__ void __launch_bounds__(512, 1)                                              \
+      NAME(const nsr_conv_args a, const uint8_t* xs, const uint8_t* wf) {                           \
+    conv_pr_body<RESID>(a, xs, wf);                                                                 \
+  }                                                                                                 \
+  extern "C" __global__ void __launch_bounds__(512, 1)                                              \
+      NAME##_st(const nsr_conv_args a, const uint8_t* xs, const uint8_t* wf) {                      \
+    conv_pr_body<RESID, true>(a, xs, wf);                                                           \
+  }
+NSR_CONV_PR1(nsrk_conv1d_pr_f16x2, false)
+NSR_CONV_PR1(nsrk_conv1d_pr_res_f16x2, true)
+
+/* Records and fragment weights for nsrk_conv1d_pr*. Record tp (tp = 0 ..
+ * T_in + 2 padding - 1, input column tp - padding) of channel chunk ch holds
+ * y = x (or snake(AdaIN(x)) in the fused form, with the row statistics in
+ * a.stats) of channels 128 ch .. 128 ch + 127 split as hi = f16(y),
+ * lo = f16(y - hi): 16 chunks of 8 hi halves, then 16 of 8 lo halves; zeros
+ * outside [0, T_in) and past C_in. One 256-lane workgroup per 64 records of
+ * one (batch, chunk): each lane loads 8 channels x 4 columns (one 16-byte
+ * load per channel, 64 consecutive columns per row across 16 lanes),
+ * transforms and packs them into its chunks of 4 records in LDS, then the
+ * 32 KB block is stored contiguously. Bandwidth-bound: x read once, the
+ * records written once (4 bytes per element each way). The workgroups after
+ * the records' write the fragment weights, 16 bytes per lane. Blocks are
+ * mapped XCD-contiguously (XCD x takes the x-th eighth of the logical
+ * blocks), so neighbouring blocks, which share the cache lines at their
+ * column boundary, run on one L2. */
+template <bool FUSED>
+NSR_DEV void conv_presplit(const nsr_conv_args& a, uint8_t* xs, uint8_t* wf) {
+  __shared__ __attribute__((aligned(16))) uint8_t rec[64 * CV_RS];
+  const int tid = threadIdx.x, rg = tid >> 4, cq = tid & 15;
+  const int Tp = a.T_in + 2 * a.padding;
+  const int nblk = (Tp + 63) / 64, n_ch = (a.C_in + CV_CI - 1) / CV_CI;
+  const int G = (int)gridDim.x;
+  const int lb = (G & 7) == 0 ? (int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+  const int nrb = a.B * n_ch * nblk;
+  if (lb >= nrb) {
+    /* fragment weights: 16 bytes per lane */
+    const int n_co = (a.C_out + CV_CO - 1) / CV_CO;
+    const int64_t f = (int64_t)(lb - nrb) * 256 + tid; /* 16-byte unit */
+    const int64_t nf = (int64_t)n_co * 4 * a.K * n_ch * 512;
+    if (f >= nf) return;
+    const int ln = (int)(f & 63);
+    int64_t grp = f >> 6;
+    const int g = (int)(grp & 7);
+    grp >>= 3;
+    const int ch = (int)(grp % n_ch);
+    grp /= n_ch;
+    const int k = (int)(grp % a.K);
+    const int cb = (int)(grp / a.K);
+    const int co = 32 * cb + (ln & 31), ci0 = CV_CI * ch + 16 * g + 8 * (ln >> 5);
+    uint32_t hv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint32_t lo16 = 0, hi16 = 0;
+      if (co < a.C_out) {
+        const uint16_t* wrow = a.w + ((int64_t)co * a.K + k) * a.C_in;
+        if (ci0 + 2 * e < a.C_in) lo16 = wrow[ci0 + 2 * e];
+        if (ci0 + 2 * e + 1 < a.C_in) hi16 = wrow[ci0 + 2 * e + 1];
+      }
+      hv[e] = lo16 | (hi16 << 16);
+    }
+    *(nsr_uint4*)(wf + f * 16) = nsr_uint4{hv[0], hv[1], hv[2], hv[3]};
+    return;
+  }
+  const int blk = lb % nblk;
+  const int bc = lb / nblk; /* b * n_ch + ch */
+  const int b = bc / n_ch, ch = bc - b * n_ch;
+  const int tp0 = blk * 64 + 4 * cq;
+  const int c0 = ch * CV_CI + 8 * rg; /* this lane's 8 channels */
+  const int ti0 = tp0 - a.padding;   /* its 4 input columns ti0 .. ti0 + 3 */
+  const nsr_rsrc xr = make_rsrc_uniform(a.x + (int64_t)b * a.C_in * a.T_in, (uint32_t)(4 * a.C_in * a.T_in));
+  /* Interior lanes: one 16-byte load per channel (4-byte aligned offsets). Lanes whose 4 columns cross
+   * either end of the row load each column on its own at a clamped column, so no load leaves the
+   * batch's buffer; those columns, and channels past C_in, are zeroed below. */
+  float y[8][4];
+  if (ti0 >= 0 && ti0 + 3 < a.T_in) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = min(c0 + i, a.C_in - 1);
+      const nsr_float4 v = __builtin_bit_cast(
+          nsr_float4, __builtin_amdgcn_raw_buffer_load_b128(xr, (uint32_t)((int64_t)c * a.T_in + ti0) * 4u, 0, NSR_AUX_NT));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[i][e] = v[e];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = min(c0 + i, a.C_in - 1);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int ti = min(max(ti0 + e, 0), a.T_in - 1);
+        y[i][e] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(xr, (uint32_t)((int64_t)c * a.T_in + ti) * 4u, 0, NSR_AUX_NT));
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const bool crow = c0 + i < a.C_in;
+    if constexpr (FUSED) {
+      const cv_coef cf = cv_row_coef(a, b, min(c0 + i, a.C_in - 1));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[i][e] = snake_eval(__builtin_fmaf(y[i][e] - cf.mean, cf.A, cf.bet), cf.sc);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int ti = ti0 + e;
+      y[i][e] = (crow && ti >= 0 && ti < a.T_in) ? y[i][e] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    uint32_t hi[4], lo[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const _Float16 h0 = (_Float16)y[2 * h][e], h1 = (_Float16)y[2 * h + 1][e];
+      const _Float16 l0 = (_Float16)(y[2 * h][e] - (float)h0), l1 = (_Float16)(y[2 * h + 1][e] - (float)h1);
+      hi[h] = (uint32_t)h_bits(h0) | ((uint32_t)h_bits(h1) << 16);
+      lo[h] = (uint32_t)h_bits(l0) | ((uint32_t)h_bits(l1) << 16);
+    }
+    const int r = 4 * cq + e;
+    *(nsr_uint4*)(rec + r * CV_RS + 16 * rg) = nsr_uint4{hi[0], hi[1], hi[2], hi[3]};
+    *(nsr_uint4*)(rec + r * CV_RS + 256 + 16 * rg) = nsr_uint4{lo[0], lo[1], lo[2], lo[3]};
+  }
+  __syncthreads();
+  const int nrec = min(64, Tp - blk * 64);
+  const nsr_rsrc orr = make_rsrc_uniform(xs + ((int64_t)bc * Tp + blk * 64) * CV_RB, (uint32_t)(nrec * CV_RB));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int id = tid + 256 * i; /* 16-byte chunk: record id >> 5, chunk id & 31 */
+    __builtin_amdgcn_raw_buffer_store_b128(*(const nsr_uint4*)(rec + (id >> 5) * CV_RS + 16 * (id & 31)), orr,
+                                           (uint32_t)(16 * id), 0, NSR_AUX_NT);
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256) nsrk_conv_presplit(const nsr_conv_args a, uint8_t* xs, uint8_t* wf) {
+  conv_presplit<false>(a, xs, wf);
+}
+extern "C" __global__ void __launch_bounds__(256)
+    nsrk_conv_presplit_adain_snake(const nsr_conv_args a, uint8_t* xs, uint8_t* wf) {
+  conv_presplit<true>(a, xs, wf);
+}
+
+
+
 
 /* NP = ceil(TL / 8) staged columns per lane: TL <= 72, 96, 128 */
 /* OCC, OCCF: workgroups per CU the register budget of the plain and the

@@ -1405,17 +1405,69 @@ nsr_status nsr_conv1d_pack_f16(const void* w, int64_t C_out, int64_t C_in, int64
   return launch(K_nsrk_conv1d_pack, cdiv_u(C_out * C_in * K, 256), 1, 256, 0, stream, params);
 }
 
+// Records of the pre-split conv: B x ceil(C_in / 128) x (T_in + 2 padding) records of 512 bytes, then the
+// weights in MFMA fragment order, ceil(C_out / 128) x 4 x K x ceil(C_in / 128) x 8 KB.
+static int64_t conv_records_only_bytes(int64_t B, int64_t C_in, int64_t Tp) {
+  return (B * ((C_in + 127) / 128) * Tp * 512 + 255) / 256 * 256;
+}
+static int64_t conv_records_bytes(int64_t B, int64_t C_in, int64_t C_out, int64_t K, int64_t Tp) {
+  return conv_records_only_bytes(B, C_in, Tp) + (C_out + 127) / 128 * 4 * K * ((C_in + 127) / 128) * 8192;
+}
+
+// The record path: a bandwidth-bound pass writes the input's records (AdaIN + Snake when fused, the f16
+// hi / lo split, [t][ci] order) and the weights in fragment order into the caller's workspace, then the MFMA
+// kernel reads them with no per-element VALU work. Taken when `records` is given and the rows qualify; else
+// the one-launch kernels.
+static constexpr int kCvTW = 128;
+static constexpr unsigned kCvRingLds = 256 * 528 + 56 * 512;  // record ring + the output staging rows after it
+static nsr_status conv_records(bool fused, nsr_conv_args& a, char* records, nsr_stream_t stream, const char* what,
+                               bool* emitted = nullptr) {
+  DeviceModule* dm = nullptr;
+  nsr_status st = current_module(&dm);
+  if (st != NSR_OK) return st;
+  const int64_t D = (int64_t)(a.K - 1) * a.dilation;
+  const int64_t TLe = kCvTW + D + (D & 1);
+  const bool rows16 = a.T_out % 4 == 0 && aligned(a.out, 16) && (!a.residual || aligned(a.residual, 16));
+  // TLe <= 184 leaves 72 ring slots outside a window, which with the 56 rows after the ring stage a 128-row tile.
+  // Below K = 7 the records pass (x read, records written) costs more than the one-launch kernels lose to
+  // their per-element work (measured on MI355X at [8, 128, 115200]: K = 3 about 540 us against 370 us).
+  if (!records || a.K < 7 || !rows16 || TLe > 184 || a.C_out % 2 != 0 || kCvRingLds > dm->max_lds || a.T_in <= 0)
+    return conv_launch(fused, a, stream, what, emitted);
+  const int64_t Tp = (int64_t)a.T_in + 2 * a.padding;
+  const int64_t n_ch = (a.C_in + 127) / 128, n_co = (a.C_out + 127) / 128;
+  const int64_t rec_blocks = (int64_t)a.B * n_ch * ((Tp + 63) / 64);
+  const int64_t w_blocks = n_co * 4 * a.K * n_ch * 2;  // fragment weights: 16 bytes per lane, 8 KB = 2 blocks
+  const int64_t blocks = (rec_blocks + w_blocks + 7) / 8 * 8;
+  if (blocks > 0x7fffffffLL || Tp * 512 > 0xffffffffLL) return conv_launch(fused, a, stream, what, emitted);
+  uint8_t* xs = (uint8_t*)records;
+  uint8_t* wf = (uint8_t*)records + conv_records_only_bytes(a.B, a.C_in, Tp);
+  void* pp[] = {&a, &xs, &wf};
+  st = launch(fused ? K_nsrk_conv_presplit_adain_snake : K_nsrk_conv_presplit, (unsigned)blocks, 1, 256, 0, stream, pp);
+  if (st != NSR_OK) return st;
+  a.pad_ = 1;
+  const int64_t tiles = (int64_t)cdiv_u(a.T_out, kCvTW) * n_co * a.B;
+  if (tiles > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "%s: too many tiles", what);
+  const bool stats = a.row_part != nullptr;
+  if (emitted) *emitted = stats;
+  static const KId ids[2][2] = {{K_nsrk_conv1d_pr_f16x2, K_nsrk_conv1d_pr_f16x2_st},
+                                {K_nsrk_conv1d_pr_res_f16x2, K_nsrk_conv1d_pr_res_f16x2_st}};
+  // one workgroup per CU, a multiple of 8 (the kernel's XCD split) when there are enough tiles
+  int64_t grid = std::min<int64_t>(tiles, dm->n_cu);
+  if (grid >= 8) grid = grid / 8 * 8;
+  return launch(ids[a.residual != nullptr][stats], (unsigned)grid, 1, 512, kCvRingLds, stream, pp);
+}
+
 // Launch a conv and leave the per-(b, co) statistics of its output in row_stats ([B*C_out][2]: mean,
 // 1 / sqrt(var + eps)): the aligned-row kernels emit per-32-column (mean, M2) blocks from their epilogue into
 // `part` (the caller's workspace, [B*C_out][ceil(T_out / 32)][2] f32) and a merge kernel combines them; the
 // fallback kernel's output is re-read by the row statistics kernel instead.
 static nsr_status conv_launch_stats(bool fused, nsr_conv_args& a, float eps, float* row_stats, float* part,
-                                    nsr_stream_t stream, const char* what) {
+                                    char* records, nsr_stream_t stream, const char* what) {
   const int64_t rows = (int64_t)a.B * a.C_out, nblk = ((int64_t)a.T_out + 31) / 32;
   if (rows > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "%s: too many rows", what);
   a.row_part = part;
   bool emitted = false;
-  nsr_status st = conv_launch(fused, a, stream, what, &emitted);
+  nsr_status st = conv_records(fused, a, records, stream, what, &emitted);
   if (st == NSR_OK && emitted) {
     nsr_rowstats_args m;
     std::memset(&m, 0, sizeof(m));
@@ -1447,12 +1499,12 @@ static nsr_status conv_launch_stats(bool fused, nsr_conv_args& a, float eps, flo
 // Workspace parts of the conv entry points, each at a 256-byte aligned offset in the order of the flags.
 static int64_t ws_round(int64_t b) { return (b + 255) / 256 * 256; }
 
-static void conv_ws_layout(int64_t B, int64_t C_in, int64_t C_out, int64_t T_out, int64_t K, unsigned parts,
-                           int64_t off[3], int64_t* total) {
+static void conv_ws_layout(int64_t B, int64_t C_in, int64_t C_out, int64_t T_out, int64_t K, int64_t Tp,
+                           unsigned parts, int64_t off[4], int64_t* total) {
   int64_t o = 0;
-  const int64_t sz[3] = {ws_round(C_out * C_in * K * 2), ws_round(B * C_in * 2 * 4),
-                         ws_round(B * C_out * ((T_out + 31) / 32) * 2 * 4)};
-  for (int i = 0; i < 3; ++i) {
+  const int64_t sz[4] = {ws_round(C_out * C_in * K * 2), ws_round(B * C_in * 2 * 4),
+                         ws_round(B * C_out * ((T_out + 31) / 32) * 2 * 4), ws_round(conv_records_bytes(B, C_in, C_out, K, Tp))};
+  for (int i = 0; i < 4; ++i) {
     off[i] = -1;
     if (parts & (1u << i)) {
       off[i] = o;
@@ -1462,21 +1514,26 @@ static void conv_ws_layout(int64_t B, int64_t C_in, int64_t C_out, int64_t T_out
   *total = o;
 }
 
-// Check the caller's workspace and return the address of each requested part.
+// Check the caller's workspace and return the address of each requested part. The records part is
+// optional: present (ptr[3]) when the workspace also covers it, after the required parts.
 static nsr_status conv_ws_parts(void* workspace, int64_t workspace_bytes, int64_t B, int64_t C_in, int64_t C_out,
-                                int64_t T_out, int64_t K, unsigned parts, char* ptr[3], const char* what) {
-  int64_t off[3], need = 0;
-  conv_ws_layout(B, C_in, C_out, std::max<int64_t>(T_out, 0), K, parts, off, &need);
+                                int64_t T_out, int64_t K, int64_t Tp, unsigned parts, char* ptr[4],
+                                const char* what) {
+  int64_t off[4], need = 0;
+  conv_ws_layout(B, C_in, C_out, std::max<int64_t>(T_out, 0), K, Tp, parts, off, &need);
   if (need > 0 && (!workspace || !aligned(workspace, 256) || workspace_bytes < need))
     return fail(NSR_ERR_BAD_ARG, "%s: needs a 256-byte aligned workspace of %lld bytes (nsr_conv1d_workspace_bytes)",
                 what, (long long)need);
-  for (int i = 0; i < 3; ++i) ptr[i] = off[i] >= 0 ? (char*)workspace + off[i] : nullptr;
+  for (int i = 0; i < 4; ++i) ptr[i] = off[i] >= 0 ? (char*)workspace + off[i] : nullptr;
+  int64_t roff[4], rneed = 0;
+  conv_ws_layout(B, C_in, C_out, std::max<int64_t>(T_out, 0), K, Tp, parts | NSR_WS_RECORDS, roff, &rneed);
+  if (workspace && aligned(workspace, 256) && workspace_bytes >= rneed) ptr[3] = (char*)workspace + roff[3];
   return NSR_OK;
 }
 
-nsr_status nsr_conv1d_f16w_packed(const float* x, const void* w_packed, const void* bias, const float* residual,
-                                  float* out, int64_t B, int64_t C_in, int64_t C_out, int64_t T_in, int64_t K,
-                                  int64_t padding, int64_t dilation, nsr_stream_t stream) {
+static nsr_status conv_packed_impl(const float* x, const void* w_packed, const void* bias, const float* residual,
+                                   float* out, int64_t B, int64_t C_in, int64_t C_out, int64_t T_in, int64_t K,
+                                   int64_t padding, int64_t dilation, char* records, nsr_stream_t stream) {
   int64_t T_out = 0;
   nsr_status st = conv_validate(x, w_packed, 16, out, B, C_in, C_out, T_in, K, padding, dilation, &T_out,
                                 "conv1d_f16w_packed");
@@ -1499,7 +1556,14 @@ nsr_status nsr_conv1d_f16w_packed(const float* x, const void* w_packed, const vo
   a.K = (int32_t)K;
   a.padding = (int32_t)padding;
   a.dilation = (int32_t)dilation;
-  return conv_launch(false, a, stream, "conv1d_f16w_packed");
+  return conv_records(false, a, records, stream, "conv1d_f16w_packed");
+}
+
+nsr_status nsr_conv1d_f16w_packed(const float* x, const void* w_packed, const void* bias, const float* residual,
+                                  float* out, int64_t B, int64_t C_in, int64_t C_out, int64_t T_in, int64_t K,
+                                  int64_t padding, int64_t dilation, nsr_stream_t stream) {
+  return conv_packed_impl(x, w_packed, bias, residual, out, B, C_in, C_out, T_in, K, padding, dilation, nullptr,
+                          stream);
 }
 
 nsr_status nsr_conv1d_f32io(const float* x, const void* w, const void* bias, float* out, int64_t B, int64_t C_in,
@@ -1511,15 +1575,16 @@ nsr_status nsr_conv1d_f32io(const float* x, const void* w, const void* bias, flo
   nsr_status st = conv_validate(x, w, 2, out, B, C_in, C_out, T_in, K, padding, dilation, &T_out, "conv1d_f32io");
   if (st != NSR_OK) return st;
   if (bias && !aligned(bias, 2)) return fail(NSR_ERR_BAD_ARG, "conv1d_f32io: misaligned bias");
-  char* part[3];
-  st = conv_ws_parts(workspace, workspace_bytes, B, C_in, C_out, T_out, K, NSR_WS_PACKED_WEIGHTS, part,
-                     "conv1d_f32io");
+  char* part[4];
+  st = conv_ws_parts(workspace, workspace_bytes, B, C_in, C_out, T_out, K, T_in + 2 * padding, NSR_WS_PACKED_WEIGHTS,
+                     part, "conv1d_f32io");
   if (st != NSR_OK) return st;
   if (B == 0 || T_out <= 0) return NSR_OK;
   // pack the weights into the caller's workspace, then convolve
   st = nsr_conv1d_pack_f16(w, C_out, C_in, K, part[0], stream);
   if (st != NSR_OK) return st;
-  return nsr_conv1d_f16w_packed(x, part[0], bias, nullptr, out, B, C_in, C_out, T_in, K, padding, dilation, stream);
+  return conv_packed_impl(x, part[0], bias, nullptr, out, B, C_in, C_out, T_in, K, padding, dilation, part[3],
+                          stream);
 }
 
 static nsr_status adain_conv_impl(const float* x, const float* x_stats, const void* gamma, const void* beta,
@@ -1540,8 +1605,8 @@ static nsr_status adain_conv_impl(const float* x, const float* x_stats, const vo
   if ((bias && !aligned(bias, 2)) || (residual && !aligned(residual, 4)))
     return fail(NSR_ERR_BAD_ARG, "%s: misaligned bias or residual", what);
   const unsigned parts = (x_stats ? 0u : NSR_WS_IN_STATS) | (out_stats ? NSR_WS_OUT_STATS : 0u);
-  char* part[3];
-  st = conv_ws_parts(workspace, workspace_bytes, B, C_in, C_out, T_out, K, parts, part, what);
+  char* part[4];
+  st = conv_ws_parts(workspace, workspace_bytes, B, C_in, C_out, T_out, K, T + 2 * padding, parts, part, what);
   if (st != NSR_OK) return st;
   if (B == 0 || T_out <= 0) return NSR_OK;
   if (T == 0) return fail(NSR_ERR_BAD_ARG, "%s: T == 0 (an empty row has no statistics)", what);
@@ -1585,8 +1650,8 @@ static nsr_status adain_conv_impl(const float* x, const float* x_stats, const vo
     a.padding = (int32_t)padding;
     a.dilation = (int32_t)dilation;
     a.pdt = param_dtype == NSR_F32 ? 0 : 1;
-    st = out_stats ? conv_launch_stats(true, a, eps, out_stats, (float*)part[2], stream, what)
-                   : conv_launch(true, a, stream, what);
+    st = out_stats ? conv_launch_stats(true, a, eps, out_stats, (float*)part[2], part[3], stream, what)
+                   : conv_records(true, a, part[3], stream, what);
   }
   return st;
 }
@@ -1626,8 +1691,9 @@ nsr_status nsr_conv1d_f16w_packed_stats(const float* x, const void* w_packed, co
   if ((bias && !aligned(bias, 2)) || (residual && !aligned(residual, 4)))
     return fail(NSR_ERR_BAD_ARG, "%s: misaligned bias or residual", what);
   if (!(eps >= 0.0f)) return fail(NSR_ERR_BAD_ARG, "%s: eps must be >= 0", what);
-  char* part[3];
-  st = conv_ws_parts(workspace, workspace_bytes, B, C_in, C_out, T_out, K, NSR_WS_OUT_STATS, part, what);
+  char* part[4];
+  st = conv_ws_parts(workspace, workspace_bytes, B, C_in, C_out, T_out, K, T_in + 2 * padding, NSR_WS_OUT_STATS, part,
+                     what);
   if (st != NSR_OK) return st;
   if (B == 0 || T_out <= 0) return NSR_OK;
   if (T_in == 0) return fail(NSR_ERR_BAD_ARG, "%s: T_in == 0", what);
@@ -1646,22 +1712,22 @@ nsr_status nsr_conv1d_f16w_packed_stats(const float* x, const void* w_packed, co
   a.K = (int32_t)K;
   a.padding = (int32_t)padding;
   a.dilation = (int32_t)dilation;
-  return conv_launch_stats(false, a, eps, out_stats, (float*)part[2], stream, what);
+  return conv_launch_stats(false, a, eps, out_stats, (float*)part[2], part[3], stream, what);
 }
 
 nsr_status nsr_conv1d_workspace_bytes(int64_t B, int64_t C_in, int64_t C_out, int64_t T_in, int64_t K,
                                       int64_t padding, int64_t dilation, unsigned parts, int64_t* bytes) {
   if (!bytes) return fail(NSR_ERR_BAD_ARG, "conv1d_workspace_bytes: null result pointer");
   *bytes = 0;
-  if (parts & ~(unsigned)(NSR_WS_PACKED_WEIGHTS | NSR_WS_IN_STATS | NSR_WS_OUT_STATS))
+  if (parts & ~(unsigned)(NSR_WS_PACKED_WEIGHTS | NSR_WS_IN_STATS | NSR_WS_OUT_STATS | NSR_WS_RECORDS))
     return fail(NSR_ERR_BAD_ARG, "conv1d_workspace_bytes: unknown parts 0x%x", parts);
   if (B < 0 || C_in <= 0 || C_out <= 0 || T_in < 0 || K <= 0 || padding < 0 || dilation <= 0 || B > 65535 ||
       C_in > (1 << 20) || C_out > (1 << 24) || K > 4096 || T_in >= (1LL << 23) || padding > (1 << 24) ||
       dilation > (1 << 20))
     return fail(NSR_ERR_BAD_ARG, "conv1d_workspace_bytes: bad shape");
   const int64_t T_out = std::max<int64_t>(0, T_in + 2 * padding - dilation * (K - 1));
-  int64_t off[3];
-  conv_ws_layout(B, C_in, C_out, T_out, K, parts, off, bytes);
+  int64_t off[4];
+  conv_ws_layout(B, C_in, C_out, T_out, K, T_in + 2 * padding, parts, off, bytes);
   return NSR_OK;
 }
 

@@ -157,7 +157,7 @@ def test_version_and_header_is_plain_c():
     lambda L: L.nsr_conv1d_f32io(16, 16, NULL, 16, 1, 16, 16, 64, 3, 1, 1, 1, 272, 1 << 20, NULL),
     lambda L: L.nsr_adain_snake_conv1d_f32(16, 16, 16, 16, 0, 0, 0, 16, NULL, NULL, 16, 1, 16, 16, 64, 3, 1, 1,
                                            C.c_float(1e-5), NULL, 0, NULL),
-    lambda L: L.nsr_conv1d_workspace_bytes(1, 16, 16, 64, 3, 1, 1, 8, C.byref(C.c_int64())),
+    lambda L: L.nsr_conv1d_workspace_bytes(1, 16, 16, 64, 3, 1, 1, 16, C.byref(C.c_int64())),
     # snake: bf16 x, seq_len not dividing n_elements, zero channels, misaligned f32 x
     lambda L: L.nsr_snake(16, 2, 16, 0, 16, 8, 1, 8, NULL),
     lambda L: L.nsr_snake(16, 0, 16, 0, 16, 10, 1, 4, NULL),
