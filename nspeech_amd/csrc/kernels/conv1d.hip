@@ -1459,6 +1459,7 @@ NSR_CONV_PR1(nsrk_conv1d_pr_res_f16x2, true)
 template <bool FUSED>
 NSR_DEV void conv_presplit(const nsr_conv_args& a, uint8_t* xs, uint8_t* wf) {
   __shared__ __attribute__((aligned(16))) uint8_t rec[64 * CV_RS];
+  __shared__ __attribute__((aligned(16))) float coef[FUSED ? CV_CI * 12 : 4];
   const int tid = threadIdx.x, rg = tid >> 4, cq = tid & 15;
   const int Tp = a.T_in + 2 * a.padding;
   const int nblk = (Tp + 63) / 64, n_ch = (a.C_in + CV_CI - 1) / CV_CI;
@@ -1526,13 +1527,38 @@ NSR_DEV void conv_presplit(const nsr_conv_args& a, uint8_t* xs, uint8_t* wf) {
       }
     }
   }
+  if constexpr (FUSED) {
+    /* the AdaIN + Snake coefficients of the 128 channels, once per workgroup (lane c: channel 128 ch + c),
+     * then each lane reads its 8 channels' from LDS */
+    if (tid < CV_CI) {
+      const cv_coef cf = cv_row_coef(a, b, min(ch * CV_CI + tid, a.C_in - 1));
+      *(nsr_float4*)(coef + 12 * tid) = nsr_float4{cf.mean, cf.A, cf.bet, cf.sc.a_pi};
+      *(nsr_float4*)(coef + 12 * tid + 4) = nsr_float4{cf.sc.c[0], cf.sc.c[1], cf.sc.c[2], cf.sc.c[3]};
+      *(nsr_float4*)(coef + 12 * tid + 8) = nsr_float4{cf.sc.c[4], cf.sc.c[5], cf.sc.c[6], 0.f};
+    }
+    __syncthreads();
+  }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const bool crow = c0 + i < a.C_in;
     if constexpr (FUSED) {
-      const cv_coef cf = cv_row_coef(a, b, min(c0 + i, a.C_in - 1));
+      const float* cp = coef + 12 * (8 * rg + i);
+      const nsr_float4 q0 = *(const nsr_float4*)cp, q1 = *(const nsr_float4*)(cp + 4), q2 = *(const nsr_float4*)(cp + 8);
+      cv_coef cf;
+      cf.mean = q0[0];
+      cf.A = q0[1];
+      cf.bet = q0[2];
+      cf.sc.a_pi = q0[3];
+      cf.sc.c[0] = q1[0];
+      cf.sc.c[1] = q1[1];
+      cf.sc.c[2] = q1[2];
+      cf.sc.c[3] = q1[3];
+      cf.sc.c[4] = q2[0];
+      cf.sc.c[5] = q2[1];
+      cf.sc.c[6] = q2[2];
 #pragma unroll
       for (int e = 0; e < 4; ++e) y[i][e] = snake_eval(__builtin_fmaf(y[i][e] - cf.mean, cf.A, cf.bet), cf.sc);
+      __builtin_amdgcn_sched_barrier(0); /* one channel's coefficients live at a time */
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
