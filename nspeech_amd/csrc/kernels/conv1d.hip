@@ -1159,7 +1159,6 @@ NSR_DEV void conv_pr_body(const nsr_conv_args& a, const uint8_t* xs, const uint8
         }
       }
       const bool staged = n >= 1 && ip.ch == n_ch - 1;
-      if (staged) read_staged();
       /* the rounds of each phase as bit masks, computed once per transition (scalar work here is shared
        * with the consumers' waves: one test per round and phase below) */
       uint32_t pm[3] = {0u, 0u, 0u};
@@ -1180,6 +1179,9 @@ NSR_DEV void conv_pr_body(const nsr_conv_args& a, const uint8_t* xs, const uint8
         for (int r = 0; r < CV_NRW; ++r)
           if ((pm[ph] >> r) & 1u) *waddr[r] = yr[r];
       };
+      /* the staged rows are read once the records have arrived (not at the item's start, where their
+       * LDS reads would meet the consumers' first tap), then this wave's records overwrite their slots */
+      if (staged) read_staged();
       write_phase(0);
       if (staged) store_staged(ip, jw_p, gap);
       const bool has_next2 = n + 2 < items;
@@ -1576,18 +1578,21 @@ NSR_DEV void conv_presplit(const nsr_conv_args& a, uint8_t* xs, uint8_t* wf) {
       hi[h] = (uint32_t)h_bits(h0) | ((uint32_t)h_bits(h1) << 16);
       lo[h] = (uint32_t)h_bits(l0) | ((uint32_t)h_bits(l1) << 16);
     }
-    const int r = 4 * cq + e;
-    *(nsr_uint4*)(rec + r * CV_RS + 16 * rg) = nsr_uint4{hi[0], hi[1], hi[2], hi[3]};
-    *(nsr_uint4*)(rec + r * CV_RS + 256 + 16 * rg) = nsr_uint4{lo[0], lo[1], lo[2], lo[3]};
+    /* record 4 cq + e sits in LDS slot 16 e + cq: the 16 lanes of one chunk (cq = 0 .. 15) write 16
+     * consecutive slots, which the 528-byte stride puts in 16 different bank groups */
+    const int sl = 16 * e + cq;
+    *(nsr_uint4*)(rec + sl * CV_RS + 16 * rg) = nsr_uint4{hi[0], hi[1], hi[2], hi[3]};
+    *(nsr_uint4*)(rec + sl * CV_RS + 256 + 16 * rg) = nsr_uint4{lo[0], lo[1], lo[2], lo[3]};
   }
   __syncthreads();
   const int nrec = min(64, Tp - blk * 64);
   const nsr_rsrc orr = make_rsrc_uniform(xs + ((int64_t)bc * Tp + blk * 64) * CV_RB, (uint32_t)(nrec * CV_RB));
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int id = tid + 256 * i; /* 16-byte chunk: record id >> 5, chunk id & 31 */
-    __builtin_amdgcn_raw_buffer_store_b128(*(const nsr_uint4*)(rec + (id >> 5) * CV_RS + 16 * (id & 31)), orr,
-                                           (uint32_t)(16 * id), 0, NSR_AUX_NT);
+    const int id = tid + 256 * i; /* 16-byte chunk: slot id >> 5, chunk id & 31 */
+    const int sl = id >> 5, r = 4 * (sl & 15) + (sl >> 4); /* the slot's record */
+    __builtin_amdgcn_raw_buffer_store_b128(*(const nsr_uint4*)(rec + sl * CV_RS + 16 * (id & 31)), orr,
+                                           (uint32_t)(r * CV_RB + 16 * (id & 31)), 0, NSR_AUX_NT);
   }
 }
 
