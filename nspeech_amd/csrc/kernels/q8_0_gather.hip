@@ -23,11 +23,23 @@
 
 template <int ACT, bool IDS_I64>
 NSR_DEV void q8_0_gather_body(const nsr_q8_args& a) {
-  const uint32_t f = blockIdx.x * 256u + threadIdx.x; /* float4 index */
-  if (f >= (uint32_t)a.total4) return;
   const uint32_t d4 = (uint32_t)a.d4;
-  const uint32_t row = f / d4;
-  const uint32_t c4 = f - row * d4;
+  uint32_t f, row, c4; /* float4 index, its id's position, its float4 within the row */
+  if (a.ipw > 0) {
+    /* whole ids per workgroup: no table row is split between two workgroups (which may sit on two
+     * XCDs and each fetch the row's shared lines) */
+    const uint32_t rl = threadIdx.x / d4;
+    if (rl >= (uint32_t)a.ipw) return;
+    row = blockIdx.x * (uint32_t)a.ipw + rl;
+    if (row >= (uint32_t)a.n_ids) return;
+    c4 = threadIdx.x - rl * d4;
+    f = row * d4 + c4;
+  } else {
+    f = blockIdx.x * 256u + threadIdx.x;
+    if (f >= (uint32_t)a.total4) return;
+    row = f / d4;
+    c4 = f - row * d4;
+  }
 
   int64_t id;
   if constexpr (IDS_I64) {

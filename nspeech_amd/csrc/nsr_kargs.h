@@ -24,6 +24,8 @@ typedef struct nsr_q8_args {
   int32_t row_bytes;       /* 34 * d / 32 */
   int32_t act;             /* nsr_act */
   int32_t ids_i64;         /* 1: ids are int64 */
+  int32_t ipw;             /* ids per 256-lane workgroup (whole rows per workgroup); 0: one flat grid */
+  int32_t pad_;
 } nsr_q8_args;
 
 typedef struct nsr_ln_args {
