@@ -58,8 +58,8 @@ CONFIG_WORKLOADS = ["c4b", "c4a", "c0", "c1", "c1t", "c2", "c3", "c2u", "c2h"]
 NEXT_WORKLOADS = ["dec", "dec2", "attn", "attnx", "q8fc1", "q8fc2", "q8fc1r", "q8fc2r", "q8conv", "kconv3", "kconv7",
                   "kconv11", "kconv7f", "kconv11f", "kconv3u", "kchain3", "kchain11", "mrf", "istft"]
 # same-size copies: algorithmic bytes of the config each one calibrates
-COPY_SIZES = {"c1t": 8519680, "c3": 8642560, "c2": 19666944, "c4a": 196616192, "c4b": 943727104}
-COPY_FOR = {"c1": "c1t", "c1t": "c1t", "c3": "c3", "c2": "c2", "c2u": "c2", "c4a": "c4a", "c4b": "c4b"}
+COPY_SIZES = {"c1t": 8519680, "c3": 8642560, "c2h": 9833472, "c2": 19666944, "c4a": 196616192, "c4b": 943727104}
+COPY_FOR = {"c1": "c1t", "c1t": "c1t", "c3": "c3", "c2": "c2", "c2u": "c2", "c2h": "c2h", "c4a": "c4a", "c4b": "c4b"}
 FLOOR_WORKLOADS = ["empty"] + [f"copy_{f}_{c}" for c in COPY_SIZES for f in ("f", "p4", "p8")] + ["copy_rows_c4b"]
 DEFAULT_WORKLOADS = CONFIG_WORKLOADS + FLOOR_WORKLOADS + NEXT_WORKLOADS
 MALL_DEFEAT_BYTES = 512 << 20
