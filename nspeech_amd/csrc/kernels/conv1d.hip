@@ -47,7 +47,30 @@ NSR_DEV float conv_param(const void* p, int pdt, int64_t i) {
   return pdt == 0 ? ((const float*)p)[i] : f16_bits_to_f32(((const uint16_t*)p)[i]);
 }
 
-NSR_DEV uint16_t h_bits(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
+typedef _Float16 cv_h2 __attribute__((ext_vector_type(2)));
+
+/* Two f32 values split into packed f16 halves: hi = f16(y), lo = f16(y - hi), both rounded to nearest
+ * even; y0 in the low 16 bits. Built as two-element vectors so each pair converts with one
+ * v_cvt_pk_f16_f32 instead of two conversions and a shift-or. */
+NSR_DEV void split_pair(float y0, float y1, uint32_t& hi, uint32_t& lo) {
+  const cv_h2 h = {(_Float16)y0, (_Float16)y1};
+  const cv_h2 l = {(_Float16)(y0 - (float)h[0]), (_Float16)(y1 - (float)h[1])};
+  hi = __builtin_bit_cast(uint32_t, h);
+  lo = __builtin_bit_cast(uint32_t, l);
+}
+
+/* The same split with hi widened back from the packed register (the empty asm hides where it came
+ * from, so the compiler does not convert y to f16 a second time): two VALU operations fewer per pair,
+ * one more live register; for the records pass, whose registers are not its limit. */
+NSR_DEV void split_pair_packed(float y0, float y1, uint32_t& hi, uint32_t& lo) {
+  const cv_h2 h = {(_Float16)y0, (_Float16)y1};
+  uint32_t hb = __builtin_bit_cast(uint32_t, h);
+  asm("" : "+v"(hb));
+  const cv_h2 hh = __builtin_bit_cast(cv_h2, hb);
+  const cv_h2 l = {(_Float16)(y0 - (float)hh[0]), (_Float16)(y1 - (float)hh[1])};
+  hi = hb;
+  lo = __builtin_bit_cast(uint32_t, l);
+}
 
 /* Value of lane (this lane ^ 1) / (this lane ^ 2) within its quad (DPP quad_perm). */
 NSR_DEV float quad_xor1(float v) {
@@ -195,19 +218,7 @@ NSR_DEV void conv_body(const nsr_conv_args& a) {
           const bool in = ti >= 0 && ti < a.T_in;
           uint32_t hw[2], lw[2];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float y = in ? xv[i][r] : 0.f;
-            const _Float16 hi = (_Float16)y;
-            const _Float16 lo = (_Float16)(y - (float)hi);
-            const uint32_t hb = h_bits(hi), lb = h_bits(lo);
-            if (r & 1) {
-              hw[r >> 1] |= hb << 16;
-              lw[r >> 1] |= lb << 16;
-            } else {
-              hw[r >> 1] = hb;
-              lw[r >> 1] = lb;
-            }
-          }
+          for (int r = 0; r < 2; ++r) split_pair(in ? xv[i][2 * r] : 0.f, in ? xv[i][2 * r + 1] : 0.f, hw[r], lw[r]);
           *(nsr_uint2*)(yhi + j * CV_S + 4 * lq) = nsr_uint2{hw[0], hw[1]};
           *(nsr_uint2*)(ylo + j * CV_S + 4 * lq) = nsr_uint2{lw[0], lw[1]};
         }
@@ -462,10 +473,7 @@ NSR_DEV void conv_rw_body(const nsr_conv_args& a) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             const float y0 = in ? xv[u][2 * h][e] : 0.f, y1 = in ? xv[u][2 * h + 1][e] : 0.f;
-            const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1;
-            const _Float16 l0 = (_Float16)(y0 - (float)h0), l1 = (_Float16)(y1 - (float)h1);
-            pk[u][e][h] = (uint32_t)h_bits(h0) | ((uint32_t)h_bits(h1) << 16);
-            pk[u][e][2 + h] = (uint32_t)h_bits(l0) | ((uint32_t)h_bits(l1) << 16);
+            split_pair(y0, y1, pk[u][e][h], pk[u][e][2 + h]);
           }
         }
     };
@@ -745,10 +753,7 @@ NSR_DEV void conv_pc_body(const nsr_conv_args& a) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             const float y0 = in ? xv[u][2 * h][e] : 0.f, y1 = in ? xv[u][2 * h + 1][e] : 0.f;
-            const _Float16 h0 = (_Float16)y0, h1 = (_Float16)y1;
-            const _Float16 l0 = (_Float16)(y0 - (float)h0), l1 = (_Float16)(y1 - (float)h1);
-            pk[u][e][h] = (uint32_t)h_bits(h0) | ((uint32_t)h_bits(h1) << 16);
-            pk[u][e][2 + h] = (uint32_t)h_bits(l0) | ((uint32_t)h_bits(l1) << 16);
+            split_pair(y0, y1, pk[u][e][h], pk[u][e][2 + h]);
           }
         }
     };
@@ -1448,11 +1453,16 @@ NSR_CONV_PR1(nsrk_conv1d_pr_res_f16x2, true)
  * y = x (or snake(AdaIN(x)) in the fused form, with the row statistics in
  * a.stats) of channels 128 ch .. 128 ch + 127 split as hi = f16(y),
  * lo = f16(y - hi): 16 chunks of 8 hi halves, then 16 of 8 lo halves; zeros
- * outside [0, T_in) and past C_in. One 256-lane workgroup per 64 records of
- * one (batch, chunk): each lane loads 8 channels x 4 columns (one 16-byte
- * load per channel, 64 consecutive columns per row across 16 lanes),
- * transforms and packs them into its chunks of 4 records in LDS, then the
- * 32 KB block is stored contiguously. Bandwidth-bound: x read once, the
+ * outside [0, T_in) and past C_in. One 256-lane workgroup per 64 input
+ * columns 64 j .. 64 j + 63 of one (batch, chunk), j from -ceil(padding / 64)
+ * so the blocks before column 0 cover the leading padding records; blocks
+ * are aligned to the input rows (not to the padded columns), so a row's 64
+ * columns are two whole 128-byte lines when rows start on 16 bytes. Each
+ * lane loads 8 channels x 4 columns (one 16-byte load per channel, 64
+ * consecutive columns per row across 16 lanes), transforms and packs them
+ * into its chunks of 4 records in LDS, then the block's records (64 j +
+ * padding onwards, those in [0, T_in + 2 padding)) are stored contiguously:
+ * records are 512 bytes, so the stores stay aligned. Bandwidth-bound: x read once, the
  * records written once (4 bytes per element each way). The workgroups after
  * the records' write the fragment weights, 16 bytes per lane. Blocks are
  * mapped XCD-contiguously (XCD x takes the x-th eighth of the logical
@@ -1464,7 +1474,8 @@ NSR_DEV void conv_presplit(const nsr_conv_args& a, uint8_t* xs, uint8_t* wf) {
   __shared__ __attribute__((aligned(16))) float coef[FUSED ? CV_CI * 12 : 4];
   const int tid = threadIdx.x, rg = tid >> 4, cq = tid & 15;
   const int Tp = a.T_in + 2 * a.padding;
-  const int nblk = (Tp + 63) / 64, n_ch = (a.C_in + CV_CI - 1) / CV_CI;
+  const int jlo = (a.padding + 63) / 64; /* blocks before input column 0 */
+  const int nblk = (a.T_in + a.padding + 63) / 64 + jlo, n_ch = (a.C_in + CV_CI - 1) / CV_CI;
   const int G = (int)gridDim.x;
   const int lb = (G & 7) == 0 ? (int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3) : (int)blockIdx.x;
   const int nrb = a.B * n_ch * nblk;
@@ -1497,12 +1508,13 @@ NSR_DEV void conv_presplit(const nsr_conv_args& a, uint8_t* xs, uint8_t* wf) {
     *(nsr_uint4*)(wf + f * 16) = nsr_uint4{hv[0], hv[1], hv[2], hv[3]};
     return;
   }
-  const int blk = lb % nblk;
   const int bc = lb / nblk; /* b * n_ch + ch */
+  const int j64 = (lb - bc * nblk - jlo) * 64; /* the block's first input column */
   const int b = bc / n_ch, ch = bc - b * n_ch;
-  const int tp0 = blk * 64 + 4 * cq;
   const int c0 = ch * CV_CI + 8 * rg; /* this lane's 8 channels */
-  const int ti0 = tp0 - a.padding;   /* its 4 input columns ti0 .. ti0 + 3 */
+  const int ti0 = j64 + 4 * cq;      /* its 4 input columns ti0 .. ti0 + 3 */
+  /* the whole block inside the row and the channel chunk full: nothing to zero (wave-uniform) */
+  const bool full = j64 >= 0 && j64 + 63 < a.T_in && (ch + 1) * CV_CI <= a.C_in;
   const nsr_rsrc xr = make_rsrc_uniform(a.x + (int64_t)b * a.C_in * a.T_in, (uint32_t)(4 * a.C_in * a.T_in));
   /* Interior lanes: one 16-byte load per channel (4-byte aligned offsets). Lanes whose 4 columns cross
    * either end of the row load each column on its own at a clamped column, so no load leaves the
@@ -1562,22 +1574,19 @@ NSR_DEV void conv_presplit(const nsr_conv_args& a, uint8_t* xs, uint8_t* wf) {
       for (int e = 0; e < 4; ++e) y[i][e] = snake_eval(__builtin_fmaf(y[i][e] - cf.mean, cf.A, cf.bet), cf.sc);
       __builtin_amdgcn_sched_barrier(0); /* one channel's coefficients live at a time */
     }
+    if (!full) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int ti = ti0 + e;
-      y[i][e] = (crow && ti >= 0 && ti < a.T_in) ? y[i][e] : 0.f;
+      for (int e = 0; e < 4; ++e) {
+        const int ti = ti0 + e;
+        y[i][e] = (crow && ti >= 0 && ti < a.T_in) ? y[i][e] : 0.f;
+      }
     }
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     uint32_t hi[4], lo[4];
 #pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      const _Float16 h0 = (_Float16)y[2 * h][e], h1 = (_Float16)y[2 * h + 1][e];
-      const _Float16 l0 = (_Float16)(y[2 * h][e] - (float)h0), l1 = (_Float16)(y[2 * h + 1][e] - (float)h1);
-      hi[h] = (uint32_t)h_bits(h0) | ((uint32_t)h_bits(h1) << 16);
-      lo[h] = (uint32_t)h_bits(l0) | ((uint32_t)h_bits(l1) << 16);
-    }
+    for (int h = 0; h < 4; ++h) split_pair_packed(y[2 * h][e], y[2 * h + 1][e], hi[h], lo[h]);
     /* record 4 cq + e sits in LDS slot 16 e + cq: the 16 lanes of one chunk (cq = 0 .. 15) write 16
      * consecutive slots, which the 528-byte stride puts in 16 different bank groups */
     const int sl = 16 * e + cq;
@@ -1585,14 +1594,16 @@ NSR_DEV void conv_presplit(const nsr_conv_args& a, uint8_t* xs, uint8_t* wf) {
     *(nsr_uint4*)(rec + sl * CV_RS + 256 + 16 * rg) = nsr_uint4{lo[0], lo[1], lo[2], lo[3]};
   }
   __syncthreads();
-  const int nrec = min(64, Tp - blk * 64);
-  const nsr_rsrc orr = make_rsrc_uniform(xs + ((int64_t)bc * Tp + blk * 64) * CV_RB, (uint32_t)(nrec * CV_RB));
+  /* record r of the block is tp = j64 + padding + r; the buffer covers the block's records inside
+   * [0, Tp), so stores of the others (negative or past-the-end offsets) are dropped by its range check */
+  const int tq = j64 + a.padding, tlo = max(tq, 0), thi = min(tq + 64, Tp);
+  const nsr_rsrc orr = make_rsrc_uniform(xs + ((int64_t)bc * Tp + tlo) * CV_RB, (uint32_t)((thi - tlo) * CV_RB));
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int id = tid + 256 * i; /* 16-byte chunk: slot id >> 5, chunk id & 31 */
     const int sl = id >> 5, r = 4 * (sl & 15) + (sl >> 4); /* the slot's record */
     __builtin_amdgcn_raw_buffer_store_b128(*(const nsr_uint4*)(rec + sl * CV_RS + 16 * (id & 31)), orr,
-                                           (uint32_t)(r * CV_RB + 16 * (id & 31)), 0, NSR_AUX_NT);
+                                           (uint32_t)((r + tq - tlo) * CV_RB + 16 * (id & 31)), 0, NSR_AUX_NT);
   }
 }
 

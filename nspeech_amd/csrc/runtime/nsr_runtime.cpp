@@ -1439,7 +1439,8 @@ static nsr_status conv_records(bool fused, nsr_conv_args& a, char* records, nsr_
     return conv_launch(fused, a, stream, what, emitted);
   const int64_t Tp = (int64_t)a.T_in + 2 * a.padding;
   const int64_t n_ch = (a.C_in + 127) / 128, n_co = (a.C_out + 127) / 128;
-  const int64_t rec_blocks = (int64_t)a.B * n_ch * ((Tp + 63) / 64);
+  // records pass blocks: 64 input columns each, from column -64 * ceil(padding / 64) (the leading padding)
+  const int64_t rec_blocks = (int64_t)a.B * n_ch * (((int64_t)a.T_in + a.padding + 63) / 64 + (a.padding + 63) / 64);
   const int64_t w_blocks = n_co * 4 * a.K * n_ch * 2;  // fragment weights: 16 bytes per lane, 8 KB = 2 blocks
   const int64_t blocks = (rec_blocks + w_blocks + 7) / 8 * 8;
   if (blocks > 0x7fffffffLL || Tp * 512 > 0xffffffffLL) return conv_launch(fused, a, stream, what, emitted);
