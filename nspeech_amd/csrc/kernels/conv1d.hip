@@ -1419,15 +1419,6 @@ NSR_DEV void conv_pr_body(const nsr_conv_args& a, const uint8_t* xs, const uint8
             A[m][g] = __builtin_bit_cast(nsr_h8, __builtin_amdgcn_raw_buffer_load_b128(
                                                       wr, (uint32_t)lane * 16u, ab + m * cbstride + g * 1024u, 0));
       }
-      if constexpr (!last_reload) {
-        const uint32_t ab = a_base(nxt, 0);
-#pragma unroll
-        for (int g = 0; g < 8; ++g)
-#pragma unroll
-          for (int m = 0; m < 2; ++m)
-            A[m][g] = __builtin_bit_cast(nsr_h8, __builtin_amdgcn_raw_buffer_load_b128(
-                                                      wr, (uint32_t)lane * 16u, ab + m * cbstride + g * 1024u, 0));
-      }
       __syncthreads(); /* item n + 1's window and item n's output staged */
       it = in;
       advance(in);

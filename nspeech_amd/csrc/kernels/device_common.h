@@ -106,7 +106,9 @@ template <int DT> NSR_DEV nsr_uint4 pack16(const float* v) {
       if constexpr (DT == DT_BF16) {
         r[i] = f32x2_to_bf16x2_bits(v[2 * i], v[2 * i + 1]);
       } else {
-        r[i] = f32_to_f16_bits(v[2 * i]) | (f32_to_f16_bits(v[2 * i + 1]) << 16);
+        typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+        const h2_t h = {(_Float16)v[2 * i], (_Float16)v[2 * i + 1]}; /* one v_cvt_pk_f16_f32, nearest even */
+        r[i] = __builtin_bit_cast(uint32_t, h);
       }
     }
   }
@@ -244,11 +246,36 @@ NSR_DEV float act_gelu_erf(float v) {
   return v * phi;
 }
 
+/* act_gelu_erf for finite v: v Phi(v) = v (1 - h) for v >= 0 and v h below, i.e. max(v, 0) - |v| h
+ * (two operations instead of a compare, a select and a multiply; at v = +inf it would give NaN). */
+NSR_DEV float act_gelu_erf_finite(float v) {
+  const float av = __builtin_fabsf(v);
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(av, NSR_AS_P_SQRT2, 1.0f));
+  float q = __builtin_fmaf(NSR_AS_HA5, t, NSR_AS_HA4);
+  q = __builtin_fmaf(q, t, NSR_AS_HA3);
+  q = __builtin_fmaf(q, t, NSR_AS_HA2);
+  q = __builtin_fmaf(q, t, NSR_AS_HA1);
+  const float e = __builtin_amdgcn_exp2f((av * -0.72134752044448170f) * av);
+  const float h = (q * t) * e;
+  return __builtin_fmaf(-av, h, __builtin_fmaxf(v, 0.0f));
+}
+
 template <int ACT> NSR_DEV float apply_act(float v) {
   if constexpr (ACT == ACT_SILU) {
     return act_silu(v);
   } else if constexpr (ACT == ACT_GELU) {
     return act_gelu_erf(v);
+  } else {
+    return v;
+  }
+}
+
+/* apply_act for finite v (GELU in its finite-input form). */
+template <int ACT> NSR_DEV float apply_act_finite(float v) {
+  if constexpr (ACT == ACT_SILU) {
+    return act_silu(v);
+  } else if constexpr (ACT == ACT_GELU) {
+    return act_gelu_erf_finite(v);
   } else {
     return v;
   }

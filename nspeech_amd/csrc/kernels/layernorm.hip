@@ -122,6 +122,7 @@ NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
   /* gamma/beta do not depend on the row: when they fit in 64 more VGPRs
    * they are loaded once per wave, before the first row's loads */
   constexpr bool PREFETCH = NC * VEC <= 32;
+  const float goff = a.unit_offset ? 1.0f : 0.0f; /* gamma + 1 (unit offset), added once per loaded gamma */
   float gpre[PREFETCH ? NC : 1][VEC], bpre[PREFETCH ? NC : 1][VEC];
   if constexpr (PREFETCH) {
 #pragma unroll
@@ -130,10 +131,11 @@ NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
       if (j < nchunk) {
         load_param_vec<VEC>(a.gamma, pdt, j * VEC, gpre[k], 1.0f);
         load_param_vec<VEC>(a.beta, pdt, j * VEC, bpre[k], 0.0f);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) gpre[k][e] += goff;
       }
     }
   }
-  const float goff = a.unit_offset ? 1.0f : 0.0f;
 
   /* raw chunks of the row being worked on; refilled with the next row's
    * chunks while this one is reduced, when they fit in 32 VGPRs */
@@ -167,9 +169,19 @@ NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
         if constexpr (FUSED) {
           float r[VEC];
           unpack_raw<R, VEC>(rr[k], r);
+          if constexpr (H != DT_F32 && chunk_words<H, VEC>::value == 1) {
+            /* h = round_H(x + res) packed two at a time (one conversion per pair), stored as packed and
+             * widened back from the packed words: the same values as rounding each element */
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) v[k][e] = round_to<H>(v[k][e] + r[e]);
-          if (a.h) store_vec<H, VEC>(a.h, xrow + (int64_t)j * VEC, v[k]);
+            for (int e = 0; e < VEC; ++e) v[k][e] += r[e];
+            const nsr_uint4 hw = pack16<H>(v[k]);
+            unpack16<H>(hw, v[k]);
+            if (a.h) st16((char*)a.h + (xrow + (int64_t)j * VEC) * dt_size<H>::value, hw);
+          } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) v[k][e] = round_to<H>(v[k][e] + r[e]);
+            if (a.h) store_vec<H, VEC>(a.h, xrow + (int64_t)j * VEC, v[k]);
+          }
         }
 #pragma unroll
         for (int e = 0; e < VEC; ++e) sum += v[k][e];
@@ -217,10 +229,13 @@ NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
         } else {
           load_param_vec<VEC>(a.gamma, pdt, col0, g, 1.0f);
           load_param_vec<VEC>(a.beta, pdt, col0, b, 0.0f);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) g[e] += goff;
         }
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
-          o[e] = apply_act<ACT>(__builtin_fmaf(__builtin_fmaf(v[k][e], rstd, crs), g[e] + goff, b[e]));
+          /* a LayerNorm output is finite (finite parameters), so the activation's finite-input form applies */
+          o[e] = apply_act_finite<ACT>(__builtin_fmaf(__builtin_fmaf(v[k][e], rstd, crs), g[e], b[e]));
         }
         store_vec<Y, VEC>(a.y, yrow + col0, o);
       }
