@@ -193,7 +193,11 @@ NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
     const float mean = wave_sum(sum) * a.inv_n;
 
     /* centred pass; sum(d) corrects the f32 mean (corrected two-pass), which
-     * keeps rows with |mean| >> std accurate */
+     * keeps rows with |mean| >> std accurate. The correction changes the
+     * variance by (mean rounding error)^2 / var, below f32 resolution unless
+     * |mean| / std > 1e4: values held in f16 / bf16 (h, or x for a plain
+     * LayerNorm) cannot have that spread, so those rows skip it. */
+    constexpr bool CORR = H == DT_F32;
     float sq = 0.f, sd = 0.f;
 #pragma unroll
     for (int k = 0; k < NC; ++k) {
@@ -203,12 +207,12 @@ NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
         for (int e = 0; e < VEC; ++e) {
           v[k][e] -= mean;
           sq = __builtin_fmaf(v[k][e], v[k][e], sq);
-          sd += v[k][e];
+          if constexpr (CORR) sd += v[k][e];
         }
       }
     }
     sq = wave_sum(sq);
-    sd = wave_sum(sd);
+    if constexpr (CORR) sd = wave_sum(sd);
     const float c = sd * a.inv_n;
     const float var = fmaxf(__builtin_fmaf(-c, sd, sq) * a.inv_n, 0.0f);
     const float rstd = 1.0f / sqrtf(var + a.eps);

@@ -25,7 +25,22 @@ template <int ACT, bool IDS_I64>
 NSR_DEV void q8_0_gather_body(const nsr_q8_args& a) {
   const uint32_t d4 = (uint32_t)a.d4;
   uint32_t f, row, c4; /* float4 index, its id's position, its float4 within the row */
-  if (a.ipw > 0) {
+  int64_t id;
+  if (a.gw > 0) {
+    /* whole waves per id: the id is wave-uniform, read once per wave through the scalar cache (a
+     * constant-address-space load at a uniform address) instead of by every lane */
+    const uint32_t gw = (uint32_t)a.gw, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    row = blockIdx.x * (uint32_t)a.ipw + wave / gw;
+    if (row >= (uint32_t)a.n_ids) return;
+    c4 = (wave % gw) * 64u + (threadIdx.x & 63u);
+    if (c4 >= d4) return;
+    f = row * d4 + c4;
+    if constexpr (IDS_I64) {
+      id = ((const __attribute__((address_space(4))) int64_t*)a.ids)[row];
+    } else {
+      id = (int64_t)((const __attribute__((address_space(4))) uint32_t*)a.ids)[row];
+    }
+  } else if (a.ipw > 0) {
     /* whole ids per workgroup: no table row is split between two workgroups (which may sit on two
      * XCDs and each fetch the row's shared lines) */
     const uint32_t rl = threadIdx.x / d4;
@@ -40,12 +55,12 @@ NSR_DEV void q8_0_gather_body(const nsr_q8_args& a) {
     row = f / d4;
     c4 = f - row * d4;
   }
-
-  int64_t id;
-  if constexpr (IDS_I64) {
-    id = ((const int64_t*)a.ids)[row];
-  } else {
-    id = (int64_t)((const uint32_t*)a.ids)[row];
+  if (a.gw == 0) {
+    if constexpr (IDS_I64) {
+      id = ((const int64_t*)a.ids)[row];
+    } else {
+      id = (int64_t)((const uint32_t*)a.ids)[row];
+    }
   }
 
   nsr_float4 o;

@@ -24,8 +24,8 @@ typedef struct nsr_q8_args {
   int32_t row_bytes;       /* 34 * d / 32 */
   int32_t act;             /* nsr_act */
   int32_t ids_i64;         /* 1: ids are int64 */
-  int32_t ipw;             /* ids per 256-lane workgroup (whole rows per workgroup); 0: one flat grid */
-  int32_t pad_;
+  int32_t ipw;             /* ids per workgroup (whole rows per workgroup); 0: one flat grid */
+  int32_t gw;              /* > 0: each id takes gw whole waves (wave-uniform id); 0: ids packed densely */
 } nsr_q8_args;
 
 typedef struct nsr_ln_args {

@@ -901,12 +901,21 @@ nsr_status nsr_q8_0_embed_gather(const void* blocks, int64_t vocab, int64_t d, c
   static const KId kGather[2][3] = {
       {K_nsrk_q8_0_gather_none_u32, K_nsrk_q8_0_gather_silu_u32, K_nsrk_q8_0_gather_gelu_u32},
       {K_nsrk_q8_0_gather_none_i64, K_nsrk_q8_0_gather_silu_i64, K_nsrk_q8_0_gather_gelu_i64}};
-  // whole ids per workgroup when a row fits one (d <= 1024), else one lane per float4 over a flat grid
-  a.ipw = a.d4 <= 256 ? 256 / a.d4 : 0;
+  // Rows of 64 .. 256 float4 (d 256 .. 1024): each id on whole waves (gw of them), ids per workgroup so
+  // it has at most 4 waves. Shorter rows: ids packed densely, whole ids per 256-lane workgroup. Longer:
+  // one lane per float4 over a flat grid.
+  unsigned block = 256;
+  if (a.d4 >= 64 && a.d4 <= 256) {
+    a.gw = (a.d4 + 63) / 64;
+    a.ipw = 4 / a.gw;
+    block = 64u * (unsigned)(a.gw * a.ipw);
+  } else {
+    a.ipw = a.d4 < 64 ? 256 / a.d4 : 0;
+  }
   const int64_t groups = a.ipw ? (n_ids + a.ipw - 1) / a.ipw : cdiv_u(total4, 256);
   if (groups > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "q8_0_embed_gather: too many ids");
   void* params[] = {&a};
-  return launch(kGather[id_dtype == NSR_IDX_I64][act], (unsigned)groups, 1, 256, 0, stream, params);
+  return launch(kGather[id_dtype == NSR_IDX_I64][act], (unsigned)groups, 1, block, 0, stream, params);
 }
 
 // ---------------------------------------------------------- elementwise --
