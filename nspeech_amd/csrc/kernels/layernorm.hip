@@ -215,7 +215,9 @@ NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
     if constexpr (CORR) sd = wave_sum(sd);
     const float c = sd * a.inv_n;
     const float var = fmaxf(__builtin_fmaf(-c, sd, sq) * a.inv_n, 0.0f);
-    const float rstd = 1.0f / sqrtf(var + a.eps);
+    /* v_rsq_f32 (about 1 ulp) instead of a correctly rounded sqrt and divide, about 30 instructions per
+     * row; var + eps > 0 is a normal number unless eps = 0 and the row is constant (then inf either way) */
+    const float rstd = __builtin_amdgcn_rsqf(var + a.eps);
     const float crs = -c * rstd; /* (d - c) * rstd = d * rstd + crs */
 
 #pragma unroll
