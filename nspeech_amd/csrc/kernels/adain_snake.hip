@@ -181,7 +181,7 @@ NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
     block_sum2<NW>(s1, s2, red);
     const float c = s1 * a.inv_t; /* f32 mean correction */
     const float var = fmaxf(__builtin_fmaf(-c, s1, s2) * a.inv_t, 0.0f);
-    const float rstd = 1.0f / sqrtf(var + a.eps);
+    const float rstd = __builtin_amdgcn_rsqf(var + a.eps); /* v_rsq_f32, about 1 ulp */
     float gam, bet, alp;
     adain_params_cvt(pr, pdt, gam, bet, alp);
     const float A = (gam + 1.0f) * rstd;
@@ -335,7 +335,7 @@ NSR_DEV void adain_resident_u(const nsr_adain_args& a, int pdt) {
   block_sum2<NW>(sq, sd, red);
   const float c = sd * a.inv_t;
   const float var = fmaxf(__builtin_fmaf(-c, sd, sq) * a.inv_t, 0.0f);
-  const float rstd = 1.0f / sqrtf(var + a.eps);
+  const float rstd = __builtin_amdgcn_rsqf(var + a.eps); /* v_rsq_f32, about 1 ulp */
   float gam, bet, alp;
   adain_params_cvt(pr, pdt, gam, bet, alp);
   const float A = (gam + 1.0f) * rstd;
@@ -474,7 +474,7 @@ NSR_DEV void adain_row_f16(const nsr_adain_h_args& a, int pdt) {
   block_sum2<NW>(sq, sd, red);
   const float c = sd * a.inv_t;
   const float var = fmaxf(__builtin_fmaf(-c, sd, sq) * a.inv_t, 0.0f);
-  const float rstd = 1.0f / sqrtf(var + a.eps);
+  const float rstd = __builtin_amdgcn_rsqf(var + a.eps); /* v_rsq_f32, about 1 ulp */
   float gam, bet, alp;
   adain_params_cvt(pr, pdt, gam, bet, alp);
   const float A = (gam + 1.0f) * rstd;
@@ -563,7 +563,7 @@ NSR_DEV void adain_row_f16a(const nsr_adain_h_args& a, int pdt) {
   block_sum2<NW>(s1, s2, red);
   const float c = s1 * a.inv_t;
   const float var = fmaxf(__builtin_fmaf(-c, s1, s2) * a.inv_t, 0.0f);
-  const float rstd = 1.0f / sqrtf(var + a.eps);
+  const float rstd = __builtin_amdgcn_rsqf(var + a.eps); /* v_rsq_f32, about 1 ulp */
   float gam, bet, alp;
   adain_params_cvt(pr, pdt, gam, bet, alp);
   const float A = (gam + 1.0f) * rstd;
