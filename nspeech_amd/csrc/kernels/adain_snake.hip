@@ -105,7 +105,7 @@ NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
    * with (NS - MK) * BLOCK <= T / 4 */
   constexpr int MK = NS < 4 ? NS : 4;
   extern __shared__ nsr_float4 lds_x[];
-  __shared__ float red[2 * NW];
+  __shared__ float red[3 * NW]; /* [0, NW): the mean's sums, [NW, 3 NW): the centred sums */
 
   const int tid = threadIdx.x;
   int64_t row = blockIdx.x;
@@ -156,7 +156,7 @@ NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
         s += valid(NV + m) ? sum4(lds_x[m * BLOCK + tid]) : 0.f;
       __builtin_amdgcn_sched_barrier(0);
     });
-    const float mean = block_sum<NW>(s, red) * a.inv_t;
+    const float mean = block_sum<NW, false>(s, red) * a.inv_t;
 
     /* pass 2: centred sums; the VGPR slots keep x - mean (0 outside the row) */
     float s1 = 0.f, s2 = 0.f;
@@ -178,7 +178,7 @@ NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
       }
       __builtin_amdgcn_sched_barrier(0);
     });
-    block_sum2<NW>(s1, s2, red);
+    block_sum2<NW, false>(s1, s2, red + NW);
     const float c = s1 * a.inv_t; /* f32 mean correction */
     const float var = fmaxf(__builtin_fmaf(-c, s1, s2) * a.inv_t, 0.0f);
     const float rstd = __builtin_amdgcn_rsqf(var + a.eps); /* v_rsq_f32, about 1 ulp */
@@ -272,7 +272,7 @@ template <int BLOCK, int NV>
 NSR_DEV void adain_resident_u(const nsr_adain_args& a, int pdt) {
   NSR_NO_CONTRACT
   constexpr int NW = BLOCK / 64;
-  __shared__ float red[2 * NW];
+  __shared__ float red[3 * NW]; /* [0, NW): the mean's sums, [NW, 3 NW): the centred sums */
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const int64_t T = a.T;
@@ -316,7 +316,7 @@ NSR_DEV void adain_resident_u(const nsr_adain_args& a, int pdt) {
   float sum = xe;
 #pragma unroll
   for (int k = 0; k < NV; ++k) sum += sum4(v[k]);
-  const float mean = block_sum<NW>(sum, red) * a.inv_t;
+  const float mean = block_sum<NW, false>(sum, red) * a.inv_t;
 
   float sq = 0.f, sd = 0.f;
 #pragma unroll
@@ -332,7 +332,7 @@ NSR_DEV void adain_resident_u(const nsr_adain_args& a, int pdt) {
     sq = __builtin_fmaf(d, d, sq);
     sd += d;
   }
-  block_sum2<NW>(sq, sd, red);
+  block_sum2<NW, false>(sq, sd, red + NW);
   const float c = sd * a.inv_t;
   const float var = fmaxf(__builtin_fmaf(-c, sd, sq) * a.inv_t, 0.0f);
   const float rstd = __builtin_amdgcn_rsqf(var + a.eps); /* v_rsq_f32, about 1 ulp */
@@ -395,7 +395,7 @@ template <int BLOCK, int NV>
 NSR_DEV void adain_row_f16(const nsr_adain_h_args& a, int pdt) {
   NSR_NO_CONTRACT
   constexpr int NW = BLOCK / 64;
-  __shared__ float red[2 * NW];
+  __shared__ float red[3 * NW]; /* [0, NW): the mean's sums, [NW, 3 NW): the centred sums */
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   if (row >= a.n_rows) return; /* whole workgroup: the grid is one per row */
@@ -444,7 +444,7 @@ NSR_DEV void adain_row_f16(const nsr_adain_h_args& a, int pdt) {
     unpack16<DT_F16>(v[k], f);
     sum += ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
   }
-  const float mean = block_sum<NW>(sum, red) * a.inv_t;
+  const float mean = block_sum<NW, false>(sum, red) * a.inv_t;
 
   /* the chunks stay raw (4 VGPRs each) between passes: an empty asm that
    * "modifies" them stops the compiler keeping their unpacked floats (8) live */
@@ -471,7 +471,7 @@ NSR_DEV void adain_row_f16(const nsr_adain_h_args& a, int pdt) {
     sq = __builtin_fmaf(d, d, sq);
     sd += d;
   }
-  block_sum2<NW>(sq, sd, red);
+  block_sum2<NW, false>(sq, sd, red + NW);
   const float c = sd * a.inv_t;
   const float var = fmaxf(__builtin_fmaf(-c, sd, sq) * a.inv_t, 0.0f);
   const float rstd = __builtin_amdgcn_rsqf(var + a.eps); /* v_rsq_f32, about 1 ulp */
@@ -525,7 +525,7 @@ template <int NV>
 NSR_DEV void adain_row_f16a(const nsr_adain_h_args& a, int pdt) {
   NSR_NO_CONTRACT
   constexpr int BLOCK = 256, NW = BLOCK / 64;
-  __shared__ float red[2 * NW];
+  __shared__ float red[3 * NW]; /* [0, NW): the mean's sums, [NW, 3 NW): the centred sums */
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   if (row >= a.n_rows) return;
@@ -548,7 +548,7 @@ NSR_DEV void adain_row_f16a(const nsr_adain_h_args& a, int pdt) {
     const float t = ((f[k][0] + f[k][1]) + (f[k][2] + f[k][3])) + ((f[k][4] + f[k][5]) + (f[k][6] + f[k][7]));
     s += k < nvalid ? t : 0.f;
   }
-  const float mean = block_sum<NW>(s, red) * a.inv_t;
+  const float mean = block_sum<NW, false>(s, red) * a.inv_t;
   float s1 = 0.f, s2 = 0.f;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
@@ -560,7 +560,7 @@ NSR_DEV void adain_row_f16a(const nsr_adain_h_args& a, int pdt) {
       s2 = __builtin_fmaf(f[k][e], f[k][e], s2);
     }
   }
-  block_sum2<NW>(s1, s2, red);
+  block_sum2<NW, false>(s1, s2, red + NW);
   const float c = s1 * a.inv_t;
   const float var = fmaxf(__builtin_fmaf(-c, s1, s2) * a.inv_t, 0.0f);
   const float rstd = __builtin_amdgcn_rsqf(var + a.eps); /* v_rsq_f32, about 1 ulp */

@@ -166,8 +166,11 @@ NSR_DEV float wave_sum(float v) {
 }
 
 /* Sum over a workgroup of NWAVES waves; uniform result. `red` is LDS scratch
- * of NWAVES floats; the trailing barrier makes it reusable right away. */
-template <int NWAVES>
+ * of NWAVES floats; the trailing barrier makes it reusable right away.
+ * REUSE = false drops that barrier, for callers whose next write to `red`
+ * comes after another block reduction's first barrier (two reductions on
+ * separate buffers, alternating): every wave has read `red` by then. */
+template <int NWAVES, bool REUSE = true>
 NSR_DEV float block_sum(float v, float* red) {
   v = wave_sum(v);
   if constexpr (NWAVES == 1) {
@@ -180,14 +183,14 @@ NSR_DEV float block_sum(float v, float* red) {
     float s = 0.f;
 #pragma unroll
     for (int w = 0; w < NWAVES; ++w) s += red[w];
-    __syncthreads();
+    if constexpr (REUSE) __syncthreads();
     return s;
   }
 }
 
 /* Two sums over the workgroup at once (one LDS round trip); `red` holds
- * 2 * NWAVES floats. */
-template <int NWAVES>
+ * 2 * NWAVES floats. REUSE as in block_sum. */
+template <int NWAVES, bool REUSE = true>
 NSR_DEV void block_sum2(float& a, float& b, float* red) {
   a = wave_sum(a);
   b = wave_sum(b);
@@ -205,7 +208,7 @@ NSR_DEV void block_sum2(float& a, float& b, float* red) {
       sa += red[w];
       sb += red[NWAVES + w];
     }
-    __syncthreads();
+    if constexpr (REUSE) __syncthreads();
     a = sa;
     b = sb;
   }
