@@ -22,7 +22,9 @@ labelled as such. `host_us_per_call` is the host time to enqueue one call
 from Python (ctypes + the C-ABI runtime + hipModuleLaunchKernel);
 `host_enqueue` is the same measured in C++ (nspeech_amd/host/
 enqueue_bench.cpp) for the decode-step entry points, beside a bare
-hipModuleLaunchKernel of an empty kernel.
+hipModuleLaunchKernel of an empty kernel, and per call of those entry
+points captured for 24 decoder layers into one HIP graph and replayed
+(`host_us_per_call_graph`).
 
 Floors, measured in the same run through the same runtime: an empty kernel
 (`empty`) and plain 128-bit device copies (`copy_<form>_<config>`) moving
@@ -752,6 +754,9 @@ def main():
             for nm in ("dec", "attn", "q8fc1"):
                 if nm in results:
                     results[nm]["host_us_per_call_c"] = host_enqueue[nm]
+                    # the same calls captured into one HIP graph (24 decoder layers) and replayed
+                    if "graph_replay_per_call" in host_enqueue:
+                        results[nm]["host_us_per_call_graph"] = host_enqueue["graph_replay_per_call"]
         else:
             print(f"[bench] enqueue bench failed ({r.returncode}): {r.stderr[-300:]}", file=sys.stderr, flush=True)
 

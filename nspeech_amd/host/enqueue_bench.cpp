@@ -4,7 +4,9 @@
 // entry points (called per layer per token by the reference's decoder,
 // src/moonshine/gpu_decoder.rs:483, gpu_decoder_metal.rs:144-156) at the
 // Moonshine decoder shapes, plus an empty kernel through this library and
-// the same empty kernel through a bare hipModuleLaunchKernel as the floor.
+// the same empty kernel through a bare hipModuleLaunchKernel as the floor, and
+// the decoder-step calls of 24 layers captured into one HIP graph: the host
+// cost of a replay, per captured call.
 //
 // Usage: nsr_enqueue_bench <code object dir>   (prints one JSON object)
 #include <hip/hip_runtime.h>
@@ -46,8 +48,8 @@ static void* dalloc(size_t bytes) {
 // Median over batches of the mean host time per call (us). Each batch is
 // short enough that the GPU queue never fills, and the stream is drained
 // between batches, so the time is the caller's, not a wait for queue space.
-static double host_us(hipStream_t s, const std::function<void()>& call) {
-  const int kBatch = 64, kBatches = 31;
+static double host_us(hipStream_t s, const std::function<void()>& call, int kBatch = 64) {
+  const int kBatches = 31;
   for (int i = 0; i < 2 * kBatch; ++i) call();
   CK(hipStreamSynchronize(s));
   std::vector<double> per;
@@ -113,9 +115,30 @@ int main(int argc, char** argv) {
                                NSR_F16, K, N, s));
   });
   CK(hipStreamSynchronize(s));
+
+  // The same three calls per layer for 24 decoder layers, captured once into a HIP graph (the entry points
+  // only launch kernels: no allocation, synchronisation or memset) and replayed: the host cost of a
+  // replay, per captured call. Batches of 4 replays keep the queue from filling.
+  const int kLayers = 24;
+  hipGraph_t graph;
+  hipGraphExec_t exec;
+  CK(hipStreamBeginCapture(s, hipStreamCaptureModeGlobal));
+  for (int l = 0; l < kLayers; ++l) {
+    NK(nsr_rope_qk_cache_append(q, k, v, NSR_F16, (const float*)tab, L, ck, cv, H, H, Dh, (int)rot, pos, L, s));
+    NK(nsr_attention_decode_f16(q, ck, cv, o, L, Dh, H, H, 0.125f, L * Dh, Dh, s));
+    NK(nsr_gemv_q8_t4_bias_glu(x, NSR_F16, (const uint32_t*)tq, (const uint16_t*)ts, (const float*)bias, out,
+                               NSR_F16, K, N, s));
+  }
+  CK(hipStreamEndCapture(s, &graph));
+  CK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+  const double replay = host_us(s, [&] { CK(hipGraphLaunch(exec, s)); }, 4);
+  CK(hipStreamSynchronize(s));
+  CK(hipGraphExecDestroy(exec));
+  CK(hipGraphDestroy(graph));
   std::printf(
       "{\"unit\": \"us per call, host\", \"hipModuleLaunchKernel_empty\": %.3f, \"nsr_calib_empty\": %.3f, "
-      "\"dec\": %.3f, \"attn\": %.3f, \"q8fc1\": %.3f}\n",
-      raw, empty, dec, attn, q8fc1);
+      "\"dec\": %.3f, \"attn\": %.3f, \"q8fc1\": %.3f, \"graph_replay_per_call\": %.3f, "
+      "\"graph_replay\": %.3f, \"graph_calls\": %d}\n",
+      raw, empty, dec, attn, q8fc1, replay / (3.0 * kLayers), replay, 3 * kLayers);
   return 0;
 }
