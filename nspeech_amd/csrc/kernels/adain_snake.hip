@@ -49,6 +49,14 @@ NSR_DEV adain_raw adain_params_load(const A& a, int pdt, int64_t bi, int64_t ci)
   return r;
 }
 
+/* (batch, channel) of a row = (row / C, row % C) in 32-bit arithmetic, for a row that is a workgroup
+ * index (below 2^31): a 64-bit division costs about 150 instructions ahead of the row's loads. */
+NSR_DEV void row_bc32(int64_t row, int C, int64_t& bi, int64_t& ci) {
+  const uint32_t r = (uint32_t)row, c = (uint32_t)C, q = r / c;
+  bi = (int64_t)q;
+  ci = (int64_t)(r - q * c);
+}
+
 NSR_DEV void adain_params_cvt(const adain_raw& r, int pdt, float& gam, float& bet, float& alp) {
   gam = pdt == DT_F32 ? __uint_as_float(r.g) : f16_bits_to_f32(r.g);
   bet = pdt == DT_F32 ? __uint_as_float(r.b) : f16_bits_to_f32(r.b);
@@ -125,8 +133,7 @@ NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
   auto valid = [&](int k) { return k < NS - MK || k < nvalid; };
   const nsr_float4 zero4 = {0.f, 0.f, 0.f, 0.f};
 
-  /* first row: parameters, then every slot's load */
-  adain_raw pr = adain_params_load(a, pdt, row / a.C, row % a.C);
+  /* first row: every slot's load, then the parameters */
   nsr_float4 v[NV];
   {
     const nsr_rsrc xr = make_rsrc(a.x + row * T, rbytes);
@@ -137,6 +144,9 @@ NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)((char*)lw + m * BLOCK * 16), 16, voff,
                                                (uint32_t)((NV + m) * BLOCK * 16), 0, 0);
   }
+  int64_t bi0, ci0;
+  row_bc32(row, a.C, bi0, ci0);
+  adain_raw pr = adain_params_load(a, pdt, bi0, ci0);
 
   while (true) {
     const int64_t next = row + gridDim.x;
@@ -276,8 +286,8 @@ NSR_DEV void adain_resident_u(const nsr_adain_args& a, int pdt) {
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const int64_t T = a.T;
-  const int64_t bi = row / a.C;
-  const int64_t ci = row - bi * a.C;
+  int64_t bi, ci;
+  row_bc32(row, a.C, bi, ci);
 
   const adain_raw pr = adain_params_load(a, pdt, bi, ci);
 
@@ -400,8 +410,8 @@ NSR_DEV void adain_row_f16(const nsr_adain_h_args& a, int pdt) {
   const int64_t row = blockIdx.x;
   if (row >= a.n_rows) return; /* whole workgroup: the grid is one per row */
   const int64_t T = a.T;
-  const int64_t bi = row / a.C;
-  const int64_t ci = row - bi * a.C;
+  int64_t bi, ci;
+  row_bc32(row, a.C, bi, ci);
 
   const adain_raw pr = adain_params_load(a, pdt, bi, ci);
 
@@ -533,12 +543,14 @@ NSR_DEV void adain_row_f16a(const nsr_adain_h_args& a, int pdt) {
   const int nch = (int)(T >> 3);
   const uint32_t rbytes = (uint32_t)(T * 2);
   const uint32_t voff = (uint32_t)tid * 16u;
-  const adain_raw pr = adain_params_load(a, pdt, row / a.C, row % a.C);
   const nsr_rsrc xr = make_rsrc(a.x + row * T, rbytes);
   nsr_uint4 raw[NV];
 #pragma unroll
   for (int k = 0; k < NV; ++k)
     raw[k] = __builtin_amdgcn_raw_buffer_load_b128(xr, voff, (uint32_t)(k * BLOCK * 16), NSR_AUX_NT);
+  int64_t bi, ci;
+  row_bc32(row, a.C, bi, ci);
+  const adain_raw pr = adain_params_load(a, pdt, bi, ci);
   const int nvalid = nch > tid ? (nch - tid + BLOCK - 1) / BLOCK : 0;
   float f[NV][8];
   float s = 0.f;
