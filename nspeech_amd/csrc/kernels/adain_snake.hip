@@ -286,11 +286,6 @@ NSR_DEV void adain_resident_u(const nsr_adain_args& a, int pdt) {
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const int64_t T = a.T;
-  int64_t bi, ci;
-  row_bc32(row, a.C, bi, ci);
-
-  const adain_raw pr = adain_params_load(a, pdt, bi, ci);
-
   const int64_t s = row * T;
   const int64_t a0 = s & ~(int64_t)3;
   const int lo = (int)(s - a0);        /* first row element in chunk space */
@@ -322,6 +317,10 @@ NSR_DEV void adain_resident_u(const nsr_adain_args& a, int pdt) {
   const int64_t eidx = q >= 4 ? 4 * (int64_t)jlast + (q & 3) : (int64_t)(q & 3);
   const bool eok = q >= 0 && eidx >= lo && eidx < hi && (q < 4 || jlast > 0);
   const float xe = eok ? xb[eidx] : 0.f;
+  /* the row's parameters, after its loads */
+  int64_t bi, ci;
+  row_bc32(row, a.C, bi, ci);
+  const adain_raw pr = adain_params_load(a, pdt, bi, ci);
 
   float sum = xe;
 #pragma unroll
@@ -410,11 +409,6 @@ NSR_DEV void adain_row_f16(const nsr_adain_h_args& a, int pdt) {
   const int64_t row = blockIdx.x;
   if (row >= a.n_rows) return; /* whole workgroup: the grid is one per row */
   const int64_t T = a.T;
-  int64_t bi, ci;
-  row_bc32(row, a.C, bi, ci);
-
-  const adain_raw pr = adain_params_load(a, pdt, bi, ci);
-
   const uint64_t xa = (uint64_t)(a.x + row * T);
   const uint64_t oa = (uint64_t)(a.out + row * T);
   const int lo = (int)((xa & 15) >> 1); /* first row element in chunk space */
@@ -446,6 +440,10 @@ NSR_DEV void adain_row_f16(const nsr_adain_h_args& a, int pdt) {
   const int64_t eidx = q >= 8 ? 8 * (int64_t)jlast + (q & 7) : (int64_t)(q & 7);
   const bool eok = q >= 0 && eidx >= lo && eidx < hi && (q < 8 || jlast > 0);
   const float xe = eok ? f16_bits_to_f32(xb[eidx]) : 0.f;
+  /* the row's parameters, after its loads */
+  int64_t bi, ci;
+  row_bc32(row, a.C, bi, ci);
+  const adain_raw pr = adain_params_load(a, pdt, bi, ci);
 
   float sum = xe;
 #pragma unroll

@@ -30,9 +30,12 @@ NSR_DEV void q8_0_gather_body(const nsr_q8_args& a) {
     /* whole waves per id: the id is wave-uniform, read once per wave through the scalar cache (a
      * constant-address-space load at a uniform address) instead of by every lane */
     const uint32_t gw = (uint32_t)a.gw, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    row = blockIdx.x * (uint32_t)a.ipw + wave / gw;
+    /* wave / gw for wave < 4 and gw <= 4 as a multiply and shift (exact there), not a division ahead of
+     * the id load: 256 / gw rounded up */
+    const uint32_t wq = (wave * (gw == 3u ? 86u : 256u >> (gw >> 1))) >> 8;
+    row = blockIdx.x * (uint32_t)a.ipw + wq;
     if (row >= (uint32_t)a.n_ids) return;
-    c4 = (wave % gw) * 64u + (threadIdx.x & 63u);
+    c4 = (wave - wq * gw) * 64u + (threadIdx.x & 63u);
     if (c4 >= d4) return;
     f = row * d4 + c4;
     if constexpr (IDS_I64) {
