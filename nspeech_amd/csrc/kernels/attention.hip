@@ -62,8 +62,8 @@ NSR_DEV float wave_max(float v) {
 }
 
 /* LDS of one wave: K and V rows [64][hd4 + 1] 8-byte pieces, probabilities
- * [64], P.V partials [64][4]. */
-NSR_DEV int attn_wave_lds_words(int hd4) { return 2 * 64 * (hd4 + 1) * 2 + 64 + 256; }
+ * [64], P.V partials [64][4], the wave's copy of q (up to 32 pieces). */
+NSR_DEV int attn_wave_lds_words(int hd4) { return 2 * 64 * (hd4 + 1) * 2 + 64 + 256 + 64; }
 
 /* Orders this wave's LDS writes before its later LDS reads by other lanes
  * (one wave's LDS operations execute in order; this keeps the compiler from
@@ -81,26 +81,34 @@ struct attn_state {
 };
 
 /* Walk the chunks c0 = first, first + stride, ... (< end) of query head qh
- * with this wave; q staged in ql (hd4 pieces). */
+ * with this wave. The wave loads q itself, with its first chunk's K and V
+ * (so the two latencies overlap and no workgroup barrier comes first), into
+ * its own LDS slice. */
 template <int HD4T>
-NSR_DEV void attn_walk(const nsr_attn_args& a, int qh, int first, int end, int stride, const uint2* ql,
-                       uint32_t* wl, attn_state& st) {
+NSR_DEV void attn_walk(const nsr_attn_args& a, int qh, int first, int end, int stride, uint32_t* wl,
+                       attn_state& st) {
   const int lane = threadIdx.x & 63;
   const int hd4 = HD4T ? HD4T : (a.head_dim >> 2);
   constexpr int NU = HD4T ? HD4T : NSR_ATT_MAXD / 4; /* 8-byte pieces per lane per row set */
-  const int kvh = (int)((int64_t)qh * a.n_kv_heads / a.n_q_heads);
+  /* the K/V head of this query head, in 32-bit arithmetic (head counts are small) */
+  const int kvh = a.n_kv_heads == a.n_q_heads
+                      ? qh
+                      : (int)((uint32_t)qh * (uint32_t)a.n_kv_heads / (uint32_t)a.n_q_heads);
   const uint16_t* kb = a.k + (int64_t)kvh * a.stride_kv_head;
   const uint16_t* vb = a.v + (int64_t)kvh * a.stride_kv_head;
   uint2* kl = (uint2*)wl;
   uint2* vl = kl + 64 * (hd4 + 1);
   float* pl = (float*)(vl + 64 * (hd4 + 1));
   float* red = pl + 64;
+  uint2* ql = (uint2*)(red + 256);
   /* P.V lane layout: 4 dimensions 4 dq .. 4 dq + 3, position group pg of ng */
   const int dq = lane % hd4, pg = lane / hd4, ng = 64 / hd4;
   const bool pv_lane = pg < ng;
 
   for (int c0 = first; c0 < end; c0 += stride) {
     const int n = min(64, end - c0);
+    uint2 qv = {0u, 0u};
+    if (c0 == first && lane < hd4) qv = *(const uint2*)(a.q + (int64_t)qh * a.head_dim + 4 * lane);
     /* in batches of NB pieces (all of them for the compile-time sizes; 8 at a
      * time for the run-time size, whose registers would not hold 2 x 32) */
     constexpr int NB = HD4T ? NU : 8;
@@ -124,6 +132,7 @@ NSR_DEV void attn_walk(const nsr_attn_args& a, int qh, int first, int end, int s
         }
       }
     }
+    if (c0 == first && lane < hd4) ql[lane] = qv;
     wave_lds_sync();
     float sc = -INFINITY;
     {
@@ -175,25 +184,17 @@ NSR_DEV void attn_walk(const nsr_attn_args& a, int qh, int first, int end, int s
   }
 }
 
-/* q of head qh into LDS (hd4 pieces) by the first wave's lanes. */
-NSR_DEV void attn_stage_q(const nsr_attn_args& a, int qh, uint2* ql) {
-  const int t = threadIdx.x, hd4 = a.head_dim >> 2;
-  if (t < hd4) ql[t] = *(const uint2*)(a.q + (int64_t)qh * a.head_dim + 4 * t);
-  __syncthreads();
-}
-
 /* Split: one wave per (query head, split) -> partial [m, l, acc[hd]]. */
 template <int HD4T>
 NSR_DEV void attn_partial(const nsr_attn_args& a) {
   extern __shared__ uint32_t att_lds[];
-  __shared__ uint2 ql[NSR_ATT_MAXD / 4];
   const int lane = threadIdx.x;
-  const int qh = blockIdx.x / a.n_splits, sp = blockIdx.x - qh * a.n_splits;
+  const uint32_t ns = (uint32_t)a.n_splits, qh32 = blockIdx.x / ns;
+  const int qh = (int)qh32, sp = (int)(blockIdx.x - qh32 * ns);
   const int hd = a.head_dim, hd4 = hd >> 2;
   const int p0 = sp * a.kv_per_split, p1 = min(p0 + a.kv_per_split, a.kv_len);
-  attn_stage_q(a, qh, ql);
   attn_state st = {-INFINITY, 0.f, {0.f, 0.f, 0.f, 0.f}};
-  attn_walk<HD4T>(a, qh, p0, p1, 64, ql, att_lds, st);
+  attn_walk<HD4T>(a, qh, p0, p1, 64, att_lds, st);
   float* po = a.partial + (int64_t)blockIdx.x * (hd + 2);
   if (lane == 0) {
     po[0] = st.m; /* -inf and l = 0 for an empty split */
@@ -209,15 +210,13 @@ NSR_DEV void attn_partial(const nsr_attn_args& a) {
 template <int HD4T>
 NSR_DEV void attn_head(const nsr_attn_args& a) {
   extern __shared__ uint32_t att_lds[];
-  __shared__ uint2 ql[NSR_ATT_MAXD / 4];
   __shared__ float ms[16], ls[16];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, W = blockDim.x >> 6;
   const int qh = blockIdx.x;
   const int hd = a.head_dim, hd4 = hd >> 2;
-  attn_stage_q(a, qh, ql);
   uint32_t* wl = att_lds + w * attn_wave_lds_words(hd4);
   attn_state st = {-INFINITY, 0.f, {0.f, 0.f, 0.f, 0.f}};
-  attn_walk<HD4T>(a, qh, 64 * w, a.kv_len, 64 * W, ql, wl, st);
+  attn_walk<HD4T>(a, qh, 64 * w, a.kv_len, 64 * W, wl, st);
   /* merge the waves: (m, l) and the acc rows through LDS (acc in the wave's
    * own K slice, free now) */
   float* accl = (float*)wl;

@@ -524,7 +524,7 @@ KId attn_kernel(const KId (&ids)[4], KId any, int64_t head_dim) {
   return i >= 0 ? ids[i] : any;
 }
 
-int64_t attn_wave_lds_bytes(int64_t head_dim) { return 4 * (2 * 64 * (head_dim / 4 + 1) * 2 + 64 + 256); }
+int64_t attn_wave_lds_bytes(int64_t head_dim) { return 4 * (2 * 64 * (head_dim / 4 + 1) * 2 + 64 + 256 + 64); }
 
 void attn_fill(nsr_attn_args& a, const void* q, const void* k, const void* v, void* out, float* partial,
                int64_t kv_len, int64_t head_dim, int64_t n_kv_heads, int64_t n_q_heads, float sm_scale,
