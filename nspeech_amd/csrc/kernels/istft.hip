@@ -100,7 +100,7 @@ NSR_DEV void istft_body(const nsr_istft_args& a) {
   constexpr int IA = (bins * FG + 255) / 256;    /* phase A items per lane */
   constexpr int IB = ((H + 1) * FG + 255) / 256; /* phase B items per lane */
   __shared__ float cosm[N], sinm[N]; /* cos / sin(2 pi m / N), m = 0 .. N - 1 */
-  __shared__ float win[N];
+  __shared__ float win[N], winn[N]; /* the window, and the window / N (the iDFT's scale folded in) */
   __shared__ float sre[bins * FG], sim[bins * FG]; /* [k][frame] */
   __shared__ float frames[FG * NS];                /* [frame][n], windowed */
   const int tid = threadIdx.x;
@@ -133,6 +133,7 @@ NSR_DEV void istft_body(const nsr_istft_args& a) {
     cosm[tid] = c;
     sinm[tid] = sinf(ang);
     win[tid] = 0.5f - 0.5f * c;
+    winn[tid] = (0.5f - 0.5f * c) / (float)N;
   }
 #pragma unroll
   for (int it = 0; it < IA; ++it) {
@@ -161,8 +162,9 @@ NSR_DEV void istft_body(const nsr_istft_args& a) {
         c = fmaf(sre[k * FG + fl], cosm[m], c);
         sm = fmaf(sim[k * FG + fl], sinm[m], sm);
       }
-      frames[fl * NS + n] = ((c - sm) / (float)N) * win[n];
-      if (n > 0 && n < H) frames[fl * NS + (N - n)] = ((c + sm) / (float)N) * win[N - n];
+      /* (c -/+ sm) / N * w[n] as one multiply by w[n] / N (no division per item) */
+      frames[fl * NS + n] = (c - sm) * winn[n];
+      if (n > 0 && n < H) frames[fl * NS + (N - n)] = (c + sm) * winn[N - n];
     }
   }
   __syncthreads();
