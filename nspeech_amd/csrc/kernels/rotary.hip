@@ -122,6 +122,15 @@ NSR_DEV void copy_pair(const void* src, int64_t es, void* dst, int64_t ed) {
   }
 }
 
+/* p / d for 0 <= p < 2^22 and d >= 1: a float reciprocal estimate (off by at most one) and one correction
+ * each way, instead of an integer division ahead of the loads the quotient addresses. */
+NSR_DEV int div_small(int p, int d) {
+  int q = (int)((float)p * __builtin_amdgcn_rcpf((float)d));
+  q += (q + 1) * d <= p ? 1 : 0;
+  q -= q * d > p ? 1 : 0;
+  return q;
+}
+
 template <int DT>
 NSR_DEV void rope_cache_body(const nsr_rope_cache_args& a) {
 #pragma clang fp contract(off)
@@ -131,7 +140,7 @@ NSR_DEV void rope_cache_body(const nsr_rope_cache_args& a) {
   if (p < a.nq + a.nk) {
     const bool isk = p >= a.nq;
     if (isk) p -= a.nq;
-    const int h = p / half, i = p - h * half;
+    const int h = div_small(p, half), i = p - h * half;
     void* x = isk ? a.k : a.q;
     const int64_t e = (int64_t)h * Dh + 2 * i;
     float x0, x1;
@@ -146,14 +155,14 @@ NSR_DEV void rope_cache_body(const nsr_rope_cache_args& a) {
   p -= a.nq + a.nk;
   if (p < a.nkp) {
     const int npp = (Dh - 2 * half) / 2;
-    const int h = p / npp, j = 2 * half + 2 * (p - h * npp);
+    const int h = div_small(p, npp), j = 2 * half + 2 * (p - h * npp);
     copy_pair<DT>(a.k, (int64_t)h * Dh + j, a.cache_k, ((int64_t)h * a.max_kv_len + a.pos) * Dh + j);
     return;
   }
   p -= a.nkp;
   if (p < a.nv) {
     const int nh = Dh / 2;
-    const int h = p / nh, j = 2 * (p - h * nh);
+    const int h = div_small(p, nh), j = 2 * (p - h * nh);
     copy_pair<DT>(a.v, (int64_t)h * Dh + j, a.cache_v, ((int64_t)h * a.max_kv_len + a.pos) * Dh + j);
   }
 }
