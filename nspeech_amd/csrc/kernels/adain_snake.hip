@@ -49,8 +49,8 @@ NSR_DEV adain_raw adain_params_load(const A& a, int pdt, int64_t bi, int64_t ci)
   return r;
 }
 
-/* (batch, channel) of a row = (row / C, row % C) in 32-bit arithmetic, for a row that is a workgroup
- * index (below 2^31): a 64-bit division costs about 150 instructions ahead of the row's loads. */
+/* (batch, channel) of a row = (row / C, row % C) in 32-bit arithmetic, for a row below 2^31 (a
+ * workgroup index, or any row when n_rows fits): a 64-bit division costs about 150 instructions. */
 NSR_DEV void row_bc32(int64_t row, int C, int64_t& bi, int64_t& ci) {
   const uint32_t r = (uint32_t)row, c = (uint32_t)C, q = r / c;
   bi = (int64_t)q;
@@ -200,7 +200,17 @@ NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
 
     /* store pass; each slot is refilled with the next row once its output is
      * issued (a past-the-end row reads nothing: its range is 0 bytes) */
-    if (more) pr = adain_params_load(a, pdt, next / a.C, next % a.C);
+    if (more) {
+      /* 32-bit (batch, channel) when every row index fits (uniform), not a 64-bit division ahead of the stores */
+      int64_t bn, cn;
+      if (a.n_rows <= 0x7fffffffLL) {
+        row_bc32(next, a.C, bn, cn);
+      } else {
+        bn = next / a.C;
+        cn = next - bn * a.C;
+      }
+      pr = adain_params_load(a, pdt, bn, cn);
+    }
     const nsr_rsrc orr = make_rsrc(a.out + row * T, rbytes);
     const nsr_rsrc xn = make_rsrc(a.x + (more ? next : row) * T, more ? rbytes : 0u);
     /* slot offsets are formed from a fresh copy of the lane offset and an
