@@ -614,7 +614,7 @@ NSR_ADAIN_F16A(4)
 /* ------------------------------------------------ row statistics, long rows -- */
 
 /* Sum and sum of squares of one row over 1024 lanes in f64, one HBM read:
- * 16-byte loads (four in flight per lane) when VEC4 (row 16-byte aligned,
+ * 16-byte loads (eight in flight per lane) when VEC4 (row 16-byte aligned,
  * T % 4 == 0), else element loads. In f64, var = S2/T - (S1/T)^2 keeps
  * about 16 - log10(mean^2 / var) significant digits, far more than f32
  * output needs for any |mean| / std below 1e4. `red` holds 32 doubles. */
@@ -625,11 +625,7 @@ NSR_DEV void row_sums64(const float* xr, int64_t T, double* red, double& s1, dou
   const int tid = threadIdx.x;
   if constexpr (VEC4) {
     const int64_t n4 = T >> 2;
-    int64_t i = tid;
-    for (; i + 3 * 1024 < n4; i += 4 * 1024) {
-      nsr_float4 v[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = ldf4(xr + 4 * (i + u * 1024));
+    auto acc4 = [&](const nsr_float4* v) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
 #pragma unroll
@@ -639,7 +635,47 @@ NSR_DEV void row_sums64(const float* xr, int64_t T, double* red, double& s1, dou
           a2 = __builtin_fma(x, x, a2);
         }
       }
+    };
+    /* Groups of 4096 float4 (four strided loads per lane) that every lane
+     * loads in full; the group count is uniform, so the loop branches on
+     * scalars, and the next group is issued before the current one is
+     * summed: eight loads stay in flight per lane. The loads are buffer
+     * loads at the lane's fixed offset plus a scalar group offset, so no
+     * address register is rewritten while a load into a neighbour is
+     * pending. Each lane still adds its elements in increasing order, then
+     * the tail one float4 at a time. Rows past 2^28 float4 (beyond the
+     * 32-bit buffer offset) take only the tail loop. */
+    const int64_t ngroups = n4 < (int64_t(1) << 28) ? n4 >> 12 : 0;
+    const nsr_rsrc rx = make_rsrc_uniform(xr, (uint32_t)(ngroups << 16));
+    const uint32_t vo = (uint32_t)tid * 16u;
+    auto ld4 = [&](nsr_float4* v, int64_t g) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = buf_load4(rx, vo, (uint32_t)(g << 16) + (uint32_t)u * 16384u);
+    };
+    int64_t g = 0;
+    if (ngroups > 0) {
+      nsr_float4 ga[4], gb[4]; /* two groups alternate, no register copies */
+      ld4(ga, 0);
+      for (;;) {
+        if (g + 1 >= ngroups) {
+          acc4(ga);
+          ++g;
+          break;
+        }
+        ld4(gb, g + 1);
+        acc4(ga);
+        ++g;
+        if (g + 1 >= ngroups) {
+          acc4(gb);
+          ++g;
+          break;
+        }
+        ld4(ga, g + 1);
+        acc4(gb);
+        ++g;
+      }
     }
+    int64_t i = (g << 12) + tid;
     for (; i < n4; i += 1024) {
       const nsr_float4 v = ldf4(xr + 4 * i);
 #pragma unroll
