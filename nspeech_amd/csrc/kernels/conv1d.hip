@@ -337,18 +337,22 @@ NSR_DEV float sum_lanes8(float v) {
 
 /* All eight row blocks of a wave's tile at once (m = 0..1, q = 0..3: row
  * co_lane + 32 m + 8 q), so the eight cross-lane sums are in flight together
- * and the block's column count is divided out once. */
-NSR_DEV void emit_rows8(const nsr_float4 (&ov)[2][4], int t, int tb, int T_out, int l32, int co_lane, int C_out,
-                        int64_t row0, int nblk, int blk, float* part) {
-  const int nv = max(0, min(4, T_out - t));
-  const float n = (float)max(0, min(32, T_out - tb)); /* valid columns of the block */
-  const float inv_n = 1.0f / fmaxf(n, 1.f);
+ * and the block's column count is divided out once. FULLB: all 32 columns
+ * of the block lie before T_out, so no column is masked; the arithmetic is
+ * the same either way (a masked column adds 0 to the sum and fma(0, 0, .)
+ * to M2), so a block's statistics do not depend on the variant. */
+template <bool FULLB>
+NSR_DEV void emit_rows8_v(const nsr_float4 (&ov)[2][4], int t, int tb, int T_out, int l32, int co_lane, int C_out,
+                          int64_t row0, int nblk, int blk, float* part) {
+  const int nv = FULLB ? 4 : max(0, min(4, T_out - t));
+  const float n = FULLB ? 32.f : (float)max(0, min(32, T_out - tb)); /* valid columns of the block */
+  const float inv_n = FULLB ? 1.0f / 32.0f : 1.0f / fmaxf(n, 1.f);
   float mean[8], m2[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     float s = 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) s += e < nv ? ov[i >> 2][i & 3][e] : 0.f;
+    for (int e = 0; e < 4; ++e) s += (FULLB || e < nv) ? ov[i >> 2][i & 3][e] : 0.f;
     mean[i] = s;
   }
 #pragma unroll
@@ -358,20 +362,28 @@ NSR_DEV void emit_rows8(const nsr_float4 (&ov)[2][4], int t, int tb, int T_out, 
     float qv = 0.f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float d = ov[i >> 2][i & 3][e] - mean[i];
-      qv += e < nv ? d * d : 0.f;
+      const float d = (FULLB || e < nv) ? ov[i >> 2][i & 3][e] - mean[i] : 0.f;
+      qv = __builtin_fmaf(d, d, qv);
     }
     m2[i] = qv;
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) m2[i] = sum_lanes8(m2[i]);
-  if (l32 < 4 && n > 0.f) {
+  if (l32 < 4 && (FULLB || n > 0.f)) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int co = co_lane + 32 * (i >> 2) + 8 * (i & 3);
       if (co < C_out) *(nsr_float2*)(part + 2 * ((row0 + co) * nblk + blk)) = nsr_float2{mean[i], m2[i]};
     }
   }
+}
+
+NSR_DEV void emit_rows8(const nsr_float4 (&ov)[2][4], int t, int tb, int T_out, int l32, int co_lane, int C_out,
+                        int64_t row0, int nblk, int blk, float* part) {
+  if (tb + 32 <= T_out) /* wave-uniform */
+    emit_rows8_v<true>(ov, t, tb, T_out, l32, co_lane, C_out, row0, nblk, blk, part);
+  else
+    emit_rows8_v<false>(ov, t, tb, T_out, l32, co_lane, C_out, row0, nblk, blk, part);
 }
 
 template <bool FUSED, bool RESID, int NU, bool STATS = false>
@@ -989,7 +1001,10 @@ struct cv_trans {
   int nb, ne;
 };
 
-template <bool RESID, bool STATS = false>
+/* FULL32 (STATS only): T_out % 32 == 0, so every 32-column block is whole or
+ * lies past T_out, and the statistics need no column masks (the masked form
+ * and the dispatch between the two would not fit the kernel's registers). */
+template <bool RESID, bool STATS = false, bool FULL32 = false>
 NSR_DEV void conv_pr_body(const nsr_conv_args& a, const uint8_t* xs, const uint8_t* wf) {
   extern __shared__ __attribute__((aligned(16))) uint8_t cv_ring[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1405,8 +1420,15 @@ NSR_DEV void conv_pr_body(const nsr_conv_args& a, const uint8_t* xs, const uint8
                 *(nsr_float4*)(cv_ring + stage_row(R0, R0 + 4 * hl + c4) + (uint32_t)tl * 4u) = o;
                 ov[m][q] = o;
               }
-            emit_rows8(ov, t, it.t0 + wt * 64 + tb * 32, a.T_out, l32, it.co0 + wco * 64 + 4 * hl + c4, a.C_out,
-                       (int64_t)it.b * a.C_out, (a.T_out + 31) >> 5, (it.t0 + wt * 64 + tb * 32) >> 5, a.row_part);
+            const int tbk = it.t0 + wt * 64 + tb * 32;
+            if constexpr (FULL32) {
+              if (tbk < a.T_out)
+                emit_rows8_v<true>(ov, t, tbk, a.T_out, l32, it.co0 + wco * 64 + 4 * hl + c4, a.C_out,
+                                   (int64_t)it.b * a.C_out, (a.T_out + 31) >> 5, tbk >> 5, a.row_part);
+            } else {
+              emit_rows8_v<false>(ov, t, tbk, a.T_out, l32, it.co0 + wco * 64 + 4 * hl + c4, a.C_out,
+                                  (int64_t)it.b * a.C_out, (a.T_out + 31) >> 5, tbk >> 5, a.row_part);
+            }
           }
         }
       }
@@ -1435,6 +1457,10 @@ NSR_DEV void conv_pr_body(const nsr_conv_args& a, const uint8_t* xs, const uint8
   extern "C" __global__ void __launch_bounds__(512, 1)                                              \
       NAME##_st(const nsr_conv_args a, const uint8_t* xs, const uint8_t* wf) {                      \
     conv_pr_body<RESID, true>(a, xs, wf);                                                           \
+  }                                                                                                 \
+  extern "C" __global__ void __launch_bounds__(512, 1)                                              \
+      NAME##_st32(const nsr_conv_args a, const uint8_t* xs, const uint8_t* wf) {                    \
+    conv_pr_body<RESID, true, true>(a, xs, wf);                                                     \
   }
 NSR_CONV_PR1(nsrk_conv1d_pr_f16x2, false)
 NSR_CONV_PR1(nsrk_conv1d_pr_res_f16x2, true)

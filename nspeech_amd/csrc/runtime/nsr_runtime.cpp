@@ -1463,12 +1463,15 @@ static nsr_status conv_records(bool fused, nsr_conv_args& a, char* records, nsr_
   if (tiles > 0x7fffffffLL) return fail(NSR_ERR_UNSUPPORTED, "%s: too many tiles", what);
   const bool stats = a.row_part != nullptr;
   if (emitted) *emitted = stats;
-  static const KId ids[2][2] = {{K_nsrk_conv1d_pr_f16x2, K_nsrk_conv1d_pr_f16x2_st},
-                                {K_nsrk_conv1d_pr_res_f16x2, K_nsrk_conv1d_pr_res_f16x2_st}};
+  // statistics: the _st32 kernels when every 32-column block is whole (T_out % 32 == 0: no column masks)
+  static const KId ids[2][3] = {{K_nsrk_conv1d_pr_f16x2, K_nsrk_conv1d_pr_f16x2_st, K_nsrk_conv1d_pr_f16x2_st32},
+                                {K_nsrk_conv1d_pr_res_f16x2, K_nsrk_conv1d_pr_res_f16x2_st,
+                                 K_nsrk_conv1d_pr_res_f16x2_st32}};
   // one workgroup per CU, a multiple of 8 (the kernel's XCD split) when there are enough tiles
   int64_t grid = std::min<int64_t>(tiles, dm->n_cu);
   if (grid >= 8) grid = grid / 8 * 8;
-  return launch(ids[a.residual != nullptr][stats], (unsigned)grid, 1, 512, kCvRingLds, stream, pp);
+  const int kv = stats ? (a.T_out % 32 == 0 ? 2 : 1) : 0;
+  return launch(ids[a.residual != nullptr][kv], (unsigned)grid, 1, 512, kCvRingLds, stream, pp);
 }
 
 // Launch a conv and leave the per-(b, co) statistics of its output in row_stats ([B*C_out][2]: mean,
