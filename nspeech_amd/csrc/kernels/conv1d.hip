@@ -1060,9 +1060,12 @@ NSR_DEV void conv_pr_body(const nsr_conv_args& a, const uint8_t* xs, const uint8
   auto phase_of = [&](int d) { return d >= TLe ? 0 : (d < D ? 1 : 2); };
   /* Output staging: after item n's last tap its tile (row r = output channel co0 + r, 128 columns f32)
    * goes to LDS while the ring holds window n + 1 (start nt0): rows r < FS in the ring slots outside
-   * that window, (nt0 + TLe + r) & 255, the other 128 - FS <= 56 rows after the ring. */
+   * that window, (nt0 + TLe + r) & 255, the other 128 - FS <= 56 rows after the ring. nt0 is a multiple
+   * of 128 and TLe + FS <= 256, so those slots never wrap: slot ((nt0 + TLe) & 255) + r. */
   const int FS = (CV_RING - TLe) / 8 * 8;
-  auto stage_ring = [&](int nt0, int r) { return (uint32_t)((nt0 + TLe + r) & (CV_RING - 1)) * CV_RS; };
+  auto stage_ring = [&](int nt0, int r) {
+    return (uint32_t)((nt0 + TLe) & (CV_RING - 1)) * CV_RS + (uint32_t)r * CV_RS;
+  };
   auto stage_tail = [&](int r) { return (uint32_t)(CV_RING * CV_RS + (r - FS) * 512); };
 
   if (wave >= 4) {
@@ -1374,19 +1377,26 @@ NSR_DEV void conv_pr_body(const nsr_conv_args& a, const uint8_t* xs, const uint8
         if constexpr (!STATS) {
           /* accumulator element i of lane (hl, l32) is channel 8 (i / 4) + 4 hl + i % 4 of its 32-channel
            * block at column l32: dword writes, 32 consecutive columns per half-wave, no cross-lane moves;
-           * bv[m][q] holds channel 8 q + 4 hl + c4, so the bias of element i is in quad lane i % 4 */
+           * bv[m][q] holds channel 8 q + 4 hl + c4, so the bias of element i is in quad lane i % 4. A group
+           * of 8 rows lies wholly in the ring (stride CV_RS) or after it (stride 512): its base and stride
+           * are wave-uniform, so a row's address is one add from the group's. */
+          const int wcu = __builtin_amdgcn_readfirstlane(wco);
+          const uint32_t lcol = (uint32_t)(64 * wt + l32) * 4u;
 #pragma unroll
           for (int m = 0; m < 2; ++m)
 #pragma unroll
             for (int g4 = 0; g4 < 4; ++g4) {
-              const int R0 = 64 * wco + 32 * m + 8 * g4;
+              const int R0 = 64 * wcu + 32 * m + 8 * g4;
+              const bool ring = R0 < FS;
+              const uint32_t rs = ring ? (uint32_t)CV_RS : 512u;
+              uint32_t la = stage_row(R0, R0) + (uint32_t)(4 * hl) * rs + lcol;
 #pragma unroll
               for (int c = 0; c < 4; ++c) {
                 const int i = 4 * g4 + c;
                 const float bi = quad_bcast(bv[m][g4], c);
-                const uint32_t la = stage_row(R0, R0 + 4 * hl + c) + (uint32_t)(64 * wt + l32) * 4u;
 #pragma unroll
                 for (int tb = 0; tb < 2; ++tb) *(float*)(cv_ring + la + 128u * tb) = acc[m][tb][i] + bi;
+                la += rs;
               }
             }
         } else {
