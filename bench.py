@@ -531,7 +531,7 @@ def build_workload(name):
         flops = 2 * C * C * K * TT * B
         return Workload(name, f"ResBlock stage in a chain (statistics handed along) K={K} dil={dil} f32 x[{B},{C},{TT}]"
                         + (" (record path)" if K >= 7 else " (one-launch fused conv)"), alg, x0.numel() * 4, make_set,
-                        launch, "nsrk_conv1d_pr_f16x2_st" if K >= 7 else "nsrk_conv1d_rw_adain_snake_f16x2_nu3_st",
+                        launch, "nsrk_conv1d_pr_f16x2_st32" if K >= 7 else "nsrk_conv1d_rw_adain_snake_f16x2_nu3_st",
                         "f32", flops=flops)
 
     if name == "c4a":
