@@ -724,7 +724,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs on a single MI355X (got --gpus {args.gpus}). "
-              "The kernels shard with no exchange along rows/positions; see DESIGN.md.", file=sys.stderr)
+              "The kernels shard with no exchange along rows/positions (one process per GPU, each on its own rows).",
+              file=sys.stderr)
         sys.exit(2)
     import torch
 
