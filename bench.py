@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X fused layer kernels (one JSON line on stdout).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workloads c1,c2,...]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workloads c1,c2,...] [--json-out FILE]
 
 A step is one call of a fused kernel on one batch of synthetic input already
 resident in HBM. The headline workload (`value`) is configs[4], the largest
@@ -9,22 +9,30 @@ configuration: AdaIN1d + Snake f32 x[8,128,115200] (workload c4b, the
 dominant kernel by bytes), with configs[4]'s other kernel, residual add +
 LayerNorm + GELU bf16 x,res [32,750,1024] (c4a), reported alongside in
 `config`. Every other config (c0..c3) and the next-row workloads are
-measured and reported under `per_config`.
+reported in `per_config`, one short array per workload (fields named by
+`per_config_fields`). The line stays under 4 KB; the full record of every
+workload (descriptions, kernels, warm and host figures, C++ enqueue times)
+is printed to stderr as `[bench] full {...}` and written to --json-out.
 
-Timing: W untimed warm-up calls, then the stream is held by a short spin
-kernel while the K timed calls are enqueued, so the GPU runs them back to
-back and the timing is of the GPU, not the Python launch path. HIP events
-on the launch stream bracket the K calls; `us_per_call` is their elapsed
-time / K, the average launch duration. Input/output buffer sets rotate so
-the footprint is >= 512 MB (twice the 256 MB Infinity Cache): the timed
-calls read HBM, not MALL. `warm_*` figures repeat one buffer set and are
+Timing: input/output buffer sets rotate so the bytes touched between two
+uses of a set are >= 512 MB (twice the 256 MB Infinity Cache): the timed
+calls read HBM, not MALL. Before the timed region every set is run through
+the kernel once (the touch pass, whose average is reported as
+`first_touch_us_per_call`), then W untimed warm-up calls, then the K timed
+calls continue the rotation. While the K calls are enqueued the stream is
+held by a short spin kernel, so the GPU runs them back to back and the
+timing is of the GPU, not the Python launch path. HIP events on the launch
+stream bracket the K calls; `us_per_call` is their elapsed time / K, the
+average launch duration. `warm_*` figures repeat one buffer set and are
 labelled as such. `host_us_per_call` is the host time to enqueue one call
 from Python (ctypes + the C-ABI runtime + hipModuleLaunchKernel);
 `host_enqueue` is the same measured in C++ (nspeech_amd/host/
 enqueue_bench.cpp) for the decode-step entry points, beside a bare
 hipModuleLaunchKernel of an empty kernel, and per call of those entry
 points captured for 24 decoder layers into one HIP graph and replayed
-(`host_us_per_call_graph`).
+(`host_us_per_call_graph`). `spin_clock_MHz` is the shader clock the spin
+kernel sees (its cycle counter per ms) at the start, after the MFMA conv
+workloads and at the end.
 
 Floors, measured in the same run through the same runtime: an empty kernel
 (`empty`) and plain 128-bit device copies (`copy_<form>_<config>`) moving
@@ -40,7 +48,8 @@ with `us_per_call` to within 1% (profiles/bench_workloads_trace_and_traffic.md).
 counters, calibrated on the flat copy (profiles/hbm_traffic_bench_workloads.txt).
 
 The CPU baseline is the oracle's C restatement of the reference CPU path
-(oracle/nsr_oracle.c) timed on this host on a bounded sample.
+(oracle/nsr_oracle.c) timed on this host: per config the median of 20 runs
+after 3 warm-ups, on 1 thread and on the host's threads, on a bounded sample.
 """
 from __future__ import annotations
 
@@ -75,20 +84,29 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workloads", default=",".join(DEFAULT_WORKLOADS),
                     help="comma list of " + ",".join(DEFAULT_WORKLOADS) + ",copy")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline (0 = skip)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-rotate", action="store_true", help="one buffer set (warm MALL) for all timings")
+    ap.add_argument("--no-touch-pass", action="store_true",
+                    help="skip the pass that runs every buffer set once before the warm-up")
+    ap.add_argument("--json-out", default="", help="also write every workload's full record to this file")
     return ap.parse_args()
 
 
 # ----------------------------------------------------------- workloads ---
 
 class Workload:
-    """Buffer sets and a launch(i) closure for one config."""
+    """Buffer sets and a launch(i) closure for one config.
 
-    def __init__(self, name, desc, alg_bytes, set_bytes, make_set, launch, kernel, dtype, flops=0):
+    `set_bytes` is the memory one buffer set holds; `touched` the bytes one call
+    reads or writes in it (less than `set_bytes` when a call reads a part of a
+    table). The number of sets rotated is sized on the smaller of the two, so
+    the bytes touched between two uses of a set exceed the Infinity Cache."""
+
+    def __init__(self, name, desc, alg_bytes, set_bytes, make_set, launch, kernel, dtype, flops=0, touched=None):
         self.name, self.desc, self.alg_bytes = name, desc, alg_bytes
         self.set_bytes, self.make_set, self.launch = set_bytes, make_set, launch
         self.kernel, self.dtype, self.flops = kernel, dtype, flops
+        self.touched = set_bytes if touched is None else touched
 
 
 def build_workload(name):
@@ -267,9 +285,10 @@ def build_workload(name):
             abi.check(L.nsr_q8_0_embed_gather(s["b"].data_ptr(), 32768, 416, ids.data_ptr(), 0, 4096,
                                               s["o"].data_ptr(), 1, None, stream()))
 
+        # a call reads 4096 of the 32768 table rows: the sets are counted on the bytes touched, not held
         return Workload(name, "GGUF Q8_0 gather-dequant + SiLU, table 32768x416, 4096 ids -> f32 [4096,416]",
                         configs.algorithmic_bytes("c3"), blocks0.numel() + 4096 * 416 * 4, make_set, launch,
-                        "nsrk_q8_0_gather_silu_u32", "i8xf16->f32")
+                        "nsrk_q8_0_gather_silu_u32", "i8xf16->f32", touched=configs.algorithmic_bytes("c3"))
 
     if name in ("dec", "dec2"):
         # Moonshine decoder step per layer (kernel_configs.py:102-104): q,k,v f16 [10, 64], rot 32,
@@ -565,14 +584,17 @@ def spin_rate_cycles_per_ms():
     return 2_000_000 / max(s.elapsed_time(e), 1e-3)
 
 
-def time_workload(w, steps, warmup, rotate, cyc_per_ms):
+def time_workload(w, steps, warmup, rotate, cyc_per_ms, touch_pass=True):
+    """Time one workload. Order of GPU work: one untimed-for-the-headline
+    call on every buffer set (the touch pass, so no timed call is the first
+    kernel use of its buffers; its average is `first_touch_us_per_call`),
+    `warmup` calls, then `steps` timed calls continuing the rotation where
+    the warm-up stopped, so the bytes touched between two uses of a set stay
+    above the Infinity Cache."""
     import torch
 
-    nsets = max(1, math.ceil(MALL_DEFEAT_BYTES / w.set_bytes)) if rotate else 1
+    nsets = max(1, math.ceil(MALL_DEFEAT_BYTES / min(w.set_bytes, w.touched))) if rotate else 1
     sets = [w.make_set(i) for i in range(nsets)]
-    torch.cuda.synchronize()
-    for i in range(warmup):
-        w.launch(sets[i % nsets])
     torch.cuda.synchronize()
 
     host = []
@@ -606,7 +628,12 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms):
                 break
         return t0.elapsed_time(t1) * 1e3 / len(order)
 
-    rotating = [i % nsets for i in range(steps)]
+    first_us = run_plain(list(range(nsets))) if touch_pass else None
+    torch.cuda.synchronize()
+    for i in range(warmup):
+        w.launch(sets[i % nsets])
+    torch.cuda.synchronize()
+    rotating = [(warmup + i) % nsets for i in range(steps)]
     cold_us = run_plain(rotating)            # timed region: K back-to-back calls
     warm_us = run_plain([0] * steps)         # same buffers: MALL-warm, labelled
     del sets
@@ -623,6 +650,7 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms):
         "us_per_call": round(cold_us, 3),
         "GBs": round(gbs(cold_us), 1),
         "frac_of_peak": round(gbs(cold_us) / HBM_PEAK_GBS, 4),
+        "first_touch_us_per_call": None if first_us is None else round(first_us, 3),
         "warm_us_per_call": round(warm_us, 3),
         "warm_GBs": round(gbs(warm_us), 1),
         **({"TFLOPs": round(w.flops / (cold_us * 1e-6) / 1e12, 2)} if w.flops else {}),
@@ -632,29 +660,51 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms):
 
 # -------------------------------------------------------- CPU baseline ---
 
-def cpu_baseline(budget_s, names):
-    """Oracle restatement of the reference CPU path on a bounded sample."""
+def host_cpu():
+    """(model name, threads used) of this host: the model from /proc/cpuinfo
+    (what `lscpu` prints as "Model name"), the threads from the affinity mask,
+    capped by OMP_NUM_THREADS when that is set (the GPU box's CPU share)."""
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return model, n
+
+
+CPU_RUNS, CPU_WARMUPS = 20, 3
+
+
+def cpu_baseline(names):
+    """Oracle restatement of the reference CPU path, per config: the median of
+    CPU_RUNS timed runs after CPU_WARMUPS untimed ones, on 1 thread and on the
+    host's threads, each on a bounded sample of the config."""
     import numpy as np
 
     from nspeech_amd import configs
     from oracle import restated as R
 
-    ncores = len(os.sched_getaffinity(0))
+    model, ncores = host_cpu()
     out = {}
 
-    def timed(fn, alg_bytes, seconds):
-        fn()
-        n, t0 = 0, time.perf_counter()
-        while True:
+    def timed(fn, alg_bytes):
+        for _ in range(CPU_WARMUPS):
             fn()
-            n += 1
-            dt = time.perf_counter() - t0
-            if dt >= seconds:
-                break
-        us = dt / n * 1e6
-        return {"us_per_call": round(us, 1), "GBs": round(alg_bytes / (us * 1e-6) / 1e9, 3), "calls": n}
+        runs = []
+        for _ in range(CPU_RUNS):
+            t0 = time.perf_counter()
+            fn()
+            runs.append(time.perf_counter() - t0)
+        us = float(np.median(runs)) * 1e6
+        return {"us_per_call": round(us, 1), "GBs": round(alg_bytes / (us * 1e-6) / 1e9, 3), "calls": CPU_RUNS}
 
-    per = budget_s / max(1, 2 * len(names))
     for nm in names:
         if nm == "c1" or nm == "c1t":
             c = configs.c1()
@@ -701,24 +751,83 @@ def cpu_baseline(budget_s, names):
             sample = "full config (scalar restatement of the Triton kernel, 1 thread)"
             wb = K * NW + (K // 32) * NW * 2
             galg = wb + 2 * K + (4 * NW + 2 * 2560 if nm.startswith("q8fc1") else 12 * 640)
-            r1 = timed(f1, galg, per)
+            r1 = timed(f1, galg)
             out[nm] = {"sample": sample, "threads_1": {"us_per_call": r1["us_per_call"], "GBs": r1["GBs"]}}
             continue
         else:
             continue
         alg = configs.algorithmic_bytes("c1" if nm == "c1t" else nm)
         scale = {"c4b": 1024 // 8, "c4a": 24000 // 750}.get(nm, 1)
-        r1 = timed(f1, alg / scale, per)
+        r1 = timed(f1, alg / scale)
         entry = {"sample": sample, "threads_1": {"us_per_call": round(r1["us_per_call"] * scale, 1),
                                                  "GBs": r1["GBs"]}}
         if fn is not None:
-            rn = timed(fn, alg / scale, per)
+            rn = timed(fn, alg / scale)
             entry[f"threads_{ncores}"] = {"us_per_call": round(rn["us_per_call"] * scale, 1), "GBs": rn["GBs"]}
         out[nm] = entry
-    return out, ncores
+    return out, ncores, model
 
 
 # ----------------------------------------------------------------- main ---
+
+# Fields of each workload in the stdout line's `per_config` (one array per workload). The full record of every
+# workload (description, kernel, warm and host figures) goes to stderr and to --json-out.
+PER_CONFIG_FIELDS = ["us_per_call", "GBs", "frac_of_peak", "copy_floor_us", "traffic", "first_touch_us_per_call"]
+LINE_LIMIT_BYTES = 4096
+
+
+def _finite(v):
+    """JSON-safe number: None for NaN / inf (the stdout line stays strict JSON)."""
+    if isinstance(v, float) and not math.isfinite(v):
+        return None
+    return v
+
+
+def compact_line(results, steps, warmup, cpu, clocks):
+    """The one stdout line: metric, value, the headline's roofline, the CPU
+    baseline and one short array per workload. Kept under LINE_LIMIT_BYTES."""
+    head_name = "c4b" if "c4b" in results else next(iter(results))
+    head = results[head_name]
+    companion = {}
+    if "c4a" in results and head_name == "c4b":
+        r = results["c4a"]
+        companion = {"c4a": {"workload": "configs[4]: " + r["workload"], "kernel": r["kernel"], "dtype": r["dtype"],
+                             "us_per_call": r["us_per_call"], "GBs": r["GBs"], "frac_of_peak": r["frac_of_peak"],
+                             "copy_floor_us": r.get("copy_floor_us"), "traffic": r.get("traffic")}}
+    per = {}
+    for nm, r in results.items():
+        if nm.startswith("copy_") and nm != "copy_rows_c4b":
+            continue  # each copy is the copy_floor_us of its config
+        per[nm] = [_finite(r.get(f)) for f in PER_CONFIG_FIELDS]
+        if r.get("TFLOPs") is not None:
+            per[nm].append(_finite(r["TFLOPs"]))
+    line = {
+        "metric": METRIC,
+        "value": head["GBs"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(head["us_per_call"] / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": head["dtype"],
+        "data": "synthetic (seeded numpy inputs of the benchmark configs)",
+        "config": {"workload": ("configs[4]: " if head_name == "c4b" else "") + head["workload"],
+                   "buffer_sets": head["buffer_sets"], "footprint_MB": head["footprint_MB"],
+                   "parallelism": "single GPU", **({"alongside": companion} if companion else {})},
+        "roofline": {"bound": "hbm", "achieved": head["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": head["frac_of_peak"], "traffic": head.get("traffic"), "kernel": head["kernel"],
+                     "us_per_call": head["us_per_call"], "copy_floor_us": head.get("copy_floor_us"),
+                     "row_copy_floor_us": head.get("row_copy_floor_us")},
+        "cpu_baseline": cpu,
+        "spin_clock_MHz": clocks,
+        "per_config_fields": PER_CONFIG_FIELDS + ["TFLOPs (MFMA workloads)"],
+        "per_config": per,
+    }
+    return json.loads(json.dumps(line, allow_nan=False, default=_finite))
+
 
 def main():
     args = parse()
@@ -734,14 +843,22 @@ def main():
     abi.init()
     names = [n for n in args.workloads.split(",") if n]
     cyc = spin_rate_cycles_per_ms()
+    # the spin kernel counts shader-clock cycles: its rate per ms is the clock of an idle-ish SIMD, taken before
+    # the workloads, after the MFMA conv workloads and at the end
+    clocks = {"start": round(cyc / 1e3)}
+    mfma = [n for n in names if n.startswith(("kconv", "kchain"))]
     results = {}
     for nm in names:
         w = build_workload(nm)
-        results[nm] = time_workload(w, args.steps, args.warmup, not args.no_rotate, cyc)
+        results[nm] = time_workload(w, args.steps, args.warmup, not args.no_rotate, cyc,
+                                    touch_pass=not args.no_touch_pass)
         del w
         torch.cuda.empty_cache()
         print(f"[bench] {nm}: {results[nm]['us_per_call']} us/call, {results[nm]['GBs']} GB/s "
               f"({100 * results[nm]['frac_of_peak']:.1f}% of peak)", file=sys.stderr, flush=True)
+        if mfma and nm == mfma[-1]:
+            clocks["after_mfma"] = round(spin_rate_cycles_per_ms() / 1e3)
+    clocks["end"] = round(spin_rate_cycles_per_ms() / 1e3)
 
     # host time per call of the decode-step entry points, measured in C++ (no binding overhead)
     host_enqueue = None
@@ -749,8 +866,8 @@ def main():
     if eb.exists():
         import subprocess
 
-        # under rocprofv3 (its settings reach the process as ROCPROF_* variables) the graph replay is left
-        # out: the tracer's hooks crashed inside hipGraphLaunch on this image
+        # Under rocprofv3 (its settings reach the process as ROCPROF_* variables) the graph replay is left out:
+        # a traced run ended in a segmentation fault inside hipGraphLaunch, which stays untraced.
         traced = any(k.startswith("ROCPROF_") for k in os.environ)
         r = subprocess.run([str(eb), str(eb.parent)] + (["--no-graph"] if traced else []),
                            capture_output=True, text=True, timeout=120)
@@ -777,19 +894,6 @@ def main():
             r["row_copy_floor_us"] = results["copy_rows_c4b"]["us_per_call"]
             r["frac_of_row_copy"] = round(r["row_copy_floor_us"] / r["us_per_call"], 4)
 
-    head_name = "c4b" if "c4b" in results else next(iter(results))
-    head = results[head_name]
-    cpu = None
-    if args.cpu_seconds > 0:
-        per_cfg, ncores = cpu_baseline(args.cpu_seconds, [n for n in names if n in CONFIG_WORKLOADS and n != "c1t"])
-        h = per_cfg.get(head_name) or next(iter(per_cfg.values()))
-        cpu = {"value": h["threads_1"]["GBs"], "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": "oracle C restatement of the reference CPU path (adain + snake_activation_tensor, "
-                         "src/kokoro/decoder.rs:1416-1428,1471-1476) on 8 of configs[4]'s 1024 AdaIN rows "
-                         "(x[1,8,115200]), 1 thread, scaled to the full config; "
-                         f"{ncores}-thread and per-config figures under per_config",
-               "per_config": per_cfg, "host_cores": ncores}
-
     traffic = {}
     tf = ROOT / "profiles" / "hbm_traffic_bench_workloads.txt"
     if tf.exists():
@@ -801,37 +905,29 @@ def main():
     for nm, r in results.items():
         r["traffic"] = traffic.get(nm)
 
-    companion = {}
-    if "c4a" in results and head_name == "c4b":
-        r = results["c4a"]
-        companion = {"c4a": {"workload": r["workload"], "kernel": r["kernel"], "dtype": r["dtype"],
-                             "us_per_call": r["us_per_call"], "GBs": r["GBs"], "frac_of_peak": r["frac_of_peak"],
-                             "traffic": traffic.get("c4a")}}
-    line = {
-        "metric": METRIC,
-        "value": head["GBs"],
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(head["us_per_call"] / 1e3, 6),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": head["dtype"],
-        "data": "synthetic (seeded numpy inputs of the benchmark configs; no model weights needed)",
-        "config": {"workload": ("configs[4]: " if head_name == "c4b" else "") + head["workload"],
-                   "buffer_sets": head["buffer_sets"], "footprint_MB": head["footprint_MB"],
-                   "parallelism": "single GPU", **({"alongside": companion} if companion else {})},
-        "roofline": {"bound": "hbm", "achieved": head["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": head["frac_of_peak"], "traffic": traffic.get(head_name), "kernel": head["kernel"],
-                     "us_per_call": head["us_per_call"], "copy_floor_us": head.get("copy_floor_us"),
-                     "row_copy_floor_us": head.get("row_copy_floor_us")},
-        "cpu_baseline": cpu,
-        "host_enqueue": host_enqueue,
-        "per_config": results,
-    }
-    print(json.dumps(line), flush=True)
+    cpu = None
+    cpu_names = [n for n in names if n in CONFIG_WORKLOADS and n != "c1t"]
+    if not args.no_cpu and cpu_names:
+        per_cfg, ncores, model = cpu_baseline(cpu_names)
+        head_name = "c4b" if "c4b" in per_cfg else next(iter(per_cfg))
+        h = per_cfg[head_name]
+        cpu = {"value": h["threads_1"]["GBs"], "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"oracle C restatement of the reference CPU path on {head_name}: {h['sample']}; median of "
+                         f"{CPU_RUNS} runs after {CPU_WARMUPS} warm-ups, 1 thread",
+               "cpu_model": model, "host_threads": ncores,
+               "us_per_call": {nm: [e["threads_1"]["us_per_call"], e.get(f"threads_{ncores}", {}).get("us_per_call")]
+                               for nm, e in per_cfg.items()},
+               "us_per_call_fields": ["1 thread", f"{ncores} threads"]}
+        print("[bench] cpu_baseline " + json.dumps(per_cfg), file=sys.stderr, flush=True)
+
+    full = {"per_config": results, "host_enqueue": host_enqueue, "spin_clock_MHz": clocks}
+    print("[bench] full " + json.dumps(full, default=_finite), file=sys.stderr, flush=True)
+    if args.json_out:
+        Path(args.json_out).parent.mkdir(parents=True, exist_ok=True)
+        Path(args.json_out).write_text(json.dumps(full, indent=1, default=_finite) + "\n")
+    line = compact_line(results, args.steps, args.warmup, cpu, clocks)
+    sys.stderr.flush()
+    print(json.dumps(line, allow_nan=False), flush=True)
 
 
 if __name__ == "__main__":

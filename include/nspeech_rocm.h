@@ -371,7 +371,9 @@ nsr_status nsr_attention_decode_f16(const void* q, const void* k, const void* v,
  * f32 accuracy on f16 matrix cores (each activation is split into two f16
  * halves; f32 accumulation). Requirements: C_in % 16 == 0; (K - 1) *
  * dilation <= 64; T_in, T_out < 2^23; stride != 1 returns
- * NSR_ERR_UNSUPPORTED. Rows that start 16-byte aligned (T_in % 4 == 0,
+ * NSR_ERR_UNSUPPORTED, and so do shapes whose rows of one batch reach
+ * 4 GiB (4 C_in T_in or 4 C_out T_out >= 2^32: one buffer descriptor
+ * addresses a batch's rows). The same holds for every conv entry point. Rows that start 16-byte aligned (T_in % 4 == 0,
  * T_out % 4 == 0, 16-byte aligned x / out / residual) take the faster
  * producer/consumer kernels. Packs the weights into the caller's workspace
  * (NSR_WS_PACKED_WEIGHTS, see nsr_conv1d_workspace_bytes) on every call and

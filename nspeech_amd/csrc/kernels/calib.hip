@@ -63,9 +63,9 @@ extern "C" __global__ void __launch_bounds__(512) nsrk_calib_copy_rows(const nsr
     for (int k0 = 0; k0 < ns; k0 += 8) {
       nsr_float4 v[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = buf_load4(xr, voff, (uint32_t)((k0 + u) * 512 * 16));
+      for (int u = 0; u < 8; ++u) v[u] = buf_load4(xr, voff, (uint32_t)(k0 + u) * 8192u);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) buf_store4(orr, voff, (uint32_t)((k0 + u) * 512 * 16), v[u]);
+      for (int u = 0; u < 8; ++u) buf_store4(orr, voff, (uint32_t)(k0 + u) * 8192u, v[u]);
     }
   }
 }

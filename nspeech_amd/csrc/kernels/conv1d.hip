@@ -154,7 +154,7 @@ NSR_DEV void conv_body(const nsr_conv_args& a) {
     const int c0 = ch * CV_CI, nq = min(CV_CI, a.C_in - c0) >> 2;
     if (lq >= nq) return;
     /* this (batch, chunk)'s rows through one buffer descriptor: 32-bit offsets */
-    const nsr_rsrc xr = make_rsrc_uniform(a.x + ((int64_t)b * a.C_in + c0) * a.T_in, (uint32_t)(4 * (nq * 4) * a.T_in));
+    const nsr_rsrc xr = make_rsrc_uniform(a.x + ((int64_t)b * a.C_in + c0) * a.T_in, 4u * (uint32_t)(nq * 4) * (uint32_t)a.T_in);
     const uint32_t rowoff = (uint32_t)(4 * lq) * (uint32_t)a.T_in;
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
@@ -446,7 +446,7 @@ NSR_DEV void conv_rw_body(const nsr_conv_args& a) {
       const int tile = tile_of(n);
       const int b = tile / n_t, t0 = (tile - b * n_t) * CV_TT;
       const int s0 = t0 - a.padding - dsh;
-      const nsr_rsrc xr = make_rsrc_uniform(a.x + (int64_t)b * a.C_in * a.T_in, (uint32_t)(4 * a.C_in * a.T_in));
+      const nsr_rsrc xr = make_rsrc_uniform(a.x + (int64_t)b * a.C_in * a.T_in, 4u * (uint32_t)a.C_in * (uint32_t)a.T_in);
 #pragma unroll
       for (int u = 0; u < NU; ++u) {
         /* a quad before column 0 wraps to a huge offset (range-checked to 0)
@@ -536,7 +536,7 @@ NSR_DEV void conv_rw_body(const nsr_conv_args& a) {
           bias[m][q] = co < a.C_out ? v : 0.f;
         }
     }
-    const uint32_t obytes = (uint32_t)(4 * a.C_out * a.T_out);
+    const uint32_t obytes = 4u * (uint32_t)a.C_out * (uint32_t)a.T_out;
     const int wbase = (wco * 64 + l32) * CV_S + 8 * hl;
     const int ybase = (wt * 32 + l32) * CV_S + 8 * hl;
     __syncthreads(); /* weights and tile 0 staged */
@@ -725,7 +725,7 @@ NSR_DEV void conv_pc_body(const nsr_conv_args& a) {
       const int nq = min(CV_CI, a.C_in - c0) >> 2;
       const uint32_t rowoff = (uint32_t)(4 * min(lq, nq - 1)) * (uint32_t)a.T_in;
       const int s0 = t0 - a.padding - dsh;
-      const nsr_rsrc xr = make_rsrc_uniform(a.x + ((int64_t)b * a.C_in + c0) * a.T_in, (uint32_t)(4 * nq * 4 * a.T_in));
+      const nsr_rsrc xr = make_rsrc_uniform(a.x + ((int64_t)b * a.C_in + c0) * a.T_in, 4u * (uint32_t)(nq * 4) * (uint32_t)a.T_in);
 #pragma unroll
       for (int u = 0; u < NU; ++u) {
         const uint32_t col = (uint32_t)(s0 + 4 * (jl + 8 * u));
@@ -800,7 +800,7 @@ NSR_DEV void conv_pc_body(const nsr_conv_args& a) {
   } else {
     const int wco = wave >> 1, wt = wave & 1;
     const int hl = lane >> 5, l32 = lane & 31, c4 = lane & 3;
-    const uint32_t obytes = (uint32_t)(4 * a.C_out * a.T_out);
+    const uint32_t obytes = 4u * (uint32_t)a.C_out * (uint32_t)a.T_out;
     /* weight slice (item n, tap k) -> registers: 16-byte chunks id = tid + 256 i of [128 co][16 x 8 ci] */
     nsr_uint4 wr[8];
     auto load_w = [&](int n, int k) {
@@ -1123,7 +1123,7 @@ NSR_DEV void conv_pr_body(const nsr_conv_args& a, const uint8_t* xs, const uint8
       for (int p = 0; p < 16; ++p) sv[p] = *saddr[p];
     };
     auto store_staged = [&](const cv_item& im, int jw, int gap) {
-      const uint32_t obytes = (uint32_t)(4 * a.C_out * a.T_out);
+      const uint32_t obytes = 4u * (uint32_t)a.C_out * (uint32_t)a.T_out;
       const nsr_rsrc orr = make_rsrc_uniform(a.out + (int64_t)im.b * a.C_out * a.T_out, obytes);
       /* the residual (variants without statistics add it here), loaded 4 passes ahead */
       const nsr_rsrc rr = make_rsrc_uniform(RESID ? a.residual + (int64_t)im.b * a.C_out * a.T_out : a.out, obytes);
@@ -1165,7 +1165,7 @@ NSR_DEV void conv_pr_body(const nsr_conv_args& a, const uint8_t* xs, const uint8
       const bool has_next = n + 1 < items;
       if (has_next) {
         const nsr_rsrc xr =
-            make_rsrc_uniform(xs + ((int64_t)in.b * n_ch + in.ch) * Tp * CV_RB, (uint32_t)(Tp * CV_RB));
+            make_rsrc_uniform(xs + ((int64_t)in.b * n_ch + in.ch) * Tp * CV_RB, (uint32_t)Tp * (uint32_t)CV_RB);
         /* 16 rounds always (128 new records for consecutive tiles; rounds past the new records re-read
          * the last pair), 8 more for a window that shares nothing with the current one */
 #pragma unroll
@@ -1239,7 +1239,7 @@ NSR_DEV void conv_pr_body(const nsr_conv_args& a, const uint8_t* xs, const uint8
   } else {
     const int wco = wave >> 1, wt = wave & 1;
     const int hl = lane >> 5, l32 = lane & 31, c4 = lane & 3;
-    const uint32_t obytes = (uint32_t)(4 * a.C_out * a.T_out);
+    const uint32_t obytes = 4u * (uint32_t)a.C_out * (uint32_t)a.T_out;
     const uint32_t kstride = (uint32_t)n_ch * 8192u, cbstride = (uint32_t)a.K * kstride;
     const nsr_rsrc wr = make_rsrc_uniform(wf, (uint32_t)n_co * 4u * cbstride);
     /* fragment weights of (item, tap) for this wave's 64 channels (m = 0: cb, m = 1: cb + 1) */
@@ -1542,7 +1542,7 @@ NSR_DEV void conv_presplit(const nsr_conv_args& a, uint8_t* xs, uint8_t* wf) {
   const int ti0 = j64 + 4 * cq;      /* its 4 input columns ti0 .. ti0 + 3 */
   /* the whole block inside the row and the channel chunk full: nothing to zero (wave-uniform) */
   const bool full = j64 >= 0 && j64 + 63 < a.T_in && (ch + 1) * CV_CI <= a.C_in;
-  const nsr_rsrc xr = make_rsrc_uniform(a.x + (int64_t)b * a.C_in * a.T_in, (uint32_t)(4 * a.C_in * a.T_in));
+  const nsr_rsrc xr = make_rsrc_uniform(a.x + (int64_t)b * a.C_in * a.T_in, 4u * (uint32_t)a.C_in * (uint32_t)a.T_in);
   /* Interior lanes: one 16-byte load per channel (4-byte aligned offsets). Lanes whose 4 columns cross
    * either end of the row load each column on its own at a clamped column, so no load leaves the
    * batch's buffer; those columns, and channels past C_in, are zeroed below. */

@@ -1317,6 +1317,7 @@ nsr_status nsr_gemv_q8_t4_resadd_ln(const void* x, nsr_dtype x_dtype, const uint
 namespace {
 
 constexpr int kCvTT = 64, kCvCO = 128, kCvCI = 128, kCvS = kCvCI + 8, kCvMaxTL = 128;
+constexpr int64_t kConvMaxSlabBytes = 0xffffffffLL;  // a buffer descriptor's byte range
 
 nsr_status conv_validate(const float* x, const void* w, uintptr_t w_align, float* out, int64_t B, int64_t C_in,
                          int64_t C_out, int64_t T_in, int64_t K, int64_t padding, int64_t dilation, int64_t* T_out,
@@ -1334,6 +1335,12 @@ nsr_status conv_validate(const float* x, const void* w, uintptr_t w_align, float
   if (*T_out >= (1LL << 23)) return fail(NSR_ERR_BAD_ARG, "%s: T_out=%lld too long", what, (long long)*T_out);
   if (*T_out <= 0 && T_in > 0)
     return fail(NSR_ERR_BAD_ARG, "%s: empty output (T_in + 2 padding < dilation (K - 1) + 1)", what);
+  // each batch's input, output and residual rows are addressed through one buffer descriptor, whose byte
+  // range (and every offset in it) is 32-bit
+  if (4 * C_in * T_in > kConvMaxSlabBytes || 4 * C_out * std::max<int64_t>(*T_out, 0) > kConvMaxSlabBytes)
+    return fail(NSR_ERR_UNSUPPORTED, "%s: one batch's rows (C_in %lld x T_in %lld, C_out %lld x T_out %lld f32) "
+                "exceed the %lld bytes a buffer descriptor addresses", what, (long long)C_in, (long long)T_in,
+                (long long)C_out, (long long)*T_out, (long long)kConvMaxSlabBytes);
   if (!aligned(x, 4) || !aligned(out, 4) || !aligned(w, w_align))
     return fail(NSR_ERR_BAD_ARG, "%s: misaligned pointer (weights need %u bytes)", what, (unsigned)w_align);
   return NSR_OK;

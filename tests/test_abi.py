@@ -186,3 +186,19 @@ def test_no_gpu_fails_loudly():
         abi.init()
     assert ei.value.status in (abi.NSR_ERR_HIP, abi.NSR_ERR_NOT_INIT)
     assert abi.lib().nsr_kernel_count() == 0
+
+
+def test_conv_rows_past_a_buffer_descriptor_are_unsupported():
+    """Each batch's conv input / output rows are addressed through one buffer
+    descriptor (a 32-bit byte range). Shapes whose per-batch rows reach 4 GiB
+    are rejected before any launch; the largest shape below the limit passes
+    validation (B = 0 then returns at once, with no GPU work)."""
+    L = abi.lib()
+    big_t = (1 << 23) - 1  # 4 * 128 * big_t = 2^32 - 512 bytes per batch
+    packed = lambda B, ci, co, t: L.nsr_conv1d_f16w_packed(256, 256, NULL, NULL, 256, B, ci, co, t, 1, 0, 1,  # noqa
+                                                           NULL)
+    assert packed(0, 128, 128, big_t) == abi.NSR_OK
+    assert packed(0, 256, 16, 1 << 22) == abi.NSR_ERR_UNSUPPORTED      # input rows: 4 * 256 * 2^22 = 2^32
+    assert "buffer descriptor" in L.nsr_last_error().decode()
+    assert packed(0, 16, 1024, 1 << 20) == abi.NSR_ERR_UNSUPPORTED     # output rows: 4 * 1024 * 2^20 = 2^32
+    assert packed(0, 16, 1023, 1 << 20) == abi.NSR_OK
