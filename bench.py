@@ -88,6 +88,9 @@ def parse():
     ap.add_argument("--no-rotate", action="store_true", help="one buffer set (warm MALL) for all timings")
     ap.add_argument("--no-touch-pass", action="store_true",
                     help="skip the pass that runs every buffer set once before the warm-up")
+    ap.add_argument("--sets-on-held", action="store_true",
+                    help="size the buffer-set rotation on the bytes a set holds, not the bytes a call touches "
+                         "(for comparison: a partial gather then reuses sets within the Infinity Cache)")
     ap.add_argument("--json-out", default="", help="also write every workload's full record to this file")
     return ap.parse_args()
 
@@ -584,7 +587,7 @@ def spin_rate_cycles_per_ms():
     return 2_000_000 / max(s.elapsed_time(e), 1e-3)
 
 
-def time_workload(w, steps, warmup, rotate, cyc_per_ms, touch_pass=True):
+def time_workload(w, steps, warmup, rotate, cyc_per_ms, touch_pass=True, sets_on_held=False):
     """Time one workload. Order of GPU work: one untimed-for-the-headline
     call on every buffer set (the touch pass, so no timed call is the first
     kernel use of its buffers; its average is `first_touch_us_per_call`),
@@ -593,7 +596,8 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms, touch_pass=True):
     above the Infinity Cache."""
     import torch
 
-    nsets = max(1, math.ceil(MALL_DEFEAT_BYTES / min(w.set_bytes, w.touched))) if rotate else 1
+    per_set = w.set_bytes if sets_on_held else min(w.set_bytes, w.touched)
+    nsets = max(1, math.ceil(MALL_DEFEAT_BYTES / per_set)) if rotate else 1
     sets = [w.make_set(i) for i in range(nsets)]
     torch.cuda.synchronize()
 
@@ -851,7 +855,7 @@ def main():
     for nm in names:
         w = build_workload(nm)
         results[nm] = time_workload(w, args.steps, args.warmup, not args.no_rotate, cyc,
-                                    touch_pass=not args.no_touch_pass)
+                                    touch_pass=not args.no_touch_pass, sets_on_held=args.sets_on_held)
         del w
         torch.cuda.empty_cache()
         print(f"[bench] {nm}: {results[nm]['us_per_call']} us/call, {results[nm]['GBs']} GB/s "

@@ -14,9 +14,18 @@
  *   weight columns (plain, h) or 8 x-half + 8 gate-half columns (glu) over
  *   all of K; its 256 lanes take row pairs (2 rows of one 32-row block, so
  *   one scale per column) and are reduced through LDS in a fixed order. Each
- *   row contributes only 8 bytes per workgroup, so neighbouring tiles share
- *   cache lines: tiles are ordered so that consecutive tiles run on the same
- *   XCD (workgroups are dealt round-robin to the 8 XCDs) and meet in its L2.
+ *   row contributes only 8 bytes per workgroup, so the 16 tiles of one
+ *   128-byte line of qs words (128 columns) share every line they read, and
+ *   they meet in an L2 only when they run on one XCD (workgroups are dealt
+ *   round-robin to the 8 XCDs). Two tile maps:
+ *   - line groups: XCD x takes the 16-tile groups x, x + 8, ..., so every
+ *     line comes from HBM once (grid: 16 workgroups per group on each XCD,
+ *     those past the last tile exit at once);
+ *   - contiguous runs: XCD x takes the x-th run of ceil(n / 8) tiles, which
+ *     balances the XCDs when the groups do not divide evenly, at the cost of
+ *     reading the lines of a group split between two XCDs twice.
+ *   The host takes line groups unless that leaves an XCD with more tiles
+ *   than both the balanced share and its 32 CUs.
  *
  * - t4 tiles (nsr_q8_pack_t4): tile t holds 4 weight columns for all K rows
  *   contiguously, [K][4] int8, with its scales [K/32][4] f16. A workgroup
@@ -33,13 +42,20 @@
 
 enum { GEMV_PLAIN = 0, GEMV_GLU = 1, GEMV_H = 2 };
 
-/* Tile order that puts consecutive tiles on one XCD: workgroup b runs on XCD
- * b % 8; XCD x takes the x-th contiguous run of tiles. A bijection of
- * [0, n). */
+/* Contiguous runs: workgroup b runs on XCD b % 8; XCD x takes the x-th
+ * contiguous run of tiles. A bijection of [0, n) (grid = n). */
 NSR_DEV int xcd_tile(int b, int n) {
   const int per = (n + 7) >> 3, x = b & 7, i = b >> 3;
   const int full = n - 8 * (per - 1); /* XCDs that take `per` tiles */
   return (x < full ? x * per : full * per + (x - full) * (per - 1)) + i;
+}
+
+/* Line groups: workgroup b, the (b / 8)-th on XCD b % 8, takes the next tile
+ * of that XCD's groups x, x + 8, x + 16, ...; -1 past the last tile. */
+NSR_DEV int line_group_tile(int b, int n) {
+  const int x = b & 7, i = b >> 3;
+  const int t = 16 * (x + 8 * (i >> 4)) + (i & 15);
+  return t < n ? t : -1;
 }
 
 NSR_DEV float silu_f(float g) {
@@ -58,7 +74,8 @@ NSR_DEV void gemv_ref(const nsr_gemv_args& a) {
   __shared__ float red2[256];
   __shared__ float fin[NC];
   const int tid = threadIdx.x;
-  const int t = xcd_tile(blockIdx.x, gridDim.x);
+  const int t = a.line_groups ? line_group_tile(blockIdx.x, a.n_tiles) : xcd_tile(blockIdx.x, a.n_tiles);
+  if (t < 0) return; /* the whole workgroup: no barrier is reached */
   const int64_t nw4 = a.NW >> 2;
   /* first word (per row) of each 8-column group */
   const int64_t g0 = 2 * (int64_t)t;

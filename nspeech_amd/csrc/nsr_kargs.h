@@ -119,6 +119,8 @@ typedef struct nsr_gemv_args {
   int32_t K;
   int32_t NW;              /* weight columns: N, or 2N for the GLU form */
   int32_t N;               /* output columns */
+  int32_t n_tiles;         /* reference layout: 8-column tiles (x-half tiles for the GLU form) */
+  int32_t line_groups;     /* reference layout: 1 = each 16-tile line group on one XCD, 0 = contiguous runs */
   int32_t pad_;
 } nsr_gemv_args;
 

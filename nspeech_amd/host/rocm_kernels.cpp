@@ -167,7 +167,40 @@ RocmKernels RocmKernels::load(const RocmDevice& dev) {
   nsr_check(nsr_init(nullptr), "RocmKernels::load");
   RocmKernels k;
   k.kernel_count_ = nsr_kernel_count();
+  k.device_ = dev;
+  k.gemv_weights_ = std::make_shared<GemvWeightCache>();
   return k;
+}
+
+std::pair<const uint32_t*, const uint16_t*> RocmKernels::t4_weight(hipStream_t stream, const void* qs,
+                                                                   const void* scales, size_t k, size_t nw,
+                                                                   bool glu) const {
+  if (!gemv_weights_) throw Error("RocmKernels: not loaded (RocmKernels::load)");
+  std::lock_guard<std::mutex> lk(gemv_weights_->mu);
+  for (const T4Weight& e : gemv_weights_->entries)
+    if (e.qs == qs && e.scales == scales && e.k == k && e.nw == nw && e.glu == glu)
+      return {static_cast<const uint32_t*>(e.tq.buffer().at()), static_cast<const uint16_t*>(e.ts.buffer().at())};
+  // first call with this weight: pack it once, in stream order before the caller's GEMV
+  Tensor tq = Tensor::empty(device_, {k * nw / 4}, DType::U32);
+  Tensor ts = Tensor::empty(device_, {k / 32 * nw}, DType::F16);
+  nsr_check(nsr_q8_pack_t4(static_cast<const uint32_t*>(qs), static_cast<const uint16_t*>(scales), (int64_t)k,
+                           (int64_t)nw, glu ? 1 : 0, static_cast<uint32_t*>(tq.buffer().at()),
+                           static_cast<uint16_t*>(ts.buffer().at()), stream),
+            "enc_gemv_q8 (t4 packing)");
+  gemv_weights_->entries.push_back(T4Weight{qs, scales, k, nw, glu, tq, ts});
+  return {static_cast<const uint32_t*>(tq.buffer().at()), static_cast<const uint16_t*>(ts.buffer().at())};
+}
+
+void RocmKernels::forget_gemv_weights() const {
+  if (!gemv_weights_) return;
+  std::lock_guard<std::mutex> lk(gemv_weights_->mu);
+  gemv_weights_->entries.clear();
+}
+
+size_t RocmKernels::gemv_weights_cached() const {
+  if (!gemv_weights_) return 0;
+  std::lock_guard<std::mutex> lk(gemv_weights_->mu);
+  return gemv_weights_->entries.size();
 }
 
 // --------------------------------------------------- Tensor-level (triton_*) --
@@ -389,25 +422,51 @@ void enc_attention_splitkv(Encoder enc, const RocmKernels&, const GpuBuffer& q, 
             "enc_attention_splitkv");
 }
 
-void enc_gemv_q8(Encoder enc, const RocmKernels&, const GpuBuffer& x, const GpuBuffer& qs, const GpuBuffer& scales,
-                 const GpuBuffer* bias, const GpuBuffer& out, size_t k, size_t n) {
+// The three decoder GEMVs multiply with the t4 copy of their weight (RocmKernels::t4_weight: packed on the first
+// call with a weight buffer, reused after). x is read 4 elements at a time there; an x not 8-byte aligned takes
+// the [K, N/4] kernels on the caller's layout instead.
+static bool t4_ok(const GpuBuffer& x) { return (reinterpret_cast<uintptr_t>(x.at()) & 7) == 0; }
+
+void enc_gemv_q8(Encoder enc, const RocmKernels& kernels, const GpuBuffer& x, const GpuBuffer& qs,
+                 const GpuBuffer& scales, const GpuBuffer* bias, const GpuBuffer& out, size_t k, size_t n) {
+  const float* b = bias ? static_cast<const float*>(bias->at()) : nullptr;
+  if (t4_ok(x) && k % 32 == 0 && n % 16 == 0) {
+    const auto w = kernels.t4_weight(enc, qs.at(), scales.at(), k, n, false);
+    nsr_check(nsr_gemv_q8_t4(x.at(), NSR_F16, w.first, w.second, b, out.at(), NSR_F16, (int64_t)k, (int64_t)n, enc),
+              "enc_gemv_q8");
+    return;
+  }
   nsr_check(nsr_gemv_q8(x.at(), NSR_F16, static_cast<const uint32_t*>(qs.at()), static_cast<const uint16_t*>(scales.at()),
-                        bias ? static_cast<const float*>(bias->at()) : nullptr, out.at(), NSR_F16, (int64_t)k,
-                        (int64_t)n, enc),
+                        b, out.at(), NSR_F16, (int64_t)k, (int64_t)n, enc),
             "enc_gemv_q8");
 }
 
-void enc_gemv_q8_bias_glu(Encoder enc, const RocmKernels&, const GpuBuffer& x, const GpuBuffer& qs,
+void enc_gemv_q8_bias_glu(Encoder enc, const RocmKernels& kernels, const GpuBuffer& x, const GpuBuffer& qs,
                           const GpuBuffer& scales, const GpuBuffer& bias, const GpuBuffer& out, size_t k, size_t n) {
+  if (t4_ok(x) && k % 32 == 0 && n % 16 == 0) {
+    const auto w = kernels.t4_weight(enc, qs.at(), scales.at(), k, 2 * n, true);
+    nsr_check(nsr_gemv_q8_t4_bias_glu(x.at(), NSR_F16, w.first, w.second, static_cast<const float*>(bias.at()),
+                                      out.at(), NSR_F16, (int64_t)k, (int64_t)n, enc),
+              "enc_gemv_q8_bias_glu");
+    return;
+  }
   nsr_check(nsr_gemv_q8_bias_glu(x.at(), NSR_F16, static_cast<const uint32_t*>(qs.at()),
                                  static_cast<const uint16_t*>(scales.at()), static_cast<const float*>(bias.at()),
                                  out.at(), NSR_F16, (int64_t)k, (int64_t)n, enc),
             "enc_gemv_q8_bias_glu");
 }
 
-void enc_gemv_q8_resadd_ln(Encoder enc, const RocmKernels&, const GpuBuffer& x, const GpuBuffer& qs,
+void enc_gemv_q8_resadd_ln(Encoder enc, const RocmKernels& kernels, const GpuBuffer& x, const GpuBuffer& qs,
                            const GpuBuffer& scales, const GpuBuffer& residual, const GpuBuffer& out_f32,
                            const GpuBuffer& ln_weight, const GpuBuffer& norm, size_t k, size_t dim, float eps) {
+  if (t4_ok(x) && k % 32 == 0 && dim % 16 == 0) {
+    const auto w = kernels.t4_weight(enc, qs.at(), scales.at(), k, dim, false);
+    nsr_check(nsr_gemv_q8_t4_resadd_ln(x.at(), NSR_F16, w.first, w.second, static_cast<const float*>(residual.at()),
+                                       static_cast<float*>(out_f32.at()), ln_weight.at(), NSR_F16, norm.at(), NSR_F16,
+                                       (int64_t)k, (int64_t)dim, eps, enc),
+              "enc_gemv_q8_resadd_ln");
+    return;
+  }
   nsr_check(nsr_gemv_q8_resadd_ln(x.at(), NSR_F16, static_cast<const uint32_t*>(qs.at()),
                                   static_cast<const uint16_t*>(scales.at()), static_cast<const float*>(residual.at()),
                                   static_cast<float*>(out_f32.at()), ln_weight.at(), NSR_F16, norm.at(), NSR_F16,

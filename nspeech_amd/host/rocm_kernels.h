@@ -26,6 +26,7 @@
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 namespace nspeech {
@@ -107,9 +108,32 @@ class RocmKernels {
  public:
   static RocmKernels load(const RocmDevice& dev);
   int kernel_count() const { return kernel_count_; }
+  // The t4 tile copy of a repacked-Q8 weight (qs u32 [K, NW/4], scales f16 [K/32, NW]) that the enc_gemv_q8*
+  // calls multiply with. The decoder passes the same weight buffers for every token: each is packed once
+  // (nsr_q8_pack_t4, on `stream`, ahead of that call's GEMV) on its first call and the copy reused, so the
+  // GEMVs read whole 128-byte lines (the [K, N/4] layout makes a workgroup that owns a few columns read 8 bytes
+  // of every weight row) and later calls allocate nothing. Returns the t4 qs and scales.
+  std::pair<const uint32_t*, const uint16_t*> t4_weight(hipStream_t stream, const void* qs, const void* scales,
+                                                        size_t k, size_t nw, bool glu) const;
+  // Drop the t4 copies (for a caller that rewrites or frees a weight buffer).
+  void forget_gemv_weights() const;
+  size_t gemv_weights_cached() const;
 
  private:
+  struct T4Weight {
+    const void* qs;
+    const void* scales;
+    size_t k, nw;
+    bool glu;
+    Tensor tq, ts;
+  };
+  struct GemvWeightCache {
+    std::mutex mu;
+    std::vector<T4Weight> entries;
+  };
   int kernel_count_ = 0;
+  RocmDevice device_;
+  std::shared_ptr<GemvWeightCache> gemv_weights_;
 };
 
 // The encoder of the enc_* API: launches go onto this stream.

@@ -615,6 +615,36 @@ void test_gemv_q8(const RocmDevice& dev, const RocmKernels& k) {
     err = std::max(err, scaled(h2f(h[j]), gate / (1 + std::exp(-gate)) * up));
   }
   report("enc_gemv_q8_bias_glu", err, 2e-3);
+  // the mirror packs the weight to t4 tiles on its first call and reuses the copy: a second call adds no
+  // cache entry and gives the same bits
+  if (k.gemv_weights_cached() != 1) throw Error("enc_gemv_q8_bias_glu: expected one cached t4 weight");
+  enc_gemv_q8_bias_glu(dev.stream(), k, X.buffer(), Q1.buffer(), S1.buffer(), B1.buffer(), H.buffer(), K, N);
+  dev.synchronize();
+  if (H.to_vec<uint16_t>() != h || k.gemv_weights_cached() != 1)
+    throw Error("enc_gemv_q8_bias_glu: second call differs or packed again");
+  // the plain GEMV over the x half of the same buffers (NW = N columns of a [K, N/4] weight): its own cache entry
+  {
+    std::vector<uint32_t> qp(K * N / 4);
+    std::vector<uint16_t> sp(K / 32 * N);
+    for (size_t kk = 0; kk < K; ++kk)
+      for (size_t j = 0; j < N / 4; ++j) qp[kk * (N / 4) + j] = qs1[kk * (2 * N / 4) + j];
+    for (size_t b = 0; b < K / 32; ++b)
+      for (size_t j = 0; j < N; ++j) sp[b * N + j] = sc1[b * 2 * N + j];
+    Tensor QP = Tensor::from_host(dev, qp.data(), {qp.size()}, DType::U32);
+    Tensor SP = Tensor::from_host(dev, sp.data(), {sp.size()}, DType::F16);
+    Tensor OP = Tensor::empty(dev, {N}, DType::F16);
+    enc_gemv_q8(dev.stream(), k, X.buffer(), QP.buffer(), SP.buffer(), nullptr, OP.buffer(), K, N);
+    dev.synchronize();
+    const std::vector<uint16_t> op = OP.to_vec<uint16_t>();
+    double e = 0;
+    for (size_t j = 0; j < N; ++j) {
+      double up = 0;
+      for (size_t kk = 0; kk < K; ++kk) up += (double)h2f(x[kk]) * wq(qp, sp, N, kk, j);
+      e = std::max(e, scaled(h2f(op[j]), up));
+    }
+    report("enc_gemv_q8 (t4 copy)", e, 2e-3);
+    if (k.gemv_weights_cached() != 2) throw Error("enc_gemv_q8: expected a second cached t4 weight");
+  }
   Tensor Q2 = Tensor::from_host(dev, qs2.data(), {qs2.size()}, DType::U32);
   Tensor S2 = Tensor::from_host(dev, sc2.data(), {sc2.size()}, DType::F16);
   Tensor RS = Tensor::from_host(dev, res.data(), {K}, DType::F32);
@@ -643,6 +673,9 @@ void test_gemv_q8(const RocmDevice& dev, const RocmKernels& k) {
     err_n = std::max(err_n, scaled(h2f(nm[j]), (hv[j] - mean) / std::sqrt(var + 1e-5) * h2f(lnw[j])));
   report("enc_gemv_q8_resadd_ln h", err_h, 2e-3);
   report("enc_gemv_q8_resadd_ln norm", err_n, 2e-3);
+  if (k.gemv_weights_cached() != 3) throw Error("enc_gemv_q8_resadd_ln: expected a third cached t4 weight");
+  k.forget_gemv_weights();
+  if (k.gemv_weights_cached() != 0) throw Error("forget_gemv_weights left entries");
 }
 
 }  // namespace
