@@ -100,9 +100,9 @@ NSR_DEV float sum4(nsr_float4 d) { return (d.x + d.y) + (d.z + d.w); }
  * returns 0, but a load to LDS past it leaves the LDS slot as it was); their
  * stores are dropped by the buffer range check.
  *
- * The store pass of row r refills each slot with row r + gridDim.x as soon as
- * the slot's output is stored, so on a CU the reads of the next row overlap
- * the writes of the current one, and HBM traffic stays the algorithmic
+ * The store pass of row r refills each slot with row r + gridDim.x once the
+ * slot's output is stored (stores and refills in batches of 8 slots), so on a
+ * CU the reads of the next row overlap the writes of the current one, and HBM traffic stays the algorithmic
  * 8 bytes per element (x read once, out written once). */
 template <int BLOCK, int NV, int NL>
 NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
@@ -221,18 +221,35 @@ NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
     asm volatile("s_mov_b32 %0, 0" : "=s"(so));
     lds_void* lwr = lw;
     asm volatile("" : "+s"(lwr));
+    /* in batches of SB slots: SB stores, then the SB refill loads of those slots (sched_barrier keeps the
+     * order). Measured on MI355X at [8, 128, 115200]: 160-161 us against 163-165 us with each store followed
+     * by its slot's load; batches of 4 or 6 and of 12 or more were slower than 8. */
+    constexpr int SB = 8;
+    static_for<0, (NV + SB - 1) / SB>([&](auto gc) {
+      constexpr int k0 = decltype(gc)::value * SB;
+      constexpr int k1 = k0 + SB < NV ? k0 + SB : NV;
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      buf_store4(orr, vo, (uint32_t)(k * BLOCK * 16), adain_snake4(v[k], A, Bc, sc));
-      v[k] = buf_load4(xn, vo, so + (uint32_t)(k * BLOCK * 16));
-    }
-    static_for<0, NL>([&](auto mc) {
-      constexpr int m = decltype(mc)::value;
-      const nsr_float4 d = lds_x[m * BLOCK + tid] - mean;
-      buf_store4(orr, vo, (uint32_t)((NV + m) * BLOCK * 16), adain_snake4(d, A, Bc, sc));
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xn, (lds_void*)((char*)lwr + m * BLOCK * 16), 16, vo,
-                                               so + (uint32_t)((NV + m) * BLOCK * 16), 0, 0);
-      if constexpr (m % 2 == 1) __builtin_amdgcn_sched_barrier(0);
+      for (int k = k0; k < k1; ++k) buf_store4(orr, vo, (uint32_t)(k * BLOCK * 16), adain_snake4(v[k], A, Bc, sc));
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = k0; k < k1; ++k) v[k] = buf_load4(xn, vo, so + (uint32_t)(k * BLOCK * 16));
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    static_for<0, (NL + SB - 1) / SB>([&](auto gc) {
+      constexpr int m0 = decltype(gc)::value * SB;
+      constexpr int m1 = m0 + SB < NL ? m0 + SB : NL;
+#pragma unroll
+      for (int m = m0; m < m1; ++m) {
+        const nsr_float4 d = lds_x[m * BLOCK + tid] - mean;
+        buf_store4(orr, vo, (uint32_t)((NV + m) * BLOCK * 16), adain_snake4(d, A, Bc, sc));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      /* each slot's LDS read above has completed: its value was stored */
+#pragma unroll
+      for (int m = m0; m < m1; ++m)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xn, (lds_void*)((char*)lwr + m * BLOCK * 16), 16, vo,
+                                                 so + (uint32_t)((NV + m) * BLOCK * 16), 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     });
     if (!more) break;
     row = next;
