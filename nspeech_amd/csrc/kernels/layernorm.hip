@@ -161,6 +161,9 @@ NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
 
     float v[NC][VEC];
     float sum = 0.f;
+    /* packed h words, stored once the next row's loads are issued */
+    constexpr bool PACKED_H = FUSED && H != DT_F32 && chunk_words<H, VEC>::value == 1;
+    nsr_uint4 hsave[PACKED_H ? NC : 1];
 #pragma unroll
     for (int k = 0; k < NC; ++k) {
       const int j = lane + 64 * k;
@@ -169,14 +172,13 @@ NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
         if constexpr (FUSED) {
           float r[VEC];
           unpack_raw<R, VEC>(rr[k], r);
-          if constexpr (H != DT_F32 && chunk_words<H, VEC>::value == 1) {
+          if constexpr (PACKED_H) {
             /* h = round_H(x + res) packed two at a time (one conversion per pair), stored as packed and
              * widened back from the packed words: the same values as rounding each element */
 #pragma unroll
             for (int e = 0; e < VEC; ++e) v[k][e] += r[e];
-            const nsr_uint4 hw = pack16<H>(v[k]);
-            unpack16<H>(hw, v[k]);
-            if (a.h) st16((char*)a.h + (xrow + (int64_t)j * VEC) * dt_size<H>::value, hw);
+            hsave[k] = pack16<H>(v[k]);
+            unpack16<H>(hsave[k], v[k]);
           } else {
 #pragma unroll
             for (int e = 0; e < VEC; ++e) v[k][e] = round_to<H>(v[k][e] + r[e]);
@@ -189,6 +191,15 @@ NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
     }
     if constexpr (PIPE) {
       if (more) load_row(next);
+    }
+    /* h after the next row's loads: measured on MI355X at [24000, 1024] bf16, 33.7 against 33.9-35.4 us over
+     * 200 calls when each h chunk is stored as soon as it is formed */
+    if constexpr (PACKED_H) {
+#pragma unroll
+      for (int k = 0; k < NC; ++k) {
+        const int j = lane + 64 * k;
+        if (j < nchunk && a.h) st16((char*)a.h + (xrow + (int64_t)j * VEC) * dt_size<H>::value, hsave[k]);
+      }
     }
     const float mean = wave_sum(sum) * a.inv_n;
 
