@@ -345,7 +345,10 @@ nsr_status nsr_attention_splitkv_f16(const void* q, const void* k, const void* v
  * > 262144 floats, fail with NSR_ERR_UNSUPPORTED. The call allocates
  * nothing. Every call on one GPU shares that GPU's array: calls that
  * overlap on one GPU (other streams, other host threads) race and must be
- * serialised by the caller. Same results as nsr_attention_splitkv_f16. */
+ * serialised by the caller. Same results as nsr_attention_splitkv_f16.
+ * The array's device address is resolved when the library first loads on a
+ * device (nsr_init, or the first entry point called there): under graph
+ * capture, call nsr_init on that device before capturing. */
 #define NSR_NOALLOC_SCRATCH_BYTES (1024 * 1024)
 nsr_status nsr_attention_splitkv_f16_noalloc(const void* q, const void* k, const void* v, void* out,
                                              int64_t kv_len, int64_t head_dim, int64_t n_kv_heads,

@@ -62,3 +62,43 @@ def test_decode_step_graph_replays_match_eager(dev):
         got = [_bits(q), _bits(ck[:, pos]), _bits(cv[:, pos]), _bits(o_g), _bits(y_g)]
         for name, a, b in zip(["q", "cache k row", "cache v row", "attention out", "fc1 GLU out"], got, ref):
             assert_bitexact(a, b, f"replay {r}: {name}")
+
+
+def test_noalloc_splitkv_graph_replays_match_eager(dev):
+    """nsr_attention_splitkv_f16_noalloc under capture (its fixed scratch is resolved when the library loads
+    on the device, before any capture here, since the fixture called nsr_init): three replays, with eager
+    work between them, against the caller-buffer entry point run eagerly."""
+    import math
+
+    L = abi.lib()
+    nq, nkv, hd, kv_len, splits = 10, 10, 64, 1500, 32  # Moonshine cross-attention over 30 s of encoder K/V
+    say("attention_splitkv_noalloc under graph capture; 3 replays")
+    g = configs.rng(12)
+    q = torch.from_numpy((g.standard_normal((nq, hd)) * 0.8).astype(np.float16)).cuda()
+    k = torch.from_numpy(g.standard_normal((kv_len, nkv, hd)).astype(np.float16)).cuda()
+    v = torch.from_numpy(g.standard_normal((kv_len, nkv, hd)).astype(np.float16)).cuda()
+    scale = 1.0 / math.sqrt(hd)
+    ref_out = torch.empty((nq, hd), dtype=torch.float16, device="cuda")
+    part = torch.empty(nq * splits * (hd + 2), dtype=torch.float32, device="cuda")
+    abi.check(L.nsr_attention_splitkv_f16(q.data_ptr(), k.data_ptr(), v.data_ptr(), ref_out.data_ptr(),
+                                          part.data_ptr(), kv_len, hd, nkv, nq, scale, hd, nkv * hd, splits,
+                                          torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    ref = _bits(ref_out)
+
+    out = torch.empty((nq, hd), dtype=torch.float16, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        abi.check(L.nsr_attention_splitkv_f16_noalloc(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                                      kv_len, hd, nkv, nq, scale, hd, nkv * hd, splits,
+                                                      torch.cuda.current_stream().cuda_stream))
+    for r in range(3):
+        out.zero_()  # eager work between replays on the same buffer
+        # an eager noalloc call of another shape in between leaves other partials in the shared scratch
+        small = torch.empty((4, 36), dtype=torch.float16, device="cuda")
+        abi.check(L.nsr_attention_splitkv_f16_noalloc(q.data_ptr(), k.data_ptr(), v.data_ptr(), small.data_ptr(),
+                                                      129, 36, 2, 4, 1.0 / 6.0, 36, nkv * hd, 5,
+                                                      torch.cuda.current_stream().cuda_stream))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_bitexact(_bits(out), ref, f"replay {r}: noalloc split-KV attention")
