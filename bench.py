@@ -70,7 +70,8 @@ NEXT_WORKLOADS = ["dec", "dec2", "attn", "attnx", "q8fc1", "q8fc2", "q8fc1r", "q
                   "kconv11", "kconv7f", "kconv11f", "kconv3u", "kchain3", "kchain11", "mrf", "istft"]
 # same-size copies: algorithmic bytes of the config each one calibrates
 COPY_SIZES = {"c1t": 8519680, "c3": 8642560, "c2h": 9833472, "c2": 19666944, "c4a": 196616192, "c4b": 943727104}
-COPY_FOR = {"c1": "c1t", "c1t": "c1t", "c3": "c3", "c2": "c2", "c2u": "c2", "c2h": "c2h", "c4a": "c4a", "c4b": "c4b"}
+COPY_FOR = {"c1": "c1t", "c1t": "c1t", "c3": "c3", "c2": "c2", "c2u": "c2", "c2h": "c2h", "c4a": "c4a", "c4b": "c4b",
+            "c4a_act0": "c4a", "c4a_act1": "c4a"}
 FLOOR_WORKLOADS = ["empty"] + [f"copy_{f}_{c}" for c in COPY_SIZES for f in ("f", "p4", "p8")] + ["copy_rows_c4b"]
 DEFAULT_WORKLOADS = CONFIG_WORKLOADS + FLOOR_WORKLOADS + NEXT_WORKLOADS
 MALL_DEFEAT_BYTES = 512 << 20
@@ -83,7 +84,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workloads", default=",".join(DEFAULT_WORKLOADS),
-                    help="comma list of " + ",".join(DEFAULT_WORKLOADS) + ",copy")
+                    help="comma list of " + ",".join(DEFAULT_WORKLOADS) + ",copy,c4a_act0,c4a_act1")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-rotate", action="store_true", help="one buffer set (warm MALL) for all timings")
     ap.add_argument("--no-touch-pass", action="store_true",
@@ -556,7 +557,10 @@ def build_workload(name):
                         launch, "nsrk_conv1d_pr_f16x2_st32" if K >= 7 else "nsrk_conv1d_rw_adain_snake_f16x2_nu3_st",
                         "f32", flops=flops)
 
-    if name == "c4a":
+    if name in ("c4a", "c4a_act0", "c4a_act1"):
+        # c4a_act0 / c4a_act1: the same call without the activation / with SiLU (not default workloads: they
+        # measure what the GELU epilogue costs)
+        act = {"c4a": 2, "c4a_act0": 0, "c4a_act1": 1}[name]
         c = configs.c4a()
         x0, r0 = T(c["x"]), T(c["res"])
         g, b = T(c["gamma"]), T(c["beta"])
@@ -567,9 +571,10 @@ def build_workload(name):
         def launch(s):
             abi.check(L.nsr_residual_add_layernorm(s["x"].data_ptr(), 2, s["r"].data_ptr(), 2, s["h"].data_ptr(), 2,
                                                    g.data_ptr(), b.data_ptr(), 0, s["y"].data_ptr(), 2, 24000, 1024,
-                                                   1e-5, 0, 2, stream()))
+                                                   1e-5, 0, act, stream()))
 
-        return Workload(name, "residual add + LayerNorm + GELU(erf) bf16 x,res[32,750,1024] (writes h and y)",
+        return Workload(name, "residual add + LayerNorm + " + ["no activation", "SiLU", "GELU(erf)"][act]
+                        + " bf16 x,res[32,750,1024] (writes h and y)",
                         configs.algorithmic_bytes("c4a"), 4 * x0.numel() * 2, make_set, launch,
                         "nsrk_resln_bf16_nc2", "bf16")
     raise KeyError(name)
