@@ -338,6 +338,19 @@ NSR_DEV float snake_eval(float t, const snake_consts& s) {
   return __builtin_fmaf(p, w, t);
 }
 
+/* ------------------------------------------------------ XCD tile order -- */
+
+/* Workgroups are dealt round-robin to the 8 XCDs (workgroup b runs on XCD
+ * b % 8). xcd_contiguous(b, n) gives workgroup b the tile that makes each
+ * XCD take one contiguous run of the n tiles (XCD x the x-th run), so that
+ * neighbouring tiles, which share cache lines at their edges, meet in one
+ * XCD's L2. A bijection of [0, n) for a grid of n workgroups. */
+NSR_DEV int xcd_contiguous(int b, int n) {
+  const int per = (n + 7) >> 3, x = b & 7, i = b >> 3;
+  const int full = n - 8 * (per - 1); /* XCDs that take `per` tiles */
+  return (x < full ? x * per : full * per + (x - full) * (per - 1)) + i;
+}
+
 /* ------------------------------------------------------- buffer access -- */
 
 /* Raw buffer resource over [base, base + bytes): loads past the end return

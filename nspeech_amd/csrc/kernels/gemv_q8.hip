@@ -42,14 +42,6 @@
 
 enum { GEMV_PLAIN = 0, GEMV_GLU = 1, GEMV_H = 2 };
 
-/* Contiguous runs: workgroup b runs on XCD b % 8; XCD x takes the x-th
- * contiguous run of tiles. A bijection of [0, n) (grid = n). */
-NSR_DEV int xcd_tile(int b, int n) {
-  const int per = (n + 7) >> 3, x = b & 7, i = b >> 3;
-  const int full = n - 8 * (per - 1); /* XCDs that take `per` tiles */
-  return (x < full ? x * per : full * per + (x - full) * (per - 1)) + i;
-}
-
 /* Line groups: workgroup b, the (b / 8)-th on XCD b % 8, takes the next tile
  * of that XCD's groups x, x + 8, x + 16, ...; -1 past the last tile. */
 NSR_DEV int line_group_tile(int b, int n) {
@@ -74,7 +66,7 @@ NSR_DEV void gemv_ref(const nsr_gemv_args& a) {
   __shared__ float red2[256];
   __shared__ float fin[NC];
   const int tid = threadIdx.x;
-  const int t = a.line_groups ? line_group_tile(blockIdx.x, a.n_tiles) : xcd_tile(blockIdx.x, a.n_tiles);
+  const int t = a.line_groups ? line_group_tile(blockIdx.x, a.n_tiles) : xcd_contiguous(blockIdx.x, a.n_tiles);
   if (t < 0) return; /* the whole workgroup: no barrier is reached */
   const int64_t nw4 = a.NW >> 2;
   /* first word (per row) of each 8-column group */
@@ -244,36 +236,38 @@ extern "C" __global__ void __launch_bounds__(256) nsrk_gemv_q8t4_pack(const nsr_
  * an nn::Linear [out, in] weight in the reference's GGUF files) -> the
  * GEMV layouts of W^T: a transpose of the int8 values and of the f16 block
  * scales, no arithmetic. One thread per output word (k fastest, so the
- * reads of a weight row are consecutive), then one per scale quad. */
+ * reads of a weight row are consecutive); the first four threads of each
+ * 32-row block also move that block's four scales (one each), whose bytes
+ * sit in the lines their wave reads anyway (a separate pass over the scales
+ * read every line of the weight a second time). The workgroups of a quad's
+ * rows share lines at their edges and run on one XCD (xcd_contiguous). */
 extern "C" __global__ void __launch_bounds__(256) nsrk_gemv_q8_from_q8_0(const nsr_q8_0_conv_args a) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t i = (int64_t)xcd_contiguous((int)blockIdx.x, (int)gridDim.x) * 256 + threadIdx.x;
   const int64_t K = a.K, nb = K >> 5, quads = (int64_t)a.N >> 2;
   const int64_t nw = quads * K;
   const int64_t rowb = nb * 34; /* bytes per weight row */
-  if (i < nw) {
-    const int64_t q = i / K, k = i - q * K; /* column quad q, row k of W^T */
-    uint32_t w = 0;
+  if (i >= nw) return;
+  const int64_t q = i / K, k = i - q * K; /* column quad q, row k of W^T */
+  const int64_t b = k >> 5;
+  uint32_t w = 0;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int64_t n = a.t4 ? t4_src_col(q, c, a.glu_n) : 4 * q + c;
-      w |= (uint32_t)a.blocks[n * rowb + (k >> 5) * 34 + 2 + (k & 31)] << (8 * c);
-    }
+  for (int c = 0; c < 4; ++c) {
+    const int64_t n = a.t4 ? t4_src_col(q, c, a.glu_n) : 4 * q + c;
+    w |= (uint32_t)a.blocks[n * rowb + b * 34 + 2 + (k & 31)] << (8 * c);
+  }
+  if (a.t4)
+    a.qs[i] = w;
+  else
+    a.qs[k * quads + q] = w;
+  if ((k & 31) < 4) {
+    const int c = (int)(k & 31);
+    const int64_t j = q * nb + b;
+    const int64_t n = a.t4 ? t4_src_col(q, c, a.glu_n) : 4 * q + c;
+    const uint16_t d = *(const uint16_t*)(a.blocks + n * rowb + b * 34);
     if (a.t4)
-      a.qs[i] = w;
+      a.scales[4 * j + c] = d;
     else
-      a.qs[k * quads + q] = w;
-  } else if (i < nw + quads * nb) {
-    const int64_t j = i - nw;
-    const int64_t q = j / nb, b = j - q * nb;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int64_t n = a.t4 ? t4_src_col(q, c, a.glu_n) : 4 * q + c;
-      const uint16_t d = *(const uint16_t*)(a.blocks + n * rowb + b * 34);
-      if (a.t4)
-        a.scales[4 * j + c] = d;
-      else
-        a.scales[b * a.N + n] = d;
-    }
+      a.scales[b * a.N + n] = d;
   }
 }
 

@@ -107,8 +107,11 @@ NSR_DEV void istft_body(const nsr_istft_args& a) {
   const int hop = a.hop, R = N / hop, trim = N / 2;
   const float PI = 3.14159265358979323846f;
 
+  /* groups of 64 frames overlap by R - 1 and do not start on a cache line: neighbouring groups run on one XCD
+   * (xcd_contiguous), so the lines they share come from HBM once */
+  const int grp = xcd_contiguous((int)blockIdx.x, (int)gridDim.x);
   const int step = FG - (R - 1);
-  const int64_t F0 = (int64_t)blockIdx.x * step;
+  const int64_t F0 = (int64_t)grp * step;
   const int nloc = (int)min((int64_t)FG, a.n_frames - F0); /* frames of this group */
 
   /* phase A loads first (one memory latency for all), then the tables */
@@ -174,7 +177,7 @@ NSR_DEV void istft_body(const nsr_istft_args& a) {
    * first and last groups also own the positions the signal's edges leave */
   const int64_t base = F0 * hop;
   const float inv_hop = 1.0f / (float)hop;
-  const int q_lo = blockIdx.x == 0 ? 0 : (R - 1) * hop;
+  const int q_lo = grp == 0 ? 0 : (R - 1) * hop;
   const int q_hi = F0 + FG >= a.n_frames ? (nloc - 1) * hop + N : FG * hop;
   for (int q = q_lo + tid; q < q_hi; q += 256) {
     const int64_t i = base + q - trim; /* output index */

@@ -1282,7 +1282,7 @@ static nsr_status q8_0_convert(const void* blocks, int64_t N, int64_t K, int t4,
   a.K = (int32_t)K;
   a.t4 = t4;
   a.glu_n = glu ? (int32_t)(N / 2) : 0;
-  const int64_t total = (N / 4) * K + (N / 4) * (K / 32);
+  const int64_t total = (N / 4) * K;  // one thread per output word; the first of each block moves its scales
   void* params[] = {&a};
   return launch(K_nsrk_gemv_q8_from_q8_0, cdiv_u(total, 256), 1, 256, 0, stream, params);
 }
