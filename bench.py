@@ -92,6 +92,10 @@ def parse():
     ap.add_argument("--sets-on-held", action="store_true",
                     help="size the buffer-set rotation on the bytes a set holds, not the bytes a call touches "
                          "(for comparison: a partial gather then reuses sets within the Infinity Cache)")
+    ap.add_argument("--fixed-hold", action="store_true",
+                    help="hold the stream 5 ms + 0.1 ms per call before each timed run (the sizing before the hold "
+                         "was fitted to the host's enqueue rate; an idle GPU before a burst slows the first "
+                         "milliseconds of VALU-heavy work)")
     ap.add_argument("--json-out", default="", help="also write every workload's full record to this file")
     return ap.parse_args()
 
@@ -592,7 +596,7 @@ def spin_rate_cycles_per_ms():
     return 2_000_000 / max(s.elapsed_time(e), 1e-3)
 
 
-def time_workload(w, steps, warmup, rotate, cyc_per_ms, touch_pass=True, sets_on_held=False):
+def time_workload(w, steps, warmup, rotate, cyc_per_ms, touch_pass=True, sets_on_held=False, fixed_hold=False):
     """Time one workload. Order of GPU work: one untimed-for-the-headline
     call on every buffer set (the touch pass, so no timed call is the first
     kernel use of its buffers; its average is `first_touch_us_per_call`),
@@ -607,13 +611,13 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms, touch_pass=True, sets_on
     torch.cuda.synchronize()
 
     host = []
+    holds = []
+    rate = {}  # host enqueue ms per call and GPU ms per call, from the touch pass
 
-    def held(enqueue, n, per_call_ms):
-        """Hold the stream with a spin kernel while `enqueue` issues n calls,
-        so the GPU then runs them back to back. Returns True when the host
-        finished enqueueing before the hold expired (else the timing would
-        include host launch gaps and the caller retries with a longer hold)."""
-        hold_ms = 5.0 + per_call_ms * n
+    def held(enqueue, n, hold_ms):
+        """Hold the stream with a spin kernel for hold_ms while `enqueue`
+        issues n calls, so the GPU then runs them back to back. Returns the
+        host's enqueue time in ms."""
         torch.cuda.synchronize()
         torch.cuda._sleep(int(cyc_per_ms * hold_ms))
         h0 = time.perf_counter()
@@ -621,10 +625,23 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms, touch_pass=True, sets_on
         host_ms = (time.perf_counter() - h0) * 1e3
         torch.cuda.synchronize()
         host.append(host_ms * 1e3 / n)
-        return host_ms < 0.8 * hold_ms
+        return host_ms
 
     def run_plain(order):
+        """Time `order` back to back. The hold must let the host stay ahead of
+        the GPU: call i is enqueued at about i * host rate and needed at
+        hold + i * GPU rate, so the run is kept when the host finished within
+        0.8 of (hold + the run's GPU time), else it is repeated with a longer
+        hold. The first hold is fitted to the host rate of the warm-up (or the
+        touch pass) and the GPU rate of the touch pass (0.5 ms + what the host
+        needs beyond the GPU), so the GPU sits idle as
+        briefly as the enqueue allows: an idle GPU before a burst slows the
+        first milliseconds of VALU-heavy work (residual add + LayerNorm + GELU
+        at [24000, 1024] bf16, 200 calls after 1 / 6 / 25 ms of idle: 33.5 /
+        34.3 / 34.7 us per call on MI355X). --fixed-hold (and the touch pass
+        itself) start from 5 ms + 0.1 ms per call."""
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = len(order)
 
         def enqueue():
             t0.record()
@@ -632,15 +649,26 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms, touch_pass=True, sets_on
                 w.launch(sets[i])
             t1.record()
 
-        for per_call in (0.1, 0.4, 1.6):
-            if held(enqueue, len(order), per_call):
+        tries = [5.0 + per_call * n for per_call in (0.1, 0.4, 1.6)]
+        if rate and not fixed_hold:
+            tries.insert(0, 0.5 + max(0.0, 1.25 * rate["host_ms"] * n - 0.8 * rate["gpu_ms"] * n))
+        for hold_ms in tries:
+            host_ms = held(enqueue, n, hold_ms)
+            gpu_ms = t0.elapsed_time(t1)
+            if host_ms < 0.8 * (hold_ms + gpu_ms):
                 break
-        return t0.elapsed_time(t1) * 1e3 / len(order)
+        holds.append(round(hold_ms, 2))
+        return gpu_ms * 1e3 / n
 
     first_us = run_plain(list(range(nsets))) if touch_pass else None
+    if touch_pass:
+        rate.update(host_ms=host[-1] / 1e3, gpu_ms=first_us / 1e3)
     torch.cuda.synchronize()
+    h0 = time.perf_counter()
     for i in range(warmup):
         w.launch(sets[i % nsets])
+    if rate and warmup:  # the touch pass's few calls carry first-call host costs; the warm-up's rate is steadier
+        rate["host_ms"] = min(rate["host_ms"], (time.perf_counter() - h0) * 1e3 / warmup)
     torch.cuda.synchronize()
     rotating = [(warmup + i) % nsets for i in range(steps)]
     cold_us = run_plain(rotating)            # timed region: K back-to-back calls
@@ -664,6 +692,7 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms, touch_pass=True, sets_on
         "warm_GBs": round(gbs(warm_us), 1),
         **({"TFLOPs": round(w.flops / (cold_us * 1e-6) / 1e12, 2)} if w.flops else {}),
         "host_us_per_call": round(min(host), 2),
+        "hold_ms": holds,
     }
 
 
@@ -860,7 +889,8 @@ def main():
     for nm in names:
         w = build_workload(nm)
         results[nm] = time_workload(w, args.steps, args.warmup, not args.no_rotate, cyc,
-                                    touch_pass=not args.no_touch_pass, sets_on_held=args.sets_on_held)
+                                    touch_pass=not args.no_touch_pass, sets_on_held=args.sets_on_held,
+                                    fixed_hold=args.fixed_hold)
         del w
         torch.cuda.empty_cache()
         print(f"[bench] {nm}: {results[nm]['us_per_call']} us/call, {results[nm]['GBs']} GB/s "

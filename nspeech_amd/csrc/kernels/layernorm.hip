@@ -160,9 +160,13 @@ NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
     const bool more = next < a.n_rows;
 
     float v[NC][VEC];
-    float sum = 0.f;
+    float sum = 0.f, sum2 = 0.f;
     /* packed h words, stored once the next row's loads are issued */
     constexpr bool PACKED_H = FUSED && H != DT_F32 && chunk_words<H, VEC>::value == 1;
+    /* bf16 h: sum and sum of squares straight from the packed words with v_dot2c_f32_bf16 (two products,
+     * each exact in f32, added to the f32 accumulator): one instruction per pair for each sum instead of a
+     * widening, an add and a centred fma per element, and the widening moves after the reductions */
+    constexpr bool DOT_STATS = PACKED_H && H == DT_BF16;
     nsr_uint4 hsave[PACKED_H ? NC : 1];
 #pragma unroll
     for (int k = 0; k < NC; ++k) {
@@ -178,15 +182,27 @@ NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
 #pragma unroll
             for (int e = 0; e < VEC; ++e) v[k][e] += r[e];
             hsave[k] = pack16<H>(v[k]);
-            unpack16<H>(hsave[k], v[k]);
+            if constexpr (!DOT_STATS) unpack16<H>(hsave[k], v[k]);
           } else {
 #pragma unroll
             for (int e = 0; e < VEC; ++e) v[k][e] = round_to<H>(v[k][e] + r[e]);
             if (a.h) store_vec<H, VEC>(a.h, xrow + (int64_t)j * VEC, v[k]);
           }
         }
+        if constexpr (DOT_STATS) {
+          const nsr_bf16x2 one = __builtin_bit_cast(nsr_bf16x2, 0x3f803f80u);
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) sum += v[k][e];
+          for (int i = 0; i < 4; ++i) {
+            /* a named copy: a bit_cast of the vector element itself reads element 0 with this compiler */
+            const uint32_t w = hsave[k][i];
+            const nsr_bf16x2 hw = __builtin_bit_cast(nsr_bf16x2, w);
+            sum = __builtin_amdgcn_fdot2_f32_bf16(hw, one, sum, false);
+            sum2 = __builtin_amdgcn_fdot2_f32_bf16(hw, hw, sum2, false);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) sum += v[k][e];
+        }
       }
     }
     if constexpr (PIPE) {
@@ -202,34 +218,65 @@ NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
       }
     }
     const float mean = wave_sum(sum) * a.inv_n;
-
-    /* centred pass; sum(d) corrects the f32 mean (corrected two-pass), which
-     * keeps rows with |mean| >> std accurate. The correction changes the
-     * variance by (mean rounding error)^2 / var, below f32 resolution unless
-     * |mean| / std > 1e4: values held in f16 / bf16 (h, or x for a plain
-     * LayerNorm) cannot have that spread, so those rows skip it. */
-    constexpr bool CORR = H == DT_F32;
-    float sq = 0.f, sd = 0.f;
+    float var, shift; /* v[k][e] * rstd + shift * rstd = (h - mean) * rstd */
+    if constexpr (DOT_STATS) {
+      /* one pass, var = E[h^2] - mean^2: its rounding error relative to var is about (1 + mean^2 / var)
+       * f32 ulps of the sums, so when mean^2 > var (a wave-uniform test) the row takes the centred two-pass
+       * form over the registers instead */
+      var = __builtin_fmaf(-mean, mean, wave_sum(sum2) * a.inv_n);
+      shift = -mean;
 #pragma unroll
-    for (int k = 0; k < NC; ++k) {
-      const int j = lane + 64 * k;
-      if (j < nchunk) {
+      for (int k = 0; k < NC; ++k) {
+        const int j = lane + 64 * k;
+        if (j < nchunk) unpack16<H>(hsave[k], v[k]);
+      }
+      if (mean * mean > var) {
+        float sq = 0.f;
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          v[k][e] -= mean;
-          sq = __builtin_fmaf(v[k][e], v[k][e], sq);
-          if constexpr (CORR) sd += v[k][e];
+        for (int k = 0; k < NC; ++k) {
+          const int j = lane + 64 * k;
+          if (j < nchunk) {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+              v[k][e] -= mean;
+              sq = __builtin_fmaf(v[k][e], v[k][e], sq);
+            }
+          }
+        }
+        var = wave_sum(sq) * a.inv_n;
+        shift = 0.0f;
+      }
+      var = fmaxf(var, 0.0f);
+    } else {
+      /* centred pass; sum(d) corrects the f32 mean (corrected two-pass), which
+       * keeps rows with |mean| >> std accurate. The correction changes the
+       * variance by (mean rounding error)^2 / var, below f32 resolution unless
+       * |mean| / std > 1e4: values held in f16 / bf16 (h, or x for a plain
+       * LayerNorm) cannot have that spread, so those rows skip it. */
+      constexpr bool CORR = H == DT_F32;
+      float sq = 0.f, sd = 0.f;
+#pragma unroll
+      for (int k = 0; k < NC; ++k) {
+        const int j = lane + 64 * k;
+        if (j < nchunk) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            v[k][e] -= mean;
+            sq = __builtin_fmaf(v[k][e], v[k][e], sq);
+            if constexpr (CORR) sd += v[k][e];
+          }
         }
       }
+      sq = wave_sum(sq);
+      if constexpr (CORR) sd = wave_sum(sd);
+      const float c = sd * a.inv_n;
+      var = fmaxf(__builtin_fmaf(-c, sd, sq) * a.inv_n, 0.0f);
+      shift = -c; /* (d - c) * rstd */
     }
-    sq = wave_sum(sq);
-    if constexpr (CORR) sd = wave_sum(sd);
-    const float c = sd * a.inv_n;
-    const float var = fmaxf(__builtin_fmaf(-c, sd, sq) * a.inv_n, 0.0f);
     /* v_rsq_f32 (about 1 ulp) instead of a correctly rounded sqrt and divide, about 30 instructions per
      * row; var + eps > 0 is a normal number unless eps = 0 and the row is constant (then inf either way) */
     const float rstd = __builtin_amdgcn_rsqf(var + a.eps);
-    const float crs = -c * rstd; /* (d - c) * rstd = d * rstd + crs */
+    const float crs = shift * rstd;
 
 #pragma unroll
     for (int k = 0; k < NC; ++k) {
@@ -331,7 +378,7 @@ NSR_DEV void ln_row_generic(const nsr_ln_args& a, int pdt, int act) {
     if (a.unit_offset) g += 1.0f;
     const float b = a.beta ? load_param(a.beta, pdt, c) : 0.0f;
     float o = __builtin_fmaf(d * rstd, g, b);
-    if (act == ACT_GELU) o = act_gelu_erf(o);
+    if (act == ACT_GELU) o = act_gelu_logistic(o); /* finite: a LayerNorm output */
     else if (act == ACT_SILU) o = act_silu(o);
     store_scalar<Y>(a.y, yrow + c, o);
   }

@@ -148,6 +148,55 @@ def test_resadd_variants(dev):
     assert_close(y.float().cpu().numpy(), ref, RTOL_BF16, "ragged bf16")
 
 
+@pytest.mark.parametrize("cols", [1024, 768, 512])
+def test_resadd_bf16_statistics_paths(dev, cols):
+    """bf16 h: the kernel takes one-pass statistics from the packed h words and falls back to the centred
+    two-pass form when mean^2 > var. Rows from mean 0 to |mean| / std = 300 cross that test; every row is
+    held to one bf16 rounding of the float64 LayerNorm + GELU of the same h."""
+    g = configs.rng(cols + 17)
+    ratios = np.array([0.0, 0.01, 0.5, 0.9, 1.0, 1.1, 2.0, 10.0, 30.0, 300.0])
+    rows = 4 * len(ratios)
+    std = np.repeat(np.array([1.0, 0.01, 3.0, 100.0]), len(ratios))
+    mean = np.tile(ratios, 4) * std * np.where(np.arange(rows) % 2, 1.0, -1.0)
+    x = (mean[:, None] + std[:, None] * g.standard_normal((rows, cols))).astype(np.float32)
+    r = (0.25 * std[:, None] * g.standard_normal((rows, cols))).astype(np.float32)
+    w = (1 + 0.1 * g.standard_normal(cols)).astype(np.float32)
+    b = (0.1 * g.standard_normal(cols)).astype(np.float32)
+    xb, rb = torch.from_numpy(x).bfloat16(), torch.from_numpy(r).bfloat16()
+    say("resadd bf16 statistics paths", cols)
+    h, y = abi.residual_add_layernorm(xb.cuda(), rb.cuda(), dev_tensor(w), dev_tensor(b), act="gelu")
+    torch.cuda.synchronize()
+    hr = (xb.float() + rb.float()).bfloat16()
+    assert torch.equal(h.cpu().view(torch.int16), hr.view(torch.int16)), "h = bf16(x + res)"
+    ref = CF.gelu_erf(CF.layernorm(hr.double().numpy(), w, b))
+    yf = y.float().cpu().numpy()
+    assert np.all(np.isfinite(yf))
+    err = np.abs(yf - ref)
+    bound = 2.0 ** -8 * np.abs(ref) * 1.001 + 1e-5
+    assert np.all(err <= bound), f"worst row {int(np.argmax((err - bound).max(axis=1)))}"
+
+
+def test_resadd_bf16_gelu_extreme_inputs(dev):
+    """The LayerNorm epilogue's GELU (logistic form of Phi) on pre-activations of a few 1e6 in magnitude
+    (gamma 1e6, whose squares overflow f32 inside the polynomial), near 0 (gamma 1e-6) and in between: within
+    one bf16 rounding of float64, no NaN."""
+    g = configs.rng(23)
+    rows, cols = 8, 1024
+    x = g.standard_normal((rows, cols)).astype(np.float32)
+    r = g.standard_normal((rows, cols)).astype(np.float32)
+    w = np.tile(np.array([1e6, -1e3, 30.0, 6.0, 1.0, 1e-3, 1e-6, 0.0], dtype=np.float32), cols // 8)
+    b = np.tile(np.array([0.0, 1.0, -5.0, 0.5, -40.0, 0.0, 1e-7, -2.0], dtype=np.float32), cols // 8)
+    xb, rb = torch.from_numpy(x).bfloat16(), torch.from_numpy(r).bfloat16()
+    say("resadd bf16 gelu extreme inputs")
+    _, y = abi.residual_add_layernorm(xb.cuda(), rb.cuda(), dev_tensor(w), dev_tensor(b), act="gelu")
+    torch.cuda.synchronize()
+    hr = (xb.float() + rb.float()).bfloat16()
+    ref = CF.gelu_erf(CF.layernorm(hr.double().numpy(), w, b))
+    yf = y.float().cpu().numpy()
+    assert not np.any(np.isnan(yf))
+    assert np.all(np.abs(yf - ref) <= 2.0 ** -8 * np.abs(ref) * 1.001 + 1e-5)
+
+
 def test_strided_rows(dev):
     g = configs.rng(10)
     rows, cols, ld = 20, 256, 320
