@@ -611,7 +611,7 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms, touch_pass=True, sets_on
     torch.cuda.synchronize()
 
     host = []
-    holds = []
+    holds, attempts = [], []
     rate = {}  # host enqueue ms per call and GPU ms per call, from the touch pass
 
     def held(enqueue, n, hold_ms):
@@ -652,12 +652,13 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms, touch_pass=True, sets_on
         tries = [5.0 + per_call * n for per_call in (0.1, 0.4, 1.6)]
         if rate and not fixed_hold:
             tries.insert(0, 0.5 + max(0.0, 1.25 * rate["host_ms"] * n - 0.8 * rate["gpu_ms"] * n))
-        for hold_ms in tries:
+        for k, hold_ms in enumerate(tries):
             host_ms = held(enqueue, n, hold_ms)
             gpu_ms = t0.elapsed_time(t1)
             if host_ms < 0.8 * (hold_ms + gpu_ms):
                 break
         holds.append(round(hold_ms, 2))
+        attempts.append(k + 1)
         return gpu_ms * 1e3 / n
 
     first_us = run_plain(list(range(nsets))) if touch_pass else None
@@ -693,6 +694,7 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms, touch_pass=True, sets_on
         **({"TFLOPs": round(w.flops / (cold_us * 1e-6) / 1e12, 2)} if w.flops else {}),
         "host_us_per_call": round(min(host), 2),
         "hold_ms": holds,
+        "attempts": attempts,  # runs of the touch pass, the timed calls and the same-set calls (retries first)
     }
 
 
