@@ -634,12 +634,13 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms, touch_pass=True, sets_on
         0.8 of (hold + the run's GPU time), else it is repeated with a longer
         hold. The first hold is fitted to the host rate of the warm-up (or the
         touch pass) and the GPU rate of the touch pass (0.5 ms + what the host
-        needs beyond the GPU), so the GPU sits idle as
-        briefly as the enqueue allows: an idle GPU before a burst slows the
-        first milliseconds of VALU-heavy work (residual add + LayerNorm + GELU
-        at [24000, 1024] bf16, 200 calls after 1 / 6 / 25 ms of idle: 33.5 /
-        34.3 / 34.7 us per call on MI355X). --fixed-hold (and the touch pass
-        itself) start from 5 ms + 0.1 ms per call."""
+        needs beyond the GPU), so the GPU sits idle as briefly as the enqueue
+        allows: an idle GPU slows the VALU-heavy work that follows it, from
+        about the 40th call on and for longer than 200 calls (residual add +
+        LayerNorm + GELU at [24000, 1024] bf16, 200 calls after 1 / 6 / 25 ms
+        of idle: 33.5 / 34.3 / 34.7 us per call on MI355X). The touch pass,
+        which has no rates yet, starts from 1 ms + 0.1 ms per call, and
+        --fixed-hold from the earlier 5 ms + 0.1 ms per call everywhere."""
         t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         n = len(order)
 
@@ -649,7 +650,8 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms, touch_pass=True, sets_on
                 w.launch(sets[i])
             t1.record()
 
-        tries = [5.0 + per_call * n for per_call in (0.1, 0.4, 1.6)]
+        base = 5.0 if fixed_hold else 1.0
+        tries = [base + per_call * n for per_call in (0.1, 0.4, 1.6)]
         if rate and not fixed_hold:
             tries.insert(0, 0.5 + max(0.0, 1.25 * rate["host_ms"] * n - 0.8 * rate["gpu_ms"] * n))
         for k, hold_ms in enumerate(tries):
