@@ -181,6 +181,28 @@ def test_ill_conditioned_rows_and_special_alpha(dev, T):
     assert_close(got, ref, RTOL_F32, "vs f64 (on-chip two-pass and f64 two-read statistics stay within 1e-5 here)")
 
 
+@pytest.mark.parametrize("T", [4800, 60000, 115200])
+def test_rows_across_the_statistics_switch(dev, T):
+    """The aligned row kernels take one-pass statistics and switch to the centred two-pass form when
+    4 mean^2 > var. Rows with |mean| / std from 0 to 3000, on both sides of 1/2, at the 256-lane
+    (T = 4800), 512-lane VGPR-only (60000) and 512-lane VGPR + LDS (115200) kernels: every row within
+    1e-5 of float64."""
+    g = configs.rng(41 + T)
+    ratios = np.array([0.0, 0.1, 0.45, 0.49, 0.51, 0.55, 1.0, 3.0, 30.0, 3000.0])
+    C = len(ratios)
+    std = np.array([1.0, 0.01, 50.0, 1.0, 1.0, 2.0, 1.0, 0.5, 1.0, 1e-3])
+    mean = ratios * std * np.where(np.arange(C) % 2, -1.0, 1.0)
+    x = (mean[:, None] + std[:, None] * g.standard_normal((C, T))).astype(np.float32)[None]
+    gamma = (0.1 * g.standard_normal(C)).astype(np.float32)
+    beta = (0.1 * g.standard_normal(C)).astype(np.float32)
+    alpha = g.uniform(0.5, 1.5, C).astype(np.float32)
+    say("adain+snake rows across the statistics switch", T)
+    got = _adain(x, gamma, beta, alpha)
+    ref = CF.adain_snake(x, gamma, beta, alpha)
+    for c in range(C):
+        assert_close(got[:, c], ref[:, c], RTOL_F32, f"T={T} row {c} |mean|/std={ratios[c]}")
+
+
 def test_misaligned_views(dev):
     g = configs.rng(22)
     x = g.standard_normal(2 * 3 * 500 + 1).astype(np.float32)
