@@ -336,7 +336,7 @@ template <int BLOCK, int NV>
 NSR_DEV void adain_resident_u(const nsr_adain_args& a, int pdt) {
   NSR_NO_CONTRACT
   constexpr int NW = BLOCK / 64;
-  __shared__ float red[3 * NW]; /* [0, NW): the mean's sums, [NW, 3 NW): the centred sums */
+  __shared__ float red[4 * NW]; /* [0, 2 NW): the one-pass sums, [2 NW, 4 NW): the centred sums */
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const int64_t T = a.T;
@@ -376,33 +376,43 @@ NSR_DEV void adain_resident_u(const nsr_adain_args& a, int pdt) {
   row_bc32(row, a.C, bi, ci);
   const adain_raw pr = adain_params_load(a, pdt, bi, ci);
 
-  float sum = xe;
-#pragma unroll
-  for (int k = 0; k < NV; ++k) sum += sum4(v[k]);
-  const float mean = block_sum<NW, false>(sum, red) * a.inv_t;
-
-  float sq = 0.f, sd = 0.f;
+  /* one pass (sum, sum of squares), the centred pass when 4 mean^2 > var, as adain_row */
+  float sum = xe, sq = xe * xe;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
-    const int j = jbase + BLOCK * k;
-    const nsr_float4 d = v[k] - mean;
-    v[k] = j <= jmax ? d : zero4;
+    sum += sum4(v[k]);
     sq = sumsq4(v[k], sq);
-    sd += sum4(v[k]);
   }
-  if (eok) {
-    const float d = xe - mean;
-    sq = __builtin_fmaf(d, d, sq);
-    sd += d;
+  block_sum2<NW, false>(sum, sq, red);
+  const float mean = sum * a.inv_t;
+  float var = __builtin_fmaf(-mean, mean, sq * a.inv_t);
+  float vshift = mean, ebase = 0.f; /* (x - mean - c) A + beta = (v - vshift) A + beta, v = x - ebase */
+  if (4.0f * mean * mean > var) {
+    float s2 = 0.f, sd = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int j = jbase + BLOCK * k;
+      const nsr_float4 d = v[k] - mean;
+      v[k] = j <= jmax ? d : zero4;
+      s2 = sumsq4(v[k], s2);
+      sd += sum4(v[k]);
+    }
+    if (eok) {
+      const float d = xe - mean;
+      s2 = __builtin_fmaf(d, d, s2);
+      sd += d;
+    }
+    block_sum2<NW, false>(s2, sd, red + 2 * NW);
+    vshift = sd * a.inv_t;
+    ebase = mean;
+    var = __builtin_fmaf(-vshift, sd, s2) * a.inv_t;
   }
-  block_sum2<NW, false>(sq, sd, red + NW);
-  const float c = sd * a.inv_t;
-  const float var = fmaxf(__builtin_fmaf(-c, sd, sq) * a.inv_t, 0.0f);
+  var = fmaxf(var, 0.0f);
   const float rstd = __builtin_amdgcn_rsqf(var + a.eps); /* v_rsq_f32, about 1 ulp */
   float gam, bet, alp;
   adain_params_cvt(pr, pdt, gam, bet, alp);
   const float A = (gam + 1.0f) * rstd;
-  const float Bc = __builtin_fmaf(-c, A, bet);
+  const float Bc = __builtin_fmaf(-vshift, A, bet);
   const snake_consts sc = make_snake_consts(alp);
 
 #pragma unroll
@@ -411,7 +421,7 @@ NSR_DEV void adain_resident_u(const nsr_adain_args& a, int pdt) {
     const nsr_float4 o = adain_snake4(v[k], A, Bc, sc);
     if (j <= jmax) stf4(ob + 4 * (int64_t)j, o);
   }
-  if (eok) ob[eidx] = snake_eval(__builtin_fmaf(xe - mean, A, Bc), sc);
+  if (eok) ob[eidx] = snake_eval(__builtin_fmaf(xe - ebase, A, Bc), sc);
 }
 
 #define NSR_ADAIN_RES_U(BLOCK, NV)                                                      \
@@ -580,14 +590,14 @@ NSR_ADAIN_F16(512, 32)
 
 /* f16 rows that start on 16 bytes with T % 8 == 0 (every row then does):
  * one 256-lane workgroup per row, NV chunks of 8 halves per lane loaded with
- * 16-byte buffer loads and unpacked to f32 once, then the same two passes and
+ * 16-byte buffer loads and unpacked to f32 once, then the same statistics and
  * output as the f32 row kernel (only the last chunk of a lane can reach past
  * the row; buffer loads there read 0 and stores are dropped). */
 template <int NV>
 NSR_DEV void adain_row_f16a(const nsr_adain_h_args& a, int pdt) {
   NSR_NO_CONTRACT
   constexpr int BLOCK = 256, NW = BLOCK / 64;
-  __shared__ float red[3 * NW]; /* [0, NW): the mean's sums, [NW, 3 NW): the centred sums */
+  __shared__ float red[4 * NW]; /* [0, 2 NW): the one-pass sums, [2 NW, 4 NW): the centred sums */
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   if (row >= a.n_rows) return;
@@ -605,33 +615,44 @@ NSR_DEV void adain_row_f16a(const nsr_adain_h_args& a, int pdt) {
   const adain_raw pr = adain_params_load(a, pdt, bi, ci);
   const int nvalid = nch > tid ? (nch - tid + BLOCK - 1) / BLOCK : 0;
   float f[NV][8];
-  float s = 0.f;
+  /* one pass (sum, sum of squares), the centred pass when 4 mean^2 > var, as adain_row */
+  float s = 0.f, q = 0.f;
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     unpack16<DT_F16>(raw[k], f[k]);
     const float t = ((f[k][0] + f[k][1]) + (f[k][2] + f[k][3])) + ((f[k][4] + f[k][5]) + (f[k][6] + f[k][7]));
+    float u = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) u = __builtin_fmaf(f[k][e], f[k][e], u);
     s += k < nvalid ? t : 0.f;
+    q += k < nvalid ? u : 0.f;
   }
-  const float mean = block_sum<NW, false>(s, red) * a.inv_t;
-  float s1 = 0.f, s2 = 0.f;
+  block_sum2<NW, false>(s, q, red);
+  const float mean = s * a.inv_t;
+  float var = __builtin_fmaf(-mean, mean, q * a.inv_t);
+  float vshift = mean; /* the chunks hold x (one pass) or x - mean (centred) */
+  if (4.0f * mean * mean > var) {
+    float s1 = 0.f, s2 = 0.f;
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
+    for (int k = 0; k < NV; ++k) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) f[k][e] = k < nvalid ? f[k][e] - mean : 0.f;
+      for (int e = 0; e < 8; ++e) f[k][e] = k < nvalid ? f[k][e] - mean : 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      s1 += f[k][e];
-      s2 = __builtin_fmaf(f[k][e], f[k][e], s2);
+      for (int e = 0; e < 8; ++e) {
+        s1 += f[k][e];
+        s2 = __builtin_fmaf(f[k][e], f[k][e], s2);
+      }
     }
+    block_sum2<NW, false>(s1, s2, red + 2 * NW);
+    vshift = s1 * a.inv_t;
+    var = __builtin_fmaf(-vshift, s1, s2) * a.inv_t;
   }
-  block_sum2<NW, false>(s1, s2, red + NW);
-  const float c = s1 * a.inv_t;
-  const float var = fmaxf(__builtin_fmaf(-c, s1, s2) * a.inv_t, 0.0f);
+  var = fmaxf(var, 0.0f);
   const float rstd = __builtin_amdgcn_rsqf(var + a.eps); /* v_rsq_f32, about 1 ulp */
   float gam, bet, alp;
   adain_params_cvt(pr, pdt, gam, bet, alp);
   const float A = (gam + 1.0f) * rstd;
-  const float Bc = __builtin_fmaf(-c, A, bet);
+  const float Bc = __builtin_fmaf(-vshift, A, bet);
   const snake_consts sc = make_snake_consts(alp);
   const nsr_rsrc orr = make_rsrc(a.out + row * T, rbytes);
 #pragma unroll

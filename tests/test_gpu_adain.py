@@ -181,12 +181,12 @@ def test_ill_conditioned_rows_and_special_alpha(dev, T):
     assert_close(got, ref, RTOL_F32, "vs f64 (on-chip two-pass and f64 two-read statistics stay within 1e-5 here)")
 
 
-@pytest.mark.parametrize("T", [4800, 60000, 115200])
+@pytest.mark.parametrize("T", [4800, 4801, 60000, 60001, 115200])
 def test_rows_across_the_statistics_switch(dev, T):
-    """The aligned row kernels take one-pass statistics and switch to the centred two-pass form when
+    """The row kernels take one-pass statistics and switch to the centred two-pass form when
     4 mean^2 > var. Rows with |mean| / std from 0 to 3000, on both sides of 1/2, at the 256-lane
-    (T = 4800), 512-lane VGPR-only (60000) and 512-lane VGPR + LDS (115200) kernels: every row within
-    1e-5 of float64."""
+    (T = 4800), 512-lane VGPR-only (60000) and 512-lane VGPR + LDS (115200) kernels and the
+    unaligned-row kernels (4801, 60001): every row within 1e-5 of float64."""
     g = configs.rng(41 + T)
     ratios = np.array([0.0, 0.1, 0.45, 0.49, 0.51, 0.55, 1.0, 3.0, 30.0, 3000.0])
     C = len(ratios)

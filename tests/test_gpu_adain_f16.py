@@ -56,6 +56,24 @@ def test_shapes(B, C, T):
     _check(_run(x, gamma, beta, alpha), x, gamma, beta, alpha, f"{B}x{C}x{T}")
 
 
+@pytest.mark.parametrize("T", [4800, 4801])
+def test_rows_across_the_statistics_switch(T):
+    """The aligned f16 kernel (T = 4800) takes one-pass statistics and the centred two-pass form when
+    4 mean^2 > var: rows with |mean| / std from 0 to 300 on both sides of 1/2, within the f16 bar of the
+    oracle and of float64 (the unaligned kernel, T = 4801, takes the same rows)."""
+    g = configs.rng(77 + T)
+    ratios = np.array([0.0, 0.1, 0.45, 0.49, 0.51, 0.55, 1.0, 3.0, 30.0, 300.0])
+    C = len(ratios)
+    std = np.array([1.0, 0.05, 20.0, 1.0, 1.0, 2.0, 1.0, 0.5, 1.0, 0.1])
+    mean = ratios * std * np.where(np.arange(C) % 2, -1.0, 1.0)
+    x = (mean[:, None] + std[:, None] * g.standard_normal((C, T))).astype(np.float16)[None]
+    gamma = (0.1 * g.standard_normal((1, C))).astype(np.float32)
+    beta = (0.1 * g.standard_normal(C)).astype(np.float32)
+    alpha = g.uniform(0.5, 1.5, C).astype(np.float32)
+    say("adain+snake f16 rows across the statistics switch", T)
+    _check(_run(x, gamma, beta, alpha), x, gamma, beta, alpha, f"T={T}")
+
+
 def test_kokoro_known_answer_f16_params():
     """The reference's Kokoro self-test inputs (src/kokoro/gpu_decoder.rs:84-87),
     with x rounded to f16 as the f16 path holds it."""
