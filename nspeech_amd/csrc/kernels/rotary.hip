@@ -23,49 +23,81 @@
  * scalar remainder per workgroup) reached 82% of the copy's rate (table
  * path) against 86% for this flat grid with two 32-bit divisions per lane,
  * so the flat grid is kept.
+ *
+ * At these sizes the time is the chain of memory latencies, so every load
+ * is issued before the first wait: the frequencies (or the table's cos/sin)
+ * and x together, and on the sincos path the frequencies first, so that the
+ * sincos runs while x is in flight. Reading q / k's pointers by the lane's
+ * choice (a.src[which]) compiled to a vector load from the argument block
+ * that the data load waited on; the pointers are taken as uniform copies and
+ * selected per lane instead. With the frequency load behind the data load's
+ * wait, the sincos path took 3.70 us at config 1 against 3.27-3.28 us now.
  */
 #include "device_common.h"
+
+/* a kernel-argument value as a wave-uniform copy (an SGPR) */
+NSR_DEV uint32_t rope_uni32(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+NSR_DEV uint64_t rope_uni64(uint64_t v) {
+  return ((uint64_t)rope_uni32((uint32_t)(v >> 32)) << 32) | rope_uni32((uint32_t)v);
+}
+/* 128-bit streaming access at an integer address, as global memory (a pointer rebuilt from an integer is
+ * generic and would give flat instructions) */
+typedef __attribute__((address_space(1))) nsr_float4 rope_gf4;
+NSR_DEV nsr_float4 rope_ld(uint64_t addr) { return __builtin_nontemporal_load((const rope_gf4*)addr); }
+NSR_DEV void rope_st(uint64_t addr, nsr_float4 v) { __builtin_nontemporal_store(v, (rope_gf4*)addr); }
 
 template <bool TABLE>
 NSR_DEV void rope_body(const nsr_rope_args& a) {
 #pragma clang fp contract(off)
   const uint32_t f = blockIdx.x * 256u + threadIdx.x;
-  const uint32_t nq = (uint32_t)a.n4[0];
-  const int which = f >= nq ? 1 : 0;
-  const uint32_t g = which ? f - nq : f;
-  if (g >= (uint32_t)a.n4[which]) return;
-  const float* src = which ? a.src[1] : a.src[0];
-  float* dst = which ? a.dst[1] : a.dst[0];
+  /* q or k per lane, chosen between uniform copies of the two arguments: indexed by the lane's choice
+   * (a.src[which]) they would be read from the argument block by a vector load that the data load waits on */
+  const uint32_t nq = rope_uni32((uint32_t)a.n4[0]), nk = rope_uni32((uint32_t)a.n4[1]);
+  const bool isk = f >= nq;
+  const uint32_t g = isk ? f - nq : f;
+  if (g >= (isk ? nk : nq)) return;
+  const uint64_t sq = rope_uni64((uint64_t)a.src[0]), sk = rope_uni64((uint64_t)a.src[1]);
+  const uint64_t dq = rope_uni64((uint64_t)a.dst[0]), dk = rope_uni64((uint64_t)a.dst[1]);
+  const uint64_t src = isk ? sk : sq, dst = isk ? dk : dq;
 
   const uint32_t dh4 = (uint32_t)a.dh4;
   const uint32_t row = g / dh4;
   const uint32_t c4 = g - row * dh4;
-  const nsr_float4 x = ldf4(src + (size_t)g * 4);
-  nsr_float4 o = x;
-  if (c4 < (uint32_t)a.rot4) {
-    const uint32_t t = row % (uint32_t)a.T;
-    const int64_t pos = a.pos0 + (int64_t)t;
-    const int i0 = 2 * (int)c4; /* pair index of (x.x, x.y); i0+1 for (x.z, x.w) */
-    float c0, s0, c1, s1;
+  const bool rot = c4 < (uint32_t)a.rot4;
+  /* pair index of (x.x, x.y); i0 + 1 for (x.z, x.w). Pass-through lanes read pair 0's parameters and
+   * discard them, so every load is issued before the first wait (one memory latency, not two) */
+  const int i0 = rot ? 2 * (int)c4 : 0;
+  const uint32_t t = row % (uint32_t)a.T;
+  const int64_t pos = a.pos0 + (int64_t)t;
+  float c0 = 1.f, s0 = 0.f, c1 = 1.f, s1 = 0.f;
+  nsr_float4 x;
+  if (a.rot4 > 0) { /* uniform; with no rotated pairs the table may hold no columns */
     if constexpr (TABLE) {
       const float* tb = a.table + pos * (int64_t)(2 * a.half);
       const float2 cc = *(const float2*)(tb + i0);
       const float2 ss = *(const float2*)(tb + a.half + i0);
+      x = rope_ld(src + (uint64_t)g * 16u);
       c0 = cc.x; c1 = cc.y; s0 = ss.x; s1 = ss.y;
     } else {
+      /* the frequencies are loaded first: the sincos waits only for them, while x is in flight */
+      const float2 fr = *(const float2*)(a.inv_freq + i0);
+      __builtin_amdgcn_sched_barrier(0);
+      x = rope_ld(src + (uint64_t)g * 16u);
+      __builtin_amdgcn_sched_barrier(0);
       const float p = (float)pos;
-      const float ang0 = p * a.inv_freq[i0];
-      const float ang1 = p * a.inv_freq[i0 + 1];
-      sincosf(ang0, &s0, &c0);
-      sincosf(ang1, &s1, &c1);
+      sincosf(p * fr.x, &s0, &c0);
+      sincosf(p * fr.y, &s1, &c1);
     }
-    /* x*cos + rotate_half(x)*sin with the products rounded separately */
-    o.x = x.x * c0 + (-x.y) * s0;
-    o.y = x.y * c0 + x.x * s0;
-    o.z = x.z * c1 + (-x.w) * s1;
-    o.w = x.w * c1 + x.z * s1;
+  } else {
+    x = rope_ld(src + (uint64_t)g * 16u);
   }
-  stf4(dst + (size_t)g * 4, o);
+  /* x*cos + rotate_half(x)*sin with the products rounded separately */
+  nsr_float4 o;
+  o.x = x.x * c0 + (-x.y) * s0;
+  o.y = x.y * c0 + x.x * s0;
+  o.z = x.z * c1 + (-x.w) * s1;
+  o.w = x.w * c1 + x.z * s1;
+  rope_st(dst + (uint64_t)g * 16u, rot ? o : x);
 }
 
 extern "C" __global__ void __launch_bounds__(256) nsrk_rope_table_f32(const nsr_rope_args a) {
