@@ -237,7 +237,7 @@ def build_workload(name):
             abi.check(L.nsr_adain_snake_f32(s["x"].data_ptr(), g.data_ptr(), b.data_ptr(), a.data_ptr(), 0, gs, gs,
                                             s["o"].data_ptr(), B, C, TT, 1e-5, stream()))
 
-        kern = "nsrk_adain_row_b256_v5_l0" if name == "c2" else "nsrk_adain_row_b512_v40_l18"
+        kern = "nsrk_adain_row_b256_v5_l0" if name == "c2" else "nsrk_adain_row_b512_v38_l19"
         return Workload(name, f"AdaIN1d+Snake f32 x[{B},{C},{TT}]", configs.algorithmic_bytes(name),
                         2 * x0.numel() * 4, make_set, launch, kern, "f32")
 

@@ -298,7 +298,7 @@ NSR_ADAIN_ROW(256, 5, 0)
 NSR_ADAIN_ROW(256, 6, 0)
 NSR_ADAIN_ROW(256, 7, 0)
 NSR_ADAIN_ROW(256, 8, 0)
-/* medium rows: 512 threads, VGPR slots only (T <= 90112) */
+/* medium rows: 512 threads, VGPR slots only, 5..20 slots (T <= 40960) */
 NSR_ADAIN_ROW(512, 5, 0)
 NSR_ADAIN_ROW(512, 6, 0)
 NSR_ADAIN_ROW(512, 8, 0)
@@ -306,22 +306,51 @@ NSR_ADAIN_ROW(512, 10, 0)
 NSR_ADAIN_ROW(512, 12, 0)
 NSR_ADAIN_ROW(512, 16, 0)
 NSR_ADAIN_ROW(512, 20, 0)
-NSR_ADAIN_ROW(512, 24, 0)
-NSR_ADAIN_ROW(512, 28, 0)
-NSR_ADAIN_ROW(512, 32, 0)
-NSR_ADAIN_ROW(512, 36, 0)
-NSR_ADAIN_ROW(512, 40, 0)
-NSR_ADAIN_ROW(512, 44, 0)
-/* long rows: 40 VGPR slots + 2..18 LDS slots (T <= 118784; 18 slots = 144 KiB of LDS) */
-NSR_ADAIN_ROW(512, 40, 2)
-NSR_ADAIN_ROW(512, 40, 4)
-NSR_ADAIN_ROW(512, 40, 6)
-NSR_ADAIN_ROW(512, 40, 8)
-NSR_ADAIN_ROW(512, 40, 10)
-NSR_ADAIN_ROW(512, 40, 12)
-NSR_ADAIN_ROW(512, 40, 14)
-NSR_ADAIN_ROW(512, 40, 16)
-NSR_ADAIN_ROW(512, 40, 18)
+/* long rows, 20..58 slots (T <= 118784): 19 LDS slots (152 KiB) and the rest in VGPRs. Measured on MI355X
+ * (1024 rows, us per call, minimum of 20): T = 115200 155.3-155.6 against 157.6-158.7 with 40 VGPR + 18 LDS
+ * slots (one slot past the row); T = 92160 123.0-123.4 against 134.3 (40 + 6); T = 60000 76.5-76.8 against
+ * 87.3 (32 VGPR slots only); T = 40960 53.3 against 58.9 (20 VGPR slots only). Loads that land in LDS
+ * by buffer_load ... lds cost less per slot than loads into VGPRs; below 20 slots the VGPR-only kernels,
+ * which fit several workgroups per CU, are faster (T = 24576: 33.9 against 36.1 us with 1 + 11). */
+NSR_ADAIN_ROW(512, 1, 19)
+NSR_ADAIN_ROW(512, 2, 19)
+NSR_ADAIN_ROW(512, 3, 19)
+NSR_ADAIN_ROW(512, 4, 19)
+NSR_ADAIN_ROW(512, 5, 19)
+NSR_ADAIN_ROW(512, 6, 19)
+NSR_ADAIN_ROW(512, 7, 19)
+NSR_ADAIN_ROW(512, 8, 19)
+NSR_ADAIN_ROW(512, 9, 19)
+NSR_ADAIN_ROW(512, 10, 19)
+NSR_ADAIN_ROW(512, 11, 19)
+NSR_ADAIN_ROW(512, 12, 19)
+NSR_ADAIN_ROW(512, 13, 19)
+NSR_ADAIN_ROW(512, 14, 19)
+NSR_ADAIN_ROW(512, 15, 19)
+NSR_ADAIN_ROW(512, 16, 19)
+NSR_ADAIN_ROW(512, 17, 19)
+NSR_ADAIN_ROW(512, 18, 19)
+NSR_ADAIN_ROW(512, 19, 19)
+NSR_ADAIN_ROW(512, 20, 19)
+NSR_ADAIN_ROW(512, 21, 19)
+NSR_ADAIN_ROW(512, 22, 19)
+NSR_ADAIN_ROW(512, 23, 19)
+NSR_ADAIN_ROW(512, 24, 19)
+NSR_ADAIN_ROW(512, 25, 19)
+NSR_ADAIN_ROW(512, 26, 19)
+NSR_ADAIN_ROW(512, 27, 19)
+NSR_ADAIN_ROW(512, 28, 19)
+NSR_ADAIN_ROW(512, 29, 19)
+NSR_ADAIN_ROW(512, 30, 19)
+NSR_ADAIN_ROW(512, 31, 19)
+NSR_ADAIN_ROW(512, 32, 19)
+NSR_ADAIN_ROW(512, 33, 19)
+NSR_ADAIN_ROW(512, 34, 19)
+NSR_ADAIN_ROW(512, 35, 19)
+NSR_ADAIN_ROW(512, 36, 19)
+NSR_ADAIN_ROW(512, 37, 19)
+NSR_ADAIN_ROW(512, 38, 19)
+NSR_ADAIN_ROW(512, 39, 19)
 
 /* ------------------------------------------------ unaligned resident rows -- */
 

@@ -717,31 +717,39 @@ nsr_status nsr_adain_snake_f32(const float* x, const void* gamma, const void* be
       block = 256;
       nv = (int)((nch + 255) / 256);
       kid = ids[nv - 1];
-    } else if (nch <= 512 * 44) {
-      static const int opts[] = {5, 6, 8, 10, 12, 16, 20, 24, 28, 32, 36, 40, 44};
+    } else if (nch <= 512 * 19) {
+      static const int opts[] = {5, 6, 8, 10, 12, 16, 20};
       static const KId ids[] = {K_nsrk_adain_row_b512_v5_l0,  K_nsrk_adain_row_b512_v6_l0,  K_nsrk_adain_row_b512_v8_l0,
                                 K_nsrk_adain_row_b512_v10_l0, K_nsrk_adain_row_b512_v12_l0, K_nsrk_adain_row_b512_v16_l0,
-                                K_nsrk_adain_row_b512_v20_l0, K_nsrk_adain_row_b512_v24_l0, K_nsrk_adain_row_b512_v28_l0,
-                                K_nsrk_adain_row_b512_v32_l0, K_nsrk_adain_row_b512_v36_l0, K_nsrk_adain_row_b512_v40_l0,
-                                K_nsrk_adain_row_b512_v44_l0};
+                                K_nsrk_adain_row_b512_v20_l0};
       block = 512;
-      for (int i = 0; i < 13 && !nv; ++i)
+      for (int i = 0; i < 7 && !nv; ++i)
         if (512LL * opts[i] >= nch) {
           nv = opts[i];
           kid = ids[i];
         }
-    } else if (nch <= 512 * (40 + 18)) {
-      static const KId ids[] = {K_nsrk_adain_row_b512_v40_l2,  K_nsrk_adain_row_b512_v40_l4,
-                                K_nsrk_adain_row_b512_v40_l6,  K_nsrk_adain_row_b512_v40_l8,
-                                K_nsrk_adain_row_b512_v40_l10, K_nsrk_adain_row_b512_v40_l12,
-                                K_nsrk_adain_row_b512_v40_l14, K_nsrk_adain_row_b512_v40_l16,
-                                K_nsrk_adain_row_b512_v40_l18};
+    } else if (nch <= 512 * (39 + 19)) {
+      // 20..58 slots: 19 in LDS, the rest in VGPRs, exactly as many as the row needs (an LDS slot costs less
+      // than a VGPR slot, and a slot past the row end still costs its loads, stores and sums)
+      static const KId ids[] = {
+        K_nsrk_adain_row_b512_v1_l19, K_nsrk_adain_row_b512_v2_l19, K_nsrk_adain_row_b512_v3_l19,
+        K_nsrk_adain_row_b512_v4_l19, K_nsrk_adain_row_b512_v5_l19, K_nsrk_adain_row_b512_v6_l19,
+        K_nsrk_adain_row_b512_v7_l19, K_nsrk_adain_row_b512_v8_l19, K_nsrk_adain_row_b512_v9_l19,
+        K_nsrk_adain_row_b512_v10_l19, K_nsrk_adain_row_b512_v11_l19, K_nsrk_adain_row_b512_v12_l19,
+        K_nsrk_adain_row_b512_v13_l19, K_nsrk_adain_row_b512_v14_l19, K_nsrk_adain_row_b512_v15_l19,
+        K_nsrk_adain_row_b512_v16_l19, K_nsrk_adain_row_b512_v17_l19, K_nsrk_adain_row_b512_v18_l19,
+        K_nsrk_adain_row_b512_v19_l19, K_nsrk_adain_row_b512_v20_l19, K_nsrk_adain_row_b512_v21_l19,
+        K_nsrk_adain_row_b512_v22_l19, K_nsrk_adain_row_b512_v23_l19, K_nsrk_adain_row_b512_v24_l19,
+        K_nsrk_adain_row_b512_v25_l19, K_nsrk_adain_row_b512_v26_l19, K_nsrk_adain_row_b512_v27_l19,
+        K_nsrk_adain_row_b512_v28_l19, K_nsrk_adain_row_b512_v29_l19, K_nsrk_adain_row_b512_v30_l19,
+        K_nsrk_adain_row_b512_v31_l19, K_nsrk_adain_row_b512_v32_l19, K_nsrk_adain_row_b512_v33_l19,
+        K_nsrk_adain_row_b512_v34_l19, K_nsrk_adain_row_b512_v35_l19, K_nsrk_adain_row_b512_v36_l19,
+        K_nsrk_adain_row_b512_v37_l19, K_nsrk_adain_row_b512_v38_l19, K_nsrk_adain_row_b512_v39_l19};
       block = 512;
-      nv = 40;
-      const int64_t m = (nch - 512 * 40 + 511) / 512;
-      nl = (int)((m + 1) / 2 * 2);  // built for even NL 2..18
+      nl = 19;
+      nv = (int)((nch + 511) / 512) - nl;
       lds = (unsigned)(nl * 512 * 16);
-      kid = ids[nl / 2 - 1];
+      kid = ids[nv - 1];
       if (lds + 1024 > (unsigned)dm->max_lds) block = 0;
     }
     const int ns = nv + nl;

@@ -109,18 +109,20 @@ def test_nonstationary_rows(dev, T):
 def _bucket_lengths():
     """Row lengths at both edges of every kernel variant the runtime selects:
     aligned rows (T % 4 == 0) in 16-byte chunks: 256 threads x 1..8 slots,
-    512 threads x {5..44} VGPR slots, 512 x (40 VGPR + 2..18 LDS slots), then
-    the long-row kernel; unaligned rows (T % 4 != 0) by interior-chunk count."""
+    512 threads x {5..20} VGPR slots (rows of up to 19 slots), 512 x (1..39
+    VGPR + 19 LDS slots) for rows of 20..58 slots, one kernel per slot count,
+    then the long-row kernel; unaligned rows (T % 4 != 0) by interior-chunk count."""
     Ts = set()
     for nv in range(1, 9):                                       # b256 row kernels
         Ts |= {4 * 256 * nv, 4 * (256 * (nv - 1) + 1)}
     prev = 2048
-    for nv in (5, 6, 8, 10, 12, 16, 20, 24, 28, 32, 36, 40, 44):  # b512 VGPR-only
-        Ts |= {4 * 512 * nv, 4 * (prev + 1)}
-        prev = 512 * nv
-    for nl in range(2, 19, 2):                                    # b512 + LDS slots
-        Ts |= {4 * 512 * (40 + nl), 4 * (512 * (40 + nl - 2) + 1)}
-    Ts |= {4 * (512 * 44 + 1), 4 * (512 * 58 + 1), 150000}        # first LDS bucket; long-row kernel
+    for nv in (5, 6, 8, 10, 12, 16, 20):                          # b512 VGPR-only
+        top = 512 * min(nv, 19)
+        Ts |= {4 * top, 4 * (prev + 1)}
+        prev = top
+    for ns in range(20, 59):                                      # b512, 19 LDS slots + ns - 19 VGPR slots
+        Ts |= {4 * 512 * ns, 4 * (512 * (ns - 1) + 1)}
+    Ts |= {4 * (512 * 58 + 1), 150000}                            # long-row kernel
     for need in (1, 256, 257, 1536, 1537, 2048, 2049, 6144, 8192, 8193, 12288, 16384, 16385):  # unaligned
         Ts.add(4 * need + 5)
     return sorted(Ts)
