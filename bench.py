@@ -884,6 +884,11 @@ def main():
 
     abi.init()
     names = [n for n in args.workloads.split(",") if n]
+    # every workload's inputs are built before any is timed: the host takes up to seconds to generate the
+    # larger ones, and an idle GPU slows the VALU-heavy work that follows it for longer than 200 calls
+    # (the same idle-time effect the fitted hold avoids)
+    built = {nm: build_workload(nm) for nm in names}
+    print(f"[bench] built {len(built)} workloads", file=sys.stderr, flush=True)
     cyc = spin_rate_cycles_per_ms()
     # the spin kernel counts shader-clock cycles: its rate per ms is the clock of an idle-ish SIMD, taken before
     # the workloads, after the MFMA conv workloads and at the end
@@ -891,7 +896,7 @@ def main():
     mfma = [n for n in names if n.startswith(("kconv", "kchain"))]
     results = {}
     for nm in names:
-        w = build_workload(nm)
+        w = built.pop(nm)
         results[nm] = time_workload(w, args.steps, args.warmup, not args.no_rotate, cyc,
                                     touch_pass=not args.no_touch_pass, sets_on_held=args.sets_on_held,
                                     fixed_hold=args.fixed_hold)
