@@ -97,6 +97,8 @@ def parse():
                          "was fitted to the host's enqueue rate; an idle GPU before a burst slows the first "
                          "milliseconds of VALU-heavy work)")
     ap.add_argument("--json-out", default="", help="also write every workload's full record to this file")
+    ap.add_argument("--timeline", action="store_true",
+                    help="instead of the benchmark: the c4b call's timeline per workgroup and wave (one JSON line)")
     return ap.parse_args()
 
 
@@ -700,6 +702,60 @@ def time_workload(w, steps, warmup, rotate, cyc_per_ms, touch_pass=True, sets_on
     }
 
 
+# ------------------------------------------------------------ timeline ---
+
+def timeline_c4b(launches=20, reps=5):
+    """--timeline: where a c4b call spends its time, per workgroup and wave.
+
+    nsr_calib_adain_timeline is the c4b row kernel with s_memrealtime stamps (100 MHz) written from lane 0 of
+    every wave: each workgroup's XCD and start, each wave's end and, per row, when the row's data had landed
+    for the wave. Per rep, `launches` calls run back to back and the last one's stamps are read. Prints one
+    JSON line (stdout): the workgroups' end times (from the first start) by XCD and over all, and within a
+    workgroup how far apart its waves' row data landed. The output is checked against nsr_adain_snake_f32's."""
+    import numpy as np
+    import torch
+
+    from nspeech_amd import abi, configs
+
+    L = abi.lib()
+    dev = "cuda:0"
+    stream = torch.cuda.current_stream().cuda_stream
+    c = configs.c4b()
+    x, g, b, a = (torch.from_numpy(c[k]).to(dev) for k in ("x", "gamma", "beta", "alpha"))
+    B, C, T = c["x"].shape
+    out, ref = torch.empty_like(x), torch.empty_like(x)
+    abi.check(L.nsr_adain_snake_f32(x.data_ptr(), g.data_ptr(), b.data_ptr(), a.data_ptr(), 0, C, C, ref.data_ptr(),
+                                    B, C, T, 1e-5, stream))
+    words = 80  # NSR_ADAIN_TL_WORDS
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    stamps = torch.zeros(4 * n_cu * words, dtype=torch.int64, device=dev)
+    recs = []
+    for _ in range(reps):
+        stamps.zero_()
+        torch.cuda.synchronize()
+        for _ in range(launches):
+            abi.check(L.nsr_calib_adain_timeline(x.data_ptr(), g.data_ptr(), b.data_ptr(), a.data_ptr(),
+                                                 out.data_ptr(), B, C, T, stamps.data_ptr(), stamps.numel(),
+                                                 stream))
+        torch.cuda.synchronize()
+        s = stamps.view(-1, words).cpu().numpy().astype(np.int64)
+        s = s[s[:, 1] > 0]
+        t0 = s[:, 1].min()
+        end = (s[:, 2:10].max(axis=1) - t0) / 100.0
+        xcc = s[:, 0]
+        rows = -(-B * C // len(s))
+        land = s[:, 10:10 + 8 * min(rows, 8)].reshape(len(s), -1, 8) / 100.0
+        recs.append({"span_us": round(float(end.max()), 2),
+                     "end_p10_median_max_us": [round(float(v), 2) for v in np.percentile(end, [10, 50, 100])],
+                     "end_median_by_xcd_us": {int(k): round(float(np.median(end[xcc == k])), 2)
+                                              for k in sorted(set(xcc.tolist()))},
+                     "wave_landing_spread_median_us": round(float(np.median(land.max(2) - land.min(2))), 2)})
+    line = {"timeline": "c4b AdaIN1d+Snake f32 x[8,128,115200], nsrk_adain_row_tl_b512_v38_l19",
+            "workgroups": int(len(s)), "rows_per_workgroup": int(rows), "launches_per_rep": launches,
+            "output_equals_adain_snake_f32": bool(torch.equal(out, ref)), "reps": recs}
+    print(json.dumps(line), flush=True)
+
+
 # -------------------------------------------------------- CPU baseline ---
 
 def host_cpu():
@@ -883,6 +939,9 @@ def main():
     from nspeech_amd import abi
 
     abi.init()
+    if args.timeline:
+        timeline_c4b()
+        return
     names = [n for n in args.workloads.split(",") if n]
     # every workload's inputs are built before any is timed: the host takes up to seconds to generate the
     # larger ones, and an idle GPU slows the VALU-heavy work that follows it for longer than 200 calls

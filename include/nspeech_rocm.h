@@ -603,6 +603,17 @@ nsr_status nsr_calib_copy(const void* src, void* dst, int64_t bytes, int form, i
  * 16, 16-byte aligned) row by row, the AdaIN row kernel's access structure:
  * one 512-lane workgroup per row, a persistent grid of one per CU. */
 nsr_status nsr_calib_copy_rows(const void* src, void* dst, int64_t n_rows, int64_t row_bytes, nsr_stream_t stream);
+/* nsr_calib_adain_timeline: nsr_adain_snake_f32 on the row kernel of the
+ * [8, 128, 115200] benchmark shape (rows of 114692..116736 floats, f32
+ * gamma / beta [B, C], alpha [C], eps 1e-5), with the same output, writing
+ * a timeline of the call: 80 uint64 words per workgroup into `stamps`
+ * (device memory, at least 80 x #workgroups words; #workgroups = min(B * C,
+ * #CU) for this kernel). Per workgroup: [0] its XCD, [1] its start, [2 + w]
+ * the end of wave w's last store, [10 + 8 r + w] when row r's data had
+ * landed for wave w (r < 8); times in ticks of the GPU's 100 MHz clock. */
+nsr_status nsr_calib_adain_timeline(const float* x, const float* gamma, const float* beta, const float* alpha,
+                                    float* out, int64_t B, int64_t C, int64_t T, uint64_t* stamps,
+                                    int64_t stamps_words, nsr_stream_t stream);
 
 #ifdef __cplusplus
 }

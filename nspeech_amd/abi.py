@@ -103,6 +103,7 @@ def lib() -> C.CDLL:
         L.nsr_calib_empty.argtypes = [_P]
         L.nsr_calib_copy.argtypes = [_P, _P, _I64, C.c_int, C.c_int, _P]
         L.nsr_calib_copy_rows.argtypes = [_P, _P, _I64, _I64, _P]
+        L.nsr_calib_adain_timeline.argtypes = [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _P]
         for name in ("nsr_init", "nsr_layernorm", "nsr_residual_add_layernorm", "nsr_rope_table_f32",
                      "nsr_rope_qk_cache_append", "nsr_kv_cache_append",
                      "nsr_rotary_partial_interleaved_f32", "nsr_adain_snake_f32", "nsr_adain_snake_f16",
@@ -114,7 +115,8 @@ def lib() -> C.CDLL:
                      "nsr_scale_f32", "nsr_leaky_relu_f32", "nsr_resblock_average_f32", "nsr_istft_f32", "nsr_snake",
                      "nsr_adain_snake_conv1d_chain_f32", "nsr_conv1d_f16w_packed_stats",
                      "nsr_gemv_q8_t4_bias_glu", "nsr_gemv_q8_t4_resadd_ln", "nsr_calib_empty", "nsr_calib_copy",
-                     "nsr_attention_splitkv_f16_noalloc", "nsr_conv1d_workspace_bytes", "nsr_calib_copy_rows"):
+                     "nsr_attention_splitkv_f16_noalloc", "nsr_conv1d_workspace_bytes", "nsr_calib_copy_rows",
+                     "nsr_calib_adain_timeline"):
             getattr(L, name).restype = C.c_int
         _lib = L
     return _lib

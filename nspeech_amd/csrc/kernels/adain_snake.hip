@@ -109,7 +109,7 @@ NSR_DEV float sum4(nsr_float4 d) { return (d.x + d.y) + (d.z + d.w); }
  * slot's output is stored (stores and refills in batches of 8 slots), so on a
  * CU the reads of the next row overlap the writes of the current one, and HBM traffic stays the algorithmic
  * 8 bytes per element (x read once, out written once). */
-template <int BLOCK, int NV, int NL>
+template <int BLOCK, int NV, int NL, bool TL = false>
 NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
   NSR_NO_CONTRACT
   constexpr int NW = BLOCK / 64;
@@ -126,6 +126,18 @@ NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
   const int tid = threadIdx.x;
   int64_t row = blockIdx.x;
   if (row >= a.n_rows) return;
+  /* TL: the timeline copy writes s_memrealtime stamps (NSR_ADAIN_TL_WORDS per workgroup, from lane 0 of each
+   * wave with vector stores); otherwise it is the same kernel */
+  uint64_t* const tl = TL ? a.stamps + (size_t)blockIdx.x * NSR_ADAIN_TL_WORDS : nullptr;
+  int tl_row = 0;
+  if constexpr (TL) {
+    if (tid == 0) {
+      uint32_t xcc;
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+      tl[0] = xcc;
+      tl[1] = __builtin_amdgcn_s_memrealtime();
+    }
+  }
   const int64_t T = a.T;
   const int nch = (int)(T >> 2);
   const uint32_t rbytes = (uint32_t)(T * 4);
@@ -160,6 +172,10 @@ NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
     const int64_t next = row + gridDim.x;
     const bool more = next < a.n_rows;
     NSR_WAIT_VMCNT(0); /* every slot of this row has landed (VGPRs and LDS) */
+    if constexpr (TL) {
+      if ((tid & 63) == 0 && tl_row < 8) tl[10 + 8 * tl_row + (tid >> 6)] = __builtin_amdgcn_s_memrealtime();
+      ++tl_row;
+    }
 
     /* one pass: sum and sum of squares */
     float s = 0.f, q = 0.f;
@@ -281,6 +297,10 @@ NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
     if (!more) break;
     row = next;
   }
+  if constexpr (TL) {
+    NSR_WAIT_VMCNT(0); /* this wave's last stores have completed */
+    if ((tid & 63) == 0) tl[2 + (tid >> 6)] = __builtin_amdgcn_s_memrealtime();
+  }
 }
 
 #define NSR_ADAIN_ROW(BLOCK, NV, NL)                                                        \
@@ -351,6 +371,13 @@ NSR_ADAIN_ROW(512, 36, 19)
 NSR_ADAIN_ROW(512, 37, 19)
 NSR_ADAIN_ROW(512, 38, 19)
 NSR_ADAIN_ROW(512, 39, 19)
+
+/* The c4b row kernel (T of 56-57 slots) with the timeline stamps, for the measurement entry point
+ * nsr_calib_adain_timeline: where in a call each workgroup and wave spends its time. */
+extern "C" __global__ void __launch_bounds__(512)
+    nsrk_adain_row_tl_b512_v38_l19(const nsr_adain_args a, const int pdt) {
+  adain_row<512, 38, 19, true>(a, pdt);
+}
 
 /* ------------------------------------------------ unaligned resident rows -- */
 

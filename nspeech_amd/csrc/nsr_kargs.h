@@ -90,7 +90,13 @@ typedef struct nsr_adain_args {
   int32_t lds_chunks;      /* float4 chunks per thread kept in LDS */
   float eps;
   float inv_t;             /* 1 / T */
+  uint64_t* stamps;        /* [grid][NSR_ADAIN_TL_WORDS] timeline (nsrk_adain_row_tl_* only) */
 } nsr_adain_args;
+
+/* Timeline words per workgroup of nsrk_adain_row_tl_*: [0] XCD (HW_REG_XCC_ID), [1] start,
+ * [2 + w] end of wave w's last store (w < 8), [10 + 8 r + w] when row r's data had landed for wave w
+ * (r < 8). Times are s_memrealtime ticks (100 MHz). */
+#define NSR_ADAIN_TL_WORDS 80
 
 typedef struct nsr_adain_h_args {
   const uint16_t* x;       /* [B, C, T] f16 */

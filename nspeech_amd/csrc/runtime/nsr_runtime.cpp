@@ -1827,4 +1827,46 @@ nsr_status nsr_calib_copy_rows(const void* src, void* dst, int64_t n_rows, int64
   return launch(K_nsrk_calib_copy_rows, (unsigned)std::min<int64_t>(n_rows, dm->n_cu), 1, 512, 0, stream, params);
 }
 
+nsr_status nsr_calib_adain_timeline(const float* x, const float* gamma, const float* beta, const float* alpha,
+                                    float* out, int64_t B, int64_t C, int64_t T, uint64_t* stamps,
+                                    int64_t stamps_words, nsr_stream_t stream) {
+  if (!x || !gamma || !beta || !alpha || !out || !stamps)
+    return fail(NSR_ERR_BAD_ARG, "calib_adain_timeline: null pointer");
+  // the c4b row kernel's bucket only: 57 slots of 512 lanes x 16 bytes (19 in LDS, 38 in VGPRs)
+  if (B <= 0 || C <= 0 || B * C > 0x7fffffffLL || T % 4 != 0 || T / 4 <= 512 * 56 || T / 4 > 512 * 57 ||
+      !aligned(x, 16) || !aligned(out, 16))
+    return fail(NSR_ERR_BAD_ARG,
+                "calib_adain_timeline: rows of 114692..116736 floats (T %% 4 == 0), 16-byte aligned, B, C > 0");
+  DeviceModule* dm = nullptr;
+  nsr_status st = current_module(&dm);
+  if (st != NSR_OK) return st;
+  const unsigned lds = 19u * 512u * 16u;
+  if (lds + 1024 > (unsigned)dm->max_lds) return fail(NSR_ERR_UNSUPPORTED, "calib_adain_timeline: LDS too small");
+  const KId kid = K_nsrk_adain_row_tl_b512_v38_l19;
+  const int64_t n_rows = B * C;
+  const unsigned grid = (unsigned)std::min<int64_t>(n_rows, (int64_t)occupancy(dm, kid, 512, lds) * dm->n_cu);
+  if (stamps_words < (int64_t)grid * NSR_ADAIN_TL_WORDS)
+    return fail(NSR_ERR_BAD_ARG, "calib_adain_timeline: stamps need %lld words (%u workgroups x %d)",
+                (long long)grid * NSR_ADAIN_TL_WORDS, grid, NSR_ADAIN_TL_WORDS);
+  nsr_adain_args a;
+  std::memset(&a, 0, sizeof(a));
+  a.x = x;
+  a.gamma = gamma;
+  a.beta = beta;
+  a.alpha = alpha;
+  a.out = out;
+  a.n_rows = n_rows;
+  a.T = T;
+  a.gamma_bstride = C;
+  a.beta_bstride = C;
+  a.C = (int32_t)C;
+  a.lds_chunks = 19;
+  a.eps = 1e-5f;
+  a.inv_t = 1.0f / (float)T;
+  a.stamps = stamps;
+  int pdt = 0;
+  void* params[] = {&a, &pdt};
+  return launch(kid, grid, 1, 512, lds, stream, params);
+}
+
 }  // extern "C"
