@@ -157,16 +157,28 @@ NSR_DEV void attn_walk(const nsr_attn_args& a, int qh, int first, int end, int s
     pl[lane] = p;
     wave_lds_sync();
     float part[4] = {0.f, 0.f, 0.f, 0.f};
+    auto pv_step = [&](int j) {
+      const uint2 vv = vl[j * (hd4 + 1) + dq];
+      const float pj = pl[j];
+      const nsr_h2 v01 = __builtin_bit_cast(nsr_h2, vv.x), v23 = __builtin_bit_cast(nsr_h2, vv.y);
+      part[0] = __builtin_fmaf(pj, (float)v01.x, part[0]);
+      part[1] = __builtin_fmaf(pj, (float)v01.y, part[1]);
+      part[2] = __builtin_fmaf(pj, (float)v23.x, part[2]);
+      part[3] = __builtin_fmaf(pj, (float)v23.y, part[3]);
+    };
     if (pv_lane) {
+      if constexpr (HD4T != 0) {
+        /* every row of the chunk, all reads in flight at once: rows past n hold row n - 1's values (the
+         * staging clamps) and probability 0 */
+        constexpr int NG = 64 / HD4T; /* ng at compile time */
+#pragma unroll
+        for (int jj = 0; jj < (64 + NG - 1) / NG; ++jj) {
+          const int j = pg + jj * NG;
+          if (jj * NG + NG <= 64 || j < 64) pv_step(j);
+        }
+      } else {
 #pragma unroll 4
-      for (int j = pg; j < n; j += ng) {
-        const uint2 vv = vl[j * (hd4 + 1) + dq];
-        const float pj = pl[j];
-        const nsr_h2 v01 = __builtin_bit_cast(nsr_h2, vv.x), v23 = __builtin_bit_cast(nsr_h2, vv.y);
-        part[0] = __builtin_fmaf(pj, (float)v01.x, part[0]);
-        part[1] = __builtin_fmaf(pj, (float)v01.y, part[1]);
-        part[2] = __builtin_fmaf(pj, (float)v23.x, part[2]);
-        part[3] = __builtin_fmaf(pj, (float)v23.y, part[3]);
+        for (int j = pg; j < n; j += ng) pv_step(j);
       }
     }
 #pragma unroll
@@ -230,22 +242,39 @@ NSR_DEV void attn_head(const nsr_attn_args& a) {
   }
   __syncthreads();
   if (w == 0) {
-    float m = -INFINITY;
-    for (int i = 0; i < W; ++i) m = fmaxf(m, ms[i]);
-    float l = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int i = 0; i < W; ++i) {
-      const float wt = __expf(ms[i] - m); /* 0 for a wave that had no chunk (m = -inf) */
-      l = __builtin_fmaf(ls[i], wt, l);
-      if (lane < hd4) {
-        const float* ai = (const float*)(att_lds + i * attn_wave_lds_words(hd4));
+    /* lane i < W holds wave i's m and l; every wave's acc row is read at once (rows past W read wave W - 1's
+     * with weight 0), then added in wave order: one round of LDS reads instead of a dependent one per wave */
+    const float mi = lane < W ? ms[lane] : -INFINITY;
+    const float m = wave_max(mi);
+    const float wi = lane < W ? __expf(mi - m) : 0.f; /* 0 for a wave that had no chunk (m = -inf) */
+    const float li = lane < W ? ls[lane] : 0.f;
+    float rows[8][4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(ai[4 * lane + e], wt, acc[e]);
-      }
+    for (int i = 0; i < 8; ++i) {
+      const float* ai = (const float*)(att_lds + min(i, W - 1) * attn_wave_lds_words(hd4));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rows[i][e] = lane < hd4 ? ai[4 * lane + e] : 0.f;
+    }
+    float l = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float wt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wi), i));
+      l = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(li), i)), wt, l);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(rows[i][e], wt, acc[e]);
     }
     if (lane < hd4) {
       uint16_t* o = a.out + (int64_t)qh * hd + 4 * lane;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = (uint16_t)f32_to_f16_bits(acc[e] / l);
+      const uint32_t w0 = f32_to_f16_bits(acc[0] / l) | (f32_to_f16_bits(acc[1] / l) << 16);
+      const uint32_t w1 = f32_to_f16_bits(acc[2] / l) | (f32_to_f16_bits(acc[3] / l) << 16);
+      if (((uintptr_t)a.out & 7u) == 0) {
+        *(uint2*)o = make_uint2(w0, w1);
+      } else {
+        o[0] = (uint16_t)w0;
+        o[1] = (uint16_t)(w0 >> 16);
+        o[2] = (uint16_t)w1;
+        o[3] = (uint16_t)(w1 >> 16);
+      }
     }
   }
 }
@@ -264,15 +293,39 @@ NSR_ATTN(13)
 NSR_ATTN(16)
 NSR_ATTN(32)
 
-/* One workgroup per query head, one lane per dimension (hd <= 128). The
- * splits are read 16 at a time with all 16 loads in flight (indices clamped,
- * the extras weighted 0): a loop of dependent loads would pay one memory
- * latency per split. */
+/* One workgroup per query head, one lane per dimension (hd <= 128). Up to 32
+ * splits are read in one round, more 16 at a time, with all of a round's
+ * loads in flight (indices clamped, the extras weighted 0): a loop of
+ * dependent loads would pay one memory latency per split. */
 extern "C" __global__ void __launch_bounds__(128) nsrk_attn_reduce(const nsr_attn_args a) {
   const int qh = blockIdx.x, d = threadIdx.x;
   const int hd = a.head_dim, ns = a.n_splits, st = hd + 2;
   const int dc = min(d, hd - 1);
   const float* pb = a.partial + (int64_t)qh * ns * st;
+  if (ns <= 32) {
+    /* up to 32 splits (the decoder's cross-attention takes 32): lane u loads split u's m and l, every lane the
+     * 32 acc values of its dimension, all in flight at once (one memory latency for the whole merge); the max,
+     * the weights and the sums in split order are those of the loop below */
+    const int lane = threadIdx.x & 63;
+    const float* pu = pb + (int64_t)min(lane, ns - 1) * st;
+    const float mu = lane < ns ? pu[0] : -INFINITY;
+    const float lu = lane < ns ? pu[1] : 0.f;
+    float av[32];
+#pragma unroll
+    for (int u = 0; u < 32; ++u) av[u] = pb[(int64_t)min(u, ns - 1) * st + 2 + dc];
+    __builtin_amdgcn_sched_barrier(0); /* every load issued before the max waits for m */
+    const float m = wave_max(mu);
+    const float wu = lane < ns ? __expf(mu - m) : 0.f; /* 0 for empty splits (m_s = -inf) */
+    float l = 0.f, acc = 0.f;
+#pragma unroll
+    for (int u = 0; u < 32; ++u) {
+      const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wu), u));
+      l = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(lu), u)), w, l);
+      acc = __builtin_fmaf(av[u], w, acc);
+    }
+    if (d < hd) a.out[(int64_t)qh * hd + d] = (uint16_t)f32_to_f16_bits(acc / l);
+    return;
+  }
   float m = -INFINITY;
   for (int s0 = 0; s0 < ns; s0 += 16) {
     float mv[16];

@@ -72,6 +72,8 @@ def test_attention_decode_self_cache_layout(dev, nq, nkv, hd, kv_len):
     (8, 4, 52, 333, 7),
     (8, 8, 36, 100, 3),      # head_dim 36
     (4, 2, 44, 999, 9),      # run-time head_dim 44
+    (10, 10, 64, 1500, 33),  # more than 32 splits: the reduce's 16-split rounds
+    (8, 4, 52, 2000, 48),
 ])
 def test_attention_splitkv_encoder_layout(dev, nq, nkv, hd, kv_len, n_splits):
     say("attention_splitkv encoder", nq, nkv, hd, kv_len, n_splits)
