@@ -73,6 +73,17 @@ NSR_DEV void gemv_ref(const nsr_gemv_args& a) {
   const int64_t g0 = 2 * (int64_t)t;
   const int64_t g1 = (a.N >> 2) + 2 * (int64_t)t; /* gate half (glu only) */
 
+  /* the epilogue's bias or residual for column tid < NC, loaded ahead of the weights (after the reduction it
+   * would add one more memory latency to the chain) */
+  const int64_t ecol = 4 * ((tid < 8) ? g0 : g1) + (tid & 7);
+  float pre = 0.f;
+  if (tid < NC) {
+    if constexpr (MODE == GEMV_H) {
+      pre = a.residual[ecol];
+    } else {
+      if (a.bias) pre = a.bias[ecol];
+    }
+  }
   float acc[NC];
 #pragma unroll
   for (int j = 0; j < NC; ++j) acc[j] = 0.f;
@@ -121,13 +132,13 @@ NSR_DEV void gemv_ref(const nsr_gemv_args& a) {
     float v = 0.f;
 #pragma unroll
     for (int g = 0; g < G; ++g) v += red2[NC * g + tid];
-    const int64_t col = 4 * ((tid < 8) ? g0 : g1) + (tid & 7);
+    const int64_t col = ecol;
     if constexpr (MODE == GEMV_PLAIN) {
-      store_scalar<ODT>(a.out, col, a.bias ? v + a.bias[col] : v);
+      store_scalar<ODT>(a.out, col, a.bias ? v + pre : v);
     } else if constexpr (MODE == GEMV_H) {
-      a.out_f32[col] = round_to<DT_F16>(v) + a.residual[col];
+      a.out_f32[col] = round_to<DT_F16>(v) + pre;
     } else {
-      fin[tid] = a.bias ? v + a.bias[col] : v;
+      fin[tid] = a.bias ? v + pre : v;
     }
   }
   if constexpr (MODE == GEMV_GLU) {
@@ -147,6 +158,19 @@ NSR_DEV void gemv_t4(const nsr_gemv_args& a) {
   const nsr_uint4* tile = (const nsr_uint4*)a.qs + (int64_t)t * (a.K >> 2);
   const nsr_uint2* tsc = (const nsr_uint2*)a.scales + (int64_t)t * (a.K >> 5);
   const int nchunk = a.K >> 2;
+  /* the epilogue's bias or residual, loaded ahead of the tile: after the reduction it would add one more
+   * memory latency to the chain */
+  float pre0 = 0.f, pre1 = 0.f;
+  if constexpr (MODE == GEMV_PLAIN) {
+    if (tid < 4 && a.bias) pre0 = a.bias[4 * (int64_t)t + tid];
+  } else if constexpr (MODE == GEMV_H) {
+    if (tid < 4) pre0 = a.residual[4 * (int64_t)t + tid];
+  } else {
+    if (tid < 2 && a.bias) {
+      pre0 = a.bias[2 * (int64_t)t + tid];
+      pre1 = a.bias[a.N + 2 * (int64_t)t + tid];
+    }
+  }
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   for (int j = tid; j < nchunk; j += BLOCK) {
     const nsr_uint4 q = ld16(tile + j); /* rows 4j .. 4j+3, 4 columns each */
@@ -186,10 +210,10 @@ NSR_DEV void gemv_t4(const nsr_gemv_args& a) {
     for (int w = 0; w < NWV; ++w) v += red[w][tid];
     if constexpr (MODE == GEMV_PLAIN) {
       const int64_t col = 4 * (int64_t)t + tid;
-      store_scalar<ODT>(a.out, col, a.bias ? v + a.bias[col] : v);
+      store_scalar<ODT>(a.out, col, a.bias ? v + pre0 : v);
     } else if constexpr (MODE == GEMV_H) {
       const int64_t col = 4 * (int64_t)t + tid;
-      a.out_f32[col] = round_to<DT_F16>(v) + a.residual[col];
+      a.out_f32[col] = round_to<DT_F16>(v) + pre0;
     } else {
       red[0][tid] = v; /* every wave's partials were read above */
     }
@@ -198,8 +222,8 @@ NSR_DEV void gemv_t4(const nsr_gemv_args& a) {
     __syncthreads();
     if (tid < 2) {
       const int64_t col = 2 * (int64_t)t + tid;
-      const float xv = red[0][tid] + (a.bias ? a.bias[col] : 0.f);
-      const float gv = red[0][2 + tid] + (a.bias ? a.bias[a.N + col] : 0.f);
+      const float xv = red[0][tid] + pre0; /* pre0, pre1 = 0 without a bias */
+      const float gv = red[0][2 + tid] + pre1;
       store_scalar<ODT>(a.out, col, silu_f(gv) * xv);
     }
   }
