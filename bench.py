@@ -65,14 +65,17 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
-CONFIG_WORKLOADS = ["c4b", "c4a", "c0", "c1", "c1t", "c2", "c3", "c2u", "c2h"]
+CONFIG_WORKLOADS = ["c4b", "c4a", "c0", "c1", "c1t", "c2", "c3", "c2u", "c2h", "c4bh"]
 NEXT_WORKLOADS = ["dec", "dec2", "attn", "attnx", "q8fc1", "q8fc2", "q8fc1r", "q8fc2r", "q8conv", "kconv3", "kconv7",
                   "kconv11", "kconv7f", "kconv11f", "kconv3u", "kchain3", "kchain11", "mrf", "istft"]
 # same-size copies: algorithmic bytes of the config each one calibrates
-COPY_SIZES = {"c1t": 8519680, "c3": 8642560, "c2h": 9833472, "c2": 19666944, "c4a": 196616192, "c4b": 943727104}
+COPY_SIZES = {"c1t": 8519680, "c3": 8642560, "c2h": 9833472, "c2": 19666944, "c4a": 196616192, "c4b": 943727104,
+              "c4bh": 471863552}
 COPY_FOR = {"c1": "c1t", "c1t": "c1t", "c3": "c3", "c2": "c2", "c2u": "c2", "c2h": "c2h", "c4a": "c4a", "c4b": "c4b",
-            "c4a_act0": "c4a", "c4a_act1": "c4a"}
-FLOOR_WORKLOADS = ["empty"] + [f"copy_{f}_{c}" for c in COPY_SIZES for f in ("f", "p4", "p8")] + ["copy_rows_c4b"]
+            "c4bh": "c4bh", "c4a_act0": "c4a", "c4a_act1": "c4a"}
+# c4bh gets the flat copy only: the persistent-grid forms were slower than it at every other size
+FLOOR_WORKLOADS = ["empty"] + [f"copy_{f}_{c}" for c in COPY_SIZES for f in (("f",) if c == "c4bh" else ("f", "p4", "p8"))] \
+    + ["copy_rows_c4b"]
 DEFAULT_WORKLOADS = CONFIG_WORKLOADS + FLOOR_WORKLOADS + NEXT_WORKLOADS
 MALL_DEFEAT_BYTES = 512 << 20
 METRIC = "achieved HBM GB/s (% of MI355X peak) and µs/call per fused kernel"
@@ -283,6 +286,26 @@ def build_workload(name):
         alg = 2 * 2 * B * C * TT + 2 * 3 * C
         return Workload(name, f"AdaIN1d+Snake f16 activations x[{B},{C},{TT}]", alg, alg, make_set, launch,
                         "nsrk_adain_f16a_b256_nv3", "f16")
+
+    if name == "c4bh":
+        # configs[4]'s AdaIN shape through the f16-activation entry point (the reference's GPU backend runs the
+        # Kokoro decoder in f16: KokoroGpuBackend::adain_snake): x, out f16 [8, 128, 115200], f16 parameters.
+        c = configs.c4b()
+        x0 = T(c["x"].astype(np.float16))
+        g, b, a = (T(c[n].astype(np.float16)) for n in ("gamma", "beta", "alpha"))
+        B, C, TT = c["x"].shape
+        gs = C if c["gamma"].ndim == 2 else 0
+
+        def make_set(_):
+            return {"x": x0.clone(), "o": torch.empty_like(x0)}
+
+        def launch(s):
+            abi.check(L.nsr_adain_snake_f16(s["x"].data_ptr(), g.data_ptr(), b.data_ptr(), a.data_ptr(), 1, gs, gs,
+                                            s["o"].data_ptr(), B, C, TT, 1e-5, stream()))
+
+        alg = 2 * 2 * B * C * TT + 2 * (2 * B * C + C)
+        return Workload(name, f"AdaIN1d+Snake f16 activations x[{B},{C},{TT}]", alg, 2 * x0.numel() * 2, make_set,
+                        launch, "nsrk_adain_rowh_b512_v19_l10", "f16")
 
     if name == "c3":
         c = configs.c3()

@@ -732,6 +732,219 @@ NSR_ADAIN_F16A(2)
 NSR_ADAIN_F16A(3)
 NSR_ADAIN_F16A(4)
 
+/* Long aligned f16 rows (16-byte aligned, T % 8 == 0, T > 8192): the f32 row kernel's structure over
+ * 8 halves per 16-byte slot (a persistent grid, NV VGPR slots and NL LDS slots per lane, one-pass
+ * statistics with the centred pass when 4 mean^2 > var, the next row's loads refilling each slot once its
+ * output is stored, stores and refills in batches of 8). The slots hold the raw halves: the statistics
+ * and the output widen them as they read them, and the centred pass subtracts the mean there. */
+template <int BLOCK, int NV, int NL>
+NSR_DEV void adain_row_h(const nsr_adain_h_args& a, int pdt) {
+  NSR_NO_CONTRACT
+  constexpr int NW = BLOCK / 64;
+  constexpr int NS = NV + NL;
+  /* only the last MK slots may reach past the row end: the host picks NS with (NS - MK) * BLOCK <= T / 8 */
+  constexpr int MK = NS < 4 ? NS : 4;
+  extern __shared__ nsr_uint4 lds_h[];
+  __shared__ float red[4 * NW]; /* two block-sum buffers used in turn, as adain_row */
+  int rb = 0;
+
+  const int tid = threadIdx.x;
+  int64_t row = blockIdx.x;
+  if (row >= a.n_rows) return;
+  const int64_t T = a.T;
+  const int nch = (int)(T >> 3);
+  const uint32_t rbytes = (uint32_t)(T * 2);
+  const uint32_t voff = (uint32_t)tid * 16u;
+  lds_void* const lw = (lds_void*)(lds_h + __builtin_amdgcn_readfirstlane(tid & ~63));
+  const int nvalid = nch > tid ? (nch - tid + BLOCK - 1) / BLOCK : 0;
+  auto valid = [&](int k) { return k < NS - MK || k < nvalid; };
+
+  nsr_uint4 v[NV];
+  {
+    const nsr_rsrc xr = make_rsrc(a.x + row * T, rbytes);
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+      v[k] = __builtin_amdgcn_raw_buffer_load_b128(xr, voff, (uint32_t)(k * BLOCK * 16), NSR_AUX_NT);
+#pragma unroll
+    for (int m = 0; m < NL; ++m)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)((char*)lw + m * BLOCK * 16), 16, voff,
+                                               (uint32_t)((NV + m) * BLOCK * 16), 0, 0);
+  }
+  int64_t bi0, ci0;
+  row_bc32(row, a.C, bi0, ci0);
+  adain_raw pr = adain_params_load(a, pdt, bi0, ci0);
+
+  /* sums of a slot's 8 values: SUB = false, the one-pass sums straight from the packed halves with
+   * v_dot2_f32_f16 (x0 + x1 and x0^2 + x1^2 per word, the products exact in f32); SUB = true, the centred
+   * sums of the widened values minus `sub` */
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  auto sums8 = [&](auto subc, const nsr_uint4 w, float sub, bool ok, float& s, float& q) {
+    float t = 0.f, u = 0.f;
+    if constexpr (decltype(subc)::value) {
+      float f[8];
+      unpack16<DT_F16>(w, f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] -= sub;
+      t = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) u = __builtin_fmaf(f[e], f[e], u);
+    } else {
+      const h2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t wi = w[i]; /* a named copy: a bit_cast of the vector element itself reads element 0 */
+        const h2_t hw = __builtin_bit_cast(h2_t, wi);
+        t = __builtin_amdgcn_fdot2(hw, one, t, false);
+        u = __builtin_amdgcn_fdot2(hw, hw, u, false);
+      }
+    }
+    s += ok ? t : 0.f;
+    q += ok ? u : 0.f;
+  };
+  auto all_sums = [&](auto subc, float sub, float& s, float& q) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) sums8(subc, v[k], sub, valid(k), s, q);
+    /* LDS slots in groups of four, as adain_row */
+    static_for<0, (NL + 3) / 4>([&](auto gc) {
+      constexpr int g = decltype(gc)::value;
+#pragma unroll
+      for (int m = 4 * g; m < (4 * g + 4 < NL ? 4 * g + 4 : NL); ++m)
+        sums8(subc, lds_h[m * BLOCK + tid], sub, valid(NV + m), s, q);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  while (true) {
+    const int64_t next = row + gridDim.x;
+    const bool more = next < a.n_rows;
+    NSR_WAIT_VMCNT(0); /* every slot of this row has landed (VGPRs and LDS) */
+
+    float s = 0.f, q = 0.f;
+    all_sums(std::integral_constant<bool, false>{}, 0.f, s, q);
+    block_sum2<NW, false>(s, q, red + rb);
+    rb ^= 2 * NW;
+    const float mean = s * a.inv_t;
+    float var = __builtin_fmaf(-mean, mean, q * a.inv_t);
+    /* the output is (x - sub) A + Bc with Bc = beta - vshift A: sub = 0, vshift = mean in one pass; sub = mean and
+     * vshift = the f32 mean's correction c in the centred form */
+    float sub = 0.f, vshift = mean;
+    if (4.0f * mean * mean > var) {
+      float s1 = 0.f, s2 = 0.f;
+      all_sums(std::integral_constant<bool, true>{}, mean, s1, s2);
+      block_sum2<NW, false>(s1, s2, red + rb);
+      rb ^= 2 * NW;
+      vshift = s1 * a.inv_t;
+      sub = mean;
+      var = __builtin_fmaf(-vshift, s1, s2) * a.inv_t;
+    }
+    var = fmaxf(var, 0.0f);
+    const float rstd = __builtin_amdgcn_rsqf(var + a.eps); /* v_rsq_f32, about 1 ulp */
+    float gam, bet, alp;
+    adain_params_cvt(pr, pdt, gam, bet, alp);
+    const float A = (gam + 1.0f) * rstd;
+    const float Bc = __builtin_fmaf(-vshift, A, bet);
+    const snake_consts sc = make_snake_consts(alp);
+
+    if (more) {
+      int64_t bn, cn;
+      if (a.n_rows <= 0x7fffffffLL) {
+        row_bc32(next, a.C, bn, cn);
+      } else {
+        bn = next / a.C;
+        cn = next - bn * a.C;
+      }
+      pr = adain_params_load(a, pdt, bn, cn);
+    }
+    const nsr_rsrc orr = make_rsrc(a.out + row * T, rbytes);
+    const nsr_rsrc xn = make_rsrc(a.x + (more ? next : row) * T, more ? rbytes : 0u);
+    uint32_t vo = voff, so;
+    asm volatile("" : "+v"(vo));
+    asm volatile("s_mov_b32 %0, 0" : "=s"(so));
+    lds_void* lwr = lw;
+    asm volatile("" : "+s"(lwr));
+    /* SUB = false (one pass): x A + Bc straight from each packed half (v_fma_mix_f32); SUB = true: the widened
+     * x minus the mean first, which keeps the cancellation out of rows with |mean| >> std */
+    auto out8 = [&](auto subc, const nsr_uint4 w) {
+      float f[8];
+      if constexpr (decltype(subc)::value) {
+        unpack16<DT_F16>(w, f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = snake_eval(__builtin_fmaf(f[e] - sub, A, Bc), sc);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t wi = w[i];
+          const h2_t hw = __builtin_bit_cast(h2_t, wi);
+          f[2 * i] = snake_eval(__builtin_fmaf((float)hw.x, A, Bc), sc);
+          f[2 * i + 1] = snake_eval(__builtin_fmaf((float)hw.y, A, Bc), sc);
+        }
+      }
+      return pack16<DT_F16>(f);
+    };
+    constexpr int SB = 8;
+    auto store_pass = [&](auto subc) {
+    static_for<0, (NV + SB - 1) / SB>([&](auto gc) {
+      constexpr int k0 = decltype(gc)::value * SB;
+      constexpr int k1 = k0 + SB < NV ? k0 + SB : NV;
+#pragma unroll
+      for (int k = k0; k < k1; ++k)
+        __builtin_amdgcn_raw_buffer_store_b128(out8(subc, v[k]), orr, vo + (uint32_t)(k * BLOCK * 16), 0, NSR_AUX_NT);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = k0; k < k1; ++k)
+        v[k] = __builtin_amdgcn_raw_buffer_load_b128(xn, vo, so + (uint32_t)(k * BLOCK * 16), NSR_AUX_NT);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    static_for<0, (NL + SB - 1) / SB>([&](auto gc) {
+      constexpr int m0 = decltype(gc)::value * SB;
+      constexpr int m1 = m0 + SB < NL ? m0 + SB : NL;
+#pragma unroll
+      for (int m = m0; m < m1; ++m)
+        __builtin_amdgcn_raw_buffer_store_b128(out8(subc, lds_h[m * BLOCK + tid]), orr,
+                                               vo + (uint32_t)((NV + m) * BLOCK * 16), 0, NSR_AUX_NT);
+      __builtin_amdgcn_sched_barrier(0);
+      /* each slot's LDS read above has completed: its value was stored */
+#pragma unroll
+      for (int m = m0; m < m1; ++m)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xn, (lds_void*)((char*)lwr + m * BLOCK * 16), 16, vo,
+                                                 so + (uint32_t)((NV + m) * BLOCK * 16), 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    };
+    if (sub == 0.f) {
+      store_pass(std::integral_constant<bool, false>{});
+    } else {
+      store_pass(std::integral_constant<bool, true>{});
+    }
+    if (!more) break;
+    row = next;
+  }
+}
+
+#define NSR_ADAIN_ROW_H(BLOCK, NV, NL)                                                      \
+  extern "C" __global__ void __launch_bounds__(BLOCK)                                      \
+      nsrk_adain_rowh_b##BLOCK##_v##NV##_l##NL(const nsr_adain_h_args a, const int pdt) {  \
+    adain_row_h<BLOCK, NV, NL>(a, pdt);                                                    \
+  }
+
+/* aligned f16 rows of 20-32 slots (77,832 <= T <= 131,072): 10 LDS slots (80 KB) and the VGPR slots the row
+ * still needs. Measured on MI355X at [8, 128, 115200] f16 (29 slots), minimum of 5 x 20 calls: 19 VGPR +
+ * 10 LDS slots 88.2-88.9 us, 10 + 19 88.5-89.8 us, 29 VGPR slots 92.2-92.5 us, against 113.7-118.2 us for
+ * the one-workgroup-per-row kernel above, which holds one row per CU at a time. */
+NSR_ADAIN_ROW_H(512, 10, 10)
+NSR_ADAIN_ROW_H(512, 11, 10)
+NSR_ADAIN_ROW_H(512, 12, 10)
+NSR_ADAIN_ROW_H(512, 13, 10)
+NSR_ADAIN_ROW_H(512, 14, 10)
+NSR_ADAIN_ROW_H(512, 15, 10)
+NSR_ADAIN_ROW_H(512, 16, 10)
+NSR_ADAIN_ROW_H(512, 17, 10)
+NSR_ADAIN_ROW_H(512, 18, 10)
+NSR_ADAIN_ROW_H(512, 19, 10)
+NSR_ADAIN_ROW_H(512, 20, 10)
+NSR_ADAIN_ROW_H(512, 21, 10)
+NSR_ADAIN_ROW_H(512, 22, 10)
+
 /* ------------------------------------------------ row statistics, long rows -- */
 
 /* Sum and sum of squares of one row over 1024 lanes in f64, one HBM read:

@@ -833,6 +833,43 @@ nsr_status nsr_adain_snake_f16(const void* x, const void* gamma, const void* bet
     void* params[] = {&a, &pdt};
     return launch(ids[(T / 8 + 255) / 256 - 1], (unsigned)n_rows, 1, 256, 0, stream, params);
   }
+  if (aligned(x, 16) && aligned(out, 16) && T % 8 == 0 && T / 8 > 512 * 19) {
+    // long aligned rows (20-32 slots of 512 lanes x 8 halves): the persistent row kernel, 10 slots in LDS and
+    // the rest in VGPRs, each CU's reads of its next row overlapping its writes of this one
+    static const KId ids[] = {K_nsrk_adain_rowh_b512_v10_l10, K_nsrk_adain_rowh_b512_v11_l10,
+                              K_nsrk_adain_rowh_b512_v12_l10, K_nsrk_adain_rowh_b512_v13_l10,
+                              K_nsrk_adain_rowh_b512_v14_l10, K_nsrk_adain_rowh_b512_v15_l10,
+                              K_nsrk_adain_rowh_b512_v16_l10, K_nsrk_adain_rowh_b512_v17_l10,
+                              K_nsrk_adain_rowh_b512_v18_l10, K_nsrk_adain_rowh_b512_v19_l10,
+                              K_nsrk_adain_rowh_b512_v20_l10, K_nsrk_adain_rowh_b512_v21_l10,
+                              K_nsrk_adain_rowh_b512_v22_l10};
+    const int64_t slots = (T / 8 + 511) / 512; /* 20..32 (T <= 131072) */
+    const unsigned lds = 10u * 512u * 16u;
+    DeviceModule* dm = nullptr;
+    nsr_status st = current_module(&dm);
+    if (st != NSR_OK) return st;
+    if (slots <= 32 && lds + 1024 <= (unsigned)dm->max_lds) {
+      const KId kid = ids[slots - 20];
+      nsr_adain_h_args a;
+      std::memset(&a, 0, sizeof(a));
+      a.x = (const uint16_t*)x;
+      a.gamma = gamma;
+      a.beta = beta;
+      a.alpha = alpha;
+      a.out = (uint16_t*)out;
+      a.n_rows = n_rows;
+      a.T = T;
+      a.gamma_bstride = gamma_bstride;
+      a.beta_bstride = beta_bstride;
+      a.C = (int32_t)C;
+      a.eps = eps;
+      a.inv_t = 1.0f / (float)T;
+      int pdt = param_dtype == NSR_F32 ? 0 : 1;
+      void* params[] = {&a, &pdt};
+      const unsigned grid = (unsigned)std::min<int64_t>(n_rows, (int64_t)occupancy(dm, kid, 512, lds) * dm->n_cu);
+      return launch(kid, grid, 1, 512, lds, stream, params);
+    }
+  }
   // interior 16-byte chunks of a row, at the worst offset (7 elements into its first chunk)
   const int64_t need = (T + 14) / 8 - 2;
   unsigned block = 0;
