@@ -607,7 +607,7 @@ NSR_DEV void adain_row_f16(const nsr_adain_h_args& a, int pdt) {
   adain_params_cvt(pr, pdt, gam, bet, alp);
   const float A = (gam + 1.0f) * rstd;
   const float Bc = __builtin_fmaf(-c, A, bet); /* (x - mean - c) A + beta */
-  const snake_consts sc = make_snake_consts(alp);
+  const snake_consts_h sc = make_snake_consts_h(alp); /* f16 output */
 
 #pragma unroll
   for (int k = 0; k < NV; ++k) asm volatile("" : "+v"(v[k]));
@@ -709,7 +709,7 @@ NSR_DEV void adain_row_f16a(const nsr_adain_h_args& a, int pdt) {
   adain_params_cvt(pr, pdt, gam, bet, alp);
   const float A = (gam + 1.0f) * rstd;
   const float Bc = __builtin_fmaf(-vshift, A, bet);
-  const snake_consts sc = make_snake_consts(alp);
+  const snake_consts_h sc = make_snake_consts_h(alp); /* f16 output */
   const nsr_rsrc orr = make_rsrc(a.out + row * T, rbytes);
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
@@ -843,7 +843,7 @@ NSR_DEV void adain_row_h(const nsr_adain_h_args& a, int pdt) {
     adain_params_cvt(pr, pdt, gam, bet, alp);
     const float A = (gam + 1.0f) * rstd;
     const float Bc = __builtin_fmaf(-vshift, A, bet);
-    const snake_consts sc = make_snake_consts(alp);
+    const snake_consts_h sc = make_snake_consts_h(alp); /* f16 output */
 
     if (more) {
       int64_t bn, cn;
