@@ -153,12 +153,24 @@ NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
   auto valid = [&](int k) { return k < NS - MK || k < nvalid; };
   const nsr_float4 zero4 = {0.f, 0.f, 0.f, 0.f};
 
+  /* Cache policy of the loads: VGPR slots non-temporal (streamed), LDS slots cached, and with 21 or more VGPR
+   * slots beside 19 LDS slots the first KC = 8 VGPR slots cached too. Measured on MI355X, [8, 128, T] f32,
+   * minimum / median of 5 x 20 calls, against every VGPR slot streamed: T = 115,200 (38 VGPR slots)
+   * 151.2-151.7 / 153.3-154.3 against 156.5-156.9 / 157.8-158.0 us (4, 6, 10 and 12 cached slots within
+   * 1 us of 8; all 19 LDS-slot loads streamed too: 173 us; every load cached: 180 us); T = 81,920 (21 VGPR
+   * slots) 109.8 / 111.3 against 111.4-111.8 / 112.9-114.2 us; T = 98,304 (29 VGPR slots, 5 cached)
+   * 126.1 / 127.7 against 128.7-129.5 / 129.9-130.3 us. Output is the same bits either way. */
+  constexpr int KC = (NL == 19 && NV >= 21) ? 8 : 0;
+  auto vload = [&](nsr_rsrc r, int k, uint32_t vo, uint32_t so) {
+    return k < KC ? buf_load4c(r, vo, so) : buf_load4(r, vo, so);
+  };
+
   /* first row: every slot's load, then the parameters */
   nsr_float4 v[NV];
   {
     const nsr_rsrc xr = make_rsrc(a.x + row * T, rbytes);
 #pragma unroll
-    for (int k = 0; k < NV; ++k) v[k] = buf_load4(xr, voff, (uint32_t)(k * BLOCK * 16));
+    for (int k = 0; k < NV; ++k) v[k] = vload(xr, k, voff, (uint32_t)(k * BLOCK * 16));
 #pragma unroll
     for (int m = 0; m < NL; ++m)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)((char*)lw + m * BLOCK * 16), 16, voff,
@@ -275,7 +287,7 @@ NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
       for (int k = k0; k < k1; ++k) buf_store4(orr, vo, (uint32_t)(k * BLOCK * 16), adain_snake4(v[k], A, Bc, sc));
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int k = k0; k < k1; ++k) v[k] = buf_load4(xn, vo, so + (uint32_t)(k * BLOCK * 16));
+      for (int k = k0; k < k1; ++k) v[k] = vload(xn, k, vo, so + (uint32_t)(k * BLOCK * 16));
       __builtin_amdgcn_sched_barrier(0);
     });
     static_for<0, (NL + SB - 1) / SB>([&](auto gc) {

@@ -426,6 +426,11 @@ NSR_DEV nsr_float4 buf_load4(nsr_rsrc r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(nsr_float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, NSR_AUX_NT));
 }
 
+/* buf_load4 without the non-temporal bit (the line is cached as a normal load's) */
+NSR_DEV nsr_float4 buf_load4c(nsr_rsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(nsr_float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
 /* 16-byte store at voff + off with soffset 0. Stores carry their offset in
  * the VGPR address, never in soffset: the compiler exempts MUBUF stores with
  * an SGPR soffset from the wait state that a VALU write of the store's data
