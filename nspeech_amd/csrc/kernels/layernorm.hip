@@ -86,11 +86,11 @@ NSR_DEV void load_param_vec(const void* p, int pdt, int col0, float* v, float fi
 /* Raw 16-byte words of one VEC-element chunk of dtype DT (1 or 2 words). */
 template <int DT, int VEC> struct chunk_words { static constexpr int value = VEC * dt_size<DT>::value / 16; };
 
-template <int DT, int VEC>
+template <int DT, int VEC, bool CACHED = false>
 NSR_DEV void load_raw(const void* base, int64_t elem, nsr_uint4* w) {
   const char* p = (const char*)base + elem * dt_size<DT>::value;
 #pragma unroll
-  for (int i = 0; i < chunk_words<DT, VEC>::value; ++i) w[i] = ld16(p + 16 * i);
+  for (int i = 0; i < chunk_words<DT, VEC>::value; ++i) w[i] = CACHED ? ld16_cached(p + 16 * i) : ld16(p + 16 * i);
 }
 
 template <int DT, int VEC>
@@ -146,7 +146,11 @@ NSR_DEV void ln_row_wave(const nsr_ln_args& a, int pdt) {
     for (int k = 0; k < NC; ++k) {
       const int j = lane + 64 * k;
       if (j < nchunk) {
-        load_raw<X, VEC>(a.x, r * a.ld_x + (int64_t)j * VEC, rx[k]);
+        /* fused: x loaded cached and the residual streamed. Measured on MI355X at c4a ([24000, 1024] bf16,
+         * GELU, 200 calls back to back, minimum / median of 5): 30.9-31.1 / 31.1-31.2 us against 33.3-33.4 /
+         * 33.5 us with both streamed; the residual cached instead 31.2-31.3 us, both cached 32.8-32.9 us.
+         * The same output bits. */
+        load_raw<X, VEC, FUSED>(a.x, r * a.ld_x + (int64_t)j * VEC, rx[k]);
         if constexpr (FUSED) load_raw<R, VEC>(a.res, r * a.ld_x + (int64_t)j * VEC, rr[k]);
       }
     }
