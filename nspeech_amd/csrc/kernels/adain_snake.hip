@@ -153,14 +153,15 @@ NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
   auto valid = [&](int k) { return k < NS - MK || k < nvalid; };
   const nsr_float4 zero4 = {0.f, 0.f, 0.f, 0.f};
 
-  /* Cache policy of the loads: VGPR slots non-temporal (streamed), LDS slots cached, and with 21 or more VGPR
-   * slots beside 19 LDS slots the first KC = 8 VGPR slots cached too. Measured on MI355X, [8, 128, T] f32,
-   * minimum / median of 5 x 20 calls, against every VGPR slot streamed: T = 115,200 (38 VGPR slots)
-   * 151.2-151.7 / 153.3-154.3 against 156.5-156.9 / 157.8-158.0 us (4, 6, 10 and 12 cached slots within
-   * 1 us of 8; all 19 LDS-slot loads streamed too: 173 us; every load cached: 180 us); T = 81,920 (21 VGPR
-   * slots) 109.8 / 111.3 against 111.4-111.8 / 112.9-114.2 us; T = 98,304 (29 VGPR slots, 5 cached)
-   * 126.1 / 127.7 against 128.7-129.5 / 129.9-130.3 us. Output is the same bits either way. */
-  constexpr int KC = (NL == 19 && NV >= 21) ? 8 : 0;
+  /* Cache policy of the loads: LDS slots cached, the first KC = min(NV, 8) VGPR slots cached beside 19 LDS
+   * slots, the other VGPR slots non-temporal (streamed). Measured on MI355X, [8, 128, T] f32, minimum / median
+   * of 5 x 20 calls, against every VGPR slot streamed: T = 115,200 (38 VGPR slots) 151.2-151.7 / 153.3-154.3
+   * against 156.5-156.9 / 157.8-158.0 us (4, 6, 10 and 12 cached slots within 1 us of 8; all 19 LDS-slot loads
+   * streamed too: 173 us; every load cached: 180 us); T = 81,920 (21) 109.8 / 111.3 against 111.4-111.8 /
+   * 112.9-114.2 us; T = 61,440 (11) 73.9 / 76.5 against 78.2 / 80.8 us; T = 53,248 (7, all cached) 65.3-65.5
+   * / 67.1-67.3 against 66.4-66.6 / 69.1-69.4 us; T = 40,960 (1) 51.5 / 52.7 against 53.1-53.2 / 54.6-55.1 us.
+   * Output is the same bits either way. */
+  constexpr int KC = NL == 19 ? (NV < 8 ? NV : 8) : 0;
   auto vload = [&](nsr_rsrc r, int k, uint32_t vo, uint32_t so) {
     return k < KC ? buf_load4c(r, vo, so) : buf_load4(r, vo, so);
   };
