@@ -160,8 +160,11 @@ NSR_DEV void adain_row(const nsr_adain_args& a, int pdt) {
    * streamed too: 173 us; every load cached: 180 us); T = 81,920 (21) 109.8 / 111.3 against 111.4-111.8 /
    * 112.9-114.2 us; T = 61,440 (11) 73.9 / 76.5 against 78.2 / 80.8 us; T = 53,248 (7, all cached) 65.3-65.5
    * / 67.1-67.3 against 66.4-66.6 / 69.1-69.4 us; T = 40,960 (1) 51.5 / 52.7 against 53.1-53.2 / 54.6-55.1 us.
-   * Output is the same bits either way. */
-  constexpr int KC = NL == 19 ? (NV < 8 ? NV : 8) : 0;
+   * VGPR-only 512-lane kernels of 16 and 20 slots (two workgroups per CU) cache half their slots: T = 38,912
+   * (20 slots) 51.6-51.7 against 54.9-55.3 us (8 cached: 53.1-53.3), T = 32,768 (16) 43.5 against 45.3 us;
+   * with 10 or 12 slots (three or four workgroups per CU) caching gained nothing (27.1-27.2 / 33.6-33.7
+   * against 26.9-27.2 / 33.8 us). Output is the same bits either way. */
+  constexpr int KC = NL == 19 ? (NV < 8 ? NV : 8) : (BLOCK == 512 && NV >= 16 ? NV / 2 : 0);
   auto vload = [&](nsr_rsrc r, int k, uint32_t vo, uint32_t so) {
     return k < KC ? buf_load4c(r, vo, so) : buf_load4(r, vo, so);
   };
